@@ -1,0 +1,257 @@
+// C ABI of libdsk_moe: host-side validation, workspace layout and launch
+// sequencing.  No entry point allocates device memory or synchronises; every
+// check happens on the host before the first launch, so a failed call leaves
+// the stream untouched.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "dsk_internal.h"
+
+namespace dsk {
+
+static thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return DSK_OK;
+  return fail(DSK_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+static size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+Workspace workspace_layout(const dsk_moe_desc& d) {
+  Workspace L{};
+  const size_t T = static_cast<size_t>(d.tokens), H = d.hidden, E = d.n_experts, k = d.top_k;
+  const size_t I = d.inter, Is = d.inter_shared, N = T * k;
+  size_t o = 0;
+  auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes); return at; };
+  L.scores = take(T * E * 4);
+  L.idx = take(N * 4);
+  L.wts = take(N * 4);
+  L.counts = take(E * 4);
+  L.offsets = take((E + 1) * 4);
+  L.perm = take(N * 4);
+  L.rank = take(N * 4);
+  L.active = take((E + 1) * 4);
+  const size_t xplane = (d.x_dtype == DSK_DTYPE_F32) ? T * H * 2 : 0;
+  L.xb_hi = take(xplane);
+  L.xb_lo = take(xplane);
+  L.h_hi = take(N * I * 2);
+  L.h_lo = take(N * I * 2);
+  L.hs_hi = take(T * Is * 2);
+  L.hs_lo = take(T * Is * 2);
+  L.y = take(N * H * 4);
+  L.ys = take(T * H * 4);
+  L.total = o;
+  return L;
+}
+
+}  // namespace dsk
+
+using namespace dsk;
+
+static int check_desc(const dsk_moe_desc* d) {
+  if (!d) return fail(DSK_EINVAL, "desc is NULL");
+  if (d->tokens < 1) return fail(DSK_EINVAL, "tokens=%d must be >= 1", d->tokens);
+  if (d->n_experts < 1 || d->n_experts > 1024)
+    return fail(DSK_EINVAL, "n_experts=%d must be in [1, 1024]", d->n_experts);
+  if (d->top_k < 1 || d->top_k > 16 || d->top_k > d->n_experts)
+    return fail(DSK_EINVAL, "top_k=%d must be in [1, min(16, n_experts)]", d->top_k);
+  if (d->score_func != DSK_SCORE_SIGMOID && d->score_func != DSK_SCORE_SQRTSOFTPLUS)
+    return fail(DSK_EINVAL, "unknown score_func %d", d->score_func);
+  if (d->x_dtype != DSK_DTYPE_BF16 && d->x_dtype != DSK_DTYPE_F32)
+    return fail(DSK_EINVAL, "x_dtype %d must be BF16 or F32", d->x_dtype);
+  if (d->gate_dtype != DSK_DTYPE_BF16 && d->gate_dtype != DSK_DTYPE_F32)
+    return fail(DSK_EINVAL, "gate_dtype %d must be BF16 or F32", d->gate_dtype);
+  if (d->hidden < 32 || d->hidden % 32)
+    return fail(DSK_EINVAL, "hidden=%d must be a positive multiple of 32", d->hidden);
+  if (static_cast<int64_t>(d->tokens) * d->top_k > (1 << 24))
+    return fail(DSK_EINVAL, "tokens*top_k=%lld exceeds 2^24",
+                static_cast<long long>(d->tokens) * d->top_k);
+  return DSK_OK;
+}
+
+static int check_expert_desc(const dsk_moe_desc* d) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (d->quant == DSK_QUANT_FP4) {
+    if (d->inter < 32 || d->inter % 32)
+      return fail(DSK_EINVAL, "inter=%d must be a positive multiple of 32 for FP4", d->inter);
+  } else if (d->quant == DSK_QUANT_Q3) {
+    return fail(DSK_EUNSUPPORTED, "Q3 experts are not available in this build of dsk_experts");
+  } else {
+    return fail(DSK_EINVAL, "unknown quant %d", d->quant);
+  }
+  if (d->inter_shared < 0 || d->inter_shared % 32)
+    return fail(DSK_EINVAL, "inter_shared=%d must be 0 or a positive multiple of 32", d->inter_shared);
+  if (!(d->limit > 0.0f)) return fail(DSK_EINVAL, "limit must be > 0");
+  return DSK_OK;
+}
+
+static bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+extern "C" {
+
+int dsk_abi_version(void) { return DSK_ABI_VERSION; }
+
+const char* dsk_last_error(void) { return g_err; }
+
+int dsk_workspace_size(const dsk_moe_desc* d, size_t* bytes) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!bytes) return fail(DSK_EINVAL, "bytes is NULL");
+  *bytes = workspace_layout(*d).total;
+  return DSK_OK;
+}
+
+int dsk_route(const dsk_moe_desc* d, const void* x, const void* gate_w, const float* gate_b,
+              float* scores, int32_t* idx, float* weights, void* stream) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!x || !gate_w || !gate_b || !scores || !idx || !weights)
+    return fail(DSK_EINVAL, "dsk_route: NULL pointer argument");
+  if (!aligned(x, 16) || !aligned(gate_w, 16))
+    return fail(DSK_EALIGN, "dsk_route: x and gate_w must be 16-byte aligned");
+  return hip_check(launch_route(*d, x, gate_w, gate_b, scores, idx, weights,
+                                static_cast<hipStream_t>(stream)),
+                   "dsk_route launch");
+}
+
+int dsk_dispatch(const dsk_moe_desc* d, const int32_t* idx, int32_t* counts, int32_t* offsets,
+                 int32_t* perm, int32_t* rank, int32_t* active, void* stream) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!idx || !counts || !offsets || !perm || !rank || !active)
+    return fail(DSK_EINVAL, "dsk_dispatch: NULL pointer argument");
+  return hip_check(launch_dispatch(*d, idx, counts, offsets, perm, rank, active,
+                                   static_cast<hipStream_t>(stream)),
+                   "dsk_dispatch launch");
+}
+
+int dsk_experts(const dsk_moe_desc* d, const dsk_expert_ptrs* table, const void* ws1,
+                const void* ws3, const void* ws2, const void* shared_out, const void* x,
+                const float* weights,
+                const int32_t* counts, const int32_t* offsets, const int32_t* perm,
+                const int32_t* rank, const int32_t* active, void* out, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  int rc = check_expert_desc(d);
+  if (rc) return rc;
+  if (!table || !x || !weights || !counts || !offsets || !perm || !rank || !active || !out ||
+      !workspace)
+    return fail(DSK_EINVAL, "dsk_experts: NULL pointer argument");
+  if (d->inter_shared > 0 && (!ws1 || !ws3 || !ws2))
+    return fail(DSK_EINVAL, "dsk_experts: shared expert weights are NULL but inter_shared=%d",
+                d->inter_shared);
+  if (shared_out && !aligned(shared_out, 16))
+    return fail(DSK_EALIGN, "dsk_experts: shared_out must be 16-byte aligned");
+  if (!aligned(x, 16) || !aligned(out, 16) || !aligned(workspace, 256) ||
+      (d->inter_shared > 0 && (!aligned(ws1, 16) || !aligned(ws3, 16) || !aligned(ws2, 16))))
+    return fail(DSK_EALIGN, "dsk_experts: x/out/shared weights need 16-byte, workspace 256-byte alignment");
+  const Workspace L = workspace_layout(*d);
+  if (workspace_bytes < L.total)
+    return fail(DSK_ESPACE, "workspace %zu bytes < required %zu", workspace_bytes, L.total);
+  ExpertsArgs a{};
+  a.table = table; a.ws1 = ws1; a.ws3 = ws3; a.ws2 = ws2; a.shared_out = shared_out; a.x = x; a.weights = weights;
+  a.counts = counts; a.offsets = offsets; a.perm = perm; a.rank = rank; a.active = active;
+  a.out = out; a.ws = static_cast<char*>(workspace);
+  return hip_check(launch_experts(*d, L, a, static_cast<hipStream_t>(stream)), "dsk_experts launch");
+}
+
+int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, const float* gate_b,
+                    const dsk_expert_ptrs* table, const void* ws1, const void* ws3,
+                    const void* ws2, const void* shared_out, void* out, int32_t* idx,
+                    float* weights, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  int rc = check_expert_desc(d);
+  if (rc) return rc;
+  if (!x || !gate_w || !gate_b || !table || !out || !workspace)
+    return fail(DSK_EINVAL, "dsk_moe_forward: NULL pointer argument");
+  if (d->inter_shared > 0 && (!ws1 || !ws3 || !ws2))
+    return fail(DSK_EINVAL, "dsk_moe_forward: shared expert weights are NULL but inter_shared=%d",
+                d->inter_shared);
+  if (shared_out && !aligned(shared_out, 16))
+    return fail(DSK_EALIGN, "dsk_moe_forward: shared_out must be 16-byte aligned");
+  if (!aligned(x, 16) || !aligned(gate_w, 16) || !aligned(out, 16) || !aligned(workspace, 256) ||
+      (d->inter_shared > 0 && (!aligned(ws1, 16) || !aligned(ws3, 16) || !aligned(ws2, 16))))
+    return fail(DSK_EALIGN, "dsk_moe_forward: x/gate_w/out/shared need 16-byte, workspace 256-byte alignment");
+  const Workspace L = workspace_layout(*d);
+  if (workspace_bytes < L.total)
+    return fail(DSK_ESPACE, "workspace %zu bytes < required %zu", workspace_bytes, L.total);
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* scores = reinterpret_cast<float*>(ws + L.scores);
+  int32_t* idx_buf = idx ? idx : reinterpret_cast<int32_t*>(ws + L.idx);
+  float* w_buf = weights ? weights : reinterpret_cast<float*>(ws + L.wts);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws + L.counts);
+  int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+  int32_t* perm = reinterpret_cast<int32_t*>(ws + L.perm);
+  int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
+  int32_t* active = reinterpret_cast<int32_t*>(ws + L.active);
+  rc = hip_check(launch_route(*d, x, gate_w, gate_b, scores, idx_buf, w_buf, s), "route launch");
+  if (rc) return rc;
+  rc = hip_check(launch_dispatch(*d, idx_buf, counts, offsets, perm, rank, active, s),
+                 "dispatch launch");
+  if (rc) return rc;
+  ExpertsArgs a{};
+  a.table = table; a.ws1 = ws1; a.ws3 = ws3; a.ws2 = ws2; a.shared_out = shared_out; a.x = x; a.weights = w_buf;
+  a.counts = counts; a.offsets = offsets; a.perm = perm; a.rank = rank; a.active = active;
+  a.out = out; a.ws = ws;
+  return hip_check(launch_experts(*d, L, a, s), "experts launch");
+}
+
+int dsk_fp4_dequant(const uint8_t* packed, const uint8_t* scales, int64_t rows, int64_t cols,
+                    void* out, int32_t out_dtype, void* stream) {
+  if (!packed || !scales || !out) return fail(DSK_EINVAL, "dsk_fp4_dequant: NULL pointer argument");
+  if (rows < 0 || cols < 0 || cols % 32) return fail(DSK_EINVAL, "cols=%lld must be a multiple of 32", (long long)cols);
+  if (out_dtype != DSK_DTYPE_F32 && out_dtype != DSK_DTYPE_BF16)
+    return fail(DSK_EINVAL, "out_dtype %d must be F32 or BF16", out_dtype);
+  if (!aligned(packed, 16) || !aligned(out, 16))
+    return fail(DSK_EALIGN, "dsk_fp4_dequant: packed and out must be 16-byte aligned");
+  return hip_check(launch_fp4_dequant(packed, scales, rows, cols, out, out_dtype,
+                                      static_cast<hipStream_t>(stream)),
+                   "dsk_fp4_dequant launch");
+}
+
+int dsk_fp4_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* packed, uint8_t* scales,
+                     void* stream) {
+  if (!w || !packed || !scales) return fail(DSK_EINVAL, "dsk_fp4_quantize: NULL pointer argument");
+  if (rows < 0 || cols < 0 || cols % 32) return fail(DSK_EINVAL, "cols=%lld must be a multiple of 32", (long long)cols);
+  if (!aligned(w, 16) || !aligned(packed, 16))
+    return fail(DSK_EALIGN, "dsk_fp4_quantize: w and packed must be 16-byte aligned");
+  return hip_check(launch_fp4_quantize(w, rows, cols, packed, scales, static_cast<hipStream_t>(stream)),
+                   "dsk_fp4_quantize launch");
+}
+
+int dsk_q3_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* packed, uint16_t* scales,
+                    uint16_t* biases, void* stream) {
+  if (!w || !packed || !scales || !biases) return fail(DSK_EINVAL, "dsk_q3_quantize: NULL pointer argument");
+  if (rows < 0 || cols < 0 || cols % 128) return fail(DSK_EINVAL, "cols=%lld must be a multiple of 128", (long long)cols);
+  if (!aligned(w, 4) || !aligned(packed, 4) || !aligned(scales, 2) || !aligned(biases, 2))
+    return fail(DSK_EALIGN, "dsk_q3_quantize: misaligned pointer");
+  return hip_check(launch_q3_quantize(w, rows, cols, packed, scales, biases,
+                                      static_cast<hipStream_t>(stream)),
+                   "dsk_q3_quantize launch");
+}
+
+int dsk_q3_dequant(const uint8_t* packed, const uint16_t* scales, const uint16_t* biases,
+                   int64_t rows, int64_t cols, void* out, int32_t out_dtype, void* stream) {
+  if (!packed || !scales || !biases || !out) return fail(DSK_EINVAL, "dsk_q3_dequant: NULL pointer argument");
+  if (rows < 0 || cols < 0 || cols % 128) return fail(DSK_EINVAL, "cols=%lld must be a multiple of 128", (long long)cols);
+  if (out_dtype != DSK_DTYPE_F32 && out_dtype != DSK_DTYPE_BF16)
+    return fail(DSK_EINVAL, "out_dtype %d must be F32 or BF16", out_dtype);
+  if (!aligned(packed, 4) || !aligned(out, 4))
+    return fail(DSK_EALIGN, "dsk_q3_dequant: misaligned pointer");
+  return hip_check(launch_q3_dequant(packed, scales, biases, rows, cols, out, out_dtype,
+                                     static_cast<hipStream_t>(stream)),
+                   "dsk_q3_dequant launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,485 @@
+// Routed experts, shared expert and combine of the MoE layer.
+//
+// Replaces the per-expert loop of the reference's moe_layer
+// (src/deepseeker/mlx_forward.py:388-406: gate/up qmm, clamp, SiLU, route
+// weight, w2 qmm, scatter-add), the shared expert
+// (src/deepseeker/mlx_runner.py:765-783) and the final add and cast
+// (mlx_forward.py:409-419).
+//
+// Decode-shaped products run on MFMA tiles of 16 weight rows x 16 token
+// slots (v_mfma_f32_16x16x32_bf16).  Lane l of a wave owns weight row
+// (l & 15) and token slot (l & 15); its lane group g = l >> 4 owns the
+// 32-code K chunk [128*b + 32*g, +32) of K block b, loaded as one 128-bit word
+// of FP4 codes plus one E8M0 byte (or 64 bytes of bf16 weights), so a wave
+// reads 16 rows x 64 contiguous bytes per FP4 block.  Word j of that chunk
+// (codes 32g+8j .. +8) is MFMA j's A operand; the B operand of the same lane
+// is the activation at exactly those K positions, so A and B agree on the
+// K-slot mapping.  FP4 is decoded with v_cvt_scalef32_pk_bf16_fp4 (two codes
+// per instruction, E8M0 scale applied; e2m1 x 2^k is exact in bf16).
+// Split-K: the waves of a block take K blocks round-robin and reduce their
+// 16x16 partials through LDS in a fixed order.
+//
+// Numerics: products are exact (bf16 x bf16) and accumulate in float32.
+// Activations that are not bf16 already (float32 x, the float32 intermediate
+// h) are fed as a bf16 hi/lo pair (x = hi + lo, two MFMAs), which keeps them
+// to about 2^-17 relative error.  h = silu(min(g,L)) * clip(u,-L,L) * w_route
+// is applied in float32 before the split, as in the reference (route weight
+// before w2).  The combine sums each token's expert outputs in ascending
+// expert id, then adds the shared output rounded to x's dtype, in float32.
+#include "dsk_internal.h"
+
+namespace dsk {
+namespace {
+
+constexpr int kUpWaves = 8;     // split-K ways of the gate/up kernel (K = H)
+constexpr int kDownWaves = 4;   // split-K ways of the down kernel (K = I)
+
+__device__ __forceinline__ f32x4 mfma(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ bf16x8 fp4_word_to_bf16x8(uint32_t word, float scale) {
+  bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
+  bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
+  bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
+  bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
+  u32x4 r{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+          __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)};
+  return as_bf16x8(r);
+}
+
+__device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Raw A-operand data of one lane for one K block.
+struct RawFP4 { u32x4 c; uint32_t s; };
+struct RawBF16 { u32x4 v[4]; };
+
+__device__ __forceinline__ RawFP4 load_fp4(const uint8_t* W, const uint8_t* S, int64_t row,
+                                           int K, int kc, bool ok) {
+  RawFP4 r;
+  if (ok) {
+    r.c = ldg16(W + row * (K / 2) + kc / 2);
+    r.s = S[row * (K / 32) + kc / 32];
+  } else {
+    r.c = u32x4{0u, 0u, 0u, 0u};
+    r.s = 127u;
+  }
+  return r;
+}
+
+__device__ __forceinline__ RawBF16 load_bf16w(const uint16_t* W, int64_t row, int K, int kc, bool ok) {
+  RawBF16 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    r.v[j] = ok ? ldg16(W + row * K + kc + 8 * j) : u32x4{0u, 0u, 0u, 0u};
+  return r;
+}
+
+__device__ __forceinline__ void deq(const RawFP4& r, bf16x8 a[4]) {
+  const float sc = e8m0_to_f32(r.s);
+  a[0] = fp4_word_to_bf16x8(r.c.x, sc);
+  a[1] = fp4_word_to_bf16x8(r.c.y, sc);
+  a[2] = fp4_word_to_bf16x8(r.c.z, sc);
+  a[3] = fp4_word_to_bf16x8(r.c.w, sc);
+}
+
+__device__ __forceinline__ void deq(const RawBF16& r, bf16x8 a[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) a[j] = as_bf16x8(r.v[j]);
+}
+
+// B operand (16-bit activations) of one lane for one K block.
+__device__ __forceinline__ void load_b(const uint16_t* plane, int64_t row, int K, int kc, bool ok,
+                                       bf16x8 b[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    b[j] = as_bf16x8(ok ? ldg16(plane + row * K + kc + 8 * j) : u32x4{0u, 0u, 0u, 0u});
+}
+
+__device__ __forceinline__ void split_store(uint16_t* hi, uint16_t* lo, int64_t off, const float v[4]) {
+  uint16_t h[4], l[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    h[q] = f32_to_bf16_bits(v[q]);
+    l[q] = f32_to_bf16_bits(v[q] - bf16_bits_to_f32(h[q]));
+  }
+  *reinterpret_cast<uint2*>(hi + off) = uint2{h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16)};
+  *reinterpret_cast<uint2*>(lo + off) = uint2{l[0] | (uint32_t(l[1]) << 16), l[2] | (uint32_t(l[3]) << 16)};
+}
+
+struct UpArgs {
+  int T, H, I, Is, k;
+  float limit;
+  const int32_t* counts; const int32_t* offsets; const int32_t* perm; const int32_t* active;
+  const float* wflat;
+  const dsk_expert_ptrs* table;
+  const uint16_t* xb_hi; const uint16_t* xb_lo;   // [T][H] B planes of x
+  const uint16_t* ws1; const uint16_t* ws3;       // shared [Is][H] bf16
+  uint16_t* h_hi; uint16_t* h_lo;                 // [T*k][I]   (dispatch row order)
+  uint16_t* hs_hi; uint16_t* hs_lo;               // [T][Is]
+  int tiles;                                      // I / 16
+  int routed_blocks;                              // max_slots * tiles
+};
+
+// Per-wave partial products of one 16-row tile for NT token tiles, reduced
+// across the block's waves, then the clamped SwiGLU epilogue.
+template <int NT, bool XLO, typename Raw, typename LoadA>
+__device__ __forceinline__ void up_tile(const UpArgs& p, LoadA load_a, int K, int row0,
+                                        int n_tok, int tok_base, bool shared, float (*red)[64][4]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int nblk = (K + 127) / 128;
+  for (int c0 = 0; c0 < n_tok; c0 += 16 * NT) {
+    int xrow[NT];
+    bool tv[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = c0 + 16 * nt + r16;
+      tv[nt] = n < n_tok;
+      xrow[nt] = !tv[nt] ? 0 : (shared ? n : p.perm[tok_base + n] / p.k);
+    }
+    f32x4 ag[NT], au[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) { ag[nt] = f32x4{0.f, 0.f, 0.f, 0.f}; au[nt] = ag[nt]; }
+    Raw r1, r3;
+    int blk = wave;
+    if (blk < nblk) load_a(blk, r1, r3);
+    for (; blk < nblk; blk += kUpWaves) {
+      Raw c1 = r1, c3 = r3;
+      if (blk + kUpWaves < nblk) load_a(blk + kUpWaves, r1, r3);
+      bf16x8 a1[4], a3[4];
+      deq(c1, a1);
+      deq(c3, a3);
+      const int kc = blk * 128 + g4 * 32;
+      const bool kok = kc < K;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        if (c0 + 16 * nt >= n_tok) break;
+        bf16x8 b[4];
+        load_b(p.xb_hi, xrow[nt], K, kc, kok && tv[nt], b);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { ag[nt] = mfma(a1[j], b[j], ag[nt]); au[nt] = mfma(a3[j], b[j], au[nt]); }
+        if constexpr (XLO) {
+          load_b(p.xb_lo, xrow[nt], K, kc, kok && tv[nt], b);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) { ag[nt] = mfma(a1[j], b[j], ag[nt]); au[nt] = mfma(a3[j], b[j], au[nt]); }
+        }
+      }
+    }
+    // Cross-wave reduction (fixed order: wave 0, 1, ...) and epilogue, one token tile at a time.
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (c0 + 16 * nt >= n_tok) break;
+      *reinterpret_cast<f32x4*>(&red[wave][lane][0]) = ag[nt];
+      *reinterpret_cast<f32x4*>(&red[kUpWaves + wave][lane][0]) = au[nt];
+      __syncthreads();
+      if (wave == 0 && tv[nt]) {
+        float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int w = 0; w < kUpWaves; ++w)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) { g[q] += red[w][lane][q]; u[q] += red[kUpWaves + w][lane][q]; }
+        const int n = c0 + 16 * nt + r16;
+        float wr = 1.0f;
+        int64_t dst;
+        if (shared) {
+          dst = static_cast<int64_t>(n) * p.Is;
+        } else {
+          const int dr = tok_base + n;
+          wr = p.wflat[p.perm[dr]];
+          dst = static_cast<int64_t>(dr) * p.I;
+        }
+        float h[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float gg = fminf(g[q], p.limit);
+          const float uu = fminf(fmaxf(u[q], -p.limit), p.limit);
+          h[q] = gg / (1.0f + expf(-gg)) * uu * wr;
+        }
+        const int64_t off = dst + row0 + 4 * g4;
+        if (shared) split_store(p.hs_hi, p.hs_lo, off, h);
+        else split_store(p.h_hi, p.h_lo, off, h);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <int NT, bool XLO>
+__global__ __launch_bounds__(kUpWaves * 64) void k_up_fp4(UpArgs p) {
+  __shared__ float red[2 * kUpWaves][64][4];
+  const int lane = threadIdx.x & 63;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int b = blockIdx.x;
+  if (b < p.routed_blocks) {
+    const int slot = b / p.tiles, rt = b % p.tiles;
+    if (slot >= p.active[0]) return;
+    const int e = p.active[1 + slot];
+    const dsk_expert_ptrs ep = p.table[e];
+    const int row0 = rt * 16;
+    const int64_t row = row0 + r16;
+    const int K = p.H;
+    const uint8_t* W1 = static_cast<const uint8_t*>(ep.w1);
+    const uint8_t* S1 = static_cast<const uint8_t*>(ep.s1);
+    const uint8_t* W3 = static_cast<const uint8_t*>(ep.w3);
+    const uint8_t* S3 = static_cast<const uint8_t*>(ep.s3);
+    auto load_a = [&](int blk, RawFP4& r1, RawFP4& r3) {
+      const int kc = blk * 128 + g4 * 32;
+      const bool ok = kc < K;
+      r1 = load_fp4(W1, S1, row, K, kc, ok);
+      r3 = load_fp4(W3, S3, row, K, kc, ok);
+    };
+    up_tile<NT, XLO, RawFP4>(p, load_a, K, row0, p.counts[e], p.offsets[e], false, red);
+  } else {
+    const int rt = b - p.routed_blocks;
+    const int row0 = rt * 16;
+    const int64_t row = row0 + r16;
+    const int K = p.H;
+    auto load_a = [&](int blk, RawBF16& r1, RawBF16& r3) {
+      const int kc = blk * 128 + g4 * 32;
+      const bool ok = kc < K;
+      r1 = load_bf16w(p.ws1, row, K, kc, ok);
+      r3 = load_bf16w(p.ws3, row, K, kc, ok);
+    };
+    up_tile<NT, XLO, RawBF16>(p, load_a, K, row0, p.T, 0, true, red);
+  }
+}
+
+struct DownArgs {
+  int T, H, I, Is;
+  const int32_t* counts; const int32_t* offsets; const int32_t* active;
+  const dsk_expert_ptrs* table;
+  const uint16_t* ws2;                   // shared [H][Is] bf16
+  const uint16_t* h_hi; const uint16_t* h_lo;
+  const uint16_t* hs_hi; const uint16_t* hs_lo;
+  float* y;                              // [T*k][H]
+  float* ys;                             // [T][H]
+  int tiles;                             // H / 16
+  int routed_blocks;
+};
+
+template <int NT, typename Raw, typename LoadA>
+__device__ __forceinline__ void down_tile(const DownArgs& p, LoadA load_a, int K, int row0,
+                                          int n_tok, int brow_base, const uint16_t* bhi,
+                                          const uint16_t* blo, float* out, float (*red)[64][4]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int nblk = (K + 127) / 128;
+  for (int c0 = 0; c0 < n_tok; c0 += 16 * NT) {
+    f32x4 acc[NT];
+    bool tv[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      tv[nt] = c0 + 16 * nt + r16 < n_tok;
+    }
+    Raw r;
+    int blk = wave;
+    if (blk < nblk) load_a(blk, r);
+    for (; blk < nblk; blk += kDownWaves) {
+      Raw c = r;
+      if (blk + kDownWaves < nblk) load_a(blk + kDownWaves, r);
+      bf16x8 a[4];
+      deq(c, a);
+      const int kc = blk * 128 + g4 * 32;
+      const bool kok = kc < K;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        if (c0 + 16 * nt >= n_tok) break;
+        const int64_t brow = brow_base + c0 + 16 * nt + r16;
+        bf16x8 b[4];
+        load_b(bhi, brow, K, kc, kok && tv[nt], b);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[nt] = mfma(a[j], b[j], acc[nt]);
+        load_b(blo, brow, K, kc, kok && tv[nt], b);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[nt] = mfma(a[j], b[j], acc[nt]);
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (c0 + 16 * nt >= n_tok) break;
+      *reinterpret_cast<f32x4*>(&red[wave][lane][0]) = acc[nt];
+      __syncthreads();
+      if (wave == 0 && tv[nt]) {
+        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int w = 0; w < kDownWaves; ++w) s += *reinterpret_cast<const f32x4*>(&red[w][lane][0]);
+        const int64_t brow = brow_base + c0 + 16 * nt + r16;
+        *reinterpret_cast<f32x4*>(out + brow * p.H + row0 + 4 * g4) = s;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <int NT>
+__global__ __launch_bounds__(kDownWaves * 64) void k_down_fp4(DownArgs p) {
+  __shared__ float red[kDownWaves][64][4];
+  const int lane = threadIdx.x & 63;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int b = blockIdx.x;
+  if (b < p.routed_blocks) {
+    const int slot = b / p.tiles, rt = b % p.tiles;
+    if (slot >= p.active[0]) return;
+    const int e = p.active[1 + slot];
+    const dsk_expert_ptrs ep = p.table[e];
+    const int row0 = rt * 16;
+    const int64_t row = row0 + r16;
+    const int K = p.I;
+    const uint8_t* W2 = static_cast<const uint8_t*>(ep.w2);
+    const uint8_t* S2 = static_cast<const uint8_t*>(ep.s2);
+    auto load_a = [&](int blk, RawFP4& r) {
+      const int kc = blk * 128 + g4 * 32;
+      r = load_fp4(W2, S2, row, K, kc, kc < K);
+    };
+    down_tile<NT, RawFP4>(p, load_a, K, row0, p.counts[e], p.offsets[e], p.h_hi, p.h_lo, p.y, red);
+  } else {
+    const int rt = b - p.routed_blocks;
+    const int row0 = rt * 16;
+    const int64_t row = row0 + r16;
+    const int K = p.Is;
+    auto load_a = [&](int blk, RawBF16& r) {
+      const int kc = blk * 128 + g4 * 32;
+      r = load_bf16w(p.ws2, row, K, kc, kc < K);
+    };
+    down_tile<NT, RawBF16>(p, load_a, K, row0, p.T, 0, p.hs_hi, p.hs_lo, p.ys, red);
+  }
+}
+
+// float32 x -> bf16 hi/lo planes.
+__global__ __launch_bounds__(256) void k_split_x(const float* __restrict__ x, int64_t n,
+                                                 uint16_t* __restrict__ hi, uint16_t* __restrict__ lo) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float v = x[i];
+  const uint16_t h = f32_to_bf16_bits(v);
+  hi[i] = h;
+  lo[i] = f32_to_bf16_bits(v - bf16_bits_to_f32(h));
+}
+
+// out[t] = cast( (sum over the token's expert rows in ascending expert id) + shared[t] ),
+// shared[t] = ys[t] rounded to x's dtype (fused shared expert) or a
+// precomputed x-dtype shared output.
+enum SharedMode { kNoShared = 0, kSharedF32 = 1, kSharedExt = 2 };
+
+template <bool XBF16>
+__global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, const float* __restrict__ ys,
+                                                 const void* __restrict__ shared_ext,
+                                                 const int32_t* __restrict__ rank, int H, int k,
+                                                 int shared_mode, void* __restrict__ out) {
+  const int t = blockIdx.x;
+  const int f = (blockIdx.y * 256 + threadIdx.x) * 4;
+  if (f >= H) return;
+  int rows[16];
+  int n = 0;
+  for (int j = 0; j < k; ++j) {
+    const int r = rank[static_cast<int64_t>(t) * k + j];
+    if (r < 0) continue;
+    int i = n++;
+    while (i > 0 && rows[i - 1] > r) { rows[i] = rows[i - 1]; --i; }
+    rows[i] = r;
+  }
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < n; ++i) acc += *reinterpret_cast<const f32x4*>(y + static_cast<int64_t>(rows[i]) * H + f);
+  const int64_t o = static_cast<int64_t>(t) * H + f;
+  if (shared_mode == kSharedF32) {
+    f32x4 s = *reinterpret_cast<const f32x4*>(ys + o);
+    if constexpr (XBF16) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) s[q] = bf16_bits_to_f32(f32_to_bf16_bits(s[q]));
+    }
+    acc += s;
+  } else if (shared_mode == kSharedExt) {
+    if constexpr (XBF16) {
+      const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(shared_ext) + o);
+      acc += f32x4{__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                   __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
+    } else {
+      acc += *reinterpret_cast<const f32x4*>(static_cast<const float*>(shared_ext) + o);
+    }
+  }
+  if constexpr (XBF16) {
+    uint16_t* ob = static_cast<uint16_t*>(out);
+    *reinterpret_cast<uint2*>(ob + o) =
+        uint2{f32_to_bf16_bits(acc[0]) | (uint32_t(f32_to_bf16_bits(acc[1])) << 16),
+              f32_to_bf16_bits(acc[2]) | (uint32_t(f32_to_bf16_bits(acc[3])) << 16)};
+  } else {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + o) = acc;
+  }
+}
+
+template <int NT, bool XLO>
+hipError_t launch_up(const UpArgs& a, unsigned blocks, hipStream_t s) {
+  k_up_fp4<NT, XLO><<<blocks, kUpWaves * 64, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+template <int NT>
+hipError_t launch_down(const DownArgs& a, unsigned blocks, hipStream_t s) {
+  k_down_fp4<NT><<<blocks, kDownWaves * 64, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                          hipStream_t s) {
+  const int T = d.tokens, H = d.hidden, I = d.inter, Is = d.inter_shared, k = d.top_k;
+  const int max_slots = (d.n_experts < T * k) ? d.n_experts : T * k;
+  const bool x_f32 = d.x_dtype == DSK_DTYPE_F32;
+  const uint16_t* xb_hi = static_cast<const uint16_t*>(a.x);
+  const uint16_t* xb_lo = nullptr;
+  if (x_f32) {
+    uint16_t* hi = reinterpret_cast<uint16_t*>(a.ws + L.xb_hi);
+    uint16_t* lo = reinterpret_cast<uint16_t*>(a.ws + L.xb_lo);
+    const int64_t n = static_cast<int64_t>(T) * H;
+    k_split_x<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(static_cast<const float*>(a.x), n, hi, lo);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    xb_hi = hi;
+    xb_lo = lo;
+  }
+  const int nt = (T <= 16) ? 1 : (T <= 32 ? 2 : 4);
+
+  UpArgs u{};
+  u.T = T; u.H = H; u.I = I; u.Is = Is; u.k = k; u.limit = d.limit;
+  u.counts = a.counts; u.offsets = a.offsets; u.perm = a.perm; u.active = a.active;
+  u.wflat = a.weights; u.table = a.table;
+  u.xb_hi = xb_hi; u.xb_lo = xb_lo;
+  u.ws1 = static_cast<const uint16_t*>(a.ws1); u.ws3 = static_cast<const uint16_t*>(a.ws3);
+  u.h_hi = reinterpret_cast<uint16_t*>(a.ws + L.h_hi);
+  u.h_lo = reinterpret_cast<uint16_t*>(a.ws + L.h_lo);
+  u.hs_hi = reinterpret_cast<uint16_t*>(a.ws + L.hs_hi);
+  u.hs_lo = reinterpret_cast<uint16_t*>(a.ws + L.hs_lo);
+  u.tiles = I / 16;
+  u.routed_blocks = max_slots * u.tiles;
+  const unsigned up_blocks = static_cast<unsigned>(u.routed_blocks + (Is > 0 ? Is / 16 : 0));
+  hipError_t e;
+  if (x_f32) e = nt == 1 ? launch_up<1, true>(u, up_blocks, s) : nt == 2 ? launch_up<2, true>(u, up_blocks, s) : launch_up<4, true>(u, up_blocks, s);
+  else e = nt == 1 ? launch_up<1, false>(u, up_blocks, s) : nt == 2 ? launch_up<2, false>(u, up_blocks, s) : launch_up<4, false>(u, up_blocks, s);
+  if (e != hipSuccess) return e;
+
+  DownArgs dn{};
+  dn.T = T; dn.H = H; dn.I = I; dn.Is = Is;
+  dn.counts = a.counts; dn.offsets = a.offsets; dn.active = a.active; dn.table = a.table;
+  dn.ws2 = static_cast<const uint16_t*>(a.ws2);
+  dn.h_hi = u.h_hi; dn.h_lo = u.h_lo; dn.hs_hi = u.hs_hi; dn.hs_lo = u.hs_lo;
+  dn.y = reinterpret_cast<float*>(a.ws + L.y);
+  dn.ys = reinterpret_cast<float*>(a.ws + L.ys);
+  dn.tiles = H / 16;
+  dn.routed_blocks = max_slots * dn.tiles;
+  const unsigned down_blocks = static_cast<unsigned>(dn.routed_blocks + (Is > 0 ? H / 16 : 0));
+  e = nt == 1 ? launch_down<1>(dn, down_blocks, s) : nt == 2 ? launch_down<2>(dn, down_blocks, s) : launch_down<4>(dn, down_blocks, s);
+  if (e != hipSuccess) return e;
+
+  dim3 cg(static_cast<unsigned>(T), static_cast<unsigned>((H + 1023) / 1024));
+  const int mode = Is > 0 ? kSharedF32 : (a.shared_out ? kSharedExt : kNoShared);
+  if (x_f32)
+    k_combine<false><<<cg, 256, 0, s>>>(dn.y, dn.ys, a.shared_out, a.rank, H, k, mode, a.out);
+  else
+    k_combine<true><<<cg, 256, 0, s>>>(dn.y, dn.ys, a.shared_out, a.rank, H, k, mode, a.out);
+  return hipGetLastError();
+}
+
+}  // namespace dsk

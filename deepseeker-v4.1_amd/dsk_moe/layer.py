@@ -1,0 +1,211 @@
+"""Drop-in MoE layer forward with the reference's call signature.
+
+``moe_layer`` keeps the signature of the reference's
+``moe_layer`` (``src/deepseeker/mlx_forward.py:257-263``) on torch tensors of
+a HIP device and runs the whole layer in libdsk_moe: router, dispatch,
+expert SwiGLU with fused dequant, shared expert, combine and cast.
+
+Arguments as in the reference:
+
+* ``x [T, H]`` bf16 or float32; ``gate_w [E, H]`` float32 or bf16;
+  ``gate_b [E]`` float32 (selection bias).
+* ``expert_fn``: a ``ResidentBank`` (every expert resident; no host sync),
+  or the reference's callable ``expert_fn(e) -> (w1, w3, w2)`` /
+  ``{"w1", "w3", "w2"}`` / ``{"w13", "w2"}`` with FP4 pairs or Q3 triples of
+  device tensors; a callable is asked only for the experts the router picked,
+  which needs one host synchronisation, as in the reference (``:294-295``).
+* ``shared_fn``: a ``SharedExpert`` (fused), any callable ``x -> [T, H]`` in
+  x's dtype (its output is added before the final cast, as in ``:409-419``),
+  or None.
+* ``top_k``, ``limit`` (SwiGLU clamp), ``trace_hook(layer, idx, w)`` (called
+  once after routing with host lists; idx in ascending key order like the
+  reference's ``argsort`` tail), ``layer_id``, ``prefetch_fn(layer, experts)``
+  (called with the unique experts, for callers that track residency).
+
+Options of the reference that only concern SSD paging or MLX scheduling are
+accepted and have no effect on the result, which the reference documents as
+identical with or without them: ``pipeline``, ``async_submit_fn``,
+``async_finalize_fn`` (``:273-285``), ``pinned_gather_fn`` (``:313-321``) and
+``stack_gateup`` (``:140-156``).  ``union_budget > 0`` (``cap_union``, which
+changes routing) is not implemented and raises.
+
+Extensions (keyword-only): ``score_func`` ("sqrtsoftplus", the reference's
+default, or "sigmoid"), ``route_scale`` (reference default 1.5), ``out``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .bank import ResidentBank, SharedExpert
+from .ops import make_desc, ptr, require_device, stream_of, workspace
+
+
+def _roles_of(weights) -> tuple:
+    """Normalise an expert_fn result to ((w1...), (w3...), (w2...))."""
+    if isinstance(weights, dict):
+        if "w13" in weights:
+            parts = weights["w13"]
+            if parts[0].shape[0] % 2:
+                raise ValueError("stacked gate/up rows must divide evenly")
+            half = [p.shape[0] // 2 for p in parts]
+            w1 = tuple(p[:n] for p, n in zip(parts, half))
+            w3 = tuple(p[n:] for p, n in zip(parts, half))
+            return w1, w3, tuple(weights["w2"])
+        return tuple(weights["w1"]), tuple(weights["w3"]), tuple(weights["w2"])
+    w1, w3, w2 = weights
+    return tuple(w1), tuple(w3), tuple(w2)
+
+
+def _table_from_weights(fetched: dict, n_experts: int, quant: str, device: torch.device,
+                        keep: list) -> torch.Tensor:
+    """Device ``dsk_expert_ptrs[E]`` from {expert: expert_fn(expert)} (others NULL)."""
+    entries = (_lib.ExpertPtrs * n_experts)()
+    arity = 2 if quant == "fp4" else 3
+    for e, weights in fetched.items():
+        vals = []
+        for parts in _roles_of(weights):
+            if len(parts) != arity:
+                raise ValueError(f"expert {e}: {quant} roles need {arity} tensors, got {len(parts)}")
+            for t in parts:
+                require_device(t)
+                keep.append(t)
+            vals.extend([parts[c].data_ptr() if c < arity else None for c in range(3)])
+        entries[e] = _lib.ExpertPtrs(*vals)
+    return torch.frombuffer(bytearray(bytes(entries)), dtype=torch.uint8).to(device)
+
+
+def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
+              expert_fn, shared_fn, top_k: int = 6, limit: float = 10.0,
+              trace_hook=None, layer_id: int = 0, prefetch_fn=None,
+              union_budget: int = 0, route_stats: dict | None = None,
+              union_strict: bool = False, pipeline: bool = False,
+              async_submit_fn=None, async_finalize_fn=None,
+              pinned_gather_fn=None, stack_gateup: bool = False, *,
+              score_func: str = "sqrtsoftplus", route_scale: float = 1.5,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """MoE layer forward on the GPU; returns ``[T, H]`` in x's dtype."""
+    if union_budget > 0:
+        raise NotImplementedError("union_budget > 0 (cap_union) is not implemented")
+    del route_stats, union_strict, pipeline, async_submit_fn, async_finalize_fn
+    del pinned_gather_fn, stack_gateup
+    dev = require_device(x, gate_w, gate_b)
+    if x.dim() != 2:
+        raise ValueError(f"x must be [T, H], got {tuple(x.shape)}")
+    t, h = x.shape
+    e = gate_w.shape[0]
+    gate_b = gate_b.to(torch.float32).contiguous()
+    if gate_w.shape != (e, h) or gate_b.shape != (e,):
+        raise ValueError("gate_w must be [E, H] and gate_b [E]")
+
+    bank = expert_fn if isinstance(expert_fn, ResidentBank) else None
+    shared = shared_fn if isinstance(shared_fn, SharedExpert) else None
+    if bank is not None:
+        quant, inter = bank.quant, bank.inter
+        if bank.n_experts != e or bank.hidden != h:
+            raise ValueError("ResidentBank geometry does not match gate_w / x")
+    if shared is not None and (shared.hidden != h):
+        raise ValueError("SharedExpert hidden size does not match x")
+
+    if out is None:
+        out = torch.empty_like(x)
+    else:
+        require_device(out)
+        if out.shape != x.shape or out.dtype != x.dtype:
+            raise ValueError("out must match x in shape and dtype")
+    stream = stream_of(dev)
+    need_host = bank is None or trace_hook is not None or prefetch_fn is not None
+
+    # Route (+ dispatch) first when the host must see the routing.
+    idx = torch.empty((t, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((t, top_k), dtype=torch.float32, device=dev)
+    keep: list = []
+    if bank is None:
+        # Learn the expert geometry from the first routed expert below.
+        quant, inter = None, None
+    probe_inter = inter if bank is not None else 32
+    desc = make_desc(tokens=t, hidden=h, n_experts=e, top_k=top_k,
+                     inter=probe_inter, inter_shared=shared.inter if shared else 0,
+                     score_func=score_func, quant=quant or "fp4", x_dtype=x.dtype,
+                     gate_dtype=gate_w.dtype, route_scale=route_scale, limit=limit)
+    if need_host:
+        scores = torch.empty((t, e), dtype=torch.float32, device=dev)
+        _lib.call("dsk_route", ctypes.byref(desc), ptr(x), ptr(gate_w), ptr(gate_b), ptr(scores),
+                  ptr(idx), ptr(w), stream)
+        idx_h = idx.cpu()
+        uniq = sorted(set(int(v) for v in idx_h.flatten().tolist() if 0 <= v < e))
+        if bank is None:
+            if not uniq:
+                raise ValueError("router selected no expert")
+            fetched = {ex: expert_fn(ex) for ex in uniq}
+            first = _roles_of(fetched[uniq[0]])
+            quant = "fp4" if len(first[0]) == 2 else "q3"
+            inter = first[0][0].shape[0]
+            desc.quant = 0 if quant == "fp4" else 1
+            desc.inter = inter
+        if prefetch_fn is not None:
+            prefetch_fn(layer_id, uniq)
+        if trace_hook is not None:
+            trace_hook(layer_id, idx_h.flip(1).tolist(), w.cpu().flip(1).tolist())
+
+    shared_out = None
+    if shared_fn is not None and shared is None:
+        shared_out = shared_fn(x)
+        if not isinstance(shared_out, torch.Tensor) or shared_out.shape != x.shape:
+            raise ValueError("shared_fn must return a [T, H] tensor")
+        shared_out = shared_out.to(x.dtype).contiguous()
+        require_device(shared_out)
+
+    table = bank.table if bank is not None else _table_from_weights(fetched, e, quant, dev, keep)
+    ws = workspace(desc, dev)
+    ws1 = shared.w1 if shared else None
+    ws3 = shared.w3 if shared else None
+    ws2 = shared.w2 if shared else None
+    if need_host:
+        from .ops import dispatch as _dispatch  # local: same device, same stream
+        d = _dispatch(idx, e)
+        _lib.call("dsk_experts", ctypes.byref(desc), ptr(table), ptr(ws1), ptr(ws3), ptr(ws2),
+                  ptr(shared_out), ptr(x), ptr(w), ptr(d["counts"]), ptr(d["offsets"]),
+                  ptr(d["perm"]), ptr(d["rank"]), ptr(d["active"]), ptr(out), ptr(ws),
+                  ws.numel(), stream)
+        keep.append(d)
+    else:
+        _lib.call("dsk_moe_forward", ctypes.byref(desc), ptr(x), ptr(gate_w), ptr(gate_b),
+                  ptr(table), ptr(ws1), ptr(ws3), ptr(ws2), ptr(shared_out), ptr(out),
+                  ptr(idx), ptr(w), ptr(ws), ws.numel(), stream)
+    if keep:
+        # Tensors referenced only through raw pointers must outlive the launches.
+        torch.cuda.current_stream(dev).synchronize()
+    return out
+
+
+class MoELayer:
+    """One resident layer: gate, bank, shared expert and configuration."""
+
+    def __init__(self, gate_w: torch.Tensor, gate_b: torch.Tensor, bank: ResidentBank,
+                 shared: SharedExpert | None, top_k: int, *, score_func: str = "sigmoid",
+                 route_scale: float = 2.5, limit: float = 10.0):
+        self.gate_w, self.gate_b, self.bank, self.shared = gate_w, gate_b.float().contiguous(), bank, shared
+        self.top_k, self.score_func, self.route_scale, self.limit = top_k, score_func, route_scale, limit
+
+    def __call__(self, x: torch.Tensor, out: torch.Tensor | None = None,
+                 idx: torch.Tensor | None = None, w: torch.Tensor | None = None) -> torch.Tensor:
+        dev = require_device(x, self.gate_w)
+        t, h = x.shape
+        desc = make_desc(tokens=t, hidden=h, n_experts=self.bank.n_experts, top_k=self.top_k,
+                         inter=self.bank.inter, inter_shared=self.shared.inter if self.shared else 0,
+                         score_func=self.score_func, quant=self.bank.quant, x_dtype=x.dtype,
+                         gate_dtype=self.gate_w.dtype, route_scale=self.route_scale,
+                         limit=self.limit)
+        if out is None:
+            out = torch.empty_like(x)
+        ws = workspace(desc, dev)
+        s = self.shared
+        _lib.call("dsk_moe_forward", ctypes.byref(desc), ptr(x), ptr(self.gate_w), ptr(self.gate_b),
+                  ptr(self.bank.table), ptr(s.w1 if s else None), ptr(s.w3 if s else None),
+                  ptr(s.w2 if s else None), ptr(None), ptr(out), ptr(idx), ptr(w), ptr(ws),
+                  ws.numel(), stream_of(dev))
+        return out

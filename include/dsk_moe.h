@@ -1,0 +1,165 @@
+/*
+ * dsk_moe.h -- C ABI of the MI355X (gfx950) MoE-layer forward library.
+ *
+ * Every entry point is stream-ordered and asynchronous: it validates its
+ * arguments on the host, launches HIP kernels on `stream` (a hipStream_t;
+ * NULL is the default stream) and returns.  No entry point allocates device
+ * memory or synchronises, except where stated.  All pointers are device
+ * pointers unless stated otherwise; the caller owns every buffer, including
+ * the workspace.  Return value: DSK_OK or a negative DSK_E* code; the
+ * message of the last failure on the calling thread is in dsk_last_error().
+ *
+ * Layouts (row-major, the reference's expert weight layout):
+ *   FP4 role [N, K]:  packed [N, K/2] u8 (two e2m1 codes per byte, low nibble
+ *                     first) + scales [N, K/32] u8 (E8M0, 2^(b-127), 0xFF = NaN)
+ *   Q3 role [N, K]:   packed [N, 3K/8] u8 (canonical 48-byte blocks of 128
+ *                     codes) + scales [N, K/64] f16 + biases [N, K/64] f16,
+ *                     W = s*q + b
+ *   roles: w1, w3 [I, H]; w2 [H, I]; used as x @ W^T.
+ *   shared expert: bf16 w1, w3 [Is, H]; w2 [H, Is].
+ */
+#ifndef DSK_MOE_H
+#define DSK_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSK_ABI_VERSION 1
+
+/* status codes */
+#define DSK_OK 0
+#define DSK_EINVAL (-1)        /* bad shape, null pointer or enum */
+#define DSK_EALIGN (-2)        /* pointer not aligned as the kernel needs */
+#define DSK_EUNSUPPORTED (-3)  /* valid request this build does not implement */
+#define DSK_EHIP (-4)          /* a HIP runtime call failed */
+#define DSK_ESPACE (-5)        /* workspace smaller than dsk_workspace_size() */
+
+/* router score functions */
+#define DSK_SCORE_SIGMOID 0       /* s = 1 / (1 + exp(-z)) */
+#define DSK_SCORE_SQRTSOFTPLUS 1  /* s = sqrt(log(1 + exp(z))) */
+
+/* routed expert formats */
+#define DSK_QUANT_FP4 0  /* e2m1 + E8M0 per 32 along K */
+#define DSK_QUANT_Q3 1   /* 3-bit affine, fp16 scale and bias per 64 along K */
+
+/* element types */
+#define DSK_DTYPE_BF16 0
+#define DSK_DTYPE_F32 1
+
+/* Layer description.  Mirrors the arguments of the reference's
+ * moe_layer(x, gate_w, gate_b, expert_fn, shared_fn, top_k, limit)
+ * (src/deepseeker/mlx_forward.py:257-263) plus the route scale of
+ * route_topk (:68-69) and the expert format. */
+typedef struct dsk_moe_desc {
+  int32_t tokens;        /* T >= 1 rows of x */
+  int32_t hidden;        /* H */
+  int32_t n_experts;     /* E, 1..1024 */
+  int32_t top_k;         /* k, 1..min(E, 16) */
+  int32_t inter;         /* I, routed expert intermediate size */
+  int32_t inter_shared;  /* Is, shared expert intermediate size; 0 = no shared expert */
+  int32_t score_func;    /* DSK_SCORE_* */
+  int32_t quant;         /* DSK_QUANT_* */
+  int32_t x_dtype;       /* DSK_DTYPE_BF16 or _F32: x and out */
+  int32_t gate_dtype;    /* DSK_DTYPE_F32 or _BF16: gate_w */
+  float route_scale;     /* multiplies the normalised weights (reference default 1.5) */
+  float limit;           /* SwiGLU clamp L (reference passes 10.0) */
+} dsk_moe_desc;
+
+/* Device pointers of one routed expert (an element of the device table
+ * indexed by expert id).  b* are Q3 biases (NULL for FP4). */
+typedef struct dsk_expert_ptrs {
+  const void* w1; const void* s1; const void* b1;
+  const void* w3; const void* s3; const void* b3;
+  const void* w2; const void* s2; const void* b2;
+} dsk_expert_ptrs;
+
+int dsk_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* dsk_last_error(void);
+
+/* Bytes of workspace dsk_moe_forward / dsk_experts need for this desc (host only). */
+int dsk_workspace_size(const dsk_moe_desc* d, size_t* bytes);
+
+/* Router: replaces sqrtsoftplus_scores + route_topk
+ * (src/deepseeker/mlx_forward.py:62-81).
+ * x [T,H] (x_dtype), gate_w [E,H] (gate_dtype), gate_b [E] f32 ->
+ * scores [T,E] f32, idx [T,k] i32 (descending key, ties to lower id),
+ * weights [T,k] f32.  Bit-exact with the fixed-order definition of the oracle. */
+int dsk_route(const dsk_moe_desc* d, const void* x, const void* gate_w,
+              const float* gate_b, float* scores, int32_t* idx, float* weights,
+              void* stream);
+
+/* Dispatch: replaces the np.unique / row discovery of moe_layer
+ * (src/deepseeker/mlx_forward.py:294-312, 388-396) and the
+ * align_block_size contract (src/deepseeker/moe_align.py:21-46).
+ * idx [T,k] i32 -> counts [E], offsets [E+1] (exclusive prefix sum),
+ * perm [T*k] (flat positions t*k+j sorted by (expert, position)),
+ * rank [T*k] (inverse of perm, -1 for dropped entries),
+ * active [E+1] (active[0] = number of experts with a routed position,
+ * then their ids ascending).  Entries < 0 or >= E are dropped. */
+int dsk_dispatch(const dsk_moe_desc* d, const int32_t* idx, int32_t* counts,
+                 int32_t* offsets, int32_t* perm, int32_t* rank, int32_t* active,
+                 void* stream);
+
+/* Experts + shared expert + combine, given routing and dispatch:
+ * replaces the per-expert loop, the shared add and the final cast of
+ * moe_layer (src/deepseeker/mlx_forward.py:388-419) and the shared expert
+ * (src/deepseeker/mlx_runner.py:765-783).
+ * table: device array [E] of dsk_expert_ptrs (entries of experts that
+ * receive no token are never read); ws1/ws3/ws2: shared expert bf16 weights
+ * (used when inter_shared > 0); shared_out: an already computed shared
+ * expert output [T,H] in x_dtype, added instead when inter_shared == 0
+ * (NULL: no shared expert); out [T,H] in x_dtype. */
+int dsk_experts(const dsk_moe_desc* d, const dsk_expert_ptrs* table,
+                const void* ws1, const void* ws3, const void* ws2,
+                const void* shared_out, const void* x, const float* weights, const int32_t* counts,
+                const int32_t* offsets, const int32_t* perm, const int32_t* rank,
+                const int32_t* active, void* out, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* Whole layer: replaces moe_layer (src/deepseeker/mlx_forward.py:257-419):
+ * dsk_route, dsk_dispatch and dsk_experts on one stream.  Shared-expert
+ * arguments as for dsk_experts.  idx / weights are optional outputs
+ * (NULL: kept in the workspace only). */
+int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w,
+                    const float* gate_b, const dsk_expert_ptrs* table,
+                    const void* ws1, const void* ws3, const void* ws2,
+                    const void* shared_out, void* out,
+                    int32_t* idx, float* weights, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* FP4 dequant: replaces metal_dequant / the Metal e2m1 kernels
+ * (src/deepseeker/metal_fp4.py:28-66, 139-155) and dequant_fp4_rowmajor
+ * (src/deepseeker/mlx_weights.py:148-166).  [rows, cols] FP4 role -> out
+ * [rows, cols] in out_dtype (f32 or bf16; exact). cols % 32 == 0. */
+int dsk_fp4_dequant(const uint8_t* packed, const uint8_t* scales, int64_t rows,
+                    int64_t cols, void* out, int32_t out_dtype, void* stream);
+
+/* FP4 quantise (spec rule: scale 2^ceil(log2(amax/6)) per 32, nearest-even
+ * e2m1, saturate at 6): stands in for mx.quantize(mode="mxfp4") used by the
+ * reference's tests and loaders.  w [rows, cols] f32. */
+int dsk_fp4_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* packed,
+                     uint8_t* scales, void* stream);
+
+/* Q3 affine quantise (group 64, fp16 scale/bias, canonical packing):
+ * replaces convert_tensor (scripts/requant_experts_3bit.py:69-83).
+ * cols % 128 == 0. */
+int dsk_q3_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* packed,
+                    uint16_t* scales, uint16_t* biases, void* stream);
+
+/* Q3 dequant: replaces mx.dequantize(bits=3, group_size=64)
+ * (scripts/requant_experts_3bit.py:74-75); out = f32(s)*q + f32(b). */
+int dsk_q3_dequant(const uint8_t* packed, const uint16_t* scales,
+                   const uint16_t* biases, int64_t rows, int64_t cols, void* out,
+                   int32_t out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSK_MOE_H */

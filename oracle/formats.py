@@ -1,0 +1,254 @@
+"""Weight formats of the routed experts, restated on the CPU with numpy.
+
+FP4 (mxfp4)
+    Two e2m1 codes per byte, low nibble first, one E8M0 scale byte per 32
+    codes along K.  A role of shape [N, K] is stored as ``packed [N, K/2] u8``
+    and ``scales [N, K/32] u8``.  Decode:
+    ``v[n, c] = FP4_TABLE[(packed[n, c>>1] >> 4*(c&1)) & 15] * 2**(scales[n, c>>5] - 127)``
+    with scale byte 0xFF decoding to NaN.  Follows the reference's
+    ``src/deepseeker/metal_fp4.py:21-26`` (table), ``:96-103`` (E8M0 LUT),
+    ``:122-131`` (``reference_dequant``) and
+    ``src/deepseeker/mlx_weights.py:66-79, 148-166``.
+    Pinned by the reference's known-answer tests (``tests/test_metal_fp4.py:35-41``,
+    ``tests/test_q3.py:132-140``) and its seeded random vectors
+    (``tests/test_metal_fp4.py:44-54``, regenerated with numpy).
+
+FP4 quantiser
+    The reference quantises with MLX (``mx.quantize(mode="mxfp4")``), whose
+    rounding is not visible here.  The workload spec fixes the rule instead:
+    per 32-group, ``scale = 2**ceil(log2(amax/6))`` (computed exactly from
+    ``frexp``), each value rounded to nearest-even on the e2m1 grid,
+    saturating at +-6, never emitting the negative-zero code 0x8.
+    Pinned by brute force: every code's decode is the grid point nearest to
+    the input (checked against an exhaustive search in the tests).
+
+Q3 affine (group 64, fp16 scale and bias)
+    ``W = s * q + b`` with ``q`` in [0, 7]; ``scales``/``biases`` are
+    ``[N, K/64] f16`` as in the reference (``src/deepseeker/mlx_weights.py:119-145``;
+    ``scripts/requant_experts_3bit.py:69-83``).  The reference's code packing is
+    MLX-internal and not visible, so the codes use this build's canonical
+    layout (3 bits per code, 48 bytes per 128 codes): see ``q3_pack``.
+    Parity with MLX's packing and its quantiser rounding is unpinned; the
+    layout is pinned by a pack/unpack round trip and a hand-built
+    known-answer vector in the tests.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+# e2m1 value of each nibble; code 8 (negative zero) decodes to +0, as in the
+# reference table.
+FP4_TABLE = np.array(
+    [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+     0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0], dtype=np.float32)
+FP4_GROUP = 32
+Q3_GROUP = 64
+Q3_BITS = 3
+Q3_SUPERBLOCK = 128          # codes per 48-byte block of the canonical layout
+Q3_SUPERBLOCK_BYTES = 48
+
+
+def e8m0_to_f32(scales: np.ndarray) -> np.ndarray:
+    """E8M0 bytes -> float32 powers of two; 0xFF -> NaN.
+
+    Follows ``src/deepseeker/metal_fp4.py:96-103`` and
+    ``src/deepseeker/mlx_weights.py:66-79``.  Byte 0 is 2**-127, a float32
+    subnormal, which is exact.
+    """
+    b = np.asarray(scales, dtype=np.uint8).astype(np.int32)
+    out = np.ldexp(np.float32(1.0), np.minimum(b, 254) - 127).astype(np.float32)
+    out[b == 0xFF] = np.nan
+    return out
+
+
+def fp4_codes(packed: np.ndarray) -> np.ndarray:
+    """[..., K/2] u8 -> [..., K] u8 nibble codes, low nibble first."""
+    p = np.asarray(packed, dtype=np.uint8)
+    out = np.empty(p.shape[:-1] + (p.shape[-1] * 2,), dtype=np.uint8)
+    out[..., 0::2] = p & 0x0F
+    out[..., 1::2] = p >> 4
+    return out
+
+
+def fp4_dequant(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """FP4 role [..., K/2] u8 + [..., K/32] u8 -> float32 [..., K].
+
+    Same arithmetic as the reference's ``reference_dequant``
+    (``src/deepseeker/metal_fp4.py:122-131``): table value times the decoded
+    scale, one float32 multiply per element (exact: both factors are short).
+    """
+    codes = fp4_codes(packed)
+    k = codes.shape[-1]
+    s = np.asarray(scales, dtype=np.uint8)
+    if s.shape[-1] * FP4_GROUP != k:
+        raise ValueError(f"scales {s.shape} do not cover K={k} in groups of 32")
+    vals = FP4_TABLE[codes]
+    gain = np.repeat(e8m0_to_f32(s), FP4_GROUP, axis=-1)
+    return (vals * gain).astype(np.float32)
+
+
+def fp4_scale_exponent(amax: np.ndarray) -> np.ndarray:
+    """Smallest integer e with 6 * 2**e >= amax, i.e. ceil(log2(amax / 6)).
+
+    Exact: with ``amax = m * 2**x`` (``frexp``, m in [0.5, 1)),
+    ``6 * 2**(x-3) = 0.75 * 2**x``, so e = x-3 when m <= 0.75, else x-2.
+    amax == 0 maps to e = 0 (scale byte 127; every code is then 0).
+    """
+    a = np.asarray(amax, dtype=np.float32)
+    m, x = np.frexp(a)
+    e = np.where(m <= 0.75, x - 3, x - 2).astype(np.int32)
+    return np.where(a == 0, 0, e).astype(np.int32)
+
+
+# Magnitude thresholds (in units of the group scale) between successive
+# e2m1 grid points 0, .5, 1, 1.5, 2, 3, 4, 6.  At a tie the code with an even
+# index wins (round-half-even on the code index): <= keeps the lower code,
+# < moves to the upper one.
+_FP4_EDGES = ((0.25, True), (0.75, False), (1.25, True), (1.75, False),
+              (2.5, True), (3.5, False), (5.0, True))
+
+
+def fp4_quantize(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """float32 [..., K] -> (packed [..., K/2] u8, scales [..., K/32] u8).
+
+    The workload-spec quantiser described in the module docstring.  NaN and
+    infinite inputs are outside its contract.
+    """
+    w = np.asarray(w, dtype=np.float32)
+    k = w.shape[-1]
+    if k % FP4_GROUP:
+        raise ValueError(f"K={k} is not a multiple of {FP4_GROUP}")
+    g = w.reshape(w.shape[:-1] + (k // FP4_GROUP, FP4_GROUP))
+    amax = np.abs(g).max(axis=-1)
+    e = fp4_scale_exponent(amax)
+    sbyte = np.clip(e + 127, 0, 254).astype(np.int32)
+    e_eff = sbyte - 127
+    q = np.ldexp(np.abs(g), -e_eff[..., None]).astype(np.float32)
+    mag = np.zeros(q.shape, dtype=np.uint8)
+    for edge, inclusive in _FP4_EDGES:
+        mag += (q > edge) if inclusive else (q >= edge)
+    code = np.where((mag != 0) & (g < 0), mag | 8, mag).astype(np.uint8)
+    code = code.reshape(w.shape)
+    packed = (code[..., 0::2] | (code[..., 1::2] << 4)).astype(np.uint8)
+    return packed, sbyte.astype(np.uint8)
+
+
+def f16_bits(a: np.ndarray) -> np.ndarray:
+    return np.asarray(a, dtype=np.float16).view(np.uint16)
+
+
+def q3_quantize_codes(w: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """float32 [N, K] -> (q [N, K] u8 in 0..7, scales f16 [N, K/64], biases f16 [N, K/64]).
+
+    Per 64-group: ``s = f16((max - min) / 7)``, ``b = f16(min)``,
+    ``q = clip(rint((w - b) / s), 0, 7)`` in float32 (q = 0 where s == 0).
+    This rule is this build's own ("MLX-style" affine, group 64, bits 3);
+    MLX's exact rounding is parity unpinned.
+    """
+    w = np.asarray(w, dtype=np.float32)
+    n, k = w.shape
+    if k % Q3_GROUP:
+        raise ValueError(f"K={k} is not a multiple of {Q3_GROUP}")
+    g = w.reshape(n, k // Q3_GROUP, Q3_GROUP)
+    wmin = g.min(axis=-1)
+    wmax = g.max(axis=-1)
+    scale32 = ((wmax - wmin) / np.float32(7.0)).astype(np.float32)
+    s16 = scale32.astype(np.float16)
+    b16 = wmin.astype(np.float16)
+    s = s16.astype(np.float32)[..., None]
+    b = b16.astype(np.float32)[..., None]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        t = ((g - b) / np.where(s == 0, np.float32(1.0), s)).astype(np.float32)
+    q = np.clip(np.rint(t), 0, 7)
+    q = np.where(s == 0, 0, q).astype(np.uint8)
+    return q.reshape(n, k), s16, b16
+
+
+def _q3_pair_table():
+    """For each of the 16 code pairs of a lane word group: (m, i)."""
+    return [(p // 4, p % 4) for p in range(16)]
+
+
+def q3_pack(q: np.ndarray) -> np.ndarray:
+    """Codes [N, K] (0..7) -> canonical packed bytes [N, 3K/8] u8.
+
+    Canonical layout (this build's; K must be a multiple of 128):
+    a row is a sequence of 128-code blocks of 48 bytes.  Within a block,
+    lane group g (0..3) owns the 12 bytes at 12*g, read as three
+    little-endian u32 words d0, d1, d2.  Lane group g holds the 32 codes
+    ``32*m + 8*g + j`` (m = 0..3, j = 0..7) of the block, as 16 pairs
+    P = 4*m + j//2 with the even-j code in the low half and the odd-j code in
+    the high half.  Pair P < 15 sits in word P // 5: low code at bit
+    3*(P % 5), high code at bit 16 + 3*(P % 5).  Pair 15 uses the spare bits:
+    bit t of its low code is bit 15 of word t, bit t of its high code is bit
+    31 of word t.
+    The 32 codes that one MFMA K-step consumes from a lane group
+    (``32*m + 8*g .. +8`` for the four g) all fall in one 64-group, and every
+    pair is one shift-and-mask away from a packed 16-bit pair.
+    """
+    q = np.asarray(q, dtype=np.uint32)
+    n, k = q.shape
+    if k % Q3_SUPERBLOCK:
+        raise ValueError(f"K={k} is not a multiple of {Q3_SUPERBLOCK}")
+    if q.size and q.max() > 7:
+        raise ValueError("q3 codes must be in 0..7")
+    nb = k // Q3_SUPERBLOCK
+    # code index within block = 32*m + 8*g + j  -> axes [N, nb, m, g, j]
+    c = q.reshape(n, nb, 4, 4, 8)
+    words = np.zeros((n, nb, 4, 3), dtype=np.uint32)   # [.., g, d]
+    for p, (m, i) in enumerate(_q3_pair_table()):
+        lo = c[:, :, m, :, 2 * i]
+        hi = c[:, :, m, :, 2 * i + 1]
+        if p < 15:
+            d, s = p // 5, 3 * (p % 5)
+            words[:, :, :, d] |= (lo << s) | (hi << (16 + s))
+        else:
+            for t in range(3):
+                words[:, :, :, t] |= (((lo >> t) & 1) << 15) | (((hi >> t) & 1) << 31)
+    return words.astype("<u4").view(np.uint8).reshape(n, nb * Q3_SUPERBLOCK_BYTES)
+
+
+def q3_unpack(packed: np.ndarray, k: int) -> np.ndarray:
+    """Canonical packed bytes [N, 3K/8] -> codes [N, K] u8 (inverse of ``q3_pack``)."""
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    n = p.shape[0]
+    if k % Q3_SUPERBLOCK or p.shape[1] != k * 3 // 8:
+        raise ValueError(f"packed {p.shape} does not hold K={k} q3 codes")
+    nb = k // Q3_SUPERBLOCK
+    words = p.reshape(n, nb, 4, 12).copy().view("<u4").reshape(n, nb, 4, 3).astype(np.uint32)
+    c = np.zeros((n, nb, 4, 4, 8), dtype=np.uint32)    # [.., m, g, j]
+    for pidx, (m, i) in enumerate(_q3_pair_table()):
+        if pidx < 15:
+            d, s = pidx // 5, 3 * (pidx % 5)
+            lo = (words[:, :, :, d] >> s) & 7
+            hi = (words[:, :, :, d] >> (16 + s)) & 7
+        else:
+            lo = np.zeros((n, nb, 4), dtype=np.uint32)
+            hi = np.zeros((n, nb, 4), dtype=np.uint32)
+            for t in range(3):
+                lo |= ((words[:, :, :, t] >> 15) & 1) << t
+                hi |= ((words[:, :, :, t] >> 31) & 1) << t
+        c[:, :, m, :, 2 * i] = lo
+        c[:, :, m, :, 2 * i + 1] = hi
+    return c.reshape(n, k).astype(np.uint8)
+
+
+def q3_quantize(w: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """float32 [N, K] -> (packed [N, 3K/8] u8, scales f16 [N, K/64], biases f16 [N, K/64])."""
+    q, s, b = q3_quantize_codes(w)
+    return q3_pack(q), s, b
+
+
+def q3_dequant(packed: np.ndarray, scales: np.ndarray, biases: np.ndarray) -> np.ndarray:
+    """Canonical q3 role -> float32 [N, K]: ``f32(s) * q + f32(b)``, two roundings.
+
+    Same closed form as the reference's affine dequant (``W = s*q + b`` per
+    64-group, ``src/deepseeker/mlx_weights.py:119-141``).
+    """
+    s = np.asarray(scales).astype(np.float32)
+    b = np.asarray(biases).astype(np.float32)
+    n, groups = s.shape
+    k = groups * Q3_GROUP
+    q = q3_unpack(packed, k).astype(np.float32).reshape(n, groups, Q3_GROUP)
+    return ((s[..., None] * q) + b[..., None]).astype(np.float32).reshape(n, k)

@@ -1,0 +1,419 @@
+"""Pins the CPU oracle before it is trusted as the checker.
+
+Each test names what it pins: the reference's own known-answer tests and
+seeded vectors (restated here, the reference cannot be imported), closed
+forms, brute force on small inputs, and invariants.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dispatch as D
+from oracle import formats as F
+from oracle import layer as L
+from oracle import router as R
+from oracle import synth
+
+
+# ------------------------------------------------------------------ FP4 decode
+def test_fp4_table_spot_values():
+    # reference tests/test_metal_fp4.py:35-41
+    assert F.FP4_TABLE[0x7] == 6.0
+    assert F.FP4_TABLE[0xF] == -6.0
+    assert F.FP4_TABLE[0x8] == 0.0
+    s = F.e8m0_to_f32(np.array([127, 128, 0xFF], dtype=np.uint8))
+    assert s[0] == 1.0 and s[1] == 2.0 and np.isnan(s[2])
+
+
+def test_fp4_table_is_e2m1():
+    # closed form of e2m1: sign | 2 exponent bits (bias 1) | 1 mantissa bit
+    for code in range(16):
+        sign = -1.0 if code & 8 else 1.0
+        e, m = (code >> 1) & 3, code & 1
+        mag = (m * 0.5) if e == 0 else (1 + m / 2) * 2.0 ** (e - 1)
+        assert F.FP4_TABLE[code] == (sign * mag if mag else 0.0)
+
+
+def test_fp4_nibble_order_low_first():
+    # reference tests/test_q3.py:132-140: byte 0x13 -> [T[3], T[1]] * 2
+    vals = F.fp4_dequant(np.array([[0x13] * 16], dtype=np.uint8), np.array([[128]], dtype=np.uint8))
+    assert vals[0, 0] == F.FP4_TABLE[3] * 2.0 and vals[0, 1] == F.FP4_TABLE[1] * 2.0
+
+
+def test_fp4_dequant_reference_random_vectors():
+    # reference tests/test_metal_fp4.py:44-54 (numpy default_rng(3), 512 bytes,
+    # scales 2^U{-3..2}); its expected values are the table times the scale.
+    rng = np.random.default_rng(3)
+    packed = rng.integers(0, 256, size=512, dtype=np.uint8)
+    scales_f = np.exp2(rng.integers(-3, 3, size=32).astype(np.float32))
+    sbytes = (np.log2(scales_f).astype(np.int32) + 127).astype(np.uint8)
+    got = F.fp4_dequant(packed[None, :], sbytes[None, :])[0]
+    raw = packed.astype(np.int64)
+    want = np.empty(1024, dtype=np.float32)
+    want[0::2] = F.FP4_TABLE[raw & 15]
+    want[1::2] = F.FP4_TABLE[raw >> 4]
+    want *= np.repeat(scales_f, 32)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_fp4_dequant_torch_crosscheck():
+    # reference tests/test_mlx_weights.py:77-87 recipe (default_rng(2), scale bytes 120..134)
+    rng = np.random.default_rng(2)
+    packed = rng.integers(0, 256, size=(4, 64), dtype=np.uint8)
+    sbytes = rng.integers(120, 135, size=(4, 4), dtype=np.uint8)
+    got = F.fp4_dequant(packed, sbytes)
+    tbl = torch.tensor(F.FP4_TABLE)
+    raw = torch.from_numpy(packed.astype(np.int64))
+    vals = torch.stack([tbl[raw & 15], tbl[raw >> 4]], dim=-1).reshape(4, 128)
+    scale = torch.pow(2.0, torch.from_numpy(sbytes.astype(np.float32)) - 127).repeat_interleave(32, 1)
+    np.testing.assert_array_equal(got, (vals * scale).numpy())
+
+
+# ------------------------------------------------------------------ FP4 quantiser
+def test_fp4_scale_exponent_is_ceil_log2():
+    rng = np.random.default_rng(5)
+    amax = np.concatenate([rng.random(2000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 2000),
+                           np.float32([6.0, 3.0, 1.5, 0.75, 6 * 2.0 ** -40, 12.0])]).astype(np.float32)
+    e = F.fp4_scale_exponent(amax)
+    for a, ee in zip(amax.astype(np.float64), e):
+        # smallest integer e with 6 * 2^e >= amax, checked exactly
+        assert 6.0 * 2.0 ** ee >= a and 6.0 * 2.0 ** (ee - 1) < a
+
+
+def test_fp4_quantize_nearest_even_brute_force():
+    rng = np.random.default_rng(7)
+    w = (rng.standard_normal((16, 256)) * 0.02).astype(np.float32)
+    w[0, :32] = np.linspace(-6, 6, 32, dtype=np.float32)        # exact grid hits and ties
+    w[1, :32] = np.float32([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 6.0] * 4) * np.float32(
+        [1, -1] * 16)
+    packed, scales = F.fp4_quantize(w)
+    deq = F.fp4_dequant(packed, scales)
+    codes = F.fp4_codes(packed)
+    grid = np.array(sorted(set(np.abs(F.FP4_TABLE).tolist())))
+    sc = np.repeat(F.e8m0_to_f32(scales), 32, axis=1)
+    for r in range(w.shape[0]):
+        for c in range(w.shape[1]):
+            q = abs(float(w[r, c])) / float(sc[r, c])
+            d = np.abs(grid - min(q, 6.0))
+            best = np.flatnonzero(d == d.min())
+            mags = [float(F.FP4_TABLE[i]) for i in range(8)]
+            cand = [mags.index(grid[b]) for b in best]
+            want = min(cand, key=lambda i: (i % 2, i))      # tie: even code index
+            assert codes[r, c] & 7 == want, (r, c, q)
+            assert not (codes[r, c] == 8)                    # never negative zero
+    assert np.all(np.abs(deq) <= np.abs(w).max() * 1.5 + 1e-9)
+
+
+# ------------------------------------------------------------------ Q3
+def test_q3_pack_roundtrip_and_geometry():
+    rng = np.random.default_rng(11)
+    q = rng.integers(0, 8, size=(5, 384), dtype=np.uint8)
+    packed = F.q3_pack(q)
+    assert packed.shape == (5, 384 * 3 // 8)
+    np.testing.assert_array_equal(F.q3_unpack(packed, 384), q)
+
+
+def test_q3_pack_known_answer():
+    # one code at a time: code 32*m + 8*g + j = 7 lands in lane group g's words
+    for m, g, j in [(0, 0, 0), (0, 0, 1), (2, 1, 4), (3, 3, 6), (3, 3, 7), (1, 2, 3)]:
+        q = np.zeros((1, 128), dtype=np.uint8)
+        q[0, 32 * m + 8 * g + j] = 5
+        words = F.q3_pack(q).view("<u4").reshape(4, 3)
+        p = 4 * m + j // 2
+        expect = np.zeros((4, 3), dtype=np.uint32)
+        if p < 15:
+            expect[g, p // 5] = 5 << (3 * (p % 5) + (16 if j % 2 else 0))
+        else:
+            for t in range(3):
+                expect[g, t] = ((5 >> t) & 1) << (31 if j % 2 else 15)
+        np.testing.assert_array_equal(words, expect)
+
+
+def test_q3_quantize_error_bound():
+    # reference tests/test_q3.py:89-105 geometry: 8 x 256 at O(0.05) scale -> rms < 0.08
+    rng = np.random.default_rng(7)
+    vals = (rng.standard_normal((8, 256)) * 0.05).astype(np.float32)
+    packed, s, b = F.q3_quantize(vals)
+    assert packed.nbytes == 8 * 24 * 4 and s.shape == (8, 4) and b.shape == (8, 4)
+    rt = F.q3_dequant(packed, s, b)
+    rms = np.sqrt(np.mean((vals.astype(np.float64) - rt) ** 2)) / np.abs(vals).max()
+    assert 0.0 < rms < 0.08
+    # every value within half a step (plus fp16 rounding of s, b) of its group
+    step = np.repeat(s.astype(np.float32), 64, axis=1)
+    assert np.all(np.abs(rt - vals) <= 0.5 * step + 2e-3)
+
+
+# ------------------------------------------------------------------ router
+def test_exp_log1p_sqrt_against_math():
+    xs = np.linspace(-700, 700, 20001)
+    got = R.exp_d(xs)
+    want = np.array([math.exp(v) for v in xs])
+    assert np.max(np.abs(got - want) / want) < 4e-16
+    u = np.linspace(0, 1, 5001)
+    assert np.max(np.abs(R.log1p_d(u) - np.array([math.log1p(v) for v in u]))) < 4e-16
+    v = np.concatenate([np.random.default_rng(0).random(20000) * 50, [0.0, 1.0, 4.0, 2.25]])
+    r = R.sqrt_round_f32(v)
+    # correctly rounded: |r - sqrt(v)| <= half an ulp, with exact rationals
+    from fractions import Fraction
+    for vv, rr in zip(v[:3000], r[:3000]):
+        rr = float(rr)
+        ulp = float(np.spacing(np.float32(rr)))
+        assert abs(Fraction(rr) ** 2 - Fraction(vv)) <= (Fraction(rr) + Fraction(ulp) / 2) * Fraction(ulp) + Fraction(ulp) ** 2
+
+
+def test_ln2_split_exact():
+    from fractions import Fraction
+    hi = Fraction(R.LN2_HI)
+    assert hi.denominator & (hi.denominator - 1) == 0
+    # k * LN2_HI exact for |k| < 2^20
+    assert float(Fraction(R.LN2_HI) * (2 ** 20 - 1)) == R.LN2_HI * (2 ** 20 - 1)
+    assert abs(float(hi + Fraction(R.LN2_LO)) - math.log(2)) == 0.0
+
+
+def _gate_scalar(x, w):
+    # the fixed order, one scalar at a time (float32 ops through numpy scalars)
+    h = x.shape[0]
+    p = [np.float32(0.0)] * 64
+    for m in range(-(-h // 256)):
+        for v in range(4):
+            for lane in range(64):
+                c = 256 * m + 4 * lane + v
+                if c < h:
+                    prod = np.float32(x[c]) * np.float32(w[c])
+                    p[lane] = np.float32(p[lane] + prod)
+                else:
+                    p[lane] = np.float32(p[lane] + np.float32(0.0))
+    for s in (32, 16, 8, 4, 2, 1):
+        p = [np.float32(p[i] + p[i ^ s]) for i in range(64)]
+    return p[0]
+
+
+def test_gate_logits_vectorised_equals_scalar_order():
+    rng = np.random.default_rng(1)
+    for h in (64, 260, 512):
+        x = rng.standard_normal((2, h)).astype(np.float32)
+        w = rng.standard_normal((3, h)).astype(np.float32)
+        z = R.gate_logits(x, w)
+        for t in range(2):
+            for e in range(3):
+                assert z[t, e] == _gate_scalar(x[t], w[e])
+
+
+def test_gate_logits_close_to_float64():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((8, 4096)).astype(np.float32)
+    w = (rng.standard_normal((16, 4096)) / 64).astype(np.float32)
+    z = R.gate_logits(x, w).astype(np.float64)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    bound = 4096 * 2.0 ** -23 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    assert np.all(np.abs(z - ref) <= bound)
+
+
+def test_router_matches_reference_torch_recipe():
+    # reference tests/test_mlx_numerics.py:69-89 (torch.manual_seed(2), n=3, dim=16, E=8, k=2)
+    torch.manual_seed(2)
+    n, dim, n_exp, top_k = 3, 16, 8, 2
+    x = torch.randn(n, dim)
+    w = torch.randn(n_exp, dim) * 0.1
+    b = torch.randn(n_exp)
+    scores = torch.sqrt(torch.nn.functional.softplus(x.float() @ w.float().T))
+    indices = (scores + b).topk(top_k, dim=-1)[1]
+    weights = scores.gather(1, indices)
+    weights = weights / (weights.sum(-1, keepdim=True) + 1e-20) * 1.5
+    idx, wt, s, _ = R.route(x.numpy(), w.numpy(), b.numpy(), top_k, R.SCORE_SQRTSOFTPLUS, 1.5)
+    got = sorted(zip(idx.ravel().tolist(), wt.ravel().tolist()))
+    want = sorted(zip(indices.numpy().ravel().tolist(), weights.numpy().ravel().tolist()))
+    assert [p[0] for p in got] == [p[0] for p in want]
+    np.testing.assert_allclose([p[1] for p in got], [p[1] for p in want], rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(s, scores.numpy(), rtol=1e-6, atol=1e-6)
+
+
+def test_sigmoid_scores_match_torch():
+    rng = np.random.default_rng(4)
+    z = np.concatenate([rng.standard_normal(5000) * 8, [0.0, -0.0, 250.0, -250.0, 1e-8]]).astype(np.float32)
+    s = R.scores_from_logits(z[None, :], R.SCORE_SIGMOID)[0]
+    ref = torch.sigmoid(torch.from_numpy(z).double()).float().numpy()
+    assert np.max(np.abs(s.astype(np.float64) - ref)) <= 6e-8
+
+
+@pytest.mark.parametrize("k", [2, 3, 4, 6])
+def test_route_weights_sum_to_scale(k):
+    # reference tests/test_batch.py:321-337
+    rng = np.random.default_rng(1)
+    s = (rng.standard_normal((5, 384)) * 0.05 + 0.4).astype(np.float32)
+    idx, w = R.topk_weights(s, np.zeros(384, np.float32), k, 1.5)
+    assert idx.shape == (5, k) and idx.min() >= 0 and idx.max() < 384
+    for row in range(5):
+        assert len(set(idx[row].tolist())) == k
+        assert abs(float(w[row].sum()) - 1.5) < 1e-4
+
+
+def test_route_bias_steers_selection_only():
+    # reference tests/test_mlx_forward.py:161-169
+    rng = np.random.default_rng(0)
+    s = (rng.standard_normal((2, 8)) * 0.01 + 0.5).astype(np.float32)
+    bias = np.array([0, 0, 0, 0, 0, 0, 0, 10.0], np.float32)
+    idx, w = R.topk_weights(s, bias, 2, 1.5)
+    assert 7 in idx[0]
+    j = list(idx[0]).index(7)
+    other = idx[0][1 - j]
+    assert abs(w[0][j] / w[0][1 - j] - s[0, 7] / s[0, other]) < 1e-6
+
+
+def test_sqrtsoftplus_nonnegative():
+    # reference tests/test_mlx_forward.py:172-177
+    s = R.scores_from_logits(np.array([[-100.0, 0.0, 100.0, -1e30, 1e30]], np.float32),
+                             R.SCORE_SQRTSOFTPLUS)
+    assert np.all(s >= 0) and s[0, 1] == np.float32(math.sqrt(math.log(2)))
+
+
+def test_topk_ties_go_to_lower_index_descending():
+    s = np.array([[0.5, 0.7, 0.7, 0.2, 0.7, -0.0, 0.0]], np.float32)
+    idx, _ = R.topk_weights(s, np.zeros(7, np.float32), 5, 1.0)
+    assert idx[0].tolist() == [1, 2, 4, 0, 3]
+    idx, _ = R.topk_weights(s, np.zeros(7, np.float32), 7, 1.0)
+    assert idx[0].tolist()[-2:] == [5, 6]        # -0 and +0 tie: lower id first
+
+
+def test_real_trace_weights_sum_to_reference_route_scale(golden):
+    # reference profiles/traces/mlx-*.jsonl: every record's weights sum to 1.5
+    d = golden("trace_routes.npz")
+    assert d["experts"].shape[1] == 6
+    np.testing.assert_allclose(d["weights"].sum(axis=1), 1.5, atol=5e-7)
+    assert d["experts"].min() >= 0 and d["experts"].max() < 384
+
+
+# ------------------------------------------------------------------ dispatch
+def test_dispatch_align_docstring_example():
+    # reference tests/test_audit.py:37-44
+    topk = np.array([[1, 2, 3], [0, 1, 3], [0, 2, 3], [0, 1, 2]])
+    sorted_ids, expert_ids, n_pad = D.align_block_size(topk, 4, 4)
+    assert n_pad == 16
+    assert list(expert_ids) == [0, 1, 2, 3]
+    assert sorted(int(i) for i in sorted_ids if i != 12) == list(range(12))
+    assert all(int(sorted_ids[i]) == 12 for i in (3, 7, 11, 15))
+    counts, offsets, perm, rank = D.dispatch(topk, 4)
+    assert perm.tolist() == [3, 6, 9, 0, 4, 10, 1, 7, 11, 2, 5, 8]
+    assert counts.tolist() == [3, 3, 3, 3] and offsets.tolist() == [0, 3, 6, 9, 12]
+    assert np.array_equal(perm[rank], np.arange(12))
+
+
+def test_dispatch_properties_random():
+    # reference tests/test_audit.py:47-60 (default_rng(0), 256 x 6, E = 384, block 16)
+    rng = np.random.default_rng(0)
+    topk = rng.integers(0, 384, size=(256, 6))
+    sorted_ids, expert_ids, n_pad = D.align_block_size(topk, 16, 384)
+    assert n_pad % 16 == 0 and len(expert_ids) == n_pad // 16
+    flat = topk.reshape(-1)
+    for expert in range(384):
+        run = [int(i) for i in sorted_ids if i != len(flat) and flat[i] == expert]
+        assert len(run) == int((flat == expert).sum())
+        assert run == sorted(run)                      # stable
+    counts, offsets, perm, rank = D.dispatch(topk, 384)
+    np.testing.assert_array_equal(perm, np.argsort(flat, kind="stable"))
+
+
+def test_dispatch_drops_negative_ids():
+    idx = np.array([[3, -1], [-1, 0], [3, 7]])
+    counts, offsets, perm, rank = D.dispatch(idx, 8)
+    assert perm.tolist() == [3, 0, 4, 5]
+    assert rank.tolist() == [1, -1, -1, 0, 2, 3]
+    assert D.active_experts(counts).tolist() == [0, 3, 7]
+
+
+def test_plan_groups_known_answer():
+    # reference tests/test_grouped.py:29-39
+    topk = [[2, 0], [1, 2], [0, 0]]
+    assert D.plan_groups(topk, 3) == {2: [(0, 0), (1, 1)], 0: [(0, 1), (2, 0), (2, 1)], 1: [(1, 0)]}
+    assert D.plan_groups([[], []], 3) == {}
+    with pytest.raises(ValueError):
+        D.plan_groups([[9]], 3)
+
+
+def test_align_rejects_bad_input():
+    with pytest.raises(ValueError):
+        D.align_block_size(np.array([1, 2, 3]), 4, 4)
+    with pytest.raises(ValueError):
+        D.align_block_size(np.array([[0, 99]]), 4, 4)
+
+
+# ------------------------------------------------------------------ layer
+@pytest.fixture(scope="module")
+def tiny():
+    spec = synth.tiny_spec()
+    d = synth.make_layer(spec, 1, 3)
+    r = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], d["shared"], spec)
+    return spec, d, r
+
+
+def test_layer_fp32_matches_fp64_brute_force(tiny):
+    spec, d, r = tiny
+    y64 = L.moe_forward_f64(d["x"], r["idx"], r["w"], d["bank"], d["shared"], spec)
+    np.testing.assert_allclose(r["y_ref"].numpy(), y64, rtol=1e-4, atol=1e-5 * np.abs(y64).max())
+
+
+def test_layer_grouped_equals_per_token(tiny):
+    # reference tests/test_grouped.py:42-59: grouped evaluation == per-(token, slot) loop
+    spec, d, r = tiny
+    x32 = d["x"].float()
+    acc = torch.zeros_like(x32)
+    for t in range(x32.shape[0]):
+        for e in sorted(r["idx"][t].tolist()):
+            j = r["idx"][t].tolist().index(e)
+            w1, w3, w2 = (torch.from_numpy(d["bank"].dequant(e, n)) for n in ("w1", "w3", "w2"))
+            h = L.swiglu(x32[t:t + 1] @ w1.T, x32[t:t + 1] @ w3.T, spec.limit) * float(r["w"][t, j])
+            acc[t] += (h @ w2.T)[0]
+    routed = r["y_ref"] - L.shared_forward(x32, *d["shared"], spec.limit).to(torch.bfloat16).float()
+    np.testing.assert_allclose(routed.numpy(), acc.numpy(), rtol=1e-5, atol=1e-6)
+
+
+def test_layer_shared_changes_output(tiny):
+    # reference tests/test_mlx_forward.py:324-353
+    spec, d, r = tiny
+    r0 = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], None, spec)
+    assert float((r["y_ref"] - r0["y_ref"]).abs().max()) > 1e-4
+    np.testing.assert_array_equal(r0["idx"], r["idx"])
+
+
+def test_layer_route_weight_before_w2_is_linear():
+    # scaling the route scale scales the routed part exactly (weights multiply h before w2)
+    spec = synth.tiny_spec()
+    spec.I_shared = 0
+    d = synth.make_layer(spec, 3, 2)
+    a = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], None, spec)["y_ref"]
+    spec.route_scale = 5.0
+    b = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], None, spec)["y_ref"]
+    np.testing.assert_allclose(b.numpy(), 2 * a.numpy(), rtol=1e-5, atol=1e-7)
+
+
+def _digest(a) -> str:
+    import hashlib
+    if isinstance(a, torch.Tensor):
+        a = a.detach().cpu()
+        a = (a.view(torch.int16) if a.dtype == torch.bfloat16 else a).numpy()
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def test_golden_cfg0_matches_oracle(golden):
+    """Generator and oracle have not drifted from the committed cfg0 fixture."""
+    import json
+    g = golden("cfg0.npz")
+    spec = synth.config0_spec()
+    d = synth.make_layer(spec, 0, 4)
+    want = json.loads(str(g["digests"]))
+    assert _digest(d["x"]) == want["x"] and _digest(d["gate_w"]) == want["gate_w"]
+    for role, parts in d["bank"].roles.items():
+        for i, p in enumerate(parts):
+            assert _digest(p) == want[f"{role}.{i}"], role
+    r = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], d["shared"], spec)
+    np.testing.assert_array_equal(r["idx"], g["idx"])
+    np.testing.assert_array_equal(r["w"], g["w"])
+    np.testing.assert_array_equal(r["perm"], g["perm"])
+    np.testing.assert_array_equal(r["counts"], g["counts"])
+    np.testing.assert_allclose(r["y_ref"].numpy(), g["y_ref"], rtol=1e-5, atol=1e-6)
+    assert abs(float(r["w"].sum(axis=1).mean()) - 2.5) < 1e-6
