@@ -1,0 +1,299 @@
+#!/usr/bin/env python3
+"""MoE-layer forward benchmark on one MI355X.
+
+Workload (default): the full-size FP4 MoE layer at decode -- hidden 4096,
+256 routed experts, top-8, expert intermediate 2048, one bf16 shared expert
+of 2048, FP4 e2m1/E8M0 routed weights quantised from N(0, 0.02), sigmoid gate
+with route scale 2.5, B = 1 token of bf16 N(0, 1).  All weights are resident
+in HBM before timing.  A step is one layer forward; steps rotate over
+``--layers`` independently drawn layers and ``--inputs`` token batches, so
+that consecutive steps read different experts (more than the 256 MB
+Infinity Cache per cycle).
+
+Prints ONE JSON line: tokens/s of the layer (the metric), the roofline of
+the dominant kernel (the routed + shared gate/up kernel: algorithmic bytes
+per launch over its HIP-event-timed average duration), and a CPU baseline
+(the oracle, timed on a bounded sample on this host's cores).
+
+    python bench.py [--steps K] [--warmup W] [--tokens T] [--no-sweep] [--no-cpu]
+    python bench.py --mode copy --bytes N      # plain copy kernel of known size
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "deepseeker-v4.1_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import dsk_moe  # noqa: E402
+from dsk_moe import _lib  # noqa: E402
+from dsk_moe import synth as gsynth  # noqa: E402
+from dsk_moe.ops import make_desc, ptr, stream_of, workspace  # noqa: E402
+
+METRIC = "MoE-layer tokens/s at B=1/64/4096; % of HBM GB/s (decode) / MFMA peak (prefill)"
+PEAK_HBM = 8.0e12          # MI355X HBM3E, bytes/s
+PEAK_BF16 = 2.5e15         # MI355X dense bf16 MFMA, FLOP/s
+H, E, K_TOP, I, IS = 4096, 256, 8, 2048, 2048
+
+
+# ------------------------------------------------------------------ HIP events
+class HipEvents:
+    """Raw hipEvent_t objects (the library records them on the layer's stream)."""
+
+    def __init__(self, n: int):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.ev = []
+        for _ in range(n):
+            h = ctypes.c_void_p()
+            if self.hip.hipEventCreate(ctypes.byref(h)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            self.ev.append(h)
+
+    def array(self, start: int, n: int):
+        return (ctypes.c_void_p * n)(*[e.value for e in self.ev[start:start + n]])
+
+    def ms(self, a: int, b: int) -> float:
+        out = ctypes.c_float()
+        if self.hip.hipEventElapsedTime(ctypes.byref(out), self.ev[a], self.ev[b]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return float(out.value)
+
+
+# ------------------------------------------------------------------ byte/flop models
+def fp4_role_bytes(n: int, k: int) -> int:
+    return n * k // 2 + n * k // 32
+
+
+def expert_bytes() -> int:
+    return 2 * fp4_role_bytes(I, H) + fp4_role_bytes(H, I)      # 13,369,344 at the full shape
+
+
+def up_kernel_bytes(u: int, t: int) -> int:
+    """Algorithmic HBM bytes of one gate/up launch: routed w1+w3 of the u active
+    experts, shared w1+w3 (bf16), x, and the h / hs planes written."""
+    return (u * 2 * fp4_role_bytes(I, H) + 2 * IS * H * 2 + t * H * 2
+            + t * K_TOP * I * 4 + t * IS * 4)
+
+
+def layer_bytes(u: int, t: int) -> int:
+    return u * expert_bytes() + 3 * IS * H * 2 + E * H * 4 + 2 * t * H * 2
+
+
+def layer_flops(t: int) -> int:
+    return 2 * t * K_TOP * 3 * H * I + 2 * t * 3 * H * IS + 2 * t * H * E
+
+
+# ------------------------------------------------------------------ timed forward
+def forward_timed(layer, x, out, idx, w, ev: HipEvents, slot: int):
+    dev = x.device
+    desc = make_desc(tokens=x.shape[0], hidden=H, n_experts=E, top_k=K_TOP, inter=I,
+                     inter_shared=IS, score_func=layer.score_func, quant=layer.bank.quant,
+                     x_dtype=x.dtype, gate_dtype=layer.gate_w.dtype,
+                     route_scale=layer.route_scale, limit=layer.limit)
+    ws = workspace(desc, dev)
+    s = layer.shared
+    _lib.call("dsk_moe_forward_timed", ctypes.byref(desc), ptr(x), ptr(layer.gate_w),
+              ptr(layer.gate_b), ptr(layer.bank.table), ptr(s.w1), ptr(s.w3), ptr(s.w2),
+              ptr(None), ptr(out), ptr(idx), ptr(w), ptr(ws), ws.numel(), stream_of(dev),
+              ev.array(slot * _lib.STAGE_EVENTS, _lib.STAGE_EVENTS))
+
+
+def run_workload(layers, t: int, steps: int, warmup: int, n_inputs: int, seed: int = 123):
+    """Time `steps` layer forwards at batch t; returns a dict of measurements."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed + t)
+    xs = [torch.randn((t, H), generator=g, device=dev).to(torch.bfloat16) for _ in range(n_inputs)]
+    out = torch.empty((t, H), dtype=torch.bfloat16, device=dev)
+    idxs = [torch.empty((t, K_TOP), dtype=torch.int32, device=dev) for _ in range(steps)]
+    ws_ = torch.empty((t, K_TOP), dtype=torch.float32, device=dev)
+    nl = len(layers)
+    for s in range(warmup):
+        layers[s % nl](xs[s % n_inputs], out=out)
+    torch.cuda.synchronize()
+    # 1) throughput: back-to-back layers, no events inside the timed region
+    t0 = time.perf_counter()
+    for s in range(steps):
+        layers[s % nl](xs[s % n_inputs], out=out, idx=idxs[s])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # 2) stage timing: same steps through the event-recording entry point
+    ev = HipEvents(steps * _lib.STAGE_EVENTS)
+    for s in range(steps):
+        forward_timed(layers[s % nl], xs[s % n_inputs], out, idxs[s], ws_, ev, s)
+    torch.cuda.synchronize()
+    st = np.array([[ev.ms(s * 6 + i, s * 6 + i + 1) for i in range(5)] for s in range(steps)])
+    uniq = [len(torch.unique(ix).tolist()) for ix in idxs]
+    return {"wall_s": wall, "stage_ms": st, "unique": uniq}
+
+
+# ------------------------------------------------------------------ CPU baseline
+def cpu_baseline(layer, n_tokens: int = 3):
+    """The oracle (torch fp32 + numpy, the reference's algorithm restated) on
+    this host, one token per layer call, experts dequantised lazily."""
+    from oracle import formats as F
+    from oracle import layer as L
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    spec = L.LayerSpec(H=H, E=E, k=K_TOP, I=I, I_shared=IS)
+    gate_w, gate_b = layer.gate_w.cpu(), layer.gate_b.cpu()
+    shared = tuple(t.cpu() for t in (layer.shared.w1, layer.shared.w3, layer.shared.w2))
+    g = torch.Generator().manual_seed(7)
+    xs = [torch.randn((1, H), generator=g).to(torch.bfloat16) for _ in range(n_tokens + 1)]
+    raw = {}
+    idx_all = set()
+    for x in xs:                                    # fetch the raw bytes the oracle will read
+        from oracle import router as R
+        idx, *_ = R.route(x.float().numpy(), gate_w.numpy(), gate_b.numpy(), K_TOP)
+        idx_all.update(int(v) for v in idx.ravel())
+    for e in idx_all:
+        raw[e] = {r: [t[e].cpu().numpy() for t in layer.bank.roles[r]] for r in ("w1", "w3", "w2")}
+
+    class HostBank:
+        quant = "fp4"
+
+        def __init__(self):
+            self.cache = {}
+
+        def dequant(self, e, role):
+            if (e, role) not in self.cache:
+                self.cache[(e, role)] = F.fp4_dequant(*raw[e][role])
+            return self.cache[(e, role)]
+
+    L.moe_forward(xs[0], gate_w, gate_b, HostBank(), shared, spec)      # warm-up
+    times = []
+    for x in xs[1:]:
+        t0 = time.perf_counter()
+        L.moe_forward(x, gate_w, gate_b, HostBank(), shared, spec)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": 1.0 / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{n_tokens} single-token layer calls (B=1) of the oracle after 1 warm-up, "
+                      f"median {med:.3f} s; experts dequantised per call; {platform.processor() or platform.machine()}, "
+                      f"torch {torch.__version__}"}
+
+
+# ------------------------------------------------------------------ copy calibration
+def copy_mode(nbytes: int, steps: int) -> None:
+    dev = torch.device("cuda:0")
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).uniform_()
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    print(json.dumps({"mode": "copy", "bytes_read": nbytes, "bytes_written": nbytes,
+                      "ms": dt * 1e3, "GBps_rw": 2 * nbytes / dt / 1e9}), flush=True)
+
+
+# ------------------------------------------------------------------ main
+def main() -> int:
+    ap = argparse.ArgumentParser(description="MoE-layer forward benchmark (one MI355X)")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--inputs", type=int, default=16)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mode", choices=("layer", "copy"), default="layer")
+    ap.add_argument("--bytes", type=int, default=1 << 30)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the MoE-layer path is built and timed on a single "
+              "MI355X (--gpus 1); multi-GPU sharding is a design note only.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 2
+    dsk_moe.load_library()
+    if args.mode == "copy":
+        copy_mode(args.bytes, args.steps)
+        return 0
+
+    t_gen = time.perf_counter()
+    layers = [gsynth.make_layer(hidden=H, n_experts=E, top_k=K_TOP, inter=I, inter_shared=IS,
+                                seed=1000 + i, device="cuda:0") for i in range(args.layers)]
+    torch.cuda.synchronize()
+    print(f"# generated {args.layers} resident layers in {time.perf_counter() - t_gen:.1f} s", file=sys.stderr, flush=True)
+
+    T = args.tokens
+    r = run_workload(layers, T, args.steps, args.warmup, args.inputs)
+    ms_step = r["wall_s"] / args.steps * 1e3
+    value = T * args.steps / r["wall_s"]
+    st = r["stage_ms"]
+    u = np.array(r["unique"])
+    up_ms = st[:, 2]
+    up_bytes = np.array([up_kernel_bytes(int(x), T) for x in u])
+    achieved = float(up_bytes.sum() / (up_ms.sum() * 1e-3))
+    layer_b = np.array([layer_bytes(int(x), T) for x in u])
+    stage_names = ["route", "dispatch", "gate_up", "down", "combine"]
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"full-size FP4 MoE layer decode, B={T}", "hidden": H,
+                   "n_experts": E, "top_k": K_TOP, "inter": I, "shared_inter": IS,
+                   "routed_format": "fp4-e2m1/e8m0-g32", "shared_format": "bf16",
+                   "gate": "sigmoid, route_scale 2.5", "tokens": T,
+                   "layers_rotated": args.layers, "inputs_rotated": args.inputs},
+        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+                     "kernel": "k_up_fp4 (routed w1/w3 + shared w1/w3, SwiGLU epilogue)",
+                     "bytes_per_launch": int(up_bytes.mean()),
+                     "avg_launch_us": round(float(up_ms.mean()) * 1e3, 2)},
+        "stage_us": {n: round(float(st[:, i].mean()) * 1e3, 2) for i, n in enumerate(stage_names)},
+        "layer_hbm_frac": round(float(layer_b.sum() / (st.sum() * 1e-3)) / PEAK_HBM, 4),
+        "layer_hbm_frac_wall": round(float(layer_b.mean() / (ms_step * 1e-3)) / PEAK_HBM, 4),
+        "unique_experts_mean": float(u.mean()),
+    }
+    if not args.no_sweep:
+        sweep = {}
+        for tb in (8, 64):
+            rs = run_workload(layers, tb, 40, 5, args.inputs, seed=77)
+            us = np.array(rs["unique"])
+            lb = np.array([layer_bytes(int(x), tb) for x in us])
+            sweep[f"B{tb}"] = {"tokens_per_s": round(tb * 40 / rs["wall_s"], 1),
+                               "ms_per_step": round(rs["wall_s"] / 40 * 1e3, 4),
+                               "unique_experts_mean": float(us.mean()),
+                               "layer_hbm_frac": round(float(lb.mean() / (rs["wall_s"] / 40)) / PEAK_HBM, 4)}
+        zl = gsynth.make_layer(hidden=H, n_experts=E, top_k=K_TOP, inter=I, inter_shared=IS,
+                               seed=3000, device="cuda:0", zipf_s=1.1)
+        rs = run_workload([zl], 4096, 5, 1, 2, seed=99)
+        step_s = rs["wall_s"] / 5
+        sweep["T4096_prefill_zipf"] = {"tokens_per_s": round(4096 / step_s, 1),
+                                       "ms_per_step": round(step_s * 1e3, 3),
+                                       "mfma_frac": round(layer_flops(4096) / step_s / PEAK_BF16, 4),
+                                       "stage_us": {n: round(float(rs["stage_ms"][:, i].mean()) * 1e3, 1)
+                                                    for i, n in enumerate(stage_names)}}
+        line["sweep"] = sweep
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(layers[0])
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -162,14 +162,15 @@ int dsk_experts(const dsk_moe_desc* d, const dsk_expert_ptrs* table, const void*
   a.table = table; a.ws1 = ws1; a.ws3 = ws3; a.ws2 = ws2; a.shared_out = shared_out; a.x = x; a.weights = weights;
   a.counts = counts; a.offsets = offsets; a.perm = perm; a.rank = rank; a.active = active;
   a.out = out; a.ws = static_cast<char*>(workspace);
-  return hip_check(launch_experts(*d, L, a, static_cast<hipStream_t>(stream)), "dsk_experts launch");
+  return hip_check(launch_experts(*d, L, a, static_cast<hipStream_t>(stream), nullptr),
+                   "dsk_experts launch");
 }
 
-int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, const float* gate_b,
-                    const dsk_expert_ptrs* table, const void* ws1, const void* ws3,
-                    const void* ws2, const void* shared_out, void* out, int32_t* idx,
-                    float* weights, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+static int forward_impl(const dsk_moe_desc* d, const void* x, const void* gate_w,
+                        const float* gate_b, const dsk_expert_ptrs* table, const void* ws1,
+                        const void* ws3, const void* ws2, const void* shared_out, void* out,
+                        int32_t* idx, float* weights, void* workspace, size_t workspace_bytes,
+                        void* stream, void* const* events) {
   int rc = check_expert_desc(d);
   if (rc) return rc;
   if (!x || !gate_w || !gate_b || !table || !out || !workspace)
@@ -182,11 +183,15 @@ int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, co
   if (!aligned(x, 16) || !aligned(gate_w, 16) || !aligned(out, 16) || !aligned(workspace, 256) ||
       (d->inter_shared > 0 && (!aligned(ws1, 16) || !aligned(ws3, 16) || !aligned(ws2, 16))))
     return fail(DSK_EALIGN, "dsk_moe_forward: x/gate_w/out/shared need 16-byte, workspace 256-byte alignment");
+  if (events)
+    for (int i = 0; i < DSK_STAGE_EVENTS; ++i)
+      if (!events[i]) return fail(DSK_EINVAL, "dsk_moe_forward_timed: event %d is NULL", i);
   const Workspace L = workspace_layout(*d);
   if (workspace_bytes < L.total)
     return fail(DSK_ESPACE, "workspace %zu bytes < required %zu", workspace_bytes, L.total);
   char* ws = static_cast<char*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipEvent_t* ev = reinterpret_cast<const hipEvent_t*>(events);
   float* scores = reinterpret_cast<float*>(ws + L.scores);
   int32_t* idx_buf = idx ? idx : reinterpret_cast<int32_t*>(ws + L.idx);
   float* w_buf = weights ? weights : reinterpret_cast<float*>(ws + L.wts);
@@ -195,16 +200,37 @@ int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, co
   int32_t* perm = reinterpret_cast<int32_t*>(ws + L.perm);
   int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
   int32_t* active = reinterpret_cast<int32_t*>(ws + L.active);
+  if (ev && (rc = hip_check(hipEventRecord(ev[0], s), "event record"))) return rc;
   rc = hip_check(launch_route(*d, x, gate_w, gate_b, scores, idx_buf, w_buf, s), "route launch");
   if (rc) return rc;
+  if (ev && (rc = hip_check(hipEventRecord(ev[1], s), "event record"))) return rc;
   rc = hip_check(launch_dispatch(*d, idx_buf, counts, offsets, perm, rank, active, s),
                  "dispatch launch");
   if (rc) return rc;
+  if (ev && (rc = hip_check(hipEventRecord(ev[2], s), "event record"))) return rc;
   ExpertsArgs a{};
-  a.table = table; a.ws1 = ws1; a.ws3 = ws3; a.ws2 = ws2; a.shared_out = shared_out; a.x = x; a.weights = w_buf;
-  a.counts = counts; a.offsets = offsets; a.perm = perm; a.rank = rank; a.active = active;
-  a.out = out; a.ws = ws;
-  return hip_check(launch_experts(*d, L, a, s), "experts launch");
+  a.table = table; a.ws1 = ws1; a.ws3 = ws3; a.ws2 = ws2; a.shared_out = shared_out; a.x = x;
+  a.weights = w_buf; a.counts = counts; a.offsets = offsets; a.perm = perm; a.rank = rank;
+  a.active = active; a.out = out; a.ws = ws;
+  return hip_check(launch_experts(*d, L, a, s, ev ? ev + 3 : nullptr), "experts launch");
+}
+
+int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, const float* gate_b,
+                    const dsk_expert_ptrs* table, const void* ws1, const void* ws3,
+                    const void* ws2, const void* shared_out, void* out, int32_t* idx,
+                    float* weights, void* workspace, size_t workspace_bytes, void* stream) {
+  return forward_impl(d, x, gate_w, gate_b, table, ws1, ws3, ws2, shared_out, out, idx, weights,
+                      workspace, workspace_bytes, stream, nullptr);
+}
+
+int dsk_moe_forward_timed(const dsk_moe_desc* d, const void* x, const void* gate_w,
+                          const float* gate_b, const dsk_expert_ptrs* table, const void* ws1,
+                          const void* ws3, const void* ws2, const void* shared_out, void* out,
+                          int32_t* idx, float* weights, void* workspace,
+                          size_t workspace_bytes, void* stream, void* const* events) {
+  if (!events) return fail(DSK_EINVAL, "dsk_moe_forward_timed: events is NULL");
+  return forward_impl(d, x, gate_w, gate_b, table, ws1, ws3, ws2, shared_out, out, idx, weights,
+                      workspace, workspace_bytes, stream, events);
 }
 
 int dsk_fp4_dequant(const uint8_t* packed, const uint8_t* scales, int64_t rows, int64_t cols,

@@ -86,8 +86,10 @@ struct ExpertsArgs {
   char* ws;                  // workspace base
 };
 
+// ev (nullable): 3 events recorded after the gate/up kernel, the down kernel
+// and the combine kernel.
 hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L,
-                          const ExpertsArgs& a, hipStream_t s);
+                          const ExpertsArgs& a, hipStream_t s, const hipEvent_t* ev);
 
 hipError_t launch_fp4_dequant(const uint8_t* packed, const uint8_t* scales,
                               int64_t rows, int64_t cols, void* out, int out_dtype,

@@ -424,7 +424,7 @@ hipError_t launch_down(const DownArgs& a, unsigned blocks, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
-                          hipStream_t s) {
+                          hipStream_t s, const hipEvent_t* ev) {
   const int T = d.tokens, H = d.hidden, I = d.inter, Is = d.inter_shared, k = d.top_k;
   const int max_slots = (d.n_experts < T * k) ? d.n_experts : T * k;
   const bool x_f32 = d.x_dtype == DSK_DTYPE_F32;
@@ -459,6 +459,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
   if (x_f32) e = nt == 1 ? launch_up<1, true>(u, up_blocks, s) : nt == 2 ? launch_up<2, true>(u, up_blocks, s) : launch_up<4, true>(u, up_blocks, s);
   else e = nt == 1 ? launch_up<1, false>(u, up_blocks, s) : nt == 2 ? launch_up<2, false>(u, up_blocks, s) : launch_up<4, false>(u, up_blocks, s);
   if (e != hipSuccess) return e;
+  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
 
   DownArgs dn{};
   dn.T = T; dn.H = H; dn.I = I; dn.Is = Is;
@@ -472,6 +473,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
   const unsigned down_blocks = static_cast<unsigned>(dn.routed_blocks + (Is > 0 ? H / 16 : 0));
   e = nt == 1 ? launch_down<1>(dn, down_blocks, s) : nt == 2 ? launch_down<2>(dn, down_blocks, s) : launch_down<4>(dn, down_blocks, s);
   if (e != hipSuccess) return e;
+  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
 
   dim3 cg(static_cast<unsigned>(T), static_cast<unsigned>((H + 1023) / 1024));
   const int mode = Is > 0 ? kSharedF32 : (a.shared_out ? kSharedExt : kNoShared);
@@ -479,7 +481,9 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
     k_combine<false><<<cg, 256, 0, s>>>(dn.y, dn.ys, a.shared_out, a.rank, H, k, mode, a.out);
   else
     k_combine<true><<<cg, 256, 0, s>>>(dn.y, dn.ys, a.shared_out, a.rank, H, k, mode, a.out);
-  return hipGetLastError();
+  e = hipGetLastError();
+  if (e == hipSuccess && ev) e = hipEventRecord(ev[2], s);
+  return e;
 }
 
 }  // namespace dsk

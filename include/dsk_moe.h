@@ -133,6 +133,19 @@ int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w,
                     int32_t* idx, float* weights, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* dsk_moe_forward that also records DSK_STAGE_EVENTS hipEvent_t (events[i],
+ * created by the caller) on the stream: before the router, after the
+ * router, after dispatch, after the gate/up kernel, after the down kernel
+ * and after the combine.  No counterpart in the reference: it is for
+ * callers that time the stages (the benchmark). */
+#define DSK_STAGE_EVENTS 6
+int dsk_moe_forward_timed(const dsk_moe_desc* d, const void* x, const void* gate_w,
+                          const float* gate_b, const dsk_expert_ptrs* table,
+                          const void* ws1, const void* ws3, const void* ws2,
+                          const void* shared_out, void* out, int32_t* idx, float* weights,
+                          void* workspace, size_t workspace_bytes, void* stream,
+                          void* const* events);
+
 /* FP4 dequant: replaces metal_dequant / the Metal e2m1 kernels
  * (src/deepseeker/metal_fp4.py:28-66, 139-155) and dequant_fp4_rowmajor
  * (src/deepseeker/mlx_weights.py:148-166).  [rows, cols] FP4 role -> out
