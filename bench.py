@@ -100,7 +100,7 @@ def layer_flops(t: int) -> int:
 
 
 # ------------------------------------------------------------------ timed forward
-def forward_timed(layer, x, out, idx, w, ev: HipEvents, slot: int):
+def forward_timed(layer, x, out, idx, w, ev: HipEvents, slot: int, repeat: int):
     dev = x.device
     desc = make_desc(tokens=x.shape[0], hidden=H, n_experts=E, top_k=K_TOP, inter=I,
                      inter_shared=IS, score_func=layer.score_func, quant=layer.bank.quant,
@@ -111,7 +111,7 @@ def forward_timed(layer, x, out, idx, w, ev: HipEvents, slot: int):
     _lib.call("dsk_moe_forward_timed", ctypes.byref(desc), ptr(x), ptr(layer.gate_w),
               ptr(layer.gate_b), ptr(layer.bank.table), ptr(s.w1), ptr(s.w3), ptr(s.w2),
               ptr(None), ptr(out), ptr(idx), ptr(w), ptr(ws), ws.numel(), stream_of(dev),
-              ev.array(slot * _lib.STAGE_EVENTS, _lib.STAGE_EVENTS))
+              ev.array(slot * _lib.STAGE_EVENTS, _lib.STAGE_EVENTS), repeat)
 
 
 def run_workload(layers, t: int, steps: int, warmup: int, n_inputs: int, seed: int = 123):
@@ -132,13 +132,15 @@ def run_workload(layers, t: int, steps: int, warmup: int, n_inputs: int, seed: i
         layers[s % nl](xs[s % n_inputs], out=out, idx=idxs[s])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # 2) stage timing: same steps through the event-recording entry point
-    ev = HipEvents(steps * _lib.STAGE_EVENTS)
-    for s in range(steps):
-        forward_timed(layers[s % nl], xs[s % n_inputs], out, idxs[s], ws_, ev, s)
+    # 2) stage timing: every stage repeated `rep` times between its events
+    rep = 10
+    n_t = min(steps, 40)
+    ev = HipEvents(n_t * _lib.STAGE_EVENTS)
+    for s in range(n_t):
+        forward_timed(layers[s % nl], xs[s % n_inputs], out, idxs[s], ws_, ev, s, rep)
     torch.cuda.synchronize()
-    st = np.array([[ev.ms(s * 6 + i, s * 6 + i + 1) for i in range(5)] for s in range(steps)])
-    uniq = [len(torch.unique(ix).tolist()) for ix in idxs]
+    st = np.array([[ev.ms(s * 6 + i, s * 6 + i + 1) / rep for i in range(5)] for s in range(n_t)])
+    uniq = [len(torch.unique(ix).tolist()) for ix in idxs[:n_t]]
     return {"wall_s": wall, "stage_ms": st, "unique": uniq}
 
 

@@ -33,6 +33,9 @@ Workspace workspace_layout(const dsk_moe_desc& d) {
   const size_t I = d.inter, Is = d.inter_shared, N = T * k;
   size_t o = 0;
   auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes); return at; };
+  // Arrival counters first, at a fixed offset for every shape, so one
+  // zero-filled workspace can serve calls of different shapes.
+  L.ctr = take(kCounterBytes);
   L.scores = take(T * E * 4);
   L.idx = take(N * 4);
   L.wts = take(N * 4);
@@ -41,6 +44,10 @@ Workspace workspace_layout(const dsk_moe_desc& d) {
   L.perm = take(N * 4);
   L.rank = take(N * 4);
   L.active = take((E + 1) * 4);
+  L.desc = take(E * sizeof(SlotDesc));
+  L.rowmap = take(static_cast<size_t>(64) * T * 4);
+  L.xrow = take(N * 4);
+  L.wrow = take(N * 4);
   const size_t xplane = (d.x_dtype == DSK_DTYPE_F32) ? T * H * 2 : 0;
   L.xb_hi = take(xplane);
   L.xb_lo = take(xplane);
@@ -112,6 +119,13 @@ int dsk_workspace_size(const dsk_moe_desc* d, size_t* bytes) {
   return DSK_OK;
 }
 
+int dsk_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  if (!workspace) return fail(DSK_EINVAL, "dsk_workspace_init: workspace is NULL");
+  if (!aligned(workspace, 256)) return fail(DSK_EALIGN, "dsk_workspace_init: workspace must be 256-byte aligned");
+  return hip_check(launch_zero_fill(workspace, workspace_bytes, static_cast<hipStream_t>(stream)),
+                   "dsk_workspace_init launch");
+}
+
 int dsk_route(const dsk_moe_desc* d, const void* x, const void* gate_w, const float* gate_b,
               float* scores, int32_t* idx, float* weights, void* stream) {
   int rc = check_desc(d);
@@ -131,8 +145,8 @@ int dsk_dispatch(const dsk_moe_desc* d, const int32_t* idx, int32_t* counts, int
   if (rc) return rc;
   if (!idx || !counts || !offsets || !perm || !rank || !active)
     return fail(DSK_EINVAL, "dsk_dispatch: NULL pointer argument");
-  return hip_check(launch_dispatch(*d, idx, counts, offsets, perm, rank, active,
-                                   static_cast<hipStream_t>(stream)),
+  DispatchOut o{counts, offsets, perm, rank, active, nullptr, nullptr, nullptr};
+  return hip_check(launch_dispatch(*d, idx, nullptr, nullptr, o, static_cast<hipStream_t>(stream)),
                    "dsk_dispatch launch");
 }
 
@@ -162,7 +176,7 @@ int dsk_experts(const dsk_moe_desc* d, const dsk_expert_ptrs* table, const void*
   a.table = table; a.ws1 = ws1; a.ws3 = ws3; a.ws2 = ws2; a.shared_out = shared_out; a.x = x; a.weights = weights;
   a.counts = counts; a.offsets = offsets; a.perm = perm; a.rank = rank; a.active = active;
   a.out = out; a.ws = static_cast<char*>(workspace);
-  return hip_check(launch_experts(*d, L, a, static_cast<hipStream_t>(stream), nullptr),
+  return hip_check(launch_experts(*d, L, a, static_cast<hipStream_t>(stream), nullptr, 1),
                    "dsk_experts launch");
 }
 
@@ -170,7 +184,7 @@ static int forward_impl(const dsk_moe_desc* d, const void* x, const void* gate_w
                         const float* gate_b, const dsk_expert_ptrs* table, const void* ws1,
                         const void* ws3, const void* ws2, const void* shared_out, void* out,
                         int32_t* idx, float* weights, void* workspace, size_t workspace_bytes,
-                        void* stream, void* const* events) {
+                        void* stream, void* const* events, int repeat) {
   int rc = check_expert_desc(d);
   if (rc) return rc;
   if (!x || !gate_w || !gate_b || !table || !out || !workspace)
@@ -186,6 +200,7 @@ static int forward_impl(const dsk_moe_desc* d, const void* x, const void* gate_w
   if (events)
     for (int i = 0; i < DSK_STAGE_EVENTS; ++i)
       if (!events[i]) return fail(DSK_EINVAL, "dsk_moe_forward_timed: event %d is NULL", i);
+  if (repeat < 1 || repeat > 1000) return fail(DSK_EINVAL, "repeat=%d must be in [1, 1000]", repeat);
   const Workspace L = workspace_layout(*d);
   if (workspace_bytes < L.total)
     return fail(DSK_ESPACE, "workspace %zu bytes < required %zu", workspace_bytes, L.total);
@@ -200,19 +215,42 @@ static int forward_impl(const dsk_moe_desc* d, const void* x, const void* gate_w
   int32_t* perm = reinterpret_cast<int32_t*>(ws + L.perm);
   int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
   int32_t* active = reinterpret_cast<int32_t*>(ws + L.active);
+  RouteArgs ra{};
+  ra.x = x; ra.gate_w = gate_w; ra.gate_b = gate_b;
+  ra.scores = scores; ra.idx = idx_buf; ra.weights = w_buf; ra.table = table;
+  ra.out = DispatchOut{counts, offsets, perm, rank, active,
+                       reinterpret_cast<SlotDesc*>(ws + L.desc),
+                       reinterpret_cast<int32_t*>(ws + L.xrow),
+                       reinterpret_cast<float*>(ws + L.wrow)};
+  ra.ctr = reinterpret_cast<unsigned int*>(ws + L.ctr);
+  const bool decode = decode_pipeline(*d);
   if (ev && (rc = hip_check(hipEventRecord(ev[0], s), "event record"))) return rc;
-  rc = hip_check(launch_route(*d, x, gate_w, gate_b, scores, idx_buf, w_buf, s), "route launch");
-  if (rc) return rc;
-  if (ev && (rc = hip_check(hipEventRecord(ev[1], s), "event record"))) return rc;
-  rc = hip_check(launch_dispatch(*d, idx_buf, counts, offsets, perm, rank, active, s),
-                 "dispatch launch");
-  if (rc) return rc;
+  if (decode) {
+    // gate kernel, then top-k + one-wave dispatch in one block
+    ra.rowmap = reinterpret_cast<int32_t*>(ws + L.rowmap);
+    for (int r = 0; r < repeat && !rc; ++r) rc = hip_check(launch_gate_scores(*d, ra, s), "gate launch");
+    if (rc) return rc;
+    if (ev && (rc = hip_check(hipEventRecord(ev[1], s), "event record"))) return rc;
+    for (int r = 0; r < repeat && !rc; ++r) rc = hip_check(launch_route_tail(*d, ra, s), "route tail launch");
+    if (rc) return rc;
+  } else {
+    for (int r = 0; r < repeat && !rc; ++r)
+      rc = hip_check(launch_route_dispatch(*d, ra, s), "route launch");
+    if (rc) return rc;
+    // the fused router also dispatches: both stage events mark its end
+    if (ev && (rc = hip_check(hipEventRecord(ev[1], s), "event record"))) return rc;
+  }
   if (ev && (rc = hip_check(hipEventRecord(ev[2], s), "event record"))) return rc;
   ExpertsArgs a{};
-  a.table = table; a.ws1 = ws1; a.ws3 = ws3; a.ws2 = ws2; a.shared_out = shared_out; a.x = x;
+  a.table = table; a.desc = ra.out.desc; a.xrow = ra.out.xrow; a.wrow = ra.out.wrow;
+  a.ws1 = ws1; a.ws3 = ws3; a.ws2 = ws2; a.shared_out = shared_out; a.x = x;
   a.weights = w_buf; a.counts = counts; a.offsets = offsets; a.perm = perm; a.rank = rank;
   a.active = active; a.out = out; a.ws = ws;
-  return hip_check(launch_experts(*d, L, a, s, ev ? ev + 3 : nullptr), "experts launch");
+  a.rowmap = ra.rowmap;
+  if (decode)
+    return hip_check(launch_experts_decode(*d, L, a, s, ev ? ev + 3 : nullptr, repeat),
+                     "decode experts launch");
+  return hip_check(launch_experts(*d, L, a, s, ev ? ev + 3 : nullptr, repeat), "experts launch");
 }
 
 int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, const float* gate_b,
@@ -220,17 +258,18 @@ int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, co
                     const void* ws2, const void* shared_out, void* out, int32_t* idx,
                     float* weights, void* workspace, size_t workspace_bytes, void* stream) {
   return forward_impl(d, x, gate_w, gate_b, table, ws1, ws3, ws2, shared_out, out, idx, weights,
-                      workspace, workspace_bytes, stream, nullptr);
+                      workspace, workspace_bytes, stream, nullptr, 1);
 }
 
 int dsk_moe_forward_timed(const dsk_moe_desc* d, const void* x, const void* gate_w,
                           const float* gate_b, const dsk_expert_ptrs* table, const void* ws1,
                           const void* ws3, const void* ws2, const void* shared_out, void* out,
                           int32_t* idx, float* weights, void* workspace,
-                          size_t workspace_bytes, void* stream, void* const* events) {
+                          size_t workspace_bytes, void* stream, void* const* events,
+                          int32_t repeat) {
   if (!events) return fail(DSK_EINVAL, "dsk_moe_forward_timed: events is NULL");
   return forward_impl(d, x, gate_w, gate_b, table, ws1, ws3, ws2, shared_out, out, idx, weights,
-                      workspace, workspace_bytes, stream, events);
+                      workspace, workspace_bytes, stream, events, repeat);
 }
 
 int dsk_fp4_dequant(const uint8_t* packed, const uint8_t* scales, int64_t rows, int64_t cols,

@@ -1,0 +1,600 @@
+// Decode pipeline of the expert products (up to 16 tokens and 64 routed
+// positions): after the fused router (which also ran the shared expert's
+// gate/up partial products),
+//   k_up_stream    routed gate/up tiles of the active experts (FP4) -> h, and
+//                  the shared expert's SwiGLU from its partials -> hs;
+//   k_down_decode[_staged]  per 16 output rows: every active expert's w2 rows (FP4) in
+//                  ascending expert id, then the shared expert's w2 rows
+//                  (bf16), and the final add and cast -- no separate combine.
+// Token slot of the MFMA tiles = token index (T <= 16), so the products of
+// all experts accumulate into one tile; tokens not routed to an expert get a
+// zero B operand.  Replaces the per-expert loop, the shared expert and the
+// combine of the reference's moe_layer (src/deepseeker/mlx_forward.py:388-419,
+// src/deepseeker/mlx_runner.py:765-783).
+#include "tile.h"
+
+namespace dsk {
+namespace {
+
+constexpr int kUpItems = 2;            // row tiles of a gate/up block
+constexpr int kUpKS = 4;               // K splits of a row tile (one wave each)
+constexpr int kUpW = kUpItems * kUpKS; // waves of a gate/up block
+constexpr int kUpXRegChunks = 1;       // x chunks per thread staged through registers
+constexpr int kUpBatch = 4;            // K blocks per weight batch (two batches in flight)
+constexpr int kDownW = 16;             // waves of a down block (split K = I and Is)
+constexpr int kDownGroup = 8;          // experts whose w2 blocks a wave holds at once
+constexpr int kDownHRegChunks = 2;     // h chunks per thread staged through registers
+
+struct DecodeArgs {
+  int T, H, I, Is, k;
+  float limit;
+  const SlotDesc* desc; const int32_t* active; const int32_t* rowmap; const float* wrow;
+  const void* x; int x_f32;
+  const uint16_t* ws1; const uint16_t* ws3;   // shared w1, w3 [Is][H] bf16
+  uint16_t* hs_hi; uint16_t* hs_lo;    // [T][Is]
+  uint16_t* h_hi; uint16_t* h_lo;      // [T*k][I] by dispatch row
+  const uint16_t* ws2;                 // shared w2 [H][Is] bf16
+  const void* shared_out;              // precomputed shared output [T][H] (x dtype) or null
+  void* out;                           // [T][H] x dtype
+  int up_tiles;                        // I / 16
+  int shared_blocks;                   // leading gate/up blocks that run shared-expert tiles
+};
+
+__device__ __forceinline__ u32x4 pack_bf16x8(const uint16_t* v) {
+  return u32x4{v[0] | (uint32_t(v[1]) << 16), v[2] | (uint32_t(v[3]) << 16),
+               v[4] | (uint32_t(v[5]) << 16), v[6] | (uint32_t(v[7]) << 16)};
+}
+
+// One x chunk (8 values at column `col` of token row t) into the LDS planes.
+__device__ __forceinline__ void put_x_chunk(uint16_t* xh, uint16_t* xl, int off, const u32x4& v0,
+                                            const u32x4& v1, bool f32) {
+  if (!f32) {
+    *reinterpret_cast<u32x4*>(xh + off) = v0;
+    return;
+  }
+  const float f[8] = {__uint_as_float(v0.x), __uint_as_float(v0.y), __uint_as_float(v0.z),
+                      __uint_as_float(v0.w), __uint_as_float(v1.x), __uint_as_float(v1.y),
+                      __uint_as_float(v1.z), __uint_as_float(v1.w)};
+  uint16_t h[8], l[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) split_bf16(f[q], h[q], l[q]);
+  *reinterpret_cast<u32x4*>(xh + off) = pack_bf16x8(h);
+  *reinterpret_cast<u32x4*>(xl + off) = pack_bf16x8(l);
+}
+
+// One batch of G K blocks of a wave's gate and up rows: FP4 codes, and either
+// one 4-byte scale window per lane (kWin: lane group g holds the four scale
+// bytes of K block kb + g, one per lane group) or one scale byte per K block.
+template <int G>
+struct UpBatch {
+  u32x4 c1[G], c3[G];
+  uint32_t s1[G], s3[G];
+  uint32_t w1[G / 4], w3[G / 4];
+};
+
+template <int G, bool kWin>
+__device__ __forceinline__ void load_batch(UpBatch<G>& b, const uint8_t* W1, const uint8_t* S1,
+                                           const uint8_t* W3, const uint8_t* S3, uint32_t row, int K,
+                                           int kb, int k1, int g4, bool rok) {
+  // 32-bit offsets from the (uniform) role base pointers: one expert role is < 4 GB
+  const uint32_t cb = row * static_cast<uint32_t>(K / 2), sb = row * static_cast<uint32_t>(K / 32);
+  if constexpr (kWin) {
+#pragma unroll
+    for (int v = 0; v < G / 4; ++v) {
+      const int kw = kb + 4 * v + g4;                 // K block whose scales this lane fetches
+      const bool ok = rok && kw < k1;
+      b.w1[v] = ok ? *reinterpret_cast<const uint32_t*>(S1 + sb + 4 * kw) : 0u;
+      b.w3[v] = ok ? *reinterpret_cast<const uint32_t*>(S3 + sb + 4 * kw) : 0u;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int kc = (kb + i) * 128 + g4 * 32;
+    const bool ok = rok && kb + i < k1 && kc < K;
+    b.c1[i] = ok ? ldg16(W1 + cb + kc / 2) : u32x4{0u, 0u, 0u, 0u};
+    b.c3[i] = ok ? ldg16(W3 + cb + kc / 2) : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (!kWin) {
+      b.s1[i] = ok ? S1[sb + kc / 32] : 127u;
+      b.s3[i] = ok ? S3[sb + kc / 32] : 127u;
+    }
+  }
+}
+
+// Scale windows -> per-lane scale bytes through a wave-private LDS tile
+// xch[2][16][20] (role, row, 16 bytes + pad).
+template <int G, bool kWin>
+__device__ __forceinline__ void batch_scales(UpBatch<G>& b, uint8_t* xch, int r16, int g4) {
+  if constexpr (kWin) {
+#pragma unroll
+    for (int v = 0; v < G / 4; ++v) {
+      uint8_t* r1 = xch + r16 * 20;
+      uint8_t* r3 = xch + 320 + r16 * 20;
+      *reinterpret_cast<uint32_t*>(r1 + 4 * g4) = b.w1[v];
+      *reinterpret_cast<uint32_t*>(r3 + 4 * g4) = b.w3[v];
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        b.s1[4 * v + i] = r1[4 * i + g4];
+        b.s3[4 * v + i] = r3[4 * i + g4];
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+}
+
+template <int G>
+__device__ __forceinline__ void mma_batch(const UpBatch<G>& b, const uint16_t* xh, const uint16_t* xl,
+                                          int K, int kb, int k1, int g4, bool tv, bool two_planes,
+                                          f32x4& ag, f32x4& au) {
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int kc = (kb + i) * 128 + g4 * 32;
+    const bool ok = tv && kb + i < k1 && kc < K;
+    const RawFP4 r1{b.c1[i], b.s1[i]}, r3{b.c3[i], b.s3[i]};
+    mma_block2(r1, r3, xh, kc, ok, ag, au);
+    if (two_planes) mma_block2(r1, r3, xl, kc, ok, ag, au);
+  }
+}
+
+// Shared-expert gate/up tile (block = 16 rows of w1 and w3, all K; wave w
+// takes the w-th K range).  Called after the block's x chunks have been
+// loaded into registers; writes them to LDS once its own weight loads are in
+// flight.
+template <bool kF32>
+__device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, uint16_t* xh, uint16_t* xl, int xs,
+                                               bool xreg, const u32x4 (&xv)[kUpXRegChunks][2], int cpr,
+                                               int xchunks, uint16_t* lds, int tid, int lane, int wave,
+                                               int r16, int g4) {
+  const int T = p.T, K = p.H;
+  const int rt = blockIdx.x;
+  const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
+  const int nblk = (K + 127) / 128;
+  const int per = (nblk + kUpW - 1) / kUpW;
+  const int k0 = min(wave * per, nblk), k1 = min(k0 + per, nblk);
+  const bool tv = r16 < T;
+  RawBF16 a1, a3, b1, b3;
+  auto ld = [&](RawBF16& r1, RawBF16& r3, int kb) {
+    const int kc = kb * 128 + g4 * 32;
+    const bool ok = kb < k1 && kc < K;
+    load_raw(r1, p.ws1, row, K, kc, ok);
+    load_raw(r3, p.ws3, row, K, kc, ok);
+  };
+  ld(a1, a3, k0);
+  ld(b1, b3, k0 + 1);
+  if (xreg) {
+#pragma unroll
+    for (int j = 0; j < kUpXRegChunks; ++j) {
+      const int c = tid + j * kUpW * 64;
+      if (c < xchunks) put_x_chunk(xh, xl, (c / cpr) * xs + (c % cpr) * 8, xv[j][0], xv[j][1], kF32);
+    }
+  }
+  __syncthreads();
+  const uint16_t* bh = xh + (tv ? r16 : 0) * xs;
+  const uint16_t* bl = xl + (tv ? r16 : 0) * xs;
+  f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
+  auto mm = [&](const RawBF16& r1, const RawBF16& r3, int kb) {
+    const int kc = kb * 128 + g4 * 32;
+    const bool ok = tv && kb < k1 && kc < K;
+    mma_block2(r1, r3, bh, kc, ok, ag, au);
+    if (kF32) mma_block2(r1, r3, bl, kc, ok, ag, au);
+  };
+  for (int kb = k0; kb < k1; kb += 2) {
+    mm(a1, a3, kb);
+    if (kb + 2 < k1) ld(a1, a3, kb + 2);
+    if (kb + 1 < k1) mm(b1, b3, kb + 1);
+    if (kb + 3 < k1) ld(b1, b3, kb + 3);
+  }
+  // K ranges added in wave order
+  float (*red)[2][64][4] = reinterpret_cast<float (*)[2][64][4]>(lds + (kF32 ? 2 : 1) * T * xs);
+  *reinterpret_cast<f32x4*>(&red[wave][0][lane][0]) = ag;
+  *reinterpret_cast<f32x4*>(&red[wave][1][lane][0]) = au;
+  __syncthreads();
+  if (wave == 0 && tv) {
+#pragma unroll
+    for (int w = 1; w < kUpW; ++w) {
+      ag += *reinterpret_cast<const f32x4*>(&red[w][0][lane][0]);
+      au += *reinterpret_cast<const f32x4*>(&red[w][1][lane][0]);
+    }
+    uint16_t hh[4], hl[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) split_bf16(silu_clamped(ag[q], au[q], p.limit), hh[q], hl[q]);
+    const int64_t off = static_cast<int64_t>(r16) * p.Is + rt * 16 + 4 * g4;
+    *reinterpret_cast<uint2*>(p.hs_hi + off) = uint2{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16)};
+    *reinterpret_cast<uint2*>(p.hs_lo + off) = uint2{hl[0] | (uint32_t(hl[1]) << 16), hl[2] | (uint32_t(hl[3]) << 16)};
+  }
+}
+
+// Gate/up of the decode pipeline.  Blocks [0, shared_blocks) each take one
+// 16-row tile of the shared expert (bf16 w1/w3, K split over the block's
+// waves, one K block per batch); hs = SwiGLU(gate, up) as bf16 hi/lo planes.
+// The other blocks take kUpItems row tiles of one active expert, kUpKS waves
+// per tile, each streaming one K range of its FP4 w1/w3 rows in batches of G
+// K blocks; h[drow] = SwiGLU(gate, up) * route weight.  Two batches are in
+// flight per wave; the tokens' activations are loaded before the weights and
+// written to LDS after the weight loads have been issued; K ranges are added
+// in wave order.
+template <int G, bool kWin, bool kF32>
+__global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 ? 3 : 4))) void k_up_stream(DecodeArgs p) {
+  extern __shared__ __align__(16) uint16_t lds_up[];
+  // wave-uniform indices in scalar registers
+  const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int groups = (p.up_tiles + kUpItems - 1) / kUpItems;
+  const bool shared_tile = static_cast<int>(blockIdx.x) < p.shared_blocks;
+  const int rb = static_cast<int>(blockIdx.x) - p.shared_blocks;
+  const int slot = shared_tile ? 0 : rb / groups;
+  if (!shared_tile && slot >= p.active[0]) return;
+  const int T = p.T, K = p.H;
+  const int item = wave / kUpKS, ks = wave % kUpKS;
+  const int rt = (rb % groups) * kUpItems + item;
+  const bool rok = rt < p.up_tiles;
+  const int drow = shared_tile ? -1 : (r16 < T ? p.rowmap[slot * T + r16] : -1);
+  const bool tv = shared_tile ? r16 < T : drow >= 0;
+  // x chunks through registers (or straight to LDS when there are many)
+  const int xs = K + 8;                       // padded LDS row stride (elements)
+  constexpr bool f32 = kF32;
+  uint16_t* xh = lds_up;
+  uint16_t* xl = lds_up + T * xs;
+  const int cpr = K / 8;                      // chunks per row
+  const int xchunks = T * cpr;
+  const bool xreg = xchunks <= kUpXRegChunks * kUpW * 64;
+  u32x4 xv[kUpXRegChunks][2];
+  if (xreg) {
+#pragma unroll
+    for (int j = 0; j < kUpXRegChunks; ++j) {
+      const int c = tid + j * kUpW * 64;
+      if (c < xchunks) {
+        const int64_t e = static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8;
+        if (!f32) {
+          xv[j][0] = ldg16(static_cast<const uint16_t*>(p.x) + e);
+        } else {
+          xv[j][0] = ldg16(static_cast<const float*>(p.x) + e);
+          xv[j][1] = ldg16(static_cast<const float*>(p.x) + e + 4);
+        }
+      }
+    }
+  } else {
+    for (int c = tid; c < xchunks; c += kUpW * 64) {
+      const int64_t e = static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8;
+      const int off = (c / cpr) * xs + (c % cpr) * 8;
+      if (!f32) put_x_chunk(xh, xl, off, ldg16(static_cast<const uint16_t*>(p.x) + e), u32x4{}, false);
+      else put_x_chunk(xh, xl, off, ldg16(static_cast<const float*>(p.x) + e),
+                       ldg16(static_cast<const float*>(p.x) + e + 4), true);
+    }
+  }
+  if (shared_tile) {
+    shared_up_tile<kF32>(p, xh, xl, xs, xreg, xv, cpr, xchunks, lds_up, tid, lane, wave, r16, g4);
+    return;
+  }
+  // weights: two batches in flight
+  const SlotDesc* d = p.desc + slot;
+  const uint8_t* W1 = static_cast<const uint8_t*>(d->p[0]);
+  const uint8_t* S1 = static_cast<const uint8_t*>(d->p[1]);
+  const uint8_t* W3 = static_cast<const uint8_t*>(d->p[3]);
+  const uint8_t* S3 = static_cast<const uint8_t*>(d->p[4]);
+  const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
+  const int nblk = (K + 127) / 128;
+  const int per = (nblk + kUpKS - 1) / kUpKS;
+  const int k0 = min(ks * per, nblk), k1 = min(k0 + per, nblk);
+  UpBatch<G> A, B;
+  load_batch<G, kWin>(A, W1, S1, W3, S3, row, K, k0, k1, g4, rok);
+  load_batch<G, kWin>(B, W1, S1, W3, S3, row, K, k0 + G, k1, g4, rok);
+  if (xreg) {
+#pragma unroll
+    for (int j = 0; j < kUpXRegChunks; ++j) {
+      const int c = tid + j * kUpW * 64;
+      if (c < xchunks) put_x_chunk(xh, xl, (c / cpr) * xs + (c % cpr) * 8, xv[j][0], xv[j][1], f32);
+    }
+  }
+  const float wr = tv ? p.wrow[drow] : 0.0f;
+  float (*red)[kUpKS][2][64][4] =
+      reinterpret_cast<float (*)[kUpKS][2][64][4]>(lds_up + (f32 ? 2 : 1) * T * xs);
+  uint8_t* xch = reinterpret_cast<uint8_t*>(red + kUpItems) + wave * 640;
+  __syncthreads();
+  const uint16_t* bh = xh + (tv ? r16 : 0) * xs;
+  const uint16_t* bl = xl + (tv ? r16 : 0) * xs;
+  f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
+  for (int kb = k0; kb < k1; kb += 2 * G) {
+    batch_scales<G, kWin>(A, xch, r16, g4);
+    mma_batch<G>(A, bh, bl, K, kb, k1, g4, tv, f32, ag, au);
+    if (kb + 2 * G < k1) load_batch<G, kWin>(A, W1, S1, W3, S3, row, K, kb + 2 * G, k1, g4, rok);
+    if (kb + G < k1) {
+      batch_scales<G, kWin>(B, xch, r16, g4);
+      mma_batch<G>(B, bh, bl, K, kb + G, k1, g4, tv, f32, ag, au);
+    }
+    if (kb + 3 * G < k1) load_batch<G, kWin>(B, W1, S1, W3, S3, row, K, kb + 3 * G, k1, g4, rok);
+  }
+  // K ranges added in order: ((r0 + r1) + r2) + r3
+  *reinterpret_cast<f32x4*>(&red[item][ks][0][lane][0]) = ag;
+  *reinterpret_cast<f32x4*>(&red[item][ks][1][lane][0]) = au;
+  __syncthreads();
+  if (ks == 0 && rok && tv) {
+#pragma unroll
+    for (int w = 1; w < kUpKS; ++w) {
+      ag += *reinterpret_cast<const f32x4*>(&red[item][w][0][lane][0]);
+      au += *reinterpret_cast<const f32x4*>(&red[item][w][1][lane][0]);
+    }
+    uint16_t hh[4], hl[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) split_bf16(silu_clamped(ag[q], au[q], p.limit) * wr, hh[q], hl[q]);
+    const int64_t off = static_cast<int64_t>(drow) * p.I + rt * 16 + 4 * g4;
+    *reinterpret_cast<uint2*>(p.h_hi + off) = uint2{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16)};
+    *reinterpret_cast<uint2*>(p.h_lo + off) = uint2{hl[0] | (uint32_t(hl[1]) << 16), hl[2] | (uint32_t(hl[3]) << 16)};
+  }
+}
+
+// acc += W(16 rows, K block) x (hi + lo) of a 16-bit activation plane pair.
+template <typename Raw>
+__device__ __forceinline__ void mma_hilo(const Raw& a, const uint16_t* hi, const uint16_t* lo, int kc,
+                                         bool ok, f32x4& acc) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bf16x8 av = a_operand(a, j);
+    acc = mfma16(av, b_operand(hi, kc, j, ok), acc);
+    acc = mfma16(av, b_operand(lo, kc, j, ok), acc);
+  }
+}
+
+// Final add and cast of one 16-row output tile (wave 0 after the reduction).
+__device__ __forceinline__ void down_epilogue(const DecodeArgs& p, f32x4 a, f32x4 sh, int row0,
+                                              int r16, int g4) {
+  const int64_t o = static_cast<int64_t>(r16) * p.H + row0 + 4 * g4;
+  if (!p.x_f32) {
+    // the shared output is rounded to x's dtype before it is added
+    if (p.Is > 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[q] += bf16_bits_to_f32(f32_to_bf16_bits(sh[q]));
+    } else if (p.shared_out) {
+      const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.shared_out) + o);
+      a += f32x4{__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                 __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
+    }
+    uint16_t* ob = static_cast<uint16_t*>(p.out);
+    *reinterpret_cast<uint2*>(ob + o) =
+        uint2{f32_to_bf16_bits(a[0]) | (uint32_t(f32_to_bf16_bits(a[1])) << 16),
+              f32_to_bf16_bits(a[2]) | (uint32_t(f32_to_bf16_bits(a[3])) << 16)};
+  } else {
+    if (p.Is > 0) a += sh;
+    else if (p.shared_out) a += *reinterpret_cast<const f32x4*>(static_cast<const float*>(p.shared_out) + o);
+    *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + o) = a;
+  }
+}
+
+// Down + combine with every routed h row (N = T*k of them) and hs staged in
+// LDS once per block; weights of up to kDownGroup experts in flight per wave.
+__global__ __launch_bounds__(kDownW * 64) void k_down_decode_staged(DecodeArgs p) {
+  extern __shared__ __align__(16) uint16_t lds_dn[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int row0 = blockIdx.x * 16;
+  const int64_t row = row0 + r16;
+  const int U = p.active[0];
+  const int N = p.T * p.k;
+  const bool tok = r16 < p.T;
+  const int I = p.I, Is = p.Is;
+  const int is = I + 8, iss = Is + 8;       // padded LDS row strides
+  uint16_t* hh = lds_dn;
+  uint16_t* hl = hh + N * is;
+  uint16_t* sh_h = hl + N * is;
+  uint16_t* sh_l = sh_h + p.T * iss;
+  float (*red)[kDownW][64][4] = reinterpret_cast<float (*)[kDownW][64][4]>(sh_l + p.T * iss);
+  const int nblk = (I + 127) / 128;
+  const int per = (nblk + kDownW - 1) / kDownW;
+  const int kb0 = min(wave * per, nblk), kb1 = min(kb0 + per, nblk);
+  const int snblk = (Is + 127) / 128;
+  const int sper = (snblk + kDownW - 1) / kDownW;
+  const int skb0 = min(wave * sper, snblk), skb1 = min(skb0 + sper, snblk);
+  // 1. activations (h rows and hs) and dispatch rows first, into registers
+  const int hch = N * (I / 8), sch = p.T * (Is / 8);
+  u32x4 hv[kDownHRegChunks][2], sv[2];
+#pragma unroll
+  for (int j = 0; j < kDownHRegChunks; ++j) {
+    const int c = tid + j * kDownW * 64;
+    if (c < hch) {
+      const int64_t e = static_cast<int64_t>(c / (I / 8)) * I + (c % (I / 8)) * 8;
+      hv[j][0] = ldg16(p.h_hi + e);
+      hv[j][1] = ldg16(p.h_lo + e);
+    }
+  }
+  if (tid < sch) {
+    const int64_t e = static_cast<int64_t>(tid / (Is / 8)) * Is + (tid % (Is / 8)) * 8;
+    sv[0] = ldg16(p.hs_hi + e);
+    sv[1] = ldg16(p.hs_lo + e);
+  }
+  int drow[kDownGroup];
+#pragma unroll
+  for (int i = 0; i < kDownGroup; ++i) drow[i] = (i < U && tok) ? p.rowmap[i * p.T + r16] : -1;
+  // 2. the first expert group's w2 blocks and the shared w2 block
+  RawFP4 r[kDownGroup];
+  RawBF16 rs;
+  {
+    const int kc = kb0 * 128 + g4 * 32;
+#pragma unroll
+    for (int i = 0; i < kDownGroup; ++i) {
+      const bool in = i < U;
+      const SlotDesc* d = p.desc + (in ? i : 0);
+      load_raw(r[i], static_cast<const uint8_t*>(d->p[6]), static_cast<const uint8_t*>(d->p[7]),
+               row, I, kc, in && kb0 < kb1 && kc < I);
+    }
+    const int skc = skb0 * 128 + g4 * 32;
+    load_raw(rs, p.ws2, row, Is, skc, Is > 0 && skb0 < skb1 && skc < Is);
+  }
+  // 3. activations to LDS while the weights are in flight
+#pragma unroll
+  for (int j = 0; j < kDownHRegChunks; ++j) {
+    const int c = tid + j * kDownW * 64;
+    if (c < hch) {
+      const int off = (c / (I / 8)) * is + (c % (I / 8)) * 8;
+      *reinterpret_cast<u32x4*>(hh + off) = hv[j][0];
+      *reinterpret_cast<u32x4*>(hl + off) = hv[j][1];
+    }
+  }
+  if (tid < sch) {
+    const int off = (tid / (Is / 8)) * iss + (tid % (Is / 8)) * 8;
+    *reinterpret_cast<u32x4*>(sh_h + off) = sv[0];
+    *reinterpret_cast<u32x4*>(sh_l + off) = sv[1];
+  }
+  __syncthreads();
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accs = acc;
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int kc = kb * 128 + g4 * 32;
+    const bool kok = kc < I;
+    for (int u0 = 0; u0 < U; u0 += kDownGroup) {
+      if (kb != kb0 || u0 != 0) {
+#pragma unroll
+        for (int i = 0; i < kDownGroup; ++i) {
+          const bool in = u0 + i < U;
+          const SlotDesc* d = p.desc + (in ? u0 + i : 0);
+          load_raw(r[i], static_cast<const uint8_t*>(d->p[6]), static_cast<const uint8_t*>(d->p[7]),
+                   row, I, kc, in && kok);
+          drow[i] = (in && tok) ? p.rowmap[(u0 + i) * p.T + r16] : -1;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kDownGroup; ++i) {
+        if (u0 + i >= U) break;
+        const bool ok = kok && drow[i] >= 0;
+        const int hb = (ok ? drow[i] : 0) * is;
+        mma_hilo(r[i], hh + hb, hl + hb, kc, ok, acc);
+      }
+    }
+  }
+  for (int kb = skb0; kb < skb1; ++kb) {
+    const int kc = kb * 128 + g4 * 32;
+    if (kb != skb0) load_raw(rs, p.ws2, row, Is, kc, kc < Is);
+    const int hb = (tok ? r16 : 0) * iss;
+    mma_hilo(rs, sh_h + hb, sh_l + hb, kc, tok && kc < Is, accs);
+  }
+  *reinterpret_cast<f32x4*>(&red[0][wave][lane][0]) = acc;
+  *reinterpret_cast<f32x4*>(&red[1][wave][lane][0]) = accs;
+  __syncthreads();
+  if (wave == 0 && tok) {
+    f32x4 a = {0.f, 0.f, 0.f, 0.f}, sh = a;
+    for (int w = 0; w < kDownW; ++w) {
+      a += *reinterpret_cast<const f32x4*>(&red[0][w][lane][0]);
+      sh += *reinterpret_cast<const f32x4*>(&red[1][w][lane][0]);
+    }
+    down_epilogue(p, a, sh, row0, r16, g4);
+  }
+}
+
+__global__ __launch_bounds__(kDownW * 64) void k_down_decode(DecodeArgs p) {
+  __shared__ float red[2][kDownW][64][4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int row0 = blockIdx.x * 16;
+  const int64_t row = row0 + r16;
+  const int U = p.active[0];
+  const bool tok = r16 < p.T;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accs = acc;
+  {
+    const int K = p.I;
+    const int nblk = (K + 127) / 128;
+    const int per = (nblk + kDownW - 1) / kDownW;
+    const int kb0 = min(wave * per, nblk), kb1 = min(kb0 + per, nblk);
+    for (int kb = kb0; kb < kb1; ++kb) {
+      const int kc = kb * 128 + g4 * 32;
+      const bool kok = kc < K;
+      for (int u0 = 0; u0 < U; u0 += kDownGroup) {
+        RawFP4 r[kDownGroup];
+        int drow[kDownGroup];
+#pragma unroll
+        for (int i = 0; i < kDownGroup; ++i) {
+          const bool in = u0 + i < U;
+          const SlotDesc* d = p.desc + (in ? u0 + i : 0);
+          load_raw(r[i], static_cast<const uint8_t*>(d->p[6]), static_cast<const uint8_t*>(d->p[7]),
+                   row, K, kc, in && kok);
+          drow[i] = (in && tok) ? p.rowmap[(u0 + i) * p.T + r16] : -1;
+        }
+#pragma unroll
+        for (int i = 0; i < kDownGroup; ++i) {
+          if (u0 + i >= U) break;
+          const bool ok = kok && drow[i] >= 0;
+          const int64_t hb = static_cast<int64_t>(ok ? drow[i] : 0) * K;
+          mma_hilo(r[i], p.h_hi + hb, p.h_lo + hb, kc, ok, acc);
+        }
+      }
+    }
+  }
+  if (p.Is > 0) {
+    const int K = p.Is;
+    const int nblk = (K + 127) / 128;
+    const int per = (nblk + kDownW - 1) / kDownW;
+    const int kb0 = min(wave * per, nblk), kb1 = min(kb0 + per, nblk);
+    for (int kb = kb0; kb < kb1; ++kb) {
+      const int kc = kb * 128 + g4 * 32;
+      RawBF16 r;
+      load_raw(r, p.ws2, row, K, kc, kc < K);
+      const int64_t hb = static_cast<int64_t>(tok ? r16 : 0) * K;
+      mma_hilo(r, p.hs_hi + hb, p.hs_lo + hb, kc, tok && kc < K, accs);
+    }
+  }
+  *reinterpret_cast<f32x4*>(&red[0][wave][lane][0]) = acc;
+  *reinterpret_cast<f32x4*>(&red[1][wave][lane][0]) = accs;
+  __syncthreads();
+  if (wave == 0 && tok) {
+    f32x4 a = {0.f, 0.f, 0.f, 0.f}, sh = a;
+    for (int w = 0; w < kDownW; ++w) {
+      a += *reinterpret_cast<const f32x4*>(&red[0][w][lane][0]);
+      sh += *reinterpret_cast<const f32x4*>(&red[1][w][lane][0]);
+    }
+    down_epilogue(p, a, sh, row0, r16, g4);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                                 hipStream_t s, const hipEvent_t* ev, int repeat) {
+  DecodeArgs p{};
+  p.T = d.tokens; p.H = d.hidden; p.I = d.inter; p.Is = d.inter_shared; p.k = d.top_k;
+  p.limit = d.limit;
+  p.desc = a.desc; p.active = a.active; p.rowmap = a.rowmap; p.wrow = a.wrow;
+  p.x = a.x; p.x_f32 = d.x_dtype == DSK_DTYPE_F32;
+  p.ws1 = static_cast<const uint16_t*>(a.ws1);
+  p.ws3 = static_cast<const uint16_t*>(a.ws3);
+  p.hs_hi = reinterpret_cast<uint16_t*>(a.ws + L.hs_hi);
+  p.hs_lo = reinterpret_cast<uint16_t*>(a.ws + L.hs_lo);
+  p.h_hi = reinterpret_cast<uint16_t*>(a.ws + L.h_hi);
+  p.h_lo = reinterpret_cast<uint16_t*>(a.ws + L.h_lo);
+  p.ws2 = static_cast<const uint16_t*>(a.ws2);
+  p.shared_out = a.shared_out;
+  p.out = a.out;
+  p.up_tiles = d.inter / 16;
+  const int groups = (p.up_tiles + kUpItems - 1) / kUpItems;
+  const int max_slots = d.n_experts < d.tokens * d.top_k ? d.n_experts : d.tokens * d.top_k;
+  p.shared_blocks = p.Is / 16;
+  const unsigned up_blocks = static_cast<unsigned>(p.shared_blocks + max_slots * groups);
+  hipError_t e;
+  const size_t up_lds = static_cast<size_t>(p.x_f32 ? 2 : 1) * p.T * (p.H + 8) * 2 + kUpLdsFixed;
+  // scale windows need 4-byte aligned scale rows (H a multiple of 128)
+  const bool win = d.hidden % 128 == 0;
+  for (int r = 0; r < repeat; ++r) {
+    if (win && !p.x_f32) k_up_stream<kUpBatch, true, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    else if (win) k_up_stream<kUpBatch, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    else if (!p.x_f32) k_up_stream<kUpBatch, false, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    else k_up_stream<kUpBatch, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
+  const size_t dn_lds = static_cast<size_t>(d.tokens) * d.top_k * (d.inter + 8) * 4 +
+                        static_cast<size_t>(d.tokens) * (d.inter_shared + 8) * 4 +
+                        2 * kDownW * 64 * 4 * sizeof(float);
+  // staged: all activations fit in LDS and in the per-thread staging registers
+  const bool staged = dn_lds <= kMaxLds &&
+                      d.tokens * d.top_k * (d.inter / 8) <= kDownHRegChunks * kDownW * 64 &&
+                      d.tokens * (d.inter_shared / 8) <= kDownW * 64;
+  for (int r = 0; r < repeat; ++r) {
+    if (staged)
+      k_down_decode_staged<<<static_cast<unsigned>(d.hidden / 16), kDownW * 64, dn_lds, s>>>(p);
+    else
+      k_down_decode<<<static_cast<unsigned>(d.hidden / 16), kDownW * 64, 0, s>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  // down and combine are one kernel here: both stage events mark its end
+  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
+  if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return e;
+  return hipSuccess;
+}
+
+}  // namespace dsk

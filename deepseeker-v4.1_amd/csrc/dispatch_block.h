@@ -1,0 +1,271 @@
+// Token -> expert dispatch run by one workgroup (device code shared by the
+// standalone dispatch kernel and the last block of the fused router).
+//
+// Same grouping as the reference's np.unique / row discovery in moe_layer
+// (src/deepseeker/mlx_forward.py:294-312, 388-396) and the moe_align_block_size
+// contract (src/deepseeker/moe_align.py:21-46): flat (token, slot) positions
+// sorted by (expert, position).  S = blockDim.x / 64 waves; wave w owns a
+// contiguous segment of positions.  Pass 1: per-wave histograms with LDS
+// integer atomics (order free, result exact).  Scan: per expert a prefix
+// over waves, then an exclusive scan over experts.  Pass 2 walks each
+// segment in 64-position chunks, in order: lanes holding the same expert
+// are found with one ballot per expert-id bit, ranked by popcount of the
+// lower lanes; the highest such lane advances the (wave, expert) cursor,
+// which keeps the permutation stable.  Besides counts / offsets / perm /
+// rank / active it writes, for the expert kernels, one descriptor per
+// active expert and the token and route weight of every dispatch row.
+#pragma once
+
+#include "dsk_internal.h"
+
+namespace dsk {
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) {
+    int o = __shfl_up(v, s, 64);
+    if (lane >= s) v += o;
+  }
+  return v;
+}
+
+// Wave-wide max / min of a uint32 without LDS: DPP exchanges inside each
+// 16-lane row (quad swaps, half-row mirror, row mirror leave every lane with
+// its row's extreme), then the four rows' values through readlane.
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+}
+constexpr int kDppQuadSwap1 = 0xB1;    // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadSwap2 = 0x4E;    // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppRowMirror = 0x140;   // row_mirror
+
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<kDppQuadSwap1>(v));
+  v = max(v, dpp_u32<kDppQuadSwap2>(v));
+  v = max(v, dpp_u32<kDppHalfMirror>(v));
+  v = max(v, dpp_u32<kDppRowMirror>(v));
+  return max(max(readlane_u32(v, 0), readlane_u32(v, 16)), max(readlane_u32(v, 32), readlane_u32(v, 48)));
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, dpp_u32<kDppQuadSwap1>(v));
+  v = min(v, dpp_u32<kDppQuadSwap2>(v));
+  v = min(v, dpp_u32<kDppHalfMirror>(v));
+  v = min(v, dpp_u32<kDppRowMirror>(v));
+  return min(min(readlane_u32(v, 0), readlane_u32(v, 16)), min(readlane_u32(v, 32), readlane_u32(v, 48)));
+}
+
+// LDS needed: (S * E + E + 32) int32.
+__device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ idx, int N, int E, int k,
+                                               int nbits, const float* __restrict__ wflat,
+                                               const dsk_expert_ptrs* __restrict__ table,
+                                               const DispatchOut& o, int32_t* lds) {
+  const int nthr = blockDim.x;
+  const int S = nthr >> 6;
+  int32_t* hist = lds;                         // [S][E]
+  int32_t* base = lds + S * E;                 // [E]
+  int32_t* wsum = base + E;                    // [16]
+  int32_t* wflag = wsum + 16;                  // [16]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  for (int i = tid; i < S * E; i += nthr) hist[i] = 0;
+  __syncthreads();
+
+  const int seg = ((N + S - 1) / S + 63) & ~63;
+  const int beg = min(wave * seg, N), end = min(beg + seg, N);
+  for (int p = beg + lane; p < end; p += 64) {
+    const int e = idx[p];
+    if (e >= 0 && e < E) atomicAdd(&hist[wave * E + e], 1);
+  }
+  __syncthreads();
+
+  const int per = (E + nthr - 1) / nthr;
+  const int e_beg = min(tid * per, E), e_end = min(e_beg + per, E);
+  int run_cnt = 0, run_act = 0;
+  for (int e = e_beg; e < e_end; ++e) {
+    int r = 0;
+    for (int w = 0; w < S; ++w) {
+      const int c = hist[w * E + e];
+      hist[w * E + e] = r;
+      r += c;
+    }
+    o.counts[e] = r;
+    base[e] = r;            // the count, until the scan below
+    run_cnt += r;
+    run_act += (r > 0);
+  }
+  const int ic = wave_incl_scan(run_cnt, lane);
+  const int ia = wave_incl_scan(run_act, lane);
+  if (lane == 63) { wsum[wave] = ic; wflag[wave] = ia; }
+  __syncthreads();
+  int off_c = 0, off_a = 0;
+  for (int w = 0; w < wave; ++w) { off_c += wsum[w]; off_a += wflag[w]; }
+  int xc = off_c + ic - run_cnt, xa = off_a + ia - run_act;
+  for (int e = e_beg; e < e_end; ++e) {
+    const int c = base[e];
+    o.offsets[e] = xc;
+    base[e] = xc;
+    if (c > 0) {
+      o.active[1 + xa] = e;
+      if (o.desc) {
+        SlotDesc d;
+        d.e = e; d.n_tok = c; d.tok_base = xc; d.pad = 0;
+        const dsk_expert_ptrs t = table[e];
+        d.p[0] = t.w1; d.p[1] = t.s1; d.p[2] = t.b1;
+        d.p[3] = t.w3; d.p[4] = t.s3; d.p[5] = t.b3;
+        d.p[6] = t.w2; d.p[7] = t.s2; d.p[8] = t.b2;
+        d.pad2 = nullptr;
+        o.desc[xa] = d;
+      }
+      ++xa;
+    }
+    xc += c;
+  }
+  if (tid == nthr - 1) {
+    o.offsets[E] = xc;
+    o.active[0] = xa;
+  }
+  __syncthreads();
+
+  const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
+  for (int c0 = beg; c0 < end; c0 += 64) {
+    const int p = c0 + lane;
+    const bool in = p < end;
+    const int e = in ? idx[p] : -1;
+    const bool ok = in && e >= 0 && e < E;
+    uint64_t mask = __ballot(ok);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = ok && ((e >> b) & 1);
+      const uint64_t bb = __ballot(bit);
+      mask &= bit ? bb : ~bb;
+    }
+    if (ok) {
+      const int rk = __popcll(mask & lt);
+      const int pos = base[e] + hist[wave * E + e] + rk;
+      o.perm[pos] = p;
+      o.rank[p] = pos;
+      if (o.xrow) {
+        o.xrow[pos] = p / k;
+        o.wrow[pos] = wflat[p];
+      }
+    } else if (in) {
+      o.rank[p] = -1;
+    }
+    // the highest lane of each group advances the cursor (after every lane read it)
+    __builtin_amdgcn_wave_barrier();
+    if (ok && lane == 63 - __clzll(mask)) hist[wave * E + e] += __popcll(mask);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// One-wave dispatch for N = T*k <= 64 positions (lane i holds position i),
+// same outputs as dispatch_block, plus rowmap[slot * T + t] = the dispatch
+// row of token t for active expert `slot` (-1 if the token is not routed to
+// it).  A position's sorted place is the number of positions with a smaller
+// (expert, position) key, counted over the wave with uniform readlanes;
+// counts come from an LDS histogram and offsets from its exclusive scan.
+// idx / wflat may point to LDS.  LDS needed: 64 + 64 * ceil(E / 64) +
+// min(E, 64) * T int32.
+__device__ __forceinline__ void dispatch_wave(const int32_t* idx, int N, int E, int k, int T,
+                                              const float* wflat,
+                                              const dsk_expert_ptrs* __restrict__ table,
+                                              const DispatchOut& o, int32_t* rowmap_out,
+                                              int32_t* lds) {
+  const int lane = threadIdx.x & 63;
+  const int per = (E + 63) / 64;         // experts per lane in the histogram
+  int32_t* sorted = lds;                 // [64] expert id at each sorted position
+  int32_t* hist = lds + 64;              // [64 * per]
+  int32_t* rmap = hist + 64 * per;       // [slots][T]
+  const int e_in = lane < N ? idx[lane] : -1;
+  const bool ok = lane < N && e_in >= 0 && e_in < E;
+  const int key = ok ? e_in : E;         // dropped positions sort last
+  for (int i = 0; i < per; ++i) hist[lane * per + i] = 0;
+  int pos = 0;
+  for (int j = 0; j < N; ++j) {
+    const int kj = __builtin_amdgcn_readlane(key, j);
+    pos += (kj < key) || (kj == key && j < lane);
+  }
+  const int n_valid = __popcll(__ballot(ok));
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  if (lane < N) sorted[pos] = key;
+  if (lane >= N) sorted[lane] = E;
+  if (ok) atomicAdd(&hist[e_in], 1);
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  // dense counts / offsets: lane handles experts [lane*per, lane*per + per)
+  int run = 0;
+  for (int i = 0; i < per; ++i) run += hist[lane * per + i];
+  int xo = wave_incl_scan(run, lane) - run;
+  for (int i = 0; i < per; ++i) {
+    const int e = lane * per + i;
+    if (e < E) {
+      const int c = hist[e];
+      o.counts[e] = c;
+      o.offsets[e] = xo;
+      xo += c;
+    }
+  }
+  // position q = lane: first position of its expert?
+  const int se = sorted[lane];
+  const bool first = lane < n_valid && (lane == 0 || sorted[lane - 1] != se);
+  const uint64_t firsts = __ballot(first);
+  const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
+  const int n_act = __popcll(firsts);
+  const int slot_here = __popcll(firsts & (lt | (1ull << lane))) - 1;   // slot of position q
+  if (lane == 0) { o.offsets[E] = n_valid; o.active[0] = n_act; }
+  if (first) {
+    const int slot = slot_here;
+    o.active[1 + slot] = se;
+    if (o.desc) {
+      const int cnt = hist[se];
+      SlotDesc d;
+      d.e = se; d.n_tok = cnt; d.tok_base = lane; d.pad = 0;
+      const dsk_expert_ptrs t = table[se];
+      d.p[0] = t.w1; d.p[1] = t.s1; d.p[2] = t.b1;
+      d.p[3] = t.w3; d.p[4] = t.s3; d.p[5] = t.b3;
+      d.p[6] = t.w2; d.p[7] = t.s2; d.p[8] = t.b2;
+      d.pad2 = nullptr;
+      o.desc[slot] = d;
+    }
+  }
+  const int n_map = n_act * T;
+  for (int i = lane; i < n_map; i += 64) rmap[i] = -1;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  const int my_slot = __shfl(slot_here, pos & 63, 64);
+  if (ok) {
+    o.perm[pos] = lane;
+    o.rank[lane] = pos;
+    if (o.xrow) {
+      o.xrow[pos] = lane / k;
+      o.wrow[pos] = wflat[lane];
+    }
+    rmap[my_slot * T + lane / k] = pos;
+  } else if (lane < N) {
+    o.rank[lane] = -1;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  if (rowmap_out)
+    for (int i = lane; i < n_map; i += 64) rowmap_out[i] = rmap[i];
+}
+
+__host__ __device__ inline int bits_for(int E) {
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  return nbits;
+}
+
+}  // namespace dsk

@@ -50,10 +50,29 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t b) {
   return __uint_as_float(bits);
 }
 
+// ---------------------------------------------------------------- dispatch
+// One active expert, written by the dispatch for the expert kernels.
+struct SlotDesc {
+  int32_t e, n_tok, tok_base, pad;
+  const void* p[9];          // w1 s1 b1 w3 s3 b3 w2 s2 b2 (copied from the table)
+  const void* pad2;
+};
+static_assert(sizeof(SlotDesc) == 96, "SlotDesc layout");
+
+struct DispatchOut {
+  int32_t* counts; int32_t* offsets; int32_t* perm; int32_t* rank; int32_t* active;
+  SlotDesc* desc;            // [E] or null
+  int32_t* xrow;             // [T*k] token of each dispatch row, or null
+  float* wrow;               // [T*k] route weight of each dispatch row
+};
+
 // ---------------------------------------------------------------- workspace
 // Regions of the caller-owned workspace used by dsk_moe_forward / dsk_experts.
 struct Workspace {
   size_t scores, idx, wts, counts, offsets, perm, rank, active;  // routing
+  size_t desc, xrow, wrow;  // dispatch descriptors
+  size_t ctr;               // arrival counters of the fused router (zero between calls)
+  size_t rowmap;            // decode pipeline: [min(E,64)][T] token -> dispatch row
   size_t xb_hi, xb_lo;      // B-operand planes of x   [T][H]  (16-bit)
   size_t h_hi, h_lo;        // routed intermediate      [T*k][I] (16-bit)
   size_t hs_hi, hs_lo;      // shared intermediate      [T][Is]  (16-bit)
@@ -64,18 +83,54 @@ struct Workspace {
 
 Workspace workspace_layout(const dsk_moe_desc& d);
 
+// Bytes reserved at the start of every workspace for the fused router's
+// arrival counters (one per token tile plus one; fused up to 64 tokens).
+constexpr size_t kCounterBytes = 1024;
+constexpr int kFusedMaxTokens = 64;
+// Decode pipeline limits and the shared expert's gate/up K split.
+constexpr int kDecodeMaxTokens = 16;
+constexpr int kDecodeMaxPositions = 64;
+constexpr size_t kMaxLds = 163840;          // LDS bytes one gfx950 workgroup may use
+constexpr size_t kUpLdsFixed = 2 * 4 * 2 * 64 * 4 * 4 + 8 * 640;   // decode gate/up: reduction + scale tiles
+inline bool decode_pipeline(const dsk_moe_desc& d) {
+  // the gate/up kernel stages the tokens' activations (bf16 hi, and lo for
+  // float32 x) plus its reduction and scale-exchange buffers in LDS
+  const size_t x_lds = static_cast<size_t>(d.x_dtype == DSK_DTYPE_F32 ? 2 : 1) * d.tokens *
+                           (d.hidden + 8) * 2 + kUpLdsFixed;
+  return d.tokens <= kDecodeMaxTokens && d.tokens * d.top_k <= kDecodeMaxPositions &&
+         x_lds <= kMaxLds;
+}
+
 // ---------------------------------------------------------------- launchers
 // All launchers assume validated arguments.
 hipError_t launch_route(const dsk_moe_desc& d, const void* x, const void* gate_w,
                         const float* gate_b, float* scores, int32_t* idx,
                         float* weights, hipStream_t s);
 
-hipError_t launch_dispatch(const dsk_moe_desc& d, const int32_t* idx, int32_t* counts,
-                           int32_t* offsets, int32_t* perm, int32_t* rank,
-                           int32_t* active, hipStream_t s);
+// Router + top-k + dispatch.  Small batches run as one kernel whose last
+// blocks do the top-k and the dispatch; larger ones as three kernels.
+struct RouteArgs {
+  const void* x; const void* gate_w; const float* gate_b;
+  float* scores; int32_t* idx; float* weights;
+  const dsk_expert_ptrs* table;
+  DispatchOut out;
+  unsigned int* ctr;        // [tokens + 1] arrival counters (fused path), zero between calls
+  // decode pipeline (tokens * top_k <= 64 and tokens <= 16): one-wave dispatch
+  // with a token -> dispatch-row map
+  int32_t* rowmap;          // [min(E, 64)][tokens] or null
+};
+// Fused router + dispatch (general path).
+hipError_t launch_route_dispatch(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
+// Decode pipeline: gate scores only, then one block of top-k + one-wave dispatch.
+hipError_t launch_gate_scores(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
+hipError_t launch_route_tail(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
+
+hipError_t launch_dispatch(const dsk_moe_desc& d, const int32_t* idx, const float* wflat,
+                           const dsk_expert_ptrs* table, const DispatchOut& o, hipStream_t s);
 
 struct ExpertsArgs {
   const dsk_expert_ptrs* table;
+  const SlotDesc* desc; const int32_t* xrow; const float* wrow;
   const void* ws1; const void* ws3; const void* ws2;
   const void* shared_out;    // precomputed shared output [T][H] in x dtype (or null)
   const void* x;
@@ -84,12 +139,23 @@ struct ExpertsArgs {
   const int32_t* rank; const int32_t* active;
   void* out;
   char* ws;                  // workspace base
+  const int32_t* rowmap;     // decode pipeline: [slot][T] dispatch row of token t, -1 if none
 };
 
 // ev (nullable): 3 events recorded after the gate/up kernel, the down kernel
 // and the combine kernel.
+// repeat: each kernel is launched that many times in a row (timing only).
 hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L,
-                          const ExpertsArgs& a, hipStream_t s, const hipEvent_t* ev);
+                          const ExpertsArgs& a, hipStream_t s, const hipEvent_t* ev, int repeat);
+
+hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t s);
+
+// Decode pipeline (decode_pipeline(d)): routed and shared gate/up in one
+// kernel, then down + shared down + combine fused per 16 output rows.  Needs
+// a.desc, a.active, a.rowmap, a.wrow from the route tail.
+hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L,
+                                 const ExpertsArgs& a, hipStream_t s, const hipEvent_t* ev,
+                                 int repeat);
 
 hipError_t launch_fp4_dequant(const uint8_t* packed, const uint8_t* scales,
                               int64_t rows, int64_t cols, void* out, int out_dtype,

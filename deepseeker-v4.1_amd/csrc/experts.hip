@@ -109,28 +109,39 @@ __device__ __forceinline__ void split_store(uint16_t* hi, uint16_t* lo, int64_t 
   *reinterpret_cast<uint2*>(lo + off) = uint2{l[0] | (uint32_t(l[1]) << 16), l[2] | (uint32_t(l[3]) << 16)};
 }
 
+
 struct UpArgs {
   int T, H, I, Is, k;
   float limit;
-  const int32_t* counts; const int32_t* offsets; const int32_t* perm; const int32_t* active;
-  const float* wflat;
-  const dsk_expert_ptrs* table;
-  const uint16_t* xb_hi; const uint16_t* xb_lo;   // [T][H] B planes of x
-  const uint16_t* ws1; const uint16_t* ws3;       // shared [Is][H] bf16
-  uint16_t* h_hi; uint16_t* h_lo;                 // [T*k][I]   (dispatch row order)
-  uint16_t* hs_hi; uint16_t* hs_lo;               // [T][Is]
-  int tiles;                                      // I / 16
-  int routed_blocks;                              // max_slots * tiles
+  const SlotDesc* desc; const int32_t* active;   // active[0] = number of descriptors
+  const int32_t* xrow; const float* wrow;        // per dispatch row: token, route weight
+  const uint16_t* xb_hi; const uint16_t* xb_lo;  // [T][H] B planes of x
+  const uint16_t* ws1; const uint16_t* ws3;      // shared [Is][H] bf16
+  uint16_t* h_hi; uint16_t* h_lo;                // [T*k][I]   (dispatch row order)
+  uint16_t* hs_hi; uint16_t* hs_lo;              // [T][Is]
+  int tiles;                                     // I / 16
+  int shared_blocks;                             // Is / 16 (blocks 0 .. shared_blocks-1)
 };
 
 // Per-wave partial products of one 16-row tile for NT token tiles, reduced
-// across the block's waves, then the clamped SwiGLU epilogue.
-template <int NT, bool XLO, typename Raw, typename LoadA>
+// across the block's waves, then the clamped SwiGLU epilogue.  Wave w owns
+// the contiguous K blocks [w*per, (w+1)*per), walked in groups of G; the
+// weight loads of a group are issued before anything that depends on the
+// routing (token rows, activations), so they are in flight first.
+template <int NT, bool XLO, int G, typename Raw, typename LoadA>
 __device__ __forceinline__ void up_tile(const UpArgs& p, LoadA load_a, int K, int row0,
                                         int n_tok, int tok_base, bool shared, float (*red)[64][4]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r16 = lane & 15, g4 = lane >> 4;
   const int nblk = (K + 127) / 128;
+  const int per = (nblk + kUpWaves - 1) / kUpWaves;
+  const int kb0 = min(wave * per, nblk), kb1 = min(kb0 + per, nblk);
+  const bool one_group = per <= G;
+  Raw r1[G], r3[G];
+  if (one_group) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) load_a(kb0 + i, kb0 + i < kb1, r1[i], r3[i]);
+  }
   for (int c0 = 0; c0 < n_tok; c0 += 16 * NT) {
     int xrow[NT];
     bool tv[NT];
@@ -138,33 +149,40 @@ __device__ __forceinline__ void up_tile(const UpArgs& p, LoadA load_a, int K, in
     for (int nt = 0; nt < NT; ++nt) {
       const int n = c0 + 16 * nt + r16;
       tv[nt] = n < n_tok;
-      xrow[nt] = !tv[nt] ? 0 : (shared ? n : p.perm[tok_base + n] / p.k);
+      xrow[nt] = !tv[nt] ? 0 : (shared ? n : p.xrow[tok_base + n]);
     }
     f32x4 ag[NT], au[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) { ag[nt] = f32x4{0.f, 0.f, 0.f, 0.f}; au[nt] = ag[nt]; }
-    Raw r1, r3;
-    int blk = wave;
-    if (blk < nblk) load_a(blk, r1, r3);
-    for (; blk < nblk; blk += kUpWaves) {
-      Raw c1 = r1, c3 = r3;
-      if (blk + kUpWaves < nblk) load_a(blk + kUpWaves, r1, r3);
-      bf16x8 a1[4], a3[4];
-      deq(c1, a1);
-      deq(c3, a3);
-      const int kc = blk * 128 + g4 * 32;
-      const bool kok = kc < K;
+    for (int gb = kb0; gb < kb1; gb += G) {
+      if (!one_group) {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        if (c0 + 16 * nt >= n_tok) break;
-        bf16x8 b[4];
-        load_b(p.xb_hi, xrow[nt], K, kc, kok && tv[nt], b);
+        for (int i = 0; i < G; ++i) load_a(gb + i, gb + i < kb1, r1[i], r3[i]);
+      }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) { ag[nt] = mfma(a1[j], b[j], ag[nt]); au[nt] = mfma(a3[j], b[j], au[nt]); }
-        if constexpr (XLO) {
-          load_b(p.xb_lo, xrow[nt], K, kc, kok && tv[nt], b);
+      for (int i = 0; i < G; ++i) {
+        const int kc = (gb + i) * 128 + g4 * 32;
+        const bool kok = gb + i < kb1 && kc < K;
+        bf16x8 a1[4], a3[4];
+        deq(r1[i], a1);
+        deq(r3[i], a3);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) { ag[nt] = mfma(a1[j], b[j], ag[nt]); au[nt] = mfma(a3[j], b[j], au[nt]); }
+        for (int nt = 0; nt < NT; ++nt) {
+          bf16x8 b[4];
+          load_b(p.xb_hi, xrow[nt], K, kc, kok && tv[nt], b);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            ag[nt] = mfma(a1[j], b[j], ag[nt]);
+            au[nt] = mfma(a3[j], b[j], au[nt]);
+          }
+          if constexpr (XLO) {
+            load_b(p.xb_lo, xrow[nt], K, kc, kok && tv[nt], b);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              ag[nt] = mfma(a1[j], b[j], ag[nt]);
+              au[nt] = mfma(a3[j], b[j], au[nt]);
+            }
+          }
         }
       }
     }
@@ -187,7 +205,7 @@ __device__ __forceinline__ void up_tile(const UpArgs& p, LoadA load_a, int K, in
           dst = static_cast<int64_t>(n) * p.Is;
         } else {
           const int dr = tok_base + n;
-          wr = p.wflat[p.perm[dr]];
+          wr = p.wrow[dr];
           dst = static_cast<int64_t>(dr) * p.I;
         }
         float h[4];
@@ -206,66 +224,77 @@ __device__ __forceinline__ void up_tile(const UpArgs& p, LoadA load_a, int K, in
   }
 }
 
+// Load-group sizes (K blocks whose weights one wave holds at once): FP4 is
+// 20 bytes per lane, role and block; bf16 is 64.
+constexpr int kGroupFP4 = 4;
+constexpr int kGroupBF16 = 2;
+
 template <int NT, bool XLO>
 __global__ __launch_bounds__(kUpWaves * 64) void k_up_fp4(UpArgs p) {
   __shared__ float red[2 * kUpWaves][64][4];
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15, g4 = lane >> 4;
   const int b = blockIdx.x;
-  if (b < p.routed_blocks) {
-    const int slot = b / p.tiles, rt = b % p.tiles;
+  if (b >= p.shared_blocks) {
+    const int rb = b - p.shared_blocks;
+    const int slot = rb / p.tiles, rt = rb % p.tiles;
     if (slot >= p.active[0]) return;
-    const int e = p.active[1 + slot];
-    const dsk_expert_ptrs ep = p.table[e];
+    const SlotDesc* d = p.desc + slot;
     const int row0 = rt * 16;
     const int64_t row = row0 + r16;
     const int K = p.H;
-    const uint8_t* W1 = static_cast<const uint8_t*>(ep.w1);
-    const uint8_t* S1 = static_cast<const uint8_t*>(ep.s1);
-    const uint8_t* W3 = static_cast<const uint8_t*>(ep.w3);
-    const uint8_t* S3 = static_cast<const uint8_t*>(ep.s3);
-    auto load_a = [&](int blk, RawFP4& r1, RawFP4& r3) {
+    const uint8_t* W1 = static_cast<const uint8_t*>(d->p[0]);
+    const uint8_t* S1 = static_cast<const uint8_t*>(d->p[1]);
+    const uint8_t* W3 = static_cast<const uint8_t*>(d->p[3]);
+    const uint8_t* S3 = static_cast<const uint8_t*>(d->p[4]);
+    auto load_a = [&](int blk, bool in, RawFP4& r1, RawFP4& r3) {
       const int kc = blk * 128 + g4 * 32;
-      const bool ok = kc < K;
+      const bool ok = in && kc < K;
       r1 = load_fp4(W1, S1, row, K, kc, ok);
       r3 = load_fp4(W3, S3, row, K, kc, ok);
     };
-    up_tile<NT, XLO, RawFP4>(p, load_a, K, row0, p.counts[e], p.offsets[e], false, red);
+    up_tile<NT, XLO, kGroupFP4, RawFP4>(p, load_a, K, row0, d->n_tok, d->tok_base, false, red);
   } else {
-    const int rt = b - p.routed_blocks;
-    const int row0 = rt * 16;
+    const int row0 = b * 16;
     const int64_t row = row0 + r16;
     const int K = p.H;
-    auto load_a = [&](int blk, RawBF16& r1, RawBF16& r3) {
+    auto load_a = [&](int blk, bool in, RawBF16& r1, RawBF16& r3) {
       const int kc = blk * 128 + g4 * 32;
-      const bool ok = kc < K;
+      const bool ok = in && kc < K;
       r1 = load_bf16w(p.ws1, row, K, kc, ok);
       r3 = load_bf16w(p.ws3, row, K, kc, ok);
     };
-    up_tile<NT, XLO, RawBF16>(p, load_a, K, row0, p.T, 0, true, red);
+    up_tile<NT, XLO, kGroupBF16, RawBF16>(p, load_a, K, row0, p.T, 0, true, red);
   }
 }
 
 struct DownArgs {
   int T, H, I, Is;
-  const int32_t* counts; const int32_t* offsets; const int32_t* active;
-  const dsk_expert_ptrs* table;
+  const SlotDesc* desc; const int32_t* active;
   const uint16_t* ws2;                   // shared [H][Is] bf16
   const uint16_t* h_hi; const uint16_t* h_lo;
   const uint16_t* hs_hi; const uint16_t* hs_lo;
   float* y;                              // [T*k][H]
   float* ys;                             // [T][H]
   int tiles;                             // H / 16
-  int routed_blocks;
+  int shared_blocks;                     // H / 16 when a shared expert is fused, else 0
 };
 
-template <int NT, typename Raw, typename LoadA>
+template <int NT, int G, typename Raw, typename LoadA>
 __device__ __forceinline__ void down_tile(const DownArgs& p, LoadA load_a, int K, int row0,
                                           int n_tok, int brow_base, const uint16_t* bhi,
                                           const uint16_t* blo, float* out, float (*red)[64][4]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r16 = lane & 15, g4 = lane >> 4;
   const int nblk = (K + 127) / 128;
+  const int per = (nblk + kDownWaves - 1) / kDownWaves;
+  const int kb0 = min(wave * per, nblk), kb1 = min(kb0 + per, nblk);
+  const bool one_group = per <= G;
+  Raw r[G];
+  if (one_group) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) load_a(kb0 + i, kb0 + i < kb1, r[i]);
+  }
   for (int c0 = 0; c0 < n_tok; c0 += 16 * NT) {
     f32x4 acc[NT];
     bool tv[NT];
@@ -274,27 +303,28 @@ __device__ __forceinline__ void down_tile(const DownArgs& p, LoadA load_a, int K
       acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
       tv[nt] = c0 + 16 * nt + r16 < n_tok;
     }
-    Raw r;
-    int blk = wave;
-    if (blk < nblk) load_a(blk, r);
-    for (; blk < nblk; blk += kDownWaves) {
-      Raw c = r;
-      if (blk + kDownWaves < nblk) load_a(blk + kDownWaves, r);
-      bf16x8 a[4];
-      deq(c, a);
-      const int kc = blk * 128 + g4 * 32;
-      const bool kok = kc < K;
+    for (int gb = kb0; gb < kb1; gb += G) {
+      if (!one_group) {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        if (c0 + 16 * nt >= n_tok) break;
-        const int64_t brow = brow_base + c0 + 16 * nt + r16;
-        bf16x8 b[4];
-        load_b(bhi, brow, K, kc, kok && tv[nt], b);
+        for (int i = 0; i < G; ++i) load_a(gb + i, gb + i < kb1, r[i]);
+      }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[nt] = mfma(a[j], b[j], acc[nt]);
-        load_b(blo, brow, K, kc, kok && tv[nt], b);
+      for (int i = 0; i < G; ++i) {
+        const int kc = (gb + i) * 128 + g4 * 32;
+        const bool kok = gb + i < kb1 && kc < K;
+        bf16x8 a[4];
+        deq(r[i], a);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[nt] = mfma(a[j], b[j], acc[nt]);
+        for (int nt = 0; nt < NT; ++nt) {
+          const int64_t brow = brow_base + c0 + 16 * nt + r16;
+          bf16x8 b[4];
+          load_b(bhi, brow, K, kc, kok && tv[nt], b);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[nt] = mfma(a[j], b[j], acc[nt]);
+          load_b(blo, brow, K, kc, kok && tv[nt], b);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[nt] = mfma(a[j], b[j], acc[nt]);
+        }
       }
     }
 #pragma unroll
@@ -319,31 +349,30 @@ __global__ __launch_bounds__(kDownWaves * 64) void k_down_fp4(DownArgs p) {
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15, g4 = lane >> 4;
   const int b = blockIdx.x;
-  if (b < p.routed_blocks) {
-    const int slot = b / p.tiles, rt = b % p.tiles;
+  if (b >= p.shared_blocks) {
+    const int rb = b - p.shared_blocks;
+    const int slot = rb / p.tiles, rt = rb % p.tiles;
     if (slot >= p.active[0]) return;
-    const int e = p.active[1 + slot];
-    const dsk_expert_ptrs ep = p.table[e];
+    const SlotDesc* d = p.desc + slot;
     const int row0 = rt * 16;
     const int64_t row = row0 + r16;
     const int K = p.I;
-    const uint8_t* W2 = static_cast<const uint8_t*>(ep.w2);
-    const uint8_t* S2 = static_cast<const uint8_t*>(ep.s2);
-    auto load_a = [&](int blk, RawFP4& r) {
+    const uint8_t* W2 = static_cast<const uint8_t*>(d->p[6]);
+    const uint8_t* S2 = static_cast<const uint8_t*>(d->p[7]);
+    auto load_a = [&](int blk, bool in, RawFP4& r) {
       const int kc = blk * 128 + g4 * 32;
-      r = load_fp4(W2, S2, row, K, kc, kc < K);
+      r = load_fp4(W2, S2, row, K, kc, in && kc < K);
     };
-    down_tile<NT, RawFP4>(p, load_a, K, row0, p.counts[e], p.offsets[e], p.h_hi, p.h_lo, p.y, red);
+    down_tile<NT, kGroupFP4, RawFP4>(p, load_a, K, row0, d->n_tok, d->tok_base, p.h_hi, p.h_lo, p.y, red);
   } else {
-    const int rt = b - p.routed_blocks;
-    const int row0 = rt * 16;
+    const int row0 = b * 16;
     const int64_t row = row0 + r16;
     const int K = p.Is;
-    auto load_a = [&](int blk, RawBF16& r) {
+    auto load_a = [&](int blk, bool in, RawBF16& r) {
       const int kc = blk * 128 + g4 * 32;
-      r = load_bf16w(p.ws2, row, K, kc, kc < K);
+      r = load_bf16w(p.ws2, row, K, kc, in && kc < K);
     };
-    down_tile<NT, RawBF16>(p, load_a, K, row0, p.T, 0, p.hs_hi, p.hs_lo, p.ys, red);
+    down_tile<NT, kGroupBF16, RawBF16>(p, load_a, K, row0, p.T, 0, p.hs_hi, p.hs_lo, p.ys, red);
   }
 }
 
@@ -356,6 +385,36 @@ __global__ __launch_bounds__(256) void k_split_x(const float* __restrict__ x, in
   const uint16_t h = f32_to_bf16_bits(v);
   hi[i] = h;
   lo[i] = f32_to_bf16_bits(v - bf16_bits_to_f32(h));
+}
+
+// Descriptors and row tables from a caller-supplied dispatch (dsk_experts).
+__global__ __launch_bounds__(256) void k_prepare(const int32_t* __restrict__ counts,
+                                                 const int32_t* __restrict__ offsets,
+                                                 const int32_t* __restrict__ perm,
+                                                 const int32_t* __restrict__ active,
+                                                 const float* __restrict__ wflat,
+                                                 const dsk_expert_ptrs* __restrict__ table, int N,
+                                                 int E, int k, SlotDesc* __restrict__ desc,
+                                                 int32_t* __restrict__ xrow, float* __restrict__ wrow) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int n_valid = min(offsets[E], N);
+  if (i < n_valid) {
+    const int p = perm[i];
+    xrow[i] = p / k;
+    wrow[i] = wflat[p];
+  }
+  const int n_act = min(active[0], E);
+  if (i < n_act) {
+    const int e = active[1 + i];
+    SlotDesc d;
+    d.e = e; d.n_tok = counts[e]; d.tok_base = offsets[e]; d.pad = 0;
+    const dsk_expert_ptrs t = table[e];
+    d.p[0] = t.w1; d.p[1] = t.s1; d.p[2] = t.b1;
+    d.p[3] = t.w3; d.p[4] = t.s3; d.p[5] = t.b3;
+    d.p[6] = t.w2; d.p[7] = t.s2; d.p[8] = t.b2;
+    d.pad2 = nullptr;
+    desc[i] = d;
+  }
 }
 
 // out[t] = cast( (sum over the token's expert rows in ascending expert id) + shared[t] ),
@@ -421,13 +480,43 @@ hipError_t launch_down(const DownArgs& a, unsigned blocks, hipStream_t s) {
   return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void k_zero_fill(u32x4* __restrict__ p, int64_t n16) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n16;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
 }  // namespace
 
+hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t s) {
+  const int64_t n16 = static_cast<int64_t>(bytes / 16);
+  if (n16 > 0) {
+    const int64_t blocks = (n16 + 255) / 256;
+    k_zero_fill<<<static_cast<unsigned>(blocks < 4096 ? blocks : 4096), 256, 0, s>>>(
+        static_cast<u32x4*>(p), n16);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
-                          hipStream_t s, const hipEvent_t* ev) {
+                          hipStream_t s, const hipEvent_t* ev, int repeat) {
   const int T = d.tokens, H = d.hidden, I = d.inter, Is = d.inter_shared, k = d.top_k;
   const int max_slots = (d.n_experts < T * k) ? d.n_experts : T * k;
   const bool x_f32 = d.x_dtype == DSK_DTYPE_F32;
+  hipError_t e;
+  const SlotDesc* desc = a.desc;
+  const int32_t* xrow = a.xrow;
+  const float* wrow = a.wrow;
+  if (!desc) {
+    SlotDesc* dd = reinterpret_cast<SlotDesc*>(a.ws + L.desc);
+    int32_t* xr = reinterpret_cast<int32_t*>(a.ws + L.xrow);
+    float* wr = reinterpret_cast<float*>(a.ws + L.wrow);
+    const int n = T * k > d.n_experts ? T * k : d.n_experts;
+    k_prepare<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(
+        a.counts, a.offsets, a.perm, a.active, a.weights, a.table, T * k, d.n_experts, k, dd, xr, wr);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    desc = dd; xrow = xr; wrow = wr;
+  }
   const uint16_t* xb_hi = static_cast<const uint16_t*>(a.x);
   const uint16_t* xb_lo = nullptr;
   if (x_f32) {
@@ -435,8 +524,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
     uint16_t* lo = reinterpret_cast<uint16_t*>(a.ws + L.xb_lo);
     const int64_t n = static_cast<int64_t>(T) * H;
     k_split_x<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(static_cast<const float*>(a.x), n, hi, lo);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if ((e = hipGetLastError()) != hipSuccess) return e;
     xb_hi = hi;
     xb_lo = lo;
   }
@@ -444,8 +532,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
 
   UpArgs u{};
   u.T = T; u.H = H; u.I = I; u.Is = Is; u.k = k; u.limit = d.limit;
-  u.counts = a.counts; u.offsets = a.offsets; u.perm = a.perm; u.active = a.active;
-  u.wflat = a.weights; u.table = a.table;
+  u.desc = desc; u.active = a.active; u.xrow = xrow; u.wrow = wrow;
   u.xb_hi = xb_hi; u.xb_lo = xb_lo;
   u.ws1 = static_cast<const uint16_t*>(a.ws1); u.ws3 = static_cast<const uint16_t*>(a.ws3);
   u.h_hi = reinterpret_cast<uint16_t*>(a.ws + L.h_hi);
@@ -453,35 +540,40 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
   u.hs_hi = reinterpret_cast<uint16_t*>(a.ws + L.hs_hi);
   u.hs_lo = reinterpret_cast<uint16_t*>(a.ws + L.hs_lo);
   u.tiles = I / 16;
-  u.routed_blocks = max_slots * u.tiles;
-  const unsigned up_blocks = static_cast<unsigned>(u.routed_blocks + (Is > 0 ? Is / 16 : 0));
-  hipError_t e;
-  if (x_f32) e = nt == 1 ? launch_up<1, true>(u, up_blocks, s) : nt == 2 ? launch_up<2, true>(u, up_blocks, s) : launch_up<4, true>(u, up_blocks, s);
-  else e = nt == 1 ? launch_up<1, false>(u, up_blocks, s) : nt == 2 ? launch_up<2, false>(u, up_blocks, s) : launch_up<4, false>(u, up_blocks, s);
-  if (e != hipSuccess) return e;
+  u.shared_blocks = Is > 0 ? Is / 16 : 0;
+  const unsigned up_blocks = static_cast<unsigned>(u.shared_blocks + max_slots * u.tiles);
+  for (int r = 0; r < repeat; ++r) {
+    if (x_f32) e = nt == 1 ? launch_up<1, true>(u, up_blocks, s) : nt == 2 ? launch_up<2, true>(u, up_blocks, s) : launch_up<4, true>(u, up_blocks, s);
+    else e = nt == 1 ? launch_up<1, false>(u, up_blocks, s) : nt == 2 ? launch_up<2, false>(u, up_blocks, s) : launch_up<4, false>(u, up_blocks, s);
+    if (e != hipSuccess) return e;
+  }
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
 
   DownArgs dn{};
   dn.T = T; dn.H = H; dn.I = I; dn.Is = Is;
-  dn.counts = a.counts; dn.offsets = a.offsets; dn.active = a.active; dn.table = a.table;
+  dn.desc = desc; dn.active = a.active;
   dn.ws2 = static_cast<const uint16_t*>(a.ws2);
   dn.h_hi = u.h_hi; dn.h_lo = u.h_lo; dn.hs_hi = u.hs_hi; dn.hs_lo = u.hs_lo;
   dn.y = reinterpret_cast<float*>(a.ws + L.y);
   dn.ys = reinterpret_cast<float*>(a.ws + L.ys);
   dn.tiles = H / 16;
-  dn.routed_blocks = max_slots * dn.tiles;
-  const unsigned down_blocks = static_cast<unsigned>(dn.routed_blocks + (Is > 0 ? H / 16 : 0));
-  e = nt == 1 ? launch_down<1>(dn, down_blocks, s) : nt == 2 ? launch_down<2>(dn, down_blocks, s) : launch_down<4>(dn, down_blocks, s);
-  if (e != hipSuccess) return e;
+  dn.shared_blocks = Is > 0 ? H / 16 : 0;
+  const unsigned down_blocks = static_cast<unsigned>(dn.shared_blocks + max_slots * dn.tiles);
+  for (int r = 0; r < repeat; ++r) {
+    e = nt == 1 ? launch_down<1>(dn, down_blocks, s) : nt == 2 ? launch_down<2>(dn, down_blocks, s) : launch_down<4>(dn, down_blocks, s);
+    if (e != hipSuccess) return e;
+  }
   if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
 
   dim3 cg(static_cast<unsigned>(T), static_cast<unsigned>((H + 1023) / 1024));
   const int mode = Is > 0 ? kSharedF32 : (a.shared_out ? kSharedExt : kNoShared);
-  if (x_f32)
-    k_combine<false><<<cg, 256, 0, s>>>(dn.y, dn.ys, a.shared_out, a.rank, H, k, mode, a.out);
-  else
-    k_combine<true><<<cg, 256, 0, s>>>(dn.y, dn.ys, a.shared_out, a.rank, H, k, mode, a.out);
-  e = hipGetLastError();
+  for (int r = 0; r < repeat; ++r) {
+    if (x_f32)
+      k_combine<false><<<cg, 256, 0, s>>>(dn.y, dn.ys, a.shared_out, a.rank, H, k, mode, a.out);
+    else
+      k_combine<true><<<cg, 256, 0, s>>>(dn.y, dn.ys, a.shared_out, a.rank, H, k, mode, a.out);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
   if (e == hipSuccess && ev) e = hipEventRecord(ev[2], s);
   return e;
 }

@@ -1,0 +1,232 @@
+// Router math shared by the router kernels and the fused decode kernel:
+// score functions, gate logits of a tile, biased top-k, arrival counters.
+// Every function here evaluates floating point in one fixed order without
+// contraction (the pragma opens each body), because the expert indices must
+// be bit-identical to the CPU oracle.  The order is described in route.hip.
+#pragma once
+
+#include "dispatch_block.h"
+
+namespace dsk {
+
+// ln2 split: LN2_HI keeps 32 significant bits, so k*LN2_HI is exact for |k| < 2^21.
+constexpr double kLn2Hi = 0x1.62e42fee00000p-1;
+constexpr double kLn2Lo = 0x1.a39ef35793c76p-33;
+constexpr double kLog2e = 0x1.71547652b82fep+0;
+// 1/n!, n = 0..14
+constexpr double kExpCoef[15] = {
+    0x1.0000000000000p+0, 0x1.0000000000000p+0, 0x1.0000000000000p-1, 0x1.5555555555555p-3,
+    0x1.5555555555555p-5, 0x1.1111111111111p-7, 0x1.6c16c16c16c17p-10, 0x1.a01a01a01a01ap-13,
+    0x1.a01a01a01a01ap-16, 0x1.71de3a556c734p-19, 0x1.27e4fb7789f5cp-22, 0x1.ae64567f544e4p-26,
+    0x1.1eed8eff8d898p-29, 0x1.6124613a86d09p-33, 0x1.93974a8c07c9dp-37};
+// 1/(2n+1), n = 0..18
+constexpr double kAtanhCoef[19] = {
+    0x1.0000000000000p+0, 0x1.5555555555555p-2, 0x1.999999999999ap-3, 0x1.2492492492492p-3,
+    0x1.c71c71c71c71cp-4, 0x1.745d1745d1746p-4, 0x1.3b13b13b13b14p-4, 0x1.1111111111111p-4,
+    0x1.e1e1e1e1e1e1ep-5, 0x1.af286bca1af28p-5, 0x1.8618618618618p-5, 0x1.642c8590b2164p-5,
+    0x1.47ae147ae147bp-5, 0x1.2f684bda12f68p-5, 0x1.1a7b9611a7b96p-5, 0x1.0842108421084p-5,
+    0x1.f07c1f07c1f08p-6, 0x1.d41d41d41d41dp-6, 0x1.bacf914c1bad0p-6};
+constexpr double kSigmoidClamp = 200.0;
+constexpr double kSoftplusTail = 1000.0;
+constexpr int kSegments = 4;         // waves per gate block
+constexpr int kMaxSlots = 16;        // E <= 1024 keys per lane in top-k
+
+__device__ __forceinline__ double exp_d(double x) {
+#pragma clang fp contract(off)
+  double k = rint(x * kLog2e);
+  double r = (x - k * kLn2Hi) - k * kLn2Lo;
+  double p = kExpCoef[14];
+#pragma unroll
+  for (int n = 13; n >= 0; --n) p = p * r + kExpCoef[n];
+  return ldexp(p, static_cast<int>(k));
+}
+
+__device__ __forceinline__ double log1p_d(double u) {
+#pragma clang fp contract(off)
+  double s = u / (2.0 + u);
+  double s2 = s * s;
+  double p = kAtanhCoef[18];
+#pragma unroll
+  for (int n = 17; n >= 0; --n) p = p * s2 + kAtanhCoef[n];
+  return 2.0 * (s * p);
+}
+
+// Correctly rounded float sqrt of v >= 0 (round half to even).
+__device__ __forceinline__ float sqrt_round_f32(double v) {
+#pragma clang fp contract(off)
+  float r = static_cast<float>(sqrt(v));
+  double rd = r;
+  float dn = nextafterf(r, 0.0f);
+  float up = nextafterf(r, __builtin_inff());
+  double lo = (rd + static_cast<double>(dn)) * 0.5;
+  double hi = (rd + static_cast<double>(up)) * 0.5;
+  double lo2 = lo * lo, hi2 = hi * hi;
+  bool even = (__float_as_uint(r) & 1u) == 0u;
+  if (r > 0.0f && (v < lo2 || (v == lo2 && !even))) return dn;
+  if (v > hi2 || (v == hi2 && !even)) return up;
+  return r;
+}
+
+__device__ __forceinline__ float score_of(float z, int score_func) {
+#pragma clang fp contract(off)
+  double zd = z;
+  if (score_func == DSK_SCORE_SIGMOID) {
+    double zc = fmin(fmax(zd, -kSigmoidClamp), kSigmoidClamp);
+    return static_cast<float>(1.0 / (1.0 + exp_d(-zc)));
+  }
+  double a = fabs(zd);
+  double u = (a > kSoftplusTail) ? 0.0 : exp_d(-fmin(a, kSoftplusTail));
+  double sp = fmax(zd, 0.0) + log1p_d(u);
+  return sqrt_round_f32(sp);
+}
+
+template <bool kBF16>
+__device__ __forceinline__ f32x4 load4(const void* base, int64_t elem) {
+  if constexpr (kBF16) {
+    uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + elem);
+    return f32x4{__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                 __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
+  } else {
+    return *reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + elem);
+  }
+}
+
+
+// Gate logits and scores of a TW-token x EW-expert tile by 4 waves (wave w
+// owns segment w of H; see the order above).  `gtid` is the thread index
+// within the 4-wave group; segsum is [4][TW*EW] floats of LDS.  Contains a
+// __syncthreads().
+template <int TW, int EW, bool kXBF16, bool kWBF16>
+__device__ __forceinline__ void gate_tile(const void* x, const void* gw, int T, int H, int E,
+                                          int score_func, float* scores, int t0, int e0, int wave,
+                                          int lane, int gtid, float* segsum) {
+#pragma clang fp contract(off)
+  float p[TW][EW];
+#pragma unroll
+  for (int i = 0; i < TW; ++i)
+#pragma unroll
+    for (int j = 0; j < EW; ++j) p[i][j] = 0.0f;
+  const int steps = (H + 255) / 256;
+  const int seg = (steps + kSegments - 1) / kSegments;
+  const int m0 = wave * seg, m1 = min(m0 + seg, steps);
+#pragma unroll 4
+  for (int m = m0; m < m1; ++m) {
+    const int c = 256 * m + 4 * lane;
+    const bool ok = c < H;
+    f32x4 xv[TW], wv[EW];
+#pragma unroll
+    for (int i = 0; i < TW; ++i) {
+      const int t = min(t0 + i, T - 1);
+      xv[i] = ok ? load4<kXBF16>(x, static_cast<int64_t>(t) * H + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < EW; ++j) {
+      const int e = min(e0 + j, E - 1);
+      wv[j] = ok ? load4<kWBF16>(gw, static_cast<int64_t>(e) * H + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+      for (int i = 0; i < TW; ++i)
+#pragma unroll
+        for (int j = 0; j < EW; ++j) {
+          const float prod = xv[i][v] * wv[j][v];
+          p[i][j] = p[i][j] + prod;
+        }
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1)
+#pragma unroll
+    for (int i = 0; i < TW; ++i)
+#pragma unroll
+      for (int j = 0; j < EW; ++j) p[i][j] = p[i][j] + __shfl_xor(p[i][j], s, 64);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < TW; ++i)
+#pragma unroll
+      for (int j = 0; j < EW; ++j) segsum[wave * TW * EW + i * EW + j] = p[i][j];
+  }
+  __syncthreads();
+  if (gtid < TW * EW) {
+    const int i = gtid / EW, j = gtid % EW;
+    const int t = t0 + i, e = e0 + j;
+    const float z = ((segsum[gtid] + segsum[TW * EW + gtid]) + segsum[2 * TW * EW + gtid]) +
+                    segsum[3 * TW * EW + gtid];
+    if (t < T && e < E) scores[static_cast<int64_t>(t) * E + e] = score_of(z, score_func);
+  }
+}
+
+// One wave: biased top-k and normalised weights of one token.  Lane l holds
+// the keys of experts l + 64*i, i < S.  Each round every lane takes its best
+// remaining key (lowest id among equal keys), the wave maximum key is found
+// with DPP, and among the lanes holding it the lowest expert id wins.
+// Results go to idx_row / w_row and, when given, to the LDS copies lidx / lw
+// (used by the dispatch that follows).
+template <int S>
+__device__ __forceinline__ void topk_token_s(const float* __restrict__ srow, const float* __restrict__ bias,
+                                             int E, int k, float route_scale, int32_t* __restrict__ idx_row,
+                                             float* __restrict__ w_row, int32_t* lidx, float* lw) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  // ord[i]: order-preserving bits of the key of expert lane + 64*i; 0 = taken or absent.
+  uint32_t ord[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int e = lane + 64 * i;
+    uint32_t o = 0u;
+    if (e < E) {
+      const float key = (srow[e] + bias[e]) + 0.0f;
+      const uint32_t u = __float_as_uint(key);
+      o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    }
+    ord[i] = o;
+  }
+  int my_e = 0;                         // lane j keeps the j-th selected expert
+  for (int j = 0; j < k; ++j) {
+    uint32_t bk = ord[0];
+    int bi = 0;
+#pragma unroll
+    for (int i = 1; i < S; ++i)
+      if (ord[i] > bk) { bk = ord[i]; bi = i; }      // first maximum = lowest id
+    const uint32_t m = wave_max_u32(bk);
+    int e = -1;   // only if every remaining key has the bit pattern of -NaN with all payload bits set
+    if (m != 0u) e = static_cast<int>(wave_min_u32(bk == m ? static_cast<uint32_t>(lane + 64 * bi) : ~0u));
+    if (lane == j) my_e = e;
+    if (e >= 0 && (e & 63) == lane) {
+#pragma unroll
+      for (int i = 0; i < S; ++i)
+        if (i == (e >> 6)) ord[i] = 0u;
+    }
+  }
+  const float my_s = (lane < k && my_e >= 0) ? srow[my_e] : 0.0f;
+  float acc = 0.0f;                     // every lane forms the same sum, in selection order
+  for (int j = 0; j < k; ++j) acc = acc + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_s), j));
+  const float denom = acc + 1e-20f;
+  if (lane < k) {
+    const float w = (my_s / denom) * route_scale;
+    idx_row[lane] = my_e;
+    w_row[lane] = w;
+    if (lidx) { lidx[lane] = my_e; lw[lane] = w; }
+  }
+}
+
+__device__ __forceinline__ void topk_token(const float* __restrict__ srow, const float* __restrict__ bias,
+                                           int E, int k, float route_scale, int32_t* __restrict__ idx_row,
+                                           float* __restrict__ w_row, int32_t* lidx = nullptr,
+                                           float* lw = nullptr) {
+  if (E <= 256) topk_token_s<4>(srow, bias, E, k, route_scale, idx_row, w_row, lidx, lw);
+  else topk_token_s<kMaxSlots>(srow, bias, E, k, route_scale, idx_row, w_row, lidx, lw);
+}
+
+// Arrival counter: returns true for the n-th arrival and resets the counter
+// to zero for the next call (the counter region starts zero-filled).
+__device__ __forceinline__ bool arrive_last(unsigned int* c, unsigned int n) {
+  const unsigned int old = atomicAdd(c, 1u);
+  if (old + 1u == n) {
+    atomicExch(c, 0u);
+    return true;
+  }
+  return false;
+}
+
+}  // namespace dsk

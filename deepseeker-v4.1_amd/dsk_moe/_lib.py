@@ -62,7 +62,8 @@ SIGNATURES = {
     "dsk_moe_forward": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                        _vp, _vp, _vp, _sz, _vp]),
     "dsk_moe_forward_timed": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                                             _vp, _vp, _vp, _sz, _vp, _vp]),
+                                             _vp, _vp, _vp, _sz, _vp, _vp, _i32]),
+    "dsk_workspace_init": (ctypes.c_int, [_vp, _sz, _vp]),
     "dsk_fp4_dequant": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _i32, _vp]),
     "dsk_fp4_quantize": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "dsk_q3_quantize": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),

@@ -79,7 +79,7 @@ _WS_CACHE: dict[tuple, torch.Tensor] = {}
 
 
 def workspace(desc: _lib.Desc, device: torch.device) -> torch.Tensor:
-    """A cached device workspace at least ``workspace_size(desc)`` bytes long.
+    """A cached, zero-initialised device workspace of at least ``workspace_size(desc)`` bytes.
 
     Calls that share a cached workspace must be ordered on one stream.
     """
@@ -88,6 +88,7 @@ def workspace(desc: _lib.Desc, device: torch.device) -> torch.Tensor:
     ws = _WS_CACHE.get(key)
     if ws is None or ws.numel() < need:
         ws = torch.empty(max(need, 256), dtype=torch.uint8, device=device)
+        _lib.call("dsk_workspace_init", ptr(ws), ws.numel(), stream_of(device))
         _WS_CACHE[key] = ws
     return ws
 

@@ -85,6 +85,13 @@ const char* dsk_last_error(void);
 /* Bytes of workspace dsk_moe_forward / dsk_experts need for this desc (host only). */
 int dsk_workspace_size(const dsk_moe_desc* d, size_t* bytes);
 
+/* Zero-fill a workspace (a fill kernel on `stream`, no memset node).  The
+ * fused router keeps arrival counters in the workspace: it must be
+ * zero-filled once before its first use; every completed call leaves the
+ * counters at zero again.  No counterpart in the reference (it has no
+ * device workspace). */
+int dsk_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
 /* Router: replaces sqrtsoftplus_scores + route_topk
  * (src/deepseeker/mlx_forward.py:62-81).
  * x [T,H] (x_dtype), gate_w [E,H] (gate_dtype), gate_b [E] f32 ->
@@ -135,16 +142,21 @@ int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w,
 
 /* dsk_moe_forward that also records DSK_STAGE_EVENTS hipEvent_t (events[i],
  * created by the caller) on the stream: before the router, after the
- * router, after dispatch, after the gate/up kernel, after the down kernel
- * and after the combine.  No counterpart in the reference: it is for
- * callers that time the stages (the benchmark). */
+ * router, after dispatch (the fused router dispatches too: then the same
+ * point), after the gate/up kernel, after the down kernel and after the
+ * combine.  Each stage's kernels are launched `repeat` times in a row
+ * between its events (every stage recomputes its outputs from its inputs,
+ * so the result is that of one forward); a stage's duration is its event
+ * interval / repeat, with the event overhead spread over the repeats.
+ * No counterpart in the reference: it is for callers that time the stages
+ * (the benchmark). */
 #define DSK_STAGE_EVENTS 6
 int dsk_moe_forward_timed(const dsk_moe_desc* d, const void* x, const void* gate_w,
                           const float* gate_b, const dsk_expert_ptrs* table,
                           const void* ws1, const void* ws3, const void* ws2,
                           const void* shared_out, void* out, int32_t* idx, float* weights,
                           void* workspace, size_t workspace_bytes, void* stream,
-                          void* const* events);
+                          void* const* events, int32_t repeat);
 
 /* FP4 dequant: replaces metal_dequant / the Metal e2m1 kernels
  * (src/deepseeker/metal_fp4.py:28-66, 139-155) and dequant_fp4_rowmajor

@@ -10,12 +10,15 @@ the reference default is sqrt-softplus with 1.5.  Both are supported.
 Routing indices must be bit-identical between this oracle and the GPU, so
 every floating-point step has one defined order that the HIP kernel mirrors:
 
-1. Gate logit ``z[t, e]``: 64 partial sums; partial ``l`` accumulates, for
-   ``m = 0, 1, ...`` and then ``v = 0..3``, the float32 product
-   ``x[256*m + 4*l + v] * W[256*m + 4*l + v]`` (product rounded, then sum
-   rounded; no fused multiply-add; positions >= H contribute +0).  The 64
-   partials are then combined by an XOR butterfly: for s = 32, 16, 8, 4, 2, 1,
-   ``p[l] = p[l] + p[l ^ s]``; ``z = p[0]``.
+1. Gate logit ``z[t, e]``: H is cut into 256-element steps ``m`` (positions
+   >= H contribute +0) and the steps into 4 segments of ``S = ceil(steps/4)``
+   consecutive steps (segment w holds steps [w*S, (w+1)*S)).  In each segment,
+   64 partial sums: partial ``l`` accumulates, for its steps ``m`` in order and
+   then ``v = 0..3``, the float32 product ``x[256*m + 4*l + v] * W[256*m + 4*l + v]``
+   (product rounded, then sum rounded; no fused multiply-add).  The 64
+   partials are combined by an XOR butterfly (for s = 32, 16, 8, 4, 2, 1:
+   ``p[l] = p[l] + p[l ^ s]``) into the segment sum ``s_w = p[0]``, and
+   ``z = ((s_0 + s_1) + s_2) + s_3``.
 2. Scores are computed in float64 from ``z`` with this module's own ``exp``
    (Cody-Waite reduction by ln2 split in a 32-bit-exact high part and a low
    part, degree-14 Taylor polynomial in Horner form, ``ldexp``) and
@@ -115,8 +118,11 @@ def sqrt_round_f32(v: np.ndarray) -> np.ndarray:
     return out.astype(np.float32)
 
 
+GATE_SEGMENTS = 4
+
+
 def gate_logits(x: np.ndarray, gate_w: np.ndarray, chunk_elems: int = 1 << 24) -> np.ndarray:
-    """z = f32(x) @ f32(W).T in the fixed lane order described in the module docstring.
+    """z = f32(x) @ f32(W).T in the fixed segment/lane order described in the module docstring.
 
     x: [T, H] (any float dtype, converted exactly to float32), gate_w: [E, H].
     """
@@ -131,18 +137,22 @@ def gate_logits(x: np.ndarray, gate_w: np.ndarray, chunk_elems: int = 1 << 24) -
         w = np.pad(w, ((0, 0), (0, hp - h)))
     xr = x.reshape(t, steps, GATE_LANES, GATE_VEC)
     wr = w.reshape(e, steps, GATE_LANES, GATE_VEC)
+    seg = -(-steps // GATE_SEGMENTS)
     out = np.empty((t, e), dtype=np.float32)
     tc = max(1, chunk_elems // max(1, e * GATE_LANES))
     lanes = np.arange(GATE_LANES)
     for t0 in range(0, t, tc):
         xs = xr[t0:t0 + tc]
-        p = np.zeros((xs.shape[0], e, GATE_LANES), dtype=np.float32)
-        for m in range(steps):
-            for v in range(GATE_VEC):
-                p = p + xs[:, None, m, :, v] * wr[None, :, m, :, v]
-        for s in (32, 16, 8, 4, 2, 1):
-            p = p + p[:, :, lanes ^ s]
-        out[t0:t0 + tc] = p[:, :, 0]
+        z = None
+        for sw in range(GATE_SEGMENTS):
+            p = np.zeros((xs.shape[0], e, GATE_LANES), dtype=np.float32)
+            for m in range(sw * seg, min((sw + 1) * seg, steps)):
+                for v in range(GATE_VEC):
+                    p = p + xs[:, None, m, :, v] * wr[None, :, m, :, v]
+            for s in (32, 16, 8, 4, 2, 1):
+                p = p + p[:, :, lanes ^ s]
+            z = p[:, :, 0] if z is None else (z + p[:, :, 0]).astype(np.float32)
+        out[t0:t0 + tc] = z
     return out
 
 

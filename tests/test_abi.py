@@ -15,7 +15,7 @@ from oracle import router as R
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "dsk_moe.h"
-ROUTE_SRC = ROOT / "deepseeker-v4.1_amd" / "csrc" / "route.hip"
+ROUTE_SRC = ROOT / "deepseeker-v4.1_amd" / "csrc" / "gate.h"
 
 
 def declared_functions() -> list[str]:
@@ -78,7 +78,7 @@ def test_null_and_alignment_errors_before_launch():
 
 
 def test_route_constants_match_oracle():
-    """The hex constants compiled into route.hip equal the oracle's derived ones."""
+    """The hex constants of the router math (gate.h) equal the oracle's derived ones."""
     src = ROUTE_SRC.read_text()
 
     def arr(name):

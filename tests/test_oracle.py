@@ -178,24 +178,26 @@ def test_ln2_split_exact():
 def _gate_scalar(x, w):
     # the fixed order, one scalar at a time (float32 ops through numpy scalars)
     h = x.shape[0]
-    p = [np.float32(0.0)] * 64
-    for m in range(-(-h // 256)):
-        for v in range(4):
-            for lane in range(64):
-                c = 256 * m + 4 * lane + v
-                if c < h:
-                    prod = np.float32(x[c]) * np.float32(w[c])
+    steps = -(-h // 256)
+    seg = -(-steps // 4)
+    z = None
+    for sw in range(4):
+        p = [np.float32(0.0)] * 64
+        for m in range(sw * seg, min((sw + 1) * seg, steps)):
+            for v in range(4):
+                for lane in range(64):
+                    c = 256 * m + 4 * lane + v
+                    prod = np.float32(x[c]) * np.float32(w[c]) if c < h else np.float32(0.0)
                     p[lane] = np.float32(p[lane] + prod)
-                else:
-                    p[lane] = np.float32(p[lane] + np.float32(0.0))
-    for s in (32, 16, 8, 4, 2, 1):
-        p = [np.float32(p[i] + p[i ^ s]) for i in range(64)]
-    return p[0]
+        for s in (32, 16, 8, 4, 2, 1):
+            p = [np.float32(p[i] + p[i ^ s]) for i in range(64)]
+        z = p[0] if z is None else np.float32(z + p[0])
+    return z
 
 
 def test_gate_logits_vectorised_equals_scalar_order():
     rng = np.random.default_rng(1)
-    for h in (64, 260, 512):
+    for h in (64, 260, 512, 1300):
         x = rng.standard_normal((2, h)).astype(np.float32)
         w = rng.standard_normal((3, h)).astype(np.float32)
         z = R.gate_logits(x, w)
