@@ -24,6 +24,13 @@ constexpr int kUpBatch = 4;            // K blocks per weight batch (two batches
 constexpr int kDownW = 16;             // waves of a down block (split K = I and Is)
 constexpr int kDownGroup = 8;          // experts whose w2 blocks a wave holds at once
 constexpr int kDownHRegChunks = 2;     // h chunks per thread staged through registers
+// staged down kernel (all h rows in LDS)
+constexpr int kStW = 8;                // waves
+constexpr int kStKB = 2;               // K blocks of each expert per wave (I = kStW * kStKB * 128)
+constexpr int kStSlots = 2;            // experts per routed batch
+constexpr int kStMaxSlots = 16;        // active experts the staged kernel handles
+constexpr int kStRing = 4;             // routed batches in flight per wave
+constexpr int kStStage = 5;            // activation chunks per thread in flight while staging
 
 struct DecodeArgs {
   int T, H, I, Is, k;
@@ -361,120 +368,173 @@ __device__ __forceinline__ void down_epilogue(const DecodeArgs& p, f32x4 a, f32x
 }
 
 // Down + combine with every routed h row (N = T*k of them) and hs staged in
-// LDS once per block; weights of up to kDownGroup experts in flight per wave.
-__global__ __launch_bounds__(kDownW * 64) void k_down_decode_staged(DecodeArgs p) {
+// LDS once per block.  Block = 16 output rows, kStW waves; wave w owns the K
+// blocks [kStKB*w, kStKB*w + kStKB) of every expert's w2 rows and of the
+// shared w2 rows.  The activations are staged first, while nothing else is
+// in flight (their latency would otherwise queue behind the weights); then
+// the shared batch and kStRing routed batches of kStSlots experts are all
+// issued, and computed in order as they land.  The MFMA's B columns carry the hi and lo
+// planes of each token (T <= 8), so one MFMA per K step covers both; four
+// accumulator chains per wave for routed and for shared work, added in
+// order, then the waves in order, then hi + lo.
+
+struct DownBatch {
+  u32x4 c[kStSlots][kStKB];
+  uint32_t s[kStSlots][kStKB];
+};
+
+__device__ __forceinline__ void load_down_batch(DownBatch& b, const DecodeArgs& p, int u0, int U,
+                                                uint32_t row, int kb0, int g4) {
+  const int I = p.I;
+#pragma unroll
+  for (int i = 0; i < kStSlots; ++i) {
+    const bool in = u0 + i < U;
+    const SlotDesc* d = p.desc + (in ? u0 + i : 0);
+    const uint8_t* W = static_cast<const uint8_t*>(d->p[6]);
+    const uint8_t* S = static_cast<const uint8_t*>(d->p[7]);
+#pragma unroll
+    for (int j = 0; j < kStKB; ++j) {
+      const int kc = (kb0 + j) * 128 + g4 * 32;
+      const bool ok = in && kc < I;
+      b.c[i][j] = ok ? ldg16(W + row * static_cast<uint32_t>(I / 2) + kc / 2) : u32x4{0u, 0u, 0u, 0u};
+      b.s[i][j] = ok ? S[row * static_cast<uint32_t>(I / 32) + kc / 32] : 127u;
+    }
+  }
+}
+
+// acc[j] += W(16 rows, K block) x B where B column c is plane (c & 1) (hi, lo)
+// of token c >> 1: one MFMA per 32-wide K step, four independent chains.
+template <typename Raw>
+__device__ __forceinline__ void mma_cols(const Raw& a, const uint16_t* brow, int kc, bool ok, f32x4 (&acc)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = mfma16(a_operand(a, j), b_operand(brow, kc, j, ok), acc[j]);
+}
+
+__device__ __forceinline__ void mma_down_batch(const DownBatch& b, int u0, int U, const int* ldrow, int T,
+                                               int t, const uint16_t* plane, int is, int kb0, int I,
+                                               int g4, f32x4 (&acc)[4]) {
+#pragma unroll
+  for (int i = 0; i < kStSlots; ++i) {
+    if (u0 + i >= U) break;
+    const int dr = t < T ? ldrow[(u0 + i) * T + t] : -1;
+    const bool tok = dr >= 0;
+    const uint16_t* brow = plane + (tok ? dr : 0) * is;
+#pragma unroll
+    for (int j = 0; j < kStKB; ++j) {
+      const int kc = (kb0 + j) * 128 + g4 * 32;
+      mma_cols(RawFP4{b.c[i][j], b.s[i][j]}, brow, kc, tok && kc < I, acc);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) {
   extern __shared__ __align__(16) uint16_t lds_dn[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
   const int row0 = blockIdx.x * 16;
-  const int64_t row = row0 + r16;
+  const uint32_t row = static_cast<uint32_t>(row0 + r16);
   const int U = p.active[0];
   const int N = p.T * p.k;
-  const bool tok = r16 < p.T;
   const int I = p.I, Is = p.Is;
   const int is = I + 8, iss = Is + 8;       // padded LDS row strides
   uint16_t* hh = lds_dn;
   uint16_t* hl = hh + N * is;
   uint16_t* sh_h = hl + N * is;
   uint16_t* sh_l = sh_h + p.T * iss;
-  float (*red)[kDownW][64][4] = reinterpret_cast<float (*)[kDownW][64][4]>(sh_l + p.T * iss);
-  const int nblk = (I + 127) / 128;
-  const int per = (nblk + kDownW - 1) / kDownW;
-  const int kb0 = min(wave * per, nblk), kb1 = min(kb0 + per, nblk);
-  const int snblk = (Is + 127) / 128;
-  const int sper = (snblk + kDownW - 1) / kDownW;
-  const int skb0 = min(wave * sper, snblk), skb1 = min(skb0 + sper, snblk);
-  // 1. activations (h rows and hs) and dispatch rows first, into registers
+  float (*red)[kStW][64][4] = reinterpret_cast<float (*)[kStW][64][4]>(sh_l + p.T * iss);
+  int* ldrow = reinterpret_cast<int*>(red + 2);            // [U][T] dispatch rows (rowmap copy)
+  const int kb0 = wave * kStKB;
+  // 1. activations and dispatch rows, alone in flight (a short wait), into LDS
   const int hch = N * (I / 8), sch = p.T * (Is / 8);
-  u32x4 hv[kDownHRegChunks][2], sv[2];
+  // chunk c < hch: h row c / (I/8); c >= hch: hs row; kStStage chunks per thread in flight at once
+  for (int c0 = tid; c0 < hch + sch; c0 += kStStage * kStW * 64) {
+    u32x4 vh[kStStage], vl[kStStage];
 #pragma unroll
-  for (int j = 0; j < kDownHRegChunks; ++j) {
-    const int c = tid + j * kDownW * 64;
-    if (c < hch) {
-      const int64_t e = static_cast<int64_t>(c / (I / 8)) * I + (c % (I / 8)) * 8;
-      hv[j][0] = ldg16(p.h_hi + e);
-      hv[j][1] = ldg16(p.h_lo + e);
+    for (int j = 0; j < kStStage; ++j) {
+      const int c = c0 + j * kStW * 64;
+      if (c < hch) {
+        const int64_t e = static_cast<int64_t>(c / (I / 8)) * I + (c % (I / 8)) * 8;
+        vh[j] = ldg16(p.h_hi + e);
+        vl[j] = ldg16(p.h_lo + e);
+      } else if (c < hch + sch) {
+        const int cs = c - hch;
+        const int64_t e = static_cast<int64_t>(cs / (Is / 8)) * Is + (cs % (Is / 8)) * 8;
+        vh[j] = ldg16(p.hs_hi + e);
+        vl[j] = ldg16(p.hs_lo + e);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kStStage; ++j) {
+      const int c = c0 + j * kStW * 64;
+      if (c < hch) {
+        const int off = (c / (I / 8)) * is + (c % (I / 8)) * 8;
+        *reinterpret_cast<u32x4*>(hh + off) = vh[j];
+        *reinterpret_cast<u32x4*>(hl + off) = vl[j];
+      } else if (c < hch + sch) {
+        const int cs = c - hch;
+        const int off = (cs / (Is / 8)) * iss + (cs % (Is / 8)) * 8;
+        *reinterpret_cast<u32x4*>(sh_h + off) = vh[j];
+        *reinterpret_cast<u32x4*>(sh_l + off) = vl[j];
+      }
     }
   }
-  if (tid < sch) {
-    const int64_t e = static_cast<int64_t>(tid / (Is / 8)) * Is + (tid % (Is / 8)) * 8;
-    sv[0] = ldg16(p.hs_hi + e);
-    sv[1] = ldg16(p.hs_lo + e);
-  }
-  int drow[kDownGroup];
+  if (wave == 0)
+    for (int i = lane; i < U * p.T; i += 64) ldrow[i] = p.rowmap[i];
+  // 2. every weight of the block in flight: the shared batch and kStRing routed batches
+  RawBF16 rs[kStKB];
 #pragma unroll
-  for (int i = 0; i < kDownGroup; ++i) drow[i] = (i < U && tok) ? p.rowmap[i * p.T + r16] : -1;
-  // 2. the first expert group's w2 blocks and the shared w2 block
-  RawFP4 r[kDownGroup];
-  RawBF16 rs;
+  for (int j = 0; j < kStKB; ++j) {
+    const int kc = (kb0 + j) * 128 + g4 * 32;
+    load_raw(rs[j], p.ws2, row, Is, kc, Is > 0 && kc < Is);
+  }
+  DownBatch ring[kStRing];
+#pragma unroll
+  for (int q = 0; q < kStRing; ++q)
+    if (q * kStSlots < U) load_down_batch(ring[q], p, q * kStSlots, U, row, kb0, g4);
+  __syncthreads();
+  // B column r16: plane r16 & 1 (hi, lo) of token r16 >> 1
+  const int t = r16 >> 1;
+  const bool tcol = t < p.T;
+  const uint16_t* hplane = (r16 & 1) ? hl : hh;
+  const uint16_t* splane = (r16 & 1) ? sh_l : sh_h;
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[4] = {z, z, z, z}, accs[4] = {z, z, z, z};
   {
-    const int kc = kb0 * 128 + g4 * 32;
+    const uint16_t* brow = splane + (tcol ? t : 0) * iss;
 #pragma unroll
-    for (int i = 0; i < kDownGroup; ++i) {
-      const bool in = i < U;
-      const SlotDesc* d = p.desc + (in ? i : 0);
-      load_raw(r[i], static_cast<const uint8_t*>(d->p[6]), static_cast<const uint8_t*>(d->p[7]),
-               row, I, kc, in && kb0 < kb1 && kc < I);
-    }
-    const int skc = skb0 * 128 + g4 * 32;
-    load_raw(rs, p.ws2, row, Is, skc, Is > 0 && skb0 < skb1 && skc < Is);
-  }
-  // 3. activations to LDS while the weights are in flight
-#pragma unroll
-  for (int j = 0; j < kDownHRegChunks; ++j) {
-    const int c = tid + j * kDownW * 64;
-    if (c < hch) {
-      const int off = (c / (I / 8)) * is + (c % (I / 8)) * 8;
-      *reinterpret_cast<u32x4*>(hh + off) = hv[j][0];
-      *reinterpret_cast<u32x4*>(hl + off) = hv[j][1];
+    for (int j = 0; j < kStKB; ++j) {
+      const int kc = (kb0 + j) * 128 + g4 * 32;
+      mma_cols(rs[j], brow, kc, tcol && kc < Is, accs);
     }
   }
-  if (tid < sch) {
-    const int off = (tid / (Is / 8)) * iss + (tid % (Is / 8)) * 8;
-    *reinterpret_cast<u32x4*>(sh_h + off) = sv[0];
-    *reinterpret_cast<u32x4*>(sh_l + off) = sv[1];
-  }
-  __syncthreads();
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accs = acc;
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const int kc = kb * 128 + g4 * 32;
-    const bool kok = kc < I;
-    for (int u0 = 0; u0 < U; u0 += kDownGroup) {
-      if (kb != kb0 || u0 != 0) {
+  // 3. routed batches in order; batch q + kStRing reuses batch q's registers
+  for (int u0 = 0; u0 < U; u0 += kStRing * kStSlots) {
 #pragma unroll
-        for (int i = 0; i < kDownGroup; ++i) {
-          const bool in = u0 + i < U;
-          const SlotDesc* d = p.desc + (in ? u0 + i : 0);
-          load_raw(r[i], static_cast<const uint8_t*>(d->p[6]), static_cast<const uint8_t*>(d->p[7]),
-                   row, I, kc, in && kok);
-          drow[i] = (in && tok) ? p.rowmap[(u0 + i) * p.T + r16] : -1;
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < kDownGroup; ++i) {
-        if (u0 + i >= U) break;
-        const bool ok = kok && drow[i] >= 0;
-        const int hb = (ok ? drow[i] : 0) * is;
-        mma_hilo(r[i], hh + hb, hl + hb, kc, ok, acc);
+    for (int q = 0; q < kStRing; ++q) {
+      const int ub = u0 + q * kStSlots;
+      if (ub < U) {
+        mma_down_batch(ring[q], ub, U, ldrow, p.T, t, hplane, is, kb0, I, g4, acc);
+        if (ub + kStRing * kStSlots < U) load_down_batch(ring[q], p, ub + kStRing * kStSlots, U, row, kb0, g4);
       }
     }
   }
-  for (int kb = skb0; kb < skb1; ++kb) {
-    const int kc = kb * 128 + g4 * 32;
-    if (kb != skb0) load_raw(rs, p.ws2, row, Is, kc, kc < Is);
-    const int hb = (tok ? r16 : 0) * iss;
-    mma_hilo(rs, sh_h + hb, sh_l + hb, kc, tok && kc < Is, accs);
-  }
-  *reinterpret_cast<f32x4*>(&red[0][wave][lane][0]) = acc;
-  *reinterpret_cast<f32x4*>(&red[1][wave][lane][0]) = accs;
+  *reinterpret_cast<f32x4*>(&red[0][wave][lane][0]) = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+  *reinterpret_cast<f32x4*>(&red[1][wave][lane][0]) = ((accs[0] + accs[1]) + accs[2]) + accs[3];
   __syncthreads();
-  if (wave == 0 && tok) {
-    f32x4 a = {0.f, 0.f, 0.f, 0.f}, sh = a;
-    for (int w = 0; w < kDownW; ++w) {
+  if (wave == 0) {
+    f32x4 a = z, sh = z;
+    for (int w = 0; w < kStW; ++w) {
       a += *reinterpret_cast<const f32x4*>(&red[0][w][lane][0]);
       sh += *reinterpret_cast<const f32x4*>(&red[1][w][lane][0]);
     }
-    down_epilogue(p, a, sh, row0, r16, g4);
+    // hi column + lo column of each token (lanes 2t and 2t + 1)
+    f32x4 alo, slo;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      alo[q] = __shfl_xor(a[q], 1, 64);
+      slo[q] = __shfl_xor(sh[q], 1, 64);
+    }
+    if ((r16 & 1) == 0 && tcol) down_epilogue(p, a + alo, sh + slo, row0, t, g4);
   }
 }
 
@@ -577,16 +637,18 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
-  const size_t dn_lds = static_cast<size_t>(d.tokens) * d.top_k * (d.inter + 8) * 4 +
+  const int n_rows = d.tokens * d.top_k;
+  const int max_u = d.n_experts < n_rows ? d.n_experts : n_rows;
+  const size_t dn_lds = static_cast<size_t>(n_rows) * (d.inter + 8) * 4 +
                         static_cast<size_t>(d.tokens) * (d.inter_shared + 8) * 4 +
-                        2 * kDownW * 64 * 4 * sizeof(float);
-  // staged: all activations fit in LDS and in the per-thread staging registers
-  const bool staged = dn_lds <= kMaxLds &&
-                      d.tokens * d.top_k * (d.inter / 8) <= kDownHRegChunks * kDownW * 64 &&
-                      d.tokens * (d.inter_shared / 8) <= kDownW * 64;
+                        2 * kStW * 64 * 4 * sizeof(float) + static_cast<size_t>(max_u) * d.tokens * 4;
+  // staged: all activations fit in LDS, each wave's K blocks cover I (and
+  // Is), few enough experts, and at most 8 tokens (two B columns each)
+  const bool staged = dn_lds <= kMaxLds && max_u <= kStMaxSlots && d.tokens <= 8 &&
+                      d.inter == kStW * kStKB * 128 && d.inter_shared <= kStW * kStKB * 128;
   for (int r = 0; r < repeat; ++r) {
     if (staged)
-      k_down_decode_staged<<<static_cast<unsigned>(d.hidden / 16), kDownW * 64, dn_lds, s>>>(p);
+      k_down_decode_staged<<<static_cast<unsigned>(d.hidden / 16), kStW * 64, dn_lds, s>>>(p);
     else
       k_down_decode<<<static_cast<unsigned>(d.hidden / 16), kDownW * 64, 0, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;

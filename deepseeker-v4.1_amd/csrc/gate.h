@@ -95,11 +95,12 @@ __device__ __forceinline__ f32x4 load4(const void* base, int64_t elem) {
 // Gate logits and scores of a TW-token x EW-expert tile by 4 waves (wave w
 // owns segment w of H; see the order above).  `gtid` is the thread index
 // within the 4-wave group; segsum is [4][TW*EW] floats of LDS.  Contains a
-// __syncthreads().
+// __syncthreads() (reached also when !active: then nothing is loaded or
+// written).
 template <int TW, int EW, bool kXBF16, bool kWBF16>
 __device__ __forceinline__ void gate_tile(const void* x, const void* gw, int T, int H, int E,
                                           int score_func, float* scores, int t0, int e0, int wave,
-                                          int lane, int gtid, float* segsum) {
+                                          int lane, int gtid, float* segsum, bool active = true) {
 #pragma clang fp contract(off)
   float p[TW][EW];
 #pragma unroll
@@ -108,7 +109,7 @@ __device__ __forceinline__ void gate_tile(const void* x, const void* gw, int T, 
     for (int j = 0; j < EW; ++j) p[i][j] = 0.0f;
   const int steps = (H + 255) / 256;
   const int seg = (steps + kSegments - 1) / kSegments;
-  const int m0 = wave * seg, m1 = min(m0 + seg, steps);
+  const int m0 = wave * seg, m1 = active ? min(m0 + seg, steps) : m0;
 #pragma unroll 4
   for (int m = m0; m < m1; ++m) {
     const int c = 256 * m + 4 * lane;
@@ -147,7 +148,7 @@ __device__ __forceinline__ void gate_tile(const void* x, const void* gw, int T, 
       for (int j = 0; j < EW; ++j) segsum[wave * TW * EW + i * EW + j] = p[i][j];
   }
   __syncthreads();
-  if (gtid < TW * EW) {
+  if (active && gtid < TW * EW) {
     const int i = gtid / EW, j = gtid % EW;
     const int t = t0 + i, e = e0 + j;
     const float z = ((segsum[gtid] + segsum[TW * EW + gtid]) + segsum[2 * TW * EW + gtid]) +
