@@ -47,6 +47,7 @@ METRIC = "MoE-layer tokens/s at B=1/64/4096; % of HBM GB/s (decode) / MFMA peak 
 PEAK_HBM = 8.0e12          # MI355X HBM3E, bytes/s
 PEAK_BF16 = 2.5e15         # MI355X dense bf16 MFMA, FLOP/s
 H, E, K_TOP, I, IS = 4096, 256, 8, 2048, 2048
+SPIN_CYCLES = 50_000_000   # head-start kernel before the event-timed launches (~20 ms)
 
 
 # ------------------------------------------------------------------ HIP events
@@ -58,6 +59,7 @@ class HipEvents:
         self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
         self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
                                                  ctypes.c_void_p]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         self.ev = []
         for _ in range(n):
             h = ctypes.c_void_p()
@@ -67,6 +69,10 @@ class HipEvents:
 
     def array(self, start: int, n: int):
         return (ctypes.c_void_p * n)(*[e.value for e in self.ev[start:start + n]])
+
+    def record(self, i: int, stream: ctypes.c_void_p) -> None:
+        if self.hip.hipEventRecord(self.ev[i], stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
 
     def ms(self, a: int, b: int) -> float:
         out = ctypes.c_float()
@@ -97,6 +103,19 @@ def layer_bytes(u: int, t: int) -> int:
 
 def layer_flops(t: int) -> int:
     return 2 * t * K_TOP * 3 * H * I + 2 * t * 3 * H * IS + 2 * t * H * E
+
+
+def measured_traffic(kernel: str, t: int):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    measurement (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), or
+    None when no measurement for this kernel at this batch exists."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    entry = json.loads(path.read_text()).get(kernel)
+    if not entry or entry.get("workload") != f"full-size FP4 MoE layer decode, B={t}":
+        return None
+    return int(entry["bytes_per_launch"])
 
 
 # ------------------------------------------------------------------ timed forward
@@ -132,16 +151,28 @@ def run_workload(layers, t: int, steps: int, warmup: int, n_inputs: int, seed: i
         layers[s % nl](xs[s % n_inputs], out=out, idx=idxs[s])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # 2) stage timing: every stage repeated `rep` times between its events
-    rep = 10
+    # 2) stage timing: one launch per stage, events between the stages, same
+    # rotation as above (cold weights).  A spin kernel first gives the GPU a
+    # head start so that the host has queued every launch and event before the
+    # GPU reaches it: the events then time GPU work only, not submission.
+    # Each recorded event also costs GPU time (a marker packet): an empty pair
+    # of events after every step measures it, and it is subtracted from the
+    # stage times.
     n_t = min(steps, 40)
-    ev = HipEvents(n_t * _lib.STAGE_EVENTS)
+    ne = _lib.STAGE_EVENTS
+    ev = HipEvents(n_t * ne)
+    mk = HipEvents(2 * n_t)
+    stream = stream_of(dev)
+    torch.cuda._sleep(SPIN_CYCLES)
     for s in range(n_t):
-        forward_timed(layers[s % nl], xs[s % n_inputs], out, idxs[s], ws_, ev, s, rep)
+        forward_timed(layers[s % nl], xs[s % n_inputs], out, idxs[s], ws_, ev, s, 1)
+        mk.record(2 * s, stream)
+        mk.record(2 * s + 1, stream)
     torch.cuda.synchronize()
-    st = np.array([[ev.ms(s * 6 + i, s * 6 + i + 1) / rep for i in range(5)] for s in range(n_t)])
+    st = np.array([[ev.ms(s * ne + i, s * ne + i + 1) for i in range(5)] for s in range(n_t)])
+    marker = np.array([mk.ms(2 * s, 2 * s + 1) for s in range(n_t)])
     uniq = [len(torch.unique(ix).tolist()) for ix in idxs[:n_t]]
-    return {"wall_s": wall, "stage_ms": st, "unique": uniq}
+    return {"wall_s": wall, "stage_ms": st, "marker_ms": marker, "unique": uniq}
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -245,8 +276,9 @@ def main() -> int:
     ms_step = r["wall_s"] / args.steps * 1e3
     value = T * args.steps / r["wall_s"]
     st = r["stage_ms"]
+    marker_ms = float(np.median(r["marker_ms"]))
     u = np.array(r["unique"])
-    up_ms = st[:, 2]
+    up_ms = np.maximum(st[:, 2] - marker_ms, 1e-6)
     up_bytes = np.array([up_kernel_bytes(int(x), T) for x in u])
     achieved = float(up_bytes.sum() / (up_ms.sum() * 1e-3))
     layer_b = np.array([layer_bytes(int(x), T) for x in u])
@@ -262,12 +294,16 @@ def main() -> int:
                    "gate": "sigmoid, route_scale 2.5", "tokens": T,
                    "layers_rotated": args.layers, "inputs_rotated": args.inputs},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
-                     "kernel": "k_up_fp4 (routed w1/w3 + shared w1/w3, SwiGLU epilogue)",
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
+                     "traffic": measured_traffic("k_up_stream", T),
+                     "kernel": "k_up_stream (routed FP4 w1/w3 + shared bf16 w1/w3, SwiGLU epilogue)",
                      "bytes_per_launch": int(up_bytes.mean()),
-                     "avg_launch_us": round(float(up_ms.mean()) * 1e3, 2)},
-        "stage_us": {n: round(float(st[:, i].mean()) * 1e3, 2) for i, n in enumerate(stage_names)},
-        "layer_hbm_frac": round(float(layer_b.sum() / (st.sum() * 1e-3)) / PEAK_HBM, 4),
+                     "avg_launch_us": round(float(up_ms.mean()) * 1e3, 2),
+                     "timing": "HIP events around one launch per step (cold weights), minus the "
+                               "GPU time of an empty event pair"},
+        "stage_us": {n: round(max(float(st[:, i].mean()) - marker_ms, 0.0) * 1e3, 2)
+                     for i, n in enumerate(stage_names)},
+        "event_marker_us": round(marker_ms * 1e3, 2),
         "layer_hbm_frac_wall": round(float(layer_b.mean() / (ms_step * 1e-3)) / PEAK_HBM, 4),
         "unique_experts_mean": float(u.mean()),
     }

@@ -141,13 +141,16 @@ int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w,
                     size_t workspace_bytes, void* stream);
 
 /* dsk_moe_forward that also records DSK_STAGE_EVENTS hipEvent_t (events[i],
- * created by the caller) on the stream: before the router, after the
- * router, after dispatch (the fused router dispatches too: then the same
- * point), after the gate/up kernel, after the down kernel and after the
- * combine.  Each stage's kernels are launched `repeat` times in a row
- * between its events (every stage recomputes its outputs from its inputs,
- * so the result is that of one forward); a stage's duration is its event
- * interval / repeat, with the event overhead spread over the repeats.
+ * created by the caller) on the stream: before the router, after the gate
+ * scores (decode pipeline; the general path's router also dispatches, so
+ * there it is the same point as the next), after the top-k and dispatch,
+ * after the gate/up kernel, after the down kernel and after the combine
+ * (the decode pipeline combines inside the down kernel: same point).  Each
+ * stage's kernels are launched `repeat` times in a row between its events
+ * (every stage recomputes its outputs from its inputs, so the result is that
+ * of one forward); a stage's duration is its event interval / repeat.  Each
+ * event is a marker packet that itself takes GPU time (a few microseconds on
+ * MI355X): time an empty pair of events to subtract it.
  * No counterpart in the reference: it is for callers that time the stages
  * (the benchmark). */
 #define DSK_STAGE_EVENTS 6
