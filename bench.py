@@ -86,7 +86,13 @@ def fp4_role_bytes(n: int, k: int) -> int:
     return n * k // 2 + n * k // 32
 
 
-def expert_bytes() -> int:
+def q3_role_bytes(n: int, k: int) -> int:
+    return n * k * 3 // 8 + 2 * (n * k // 64) * 2                 # codes + fp16 scale + fp16 bias
+
+
+def expert_bytes(quant: str = "fp4") -> int:
+    if quant == "q3":
+        return 2 * q3_role_bytes(I, H) + q3_role_bytes(H, I)    # 11,010,048 at the full shape
     return 2 * fp4_role_bytes(I, H) + fp4_role_bytes(H, I)      # 13,369,344 at the full shape
 
 
@@ -97,8 +103,8 @@ def up_kernel_bytes(u: int, t: int) -> int:
             + t * K_TOP * I * 4 + t * IS * 4)
 
 
-def layer_bytes(u: int, t: int) -> int:
-    return u * expert_bytes() + 3 * IS * H * 2 + E * H * 4 + 2 * t * H * 2
+def layer_bytes(u: int, t: int, quant: str = "fp4") -> int:
+    return u * expert_bytes(quant) + 3 * IS * H * 2 + E * H * 4 + 2 * t * H * 2
 
 
 def layer_flops(t: int) -> int:
@@ -326,6 +332,19 @@ def main() -> int:
                                        "mfma_frac": round(layer_flops(4096) / step_s / PEAK_BF16, 4),
                                        "stage_us": {n: round(float(rs["stage_ms"][:, i].mean()) * 1e3, 1)
                                                     for i, n in enumerate(stage_names)}}
+        # routed experts in 3-bit affine (group 64, fp16 scale / bias), B = 1, 16, 64
+        q3_layers = [gsynth.make_layer(hidden=H, n_experts=E, top_k=K_TOP, inter=I, inter_shared=IS,
+                                       quant="q3", seed=2000 + i, device="cuda:0") for i in range(2)]
+        for tb in (1, 16, 64):
+            n_steps = 100 if tb == 1 else 40
+            rs = run_workload(q3_layers, tb, n_steps, 5, args.inputs, seed=55)
+            us = np.array(rs["unique"])
+            lb = np.array([layer_bytes(int(x), tb, "q3") for x in us])
+            sweep[f"q3_B{tb}"] = {"tokens_per_s": round(tb * n_steps / rs["wall_s"], 1),
+                                  "ms_per_step": round(rs["wall_s"] / n_steps * 1e3, 4),
+                                  "unique_experts_mean": float(us.mean()),
+                                  "layer_hbm_frac": round(float(lb.mean() / (rs["wall_s"] / n_steps)) / PEAK_HBM, 4)}
+        del q3_layers
         line["sweep"] = sweep
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(layers[0])

@@ -93,7 +93,8 @@ static int check_expert_desc(const dsk_moe_desc* d) {
     if (d->inter < 32 || d->inter % 32)
       return fail(DSK_EINVAL, "inter=%d must be a positive multiple of 32 for FP4", d->inter);
   } else if (d->quant == DSK_QUANT_Q3) {
-    return fail(DSK_EUNSUPPORTED, "Q3 experts are not available in this build of dsk_experts");
+    if (d->inter < 128 || d->inter % 128 || d->hidden % 128)
+      return fail(DSK_EINVAL, "Q3 needs hidden=%d and inter=%d to be multiples of 128", d->hidden, d->inter);
   } else {
     return fail(DSK_EINVAL, "unknown quant %d", d->quant);
   }

@@ -220,7 +220,7 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, uint16_t* xh
 // flight per wave; the tokens' activations are loaded before the weights and
 // written to LDS after the weight loads have been issued; K ranges are added
 // in wave order.
-template <int G, bool kWin, bool kF32>
+template <int G, bool kWin, bool kF32, bool kQ3>
 __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 ? 3 : 4))) void k_up_stream(DecodeArgs p) {
   extern __shared__ __align__(16) uint16_t lds_up[];
   // wave-uniform indices in scalar registers
@@ -273,43 +273,86 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
     shared_up_tile<kF32>(p, xh, xl, xs, xreg, xv, cpr, xchunks, lds_up, tid, lane, wave, r16, g4);
     return;
   }
-  // weights: two batches in flight
   const SlotDesc* d = p.desc + slot;
-  const uint8_t* W1 = static_cast<const uint8_t*>(d->p[0]);
-  const uint8_t* S1 = static_cast<const uint8_t*>(d->p[1]);
-  const uint8_t* W3 = static_cast<const uint8_t*>(d->p[3]);
-  const uint8_t* S3 = static_cast<const uint8_t*>(d->p[4]);
   const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
   const int nblk = (K + 127) / 128;
   const int per = (nblk + kUpKS - 1) / kUpKS;
   const int k0 = min(ks * per, nblk), k1 = min(k0 + per, nblk);
-  UpBatch<G> A, B;
-  load_batch<G, kWin>(A, W1, S1, W3, S3, row, K, k0, k1, g4, rok);
-  load_batch<G, kWin>(B, W1, S1, W3, S3, row, K, k0 + G, k1, g4, rok);
-  if (xreg) {
-#pragma unroll
-    for (int j = 0; j < kUpXRegChunks; ++j) {
-      const int c = tid + j * kUpW * 64;
-      if (c < xchunks) put_x_chunk(xh, xl, (c / cpr) * xs + (c % cpr) * 8, xv[j][0], xv[j][1], f32);
-    }
-  }
-  const float wr = tv ? p.wrow[drow] : 0.0f;
   float (*red)[kUpKS][2][64][4] =
       reinterpret_cast<float (*)[kUpKS][2][64][4]>(lds_up + (f32 ? 2 : 1) * T * xs);
-  uint8_t* xch = reinterpret_cast<uint8_t*>(red + kUpItems) + wave * 640;
-  __syncthreads();
-  const uint16_t* bh = xh + (tv ? r16 : 0) * xs;
-  const uint16_t* bl = xl + (tv ? r16 : 0) * xs;
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
-  for (int kb = k0; kb < k1; kb += 2 * G) {
-    batch_scales<G, kWin>(A, xch, r16, g4);
-    mma_batch<G>(A, bh, bl, K, kb, k1, g4, tv, f32, ag, au);
-    if (kb + 2 * G < k1) load_batch<G, kWin>(A, W1, S1, W3, S3, row, K, kb + 2 * G, k1, g4, rok);
-    if (kb + G < k1) {
-      batch_scales<G, kWin>(B, xch, r16, g4);
-      mma_batch<G>(B, bh, bl, K, kb + G, k1, g4, tv, f32, ag, au);
+  float wr = 0.0f;
+  if constexpr (kQ3) {
+    // weights: two batches of G K blocks in flight (q3 codes, scale and bias per lane)
+    RawQ3 a1[G], a3[G], b1[G], b3[G];
+    auto ld = [&](RawQ3 (&r1)[G], RawQ3 (&r3)[G], int kb) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const int kc = (kb + i) * 128 + g4 * 32;
+        const bool ok = rok && kb + i < k1 && kc < K;
+        load_role(r1[i], d->p, 0, row, K, kc, ok);
+        load_role(r3[i], d->p, 1, row, K, kc, ok);
+      }
+    };
+    ld(a1, a3, k0);
+    ld(b1, b3, k0 + G);
+    if (xreg) {
+#pragma unroll
+      for (int j = 0; j < kUpXRegChunks; ++j) {
+        const int c = tid + j * kUpW * 64;
+        if (c < xchunks) put_x_chunk(xh, xl, (c / cpr) * xs + (c % cpr) * 8, xv[j][0], xv[j][1], f32);
+      }
     }
-    if (kb + 3 * G < k1) load_batch<G, kWin>(B, W1, S1, W3, S3, row, K, kb + 3 * G, k1, g4, rok);
+    wr = tv ? p.wrow[drow] : 0.0f;
+    __syncthreads();
+    const uint16_t* bh = xh + (tv ? r16 : 0) * xs;
+    const uint16_t* bl = xl + (tv ? r16 : 0) * xs;
+    auto mm = [&](const RawQ3 (&r1)[G], const RawQ3 (&r3)[G], int kb) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const int kc = (kb + i) * 128 + g4 * 32;
+        const bool ok = tv && kb + i < k1 && kc < K;
+        mma_block2(r1[i], r3[i], bh, kc, ok, ag, au);
+        if (f32) mma_block2(r1[i], r3[i], bl, kc, ok, ag, au);
+      }
+    };
+    for (int kb = k0; kb < k1; kb += 2 * G) {
+      mm(a1, a3, kb);
+      if (kb + 2 * G < k1) ld(a1, a3, kb + 2 * G);
+      if (kb + G < k1) mm(b1, b3, kb + G);
+      if (kb + 3 * G < k1) ld(b1, b3, kb + 3 * G);
+    }
+  } else {
+    // weights: two batches in flight
+    const uint8_t* W1 = static_cast<const uint8_t*>(d->p[0]);
+    const uint8_t* S1 = static_cast<const uint8_t*>(d->p[1]);
+    const uint8_t* W3 = static_cast<const uint8_t*>(d->p[3]);
+    const uint8_t* S3 = static_cast<const uint8_t*>(d->p[4]);
+    UpBatch<G> A, B;
+    load_batch<G, kWin>(A, W1, S1, W3, S3, row, K, k0, k1, g4, rok);
+    load_batch<G, kWin>(B, W1, S1, W3, S3, row, K, k0 + G, k1, g4, rok);
+    if (xreg) {
+#pragma unroll
+      for (int j = 0; j < kUpXRegChunks; ++j) {
+        const int c = tid + j * kUpW * 64;
+        if (c < xchunks) put_x_chunk(xh, xl, (c / cpr) * xs + (c % cpr) * 8, xv[j][0], xv[j][1], f32);
+      }
+    }
+    wr = tv ? p.wrow[drow] : 0.0f;
+    uint8_t* xch = reinterpret_cast<uint8_t*>(red + kUpItems) + wave * 640;
+    __syncthreads();
+    const uint16_t* bh = xh + (tv ? r16 : 0) * xs;
+    const uint16_t* bl = xl + (tv ? r16 : 0) * xs;
+    for (int kb = k0; kb < k1; kb += 2 * G) {
+      batch_scales<G, kWin>(A, xch, r16, g4);
+      mma_batch<G>(A, bh, bl, K, kb, k1, g4, tv, f32, ag, au);
+      if (kb + 2 * G < k1) load_batch<G, kWin>(A, W1, S1, W3, S3, row, K, kb + 2 * G, k1, g4, rok);
+      if (kb + G < k1) {
+        batch_scales<G, kWin>(B, xch, r16, g4);
+        mma_batch<G>(B, bh, bl, K, kb + G, k1, g4, tv, f32, ag, au);
+      }
+      if (kb + 3 * G < k1) load_batch<G, kWin>(B, W1, S1, W3, S3, row, K, kb + 3 * G, k1, g4, rok);
+    }
   }
   // K ranges added in order: ((r0 + r1) + r2) + r3
   *reinterpret_cast<f32x4*>(&red[item][ks][0][lane][0]) = ag;
@@ -378,26 +421,23 @@ __device__ __forceinline__ void down_epilogue(const DecodeArgs& p, f32x4 a, f32x
 // accumulator chains per wave for routed and for shared work, added in
 // order, then the waves in order, then hi + lo.
 
+template <typename Raw>
 struct DownBatch {
-  u32x4 c[kStSlots][kStKB];
-  uint32_t s[kStSlots][kStKB];
+  Raw r[kStSlots][kStKB];
 };
 
-__device__ __forceinline__ void load_down_batch(DownBatch& b, const DecodeArgs& p, int u0, int U,
+template <typename Raw>
+__device__ __forceinline__ void load_down_batch(DownBatch<Raw>& b, const DecodeArgs& p, int u0, int U,
                                                 uint32_t row, int kb0, int g4) {
   const int I = p.I;
 #pragma unroll
   for (int i = 0; i < kStSlots; ++i) {
     const bool in = u0 + i < U;
     const SlotDesc* d = p.desc + (in ? u0 + i : 0);
-    const uint8_t* W = static_cast<const uint8_t*>(d->p[6]);
-    const uint8_t* S = static_cast<const uint8_t*>(d->p[7]);
 #pragma unroll
     for (int j = 0; j < kStKB; ++j) {
       const int kc = (kb0 + j) * 128 + g4 * 32;
-      const bool ok = in && kc < I;
-      b.c[i][j] = ok ? ldg16(W + row * static_cast<uint32_t>(I / 2) + kc / 2) : u32x4{0u, 0u, 0u, 0u};
-      b.s[i][j] = ok ? S[row * static_cast<uint32_t>(I / 32) + kc / 32] : 127u;
+      load_role(b.r[i][j], d->p, 2, row, I, kc, in && kc < I);
     }
   }
 }
@@ -410,7 +450,8 @@ __device__ __forceinline__ void mma_cols(const Raw& a, const uint16_t* brow, int
   for (int j = 0; j < 4; ++j) acc[j] = mfma16(a_operand(a, j), b_operand(brow, kc, j, ok), acc[j]);
 }
 
-__device__ __forceinline__ void mma_down_batch(const DownBatch& b, int u0, int U, const int* ldrow, int T,
+template <typename Raw>
+__device__ __forceinline__ void mma_down_batch(const DownBatch<Raw>& b, int u0, int U, const int* ldrow, int T,
                                                int t, const uint16_t* plane, int is, int kb0, int I,
                                                int g4, f32x4 (&acc)[4]) {
 #pragma unroll
@@ -422,11 +463,12 @@ __device__ __forceinline__ void mma_down_batch(const DownBatch& b, int u0, int U
 #pragma unroll
     for (int j = 0; j < kStKB; ++j) {
       const int kc = (kb0 + j) * 128 + g4 * 32;
-      mma_cols(RawFP4{b.c[i][j], b.s[i][j]}, brow, kc, tok && kc < I, acc);
+      mma_cols(b.r[i][j], brow, kc, tok && kc < I, acc);
     }
   }
 }
 
+template <typename Raw>
 __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) {
   extern __shared__ __align__(16) uint16_t lds_dn[];
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -487,7 +529,7 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
     const int kc = (kb0 + j) * 128 + g4 * 32;
     load_raw(rs[j], p.ws2, row, Is, kc, Is > 0 && kc < Is);
   }
-  DownBatch ring[kStRing];
+  DownBatch<Raw> ring[kStRing];
 #pragma unroll
   for (int q = 0; q < kStRing; ++q)
     if (q * kStSlots < U) load_down_batch(ring[q], p, q * kStSlots, U, row, kb0, g4);
@@ -538,6 +580,7 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
   }
 }
 
+template <typename Raw>
 __global__ __launch_bounds__(kDownW * 64) void k_down_decode(DecodeArgs p) {
   __shared__ float red[2][kDownW][64][4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -556,14 +599,13 @@ __global__ __launch_bounds__(kDownW * 64) void k_down_decode(DecodeArgs p) {
       const int kc = kb * 128 + g4 * 32;
       const bool kok = kc < K;
       for (int u0 = 0; u0 < U; u0 += kDownGroup) {
-        RawFP4 r[kDownGroup];
+        Raw r[kDownGroup];
         int drow[kDownGroup];
 #pragma unroll
         for (int i = 0; i < kDownGroup; ++i) {
           const bool in = u0 + i < U;
           const SlotDesc* d = p.desc + (in ? u0 + i : 0);
-          load_raw(r[i], static_cast<const uint8_t*>(d->p[6]), static_cast<const uint8_t*>(d->p[7]),
-                   row, K, kc, in && kok);
+          load_role(r[i], d->p, 2, row, K, kc, in && kok);
           drow[i] = (in && tok) ? p.rowmap[(u0 + i) * p.T + r16] : -1;
         }
 #pragma unroll
@@ -629,11 +671,14 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   const size_t up_lds = static_cast<size_t>(p.x_f32 ? 2 : 1) * p.T * (p.H + 8) * 2 + kUpLdsFixed;
   // scale windows need 4-byte aligned scale rows (H a multiple of 128)
   const bool win = d.hidden % 128 == 0;
+  const bool q3 = d.quant == DSK_QUANT_Q3;
   for (int r = 0; r < repeat; ++r) {
-    if (win && !p.x_f32) k_up_stream<kUpBatch, true, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-    else if (win) k_up_stream<kUpBatch, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-    else if (!p.x_f32) k_up_stream<kUpBatch, false, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-    else k_up_stream<kUpBatch, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    if (q3 && !p.x_f32) k_up_stream<kUpBatch, false, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    else if (q3) k_up_stream<kUpBatch, false, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    else if (win && !p.x_f32) k_up_stream<kUpBatch, true, false, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    else if (win) k_up_stream<kUpBatch, true, true, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    else if (!p.x_f32) k_up_stream<kUpBatch, false, false, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    else k_up_stream<kUpBatch, false, true, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
@@ -647,10 +692,11 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   const bool staged = dn_lds <= kMaxLds && max_u <= kStMaxSlots && d.tokens <= 8 &&
                       d.inter == kStW * kStKB * 128 && d.inter_shared <= kStW * kStKB * 128;
   for (int r = 0; r < repeat; ++r) {
-    if (staged)
-      k_down_decode_staged<<<static_cast<unsigned>(d.hidden / 16), kStW * 64, dn_lds, s>>>(p);
-    else
-      k_down_decode<<<static_cast<unsigned>(d.hidden / 16), kDownW * 64, 0, s>>>(p);
+    const unsigned blocks = static_cast<unsigned>(d.hidden / 16);
+    if (staged && q3) k_down_decode_staged<RawQ3><<<blocks, kStW * 64, dn_lds, s>>>(p);
+    else if (staged) k_down_decode_staged<RawFP4><<<blocks, kStW * 64, dn_lds, s>>>(p);
+    else if (q3) k_down_decode<RawQ3><<<blocks, kDownW * 64, 0, s>>>(p);
+    else k_down_decode<RawFP4><<<blocks, kDownW * 64, 0, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   // down and combine are one kernel here: both stage events mark its end

@@ -26,7 +26,7 @@
 // is applied in float32 before the split, as in the reference (route weight
 // before w2).  The combine sums each token's expert outputs in ascending
 // expert id, then adds the shared output rounded to x's dtype, in float32.
-#include "dsk_internal.h"
+#include "tile.h"
 
 namespace dsk {
 namespace {
@@ -37,24 +37,6 @@ constexpr int kDownWaves = 4;   // split-K ways of the down kernel (K = I)
 __device__ __forceinline__ f32x4 mfma(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-
-__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
-
-__device__ __forceinline__ bf16x8 fp4_word_to_bf16x8(uint32_t word, float scale) {
-  bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
-  bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
-  bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
-  bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
-  u32x4 r{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
-          __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)};
-  return as_bf16x8(r);
-}
-
-__device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
-
-// Raw A-operand data of one lane for one K block.
-struct RawFP4 { u32x4 c; uint32_t s; };
-struct RawBF16 { u32x4 v[4]; };
 
 __device__ __forceinline__ RawFP4 load_fp4(const uint8_t* W, const uint8_t* S, int64_t row,
                                            int K, int kc, bool ok) {
@@ -83,6 +65,11 @@ __device__ __forceinline__ void deq(const RawFP4& r, bf16x8 a[4]) {
   a[1] = fp4_word_to_bf16x8(r.c.y, sc);
   a[2] = fp4_word_to_bf16x8(r.c.z, sc);
   a[3] = fp4_word_to_bf16x8(r.c.w, sc);
+}
+
+__device__ __forceinline__ void deq(const RawQ3& r, bf16x8 a[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) a[j] = a_operand(r, j);
 }
 
 __device__ __forceinline__ void deq(const RawBF16& r, bf16x8 a[4]) {
@@ -229,7 +216,7 @@ __device__ __forceinline__ void up_tile(const UpArgs& p, LoadA load_a, int K, in
 constexpr int kGroupFP4 = 4;
 constexpr int kGroupBF16 = 2;
 
-template <int NT, bool XLO>
+template <int NT, bool XLO, bool kQ3>
 __global__ __launch_bounds__(kUpWaves * 64) void k_up_fp4(UpArgs p) {
   __shared__ float red[2 * kUpWaves][64][4];
   const int lane = threadIdx.x & 63;
@@ -247,13 +234,23 @@ __global__ __launch_bounds__(kUpWaves * 64) void k_up_fp4(UpArgs p) {
     const uint8_t* S1 = static_cast<const uint8_t*>(d->p[1]);
     const uint8_t* W3 = static_cast<const uint8_t*>(d->p[3]);
     const uint8_t* S3 = static_cast<const uint8_t*>(d->p[4]);
-    auto load_a = [&](int blk, bool in, RawFP4& r1, RawFP4& r3) {
-      const int kc = blk * 128 + g4 * 32;
-      const bool ok = in && kc < K;
-      r1 = load_fp4(W1, S1, row, K, kc, ok);
-      r3 = load_fp4(W3, S3, row, K, kc, ok);
-    };
-    up_tile<NT, XLO, kGroupFP4, RawFP4>(p, load_a, K, row0, d->n_tok, d->tok_base, false, red);
+    if constexpr (kQ3) {
+      auto load_a = [&](int blk, bool in, RawQ3& r1, RawQ3& r3) {
+        const int kc = blk * 128 + g4 * 32;
+        const bool ok = in && kc < K;
+        load_role(r1, d->p, 0, row, K, kc, ok);
+        load_role(r3, d->p, 1, row, K, kc, ok);
+      };
+      up_tile<NT, XLO, kGroupFP4, RawQ3>(p, load_a, K, row0, d->n_tok, d->tok_base, false, red);
+    } else {
+      auto load_a = [&](int blk, bool in, RawFP4& r1, RawFP4& r3) {
+        const int kc = blk * 128 + g4 * 32;
+        const bool ok = in && kc < K;
+        r1 = load_fp4(W1, S1, row, K, kc, ok);
+        r3 = load_fp4(W3, S3, row, K, kc, ok);
+      };
+      up_tile<NT, XLO, kGroupFP4, RawFP4>(p, load_a, K, row0, d->n_tok, d->tok_base, false, red);
+    }
   } else {
     const int row0 = b * 16;
     const int64_t row = row0 + r16;
@@ -343,7 +340,7 @@ __device__ __forceinline__ void down_tile(const DownArgs& p, LoadA load_a, int K
   }
 }
 
-template <int NT>
+template <int NT, bool kQ3>
 __global__ __launch_bounds__(kDownWaves * 64) void k_down_fp4(DownArgs p) {
   __shared__ float red[kDownWaves][64][4];
   const int lane = threadIdx.x & 63;
@@ -359,11 +356,19 @@ __global__ __launch_bounds__(kDownWaves * 64) void k_down_fp4(DownArgs p) {
     const int K = p.I;
     const uint8_t* W2 = static_cast<const uint8_t*>(d->p[6]);
     const uint8_t* S2 = static_cast<const uint8_t*>(d->p[7]);
-    auto load_a = [&](int blk, bool in, RawFP4& r) {
-      const int kc = blk * 128 + g4 * 32;
-      r = load_fp4(W2, S2, row, K, kc, in && kc < K);
-    };
-    down_tile<NT, kGroupFP4, RawFP4>(p, load_a, K, row0, d->n_tok, d->tok_base, p.h_hi, p.h_lo, p.y, red);
+    if constexpr (kQ3) {
+      auto load_a = [&](int blk, bool in, RawQ3& r) {
+        const int kc = blk * 128 + g4 * 32;
+        load_role(r, d->p, 2, row, K, kc, in && kc < K);
+      };
+      down_tile<NT, kGroupFP4, RawQ3>(p, load_a, K, row0, d->n_tok, d->tok_base, p.h_hi, p.h_lo, p.y, red);
+    } else {
+      auto load_a = [&](int blk, bool in, RawFP4& r) {
+        const int kc = blk * 128 + g4 * 32;
+        r = load_fp4(W2, S2, row, K, kc, in && kc < K);
+      };
+      down_tile<NT, kGroupFP4, RawFP4>(p, load_a, K, row0, d->n_tok, d->tok_base, p.h_hi, p.h_lo, p.y, red);
+    }
   } else {
     const int row0 = b * 16;
     const int64_t row = row0 + r16;
@@ -469,14 +474,16 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, co
 }
 
 template <int NT, bool XLO>
-hipError_t launch_up(const UpArgs& a, unsigned blocks, hipStream_t s) {
-  k_up_fp4<NT, XLO><<<blocks, kUpWaves * 64, 0, s>>>(a);
+hipError_t launch_up(const UpArgs& a, unsigned blocks, bool q3, hipStream_t s) {
+  if (q3) k_up_fp4<NT, XLO, true><<<blocks, kUpWaves * 64, 0, s>>>(a);
+  else k_up_fp4<NT, XLO, false><<<blocks, kUpWaves * 64, 0, s>>>(a);
   return hipGetLastError();
 }
 
 template <int NT>
-hipError_t launch_down(const DownArgs& a, unsigned blocks, hipStream_t s) {
-  k_down_fp4<NT><<<blocks, kDownWaves * 64, 0, s>>>(a);
+hipError_t launch_down(const DownArgs& a, unsigned blocks, bool q3, hipStream_t s) {
+  if (q3) k_down_fp4<NT, true><<<blocks, kDownWaves * 64, 0, s>>>(a);
+  else k_down_fp4<NT, false><<<blocks, kDownWaves * 64, 0, s>>>(a);
   return hipGetLastError();
 }
 
@@ -503,6 +510,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
   const int T = d.tokens, H = d.hidden, I = d.inter, Is = d.inter_shared, k = d.top_k;
   const int max_slots = (d.n_experts < T * k) ? d.n_experts : T * k;
   const bool x_f32 = d.x_dtype == DSK_DTYPE_F32;
+  const bool q3 = d.quant == DSK_QUANT_Q3;
   hipError_t e;
   const SlotDesc* desc = a.desc;
   const int32_t* xrow = a.xrow;
@@ -543,8 +551,8 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
   u.shared_blocks = Is > 0 ? Is / 16 : 0;
   const unsigned up_blocks = static_cast<unsigned>(u.shared_blocks + max_slots * u.tiles);
   for (int r = 0; r < repeat; ++r) {
-    if (x_f32) e = nt == 1 ? launch_up<1, true>(u, up_blocks, s) : nt == 2 ? launch_up<2, true>(u, up_blocks, s) : launch_up<4, true>(u, up_blocks, s);
-    else e = nt == 1 ? launch_up<1, false>(u, up_blocks, s) : nt == 2 ? launch_up<2, false>(u, up_blocks, s) : launch_up<4, false>(u, up_blocks, s);
+    if (x_f32) e = nt == 1 ? launch_up<1, true>(u, up_blocks, q3, s) : nt == 2 ? launch_up<2, true>(u, up_blocks, q3, s) : launch_up<4, true>(u, up_blocks, q3, s);
+    else e = nt == 1 ? launch_up<1, false>(u, up_blocks, q3, s) : nt == 2 ? launch_up<2, false>(u, up_blocks, q3, s) : launch_up<4, false>(u, up_blocks, q3, s);
     if (e != hipSuccess) return e;
   }
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
@@ -560,7 +568,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
   dn.shared_blocks = Is > 0 ? H / 16 : 0;
   const unsigned down_blocks = static_cast<unsigned>(dn.shared_blocks + max_slots * dn.tiles);
   for (int r = 0; r < repeat; ++r) {
-    e = nt == 1 ? launch_down<1>(dn, down_blocks, s) : nt == 2 ? launch_down<2>(dn, down_blocks, s) : launch_down<4>(dn, down_blocks, s);
+    e = nt == 1 ? launch_down<1>(dn, down_blocks, q3, s) : nt == 2 ? launch_down<2>(dn, down_blocks, q3, s) : launch_down<4>(dn, down_blocks, q3, s);
     if (e != hipSuccess) return e;
   }
   if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;

@@ -116,11 +116,11 @@ __global__ __launch_bounds__(kThreads) void k_fp4_quantize(
   scales[gidx] = static_cast<uint8_t>(sb);
 }
 
-// Canonical Q3 layout: see q3 code pair table in the quantiser below.  A
-// 128-code block of a row is 48 bytes; lane group g (0..3) owns words
-// d0..d2 at byte 12*g and holds codes 32*m + 8*g + j (m, j < 4, 8); pair
-// P = 4*m + j/2: P < 15 in word P/5 at bits 3*(P%5) (even j) and
-// 16 + 3*(P%5) (odd j); pair 15 in bits 15 / 31 of the three words.
+// Canonical Q3 layout.  A 128-code block of a row is 48 bytes; lane group g
+// (0..3) owns words d0..d2 at byte 12*g and holds the consecutive codes
+// 32*g + 8*m + j (m, j < 4, 8); pair P = 4*m + j/2: P < 15 in word P/5 at
+// bits 3*(P%5) (even j) and 16 + 3*(P%5) (odd j); pair 15 in bits 15 / 31 of
+// the three words.
 __device__ __forceinline__ void q3_block_codes(const uint32_t* wds /*[4][3]*/, uint8_t* q /*[128]*/) {
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -139,8 +139,8 @@ __device__ __forceinline__ void q3_block_codes(const uint32_t* wds /*[4][3]*/, u
         lo = ((d0 >> 15) & 1u) | (((d1 >> 15) & 1u) << 1) | (((d2 >> 15) & 1u) << 2);
         hi = ((d0 >> 31) & 1u) | (((d1 >> 31) & 1u) << 1) | (((d2 >> 31) & 1u) << 2);
       }
-      q[32 * m + 8 * g + 2 * i] = static_cast<uint8_t>(lo);
-      q[32 * m + 8 * g + 2 * i + 1] = static_cast<uint8_t>(hi);
+      q[32 * g + 8 * m + 2 * i] = static_cast<uint8_t>(lo);
+      q[32 * g + 8 * m + 2 * i + 1] = static_cast<uint8_t>(hi);
     }
   }
 }
@@ -181,7 +181,7 @@ __global__ __launch_bounds__(kThreads) void k_q3_quantize(
 #pragma unroll
     for (int p = 0; p < 16; ++p) {
       int m = p >> 2, i = p & 3;
-      uint32_t lo = q[32 * m + 8 * g + 2 * i], hi = q[32 * m + 8 * g + 2 * i + 1];
+      uint32_t lo = q[32 * g + 8 * m + 2 * i], hi = q[32 * g + 8 * m + 2 * i + 1];
       if (p < 15) {
         int s = 3 * (p % 5);
         wds[3 * g + p / 5] |= (lo << s) | (hi << (16 + s));

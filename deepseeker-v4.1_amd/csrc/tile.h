@@ -56,6 +56,83 @@ __device__ __forceinline__ void load_raw(RawBF16& r, const uint16_t* W, int64_t 
   for (int j = 0; j < 4; ++j) r.v[j] = ok ? ldg16(W + row * K + kc + 8 * j) : u32x4{0u, 0u, 0u, 0u};
 }
 
+// q3 affine (group 64, fp16 scale / bias) in the canonical layout: a
+// 128-code block of a row is 48 bytes, lane group g's 12 bytes (three LE
+// words) hold its 32 codes 32g + 8m + j as pairs P = 4m + j/2 -- P < 15 at
+// bits 3(P%5) / 16 + 3(P%5) of word P/5, pair 15 in bits 15 / 31 of the
+// three words.  A lane's 32 codes lie in one 64-group, so one scale and one
+// bias per lane and block.
+struct RawQ3 { uint32_t w[3]; uint32_t sb; };   // sb: fp16 scale (low), fp16 bias (high)
+
+__device__ __forceinline__ void load_raw(RawQ3& r, const uint8_t* W, const uint16_t* S, const uint16_t* B,
+                                         int64_t row, int K, int kc, bool ok) {
+  if (ok) {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(W + row * (K / 8 * 3) + (kc >> 7) * 48 + ((kc >> 5) & 3) * 12);
+    r.w[0] = src[0]; r.w[1] = src[1]; r.w[2] = src[2];
+    const int64_t gi = row * (K / 64) + kc / 64;
+    r.sb = static_cast<uint32_t>(S[gi]) | (static_cast<uint32_t>(B[gi]) << 16);
+  } else {
+    r.w[0] = r.w[1] = r.w[2] = 0u;
+    r.sb = 0u;
+  }
+}
+
+// Codes (lo, hi) of pair p of a lane's words.
+template <int P>
+__device__ __forceinline__ void q3_pair(const RawQ3& r, uint32_t& lo, uint32_t& hi) {
+  if constexpr (P < 15) {
+    const uint32_t t = r.w[P / 5] >> (3 * (P % 5));
+    lo = t & 7u;
+    hi = (t >> 16) & 7u;
+  } else {
+    lo = ((r.w[0] >> 15) & 1u) | ((r.w[1] >> 14) & 2u) | ((r.w[2] >> 13) & 4u);
+    hi = ((r.w[0] >> 31) & 1u) | ((r.w[1] >> 30) & 2u) | ((r.w[2] >> 29) & 4u);
+  }
+}
+
+// MFMA j's 8 dequantised weights: f32(s) * q + f32(b) (two roundings, as the
+// format defines), rounded to bf16.
+template <int J>
+__device__ __forceinline__ bf16x8 q3_operand(const RawQ3& r) {
+  const float s = f16_bits_to_f32(static_cast<uint16_t>(r.sb & 0xffffu));
+  const float b = f16_bits_to_f32(static_cast<uint16_t>(r.sb >> 16));
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t lo, hi;
+    switch (4 * J + i) {
+      case 0: q3_pair<0>(r, lo, hi); break;   case 1: q3_pair<1>(r, lo, hi); break;
+      case 2: q3_pair<2>(r, lo, hi); break;   case 3: q3_pair<3>(r, lo, hi); break;
+      case 4: q3_pair<4>(r, lo, hi); break;   case 5: q3_pair<5>(r, lo, hi); break;
+      case 6: q3_pair<6>(r, lo, hi); break;   case 7: q3_pair<7>(r, lo, hi); break;
+      case 8: q3_pair<8>(r, lo, hi); break;   case 9: q3_pair<9>(r, lo, hi); break;
+      case 10: q3_pair<10>(r, lo, hi); break; case 11: q3_pair<11>(r, lo, hi); break;
+      case 12: q3_pair<12>(r, lo, hi); break; case 13: q3_pair<13>(r, lo, hi); break;
+      case 14: q3_pair<14>(r, lo, hi); break; default: q3_pair<15>(r, lo, hi); break;
+    }
+    v[2 * i] = static_cast<__bf16>(__fadd_rn(__fmul_rn(s, static_cast<float>(lo)), b));
+    v[2 * i + 1] = static_cast<__bf16>(__fadd_rn(__fmul_rn(s, static_cast<float>(hi)), b));
+  }
+  return v;
+}
+
+__device__ __forceinline__ bf16x8 a_operand(const RawQ3& r, int j) {
+  return j == 0 ? q3_operand<0>(r) : (j == 1 ? q3_operand<1>(r) : (j == 2 ? q3_operand<2>(r) : q3_operand<3>(r)));
+}
+
+// Load one role (0: w1, 1: w3, 2: w2) of an expert from its 9 descriptor
+// pointers (codes, scales, biases per role).
+__device__ __forceinline__ void load_role(RawFP4& r, const void* const* ptr, int role, int64_t row, int K,
+                                          int kc, bool ok) {
+  load_raw(r, static_cast<const uint8_t*>(ptr[3 * role]), static_cast<const uint8_t*>(ptr[3 * role + 1]),
+           row, K, kc, ok);
+}
+__device__ __forceinline__ void load_role(RawQ3& r, const void* const* ptr, int role, int64_t row, int K,
+                                          int kc, bool ok) {
+  load_raw(r, static_cast<const uint8_t*>(ptr[3 * role]), static_cast<const uint16_t*>(ptr[3 * role + 1]),
+           static_cast<const uint16_t*>(ptr[3 * role + 2]), row, K, kc, ok);
+}
+
 __device__ __forceinline__ bf16x8 a_operand(const RawFP4& r, int j) {
   const float sc = e8m0_to_f32(r.s);
   const uint32_t w = j == 0 ? r.c.x : (j == 1 ? r.c.y : (j == 2 ? r.c.z : r.c.w));

@@ -176,16 +176,17 @@ def q3_pack(q: np.ndarray) -> np.ndarray:
     Canonical layout (this build's; K must be a multiple of 128):
     a row is a sequence of 128-code blocks of 48 bytes.  Within a block,
     lane group g (0..3) owns the 12 bytes at 12*g, read as three
-    little-endian u32 words d0, d1, d2.  Lane group g holds the 32 codes
-    ``32*m + 8*g + j`` (m = 0..3, j = 0..7) of the block, as 16 pairs
-    P = 4*m + j//2 with the even-j code in the low half and the odd-j code in
-    the high half.  Pair P < 15 sits in word P // 5: low code at bit
-    3*(P % 5), high code at bit 16 + 3*(P % 5).  Pair 15 uses the spare bits:
-    bit t of its low code is bit 15 of word t, bit t of its high code is bit
-    31 of word t.
-    The 32 codes that one MFMA K-step consumes from a lane group
-    (``32*m + 8*g .. +8`` for the four g) all fall in one 64-group, and every
-    pair is one shift-and-mask away from a packed 16-bit pair.
+    little-endian u32 words d0, d1, d2.  Lane group g holds the 32
+    consecutive codes ``32*g + 8*m + j`` (m = 0..3, j = 0..7) of the block,
+    as 16 pairs P = 4*m + j//2 with the even-j code in the low half and the
+    odd-j code in the high half.  Pair P < 15 sits in word P // 5: low code at
+    bit 3*(P % 5), high code at bit 16 + 3*(P % 5).  Pair 15 uses the spare
+    bits: bit t of its low code is bit 15 of word t, bit t of its high code
+    is bit 31 of word t.
+    A lane group's 32 codes are the same K range an FP4 lane group reads
+    (one 16-byte word of 32 codes), all in one 64-group (g < 2: the block's
+    first group), and every pair is one shift-and-mask away from a packed
+    16-bit pair.
     """
     q = np.asarray(q, dtype=np.uint32)
     n, k = q.shape
@@ -194,12 +195,12 @@ def q3_pack(q: np.ndarray) -> np.ndarray:
     if q.size and q.max() > 7:
         raise ValueError("q3 codes must be in 0..7")
     nb = k // Q3_SUPERBLOCK
-    # code index within block = 32*m + 8*g + j  -> axes [N, nb, m, g, j]
+    # code index within block = 32*g + 8*m + j  -> axes [N, nb, g, m, j]
     c = q.reshape(n, nb, 4, 4, 8)
     words = np.zeros((n, nb, 4, 3), dtype=np.uint32)   # [.., g, d]
     for p, (m, i) in enumerate(_q3_pair_table()):
-        lo = c[:, :, m, :, 2 * i]
-        hi = c[:, :, m, :, 2 * i + 1]
+        lo = c[:, :, :, m, 2 * i]
+        hi = c[:, :, :, m, 2 * i + 1]
         if p < 15:
             d, s = p // 5, 3 * (p % 5)
             words[:, :, :, d] |= (lo << s) | (hi << (16 + s))
@@ -217,7 +218,7 @@ def q3_unpack(packed: np.ndarray, k: int) -> np.ndarray:
         raise ValueError(f"packed {p.shape} does not hold K={k} q3 codes")
     nb = k // Q3_SUPERBLOCK
     words = p.reshape(n, nb, 4, 12).copy().view("<u4").reshape(n, nb, 4, 3).astype(np.uint32)
-    c = np.zeros((n, nb, 4, 4, 8), dtype=np.uint32)    # [.., m, g, j]
+    c = np.zeros((n, nb, 4, 4, 8), dtype=np.uint32)    # [.., g, m, j]
     for pidx, (m, i) in enumerate(_q3_pair_table()):
         if pidx < 15:
             d, s = pidx // 5, 3 * (pidx % 5)
@@ -229,8 +230,8 @@ def q3_unpack(packed: np.ndarray, k: int) -> np.ndarray:
             for t in range(3):
                 lo |= ((words[:, :, :, t] >> 15) & 1) << t
                 hi |= ((words[:, :, :, t] >> 31) & 1) << t
-        c[:, :, m, :, 2 * i] = lo
-        c[:, :, m, :, 2 * i + 1] = hi
+        c[:, :, :, m, 2 * i] = lo
+        c[:, :, :, m, 2 * i + 1] = hi
     return c.reshape(n, k).astype(np.uint8)
 
 

@@ -73,8 +73,10 @@ def test_null_and_alignment_errors_before_launch():
     assert rc == -1                                   # cols % 32
     rc = lib.dsk_fp4_dequant(ctypes.c_void_p(17), ctypes.c_void_p(16), 1, 64, ctypes.c_void_p(16), 1, None)
     assert rc == -2                                   # misaligned
-    rc = lib.dsk_experts(ctypes.byref(_desc(quant="q3")), *([ctypes.c_void_p(256)] * 14), 1 << 30, None)
-    assert rc == -3                                   # q3 experts not in this build
+    rc = lib.dsk_experts(ctypes.byref(_desc(quant="q3", inter=96)), *([ctypes.c_void_p(256)] * 14), 1 << 30, None)
+    assert rc == -1 and b"128" in lib.dsk_last_error()   # q3 needs K multiples of 128
+    rc = lib.dsk_experts(ctypes.byref(_desc(quant="q3", hidden=1056)), *([ctypes.c_void_p(256)] * 14), 1 << 30, None)
+    assert rc == -1                                   # hidden % 128
 
 
 def test_route_constants_match_oracle():

@@ -188,3 +188,41 @@ def test_mid_size_batch64():
     print("layer mid T=64 H=1024 E=64 k=8", flush=True)
     out = run_layer(d, spec)
     assert_layer_close(out.float(), r["y_ref"])
+
+
+# ---------------------------------------------------------------- q3 experts
+@pytest.mark.parametrize("name,spec,T", [
+    ("tiny", synth.tiny_spec(L.QUANT_Q3), 4),
+    ("cfg0-shape", L.LayerSpec(H=1024, E=64, k=6, I=512, I_shared=512, quant=L.QUANT_Q3), 4),
+    ("mid T=64", L.LayerSpec(H=1024, E=64, k=8, I=512, I_shared=512, quant=L.QUANT_Q3), 64),
+])
+def test_q3_layer(name, spec, T):
+    """q3 affine (g64, fp16 scale/bias) routed experts against the oracle."""
+    print(f"layer q3 {name} T={T}", flush=True)
+    d = synth.make_layer(spec, 11, T)
+    r = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], d["shared"], spec)
+    idx = torch.empty((T, spec.k), dtype=torch.int32, device=DEV)
+    layer = dsk_moe.MoELayer(d["gate_w"].to(DEV), d["gate_b"].to(DEV), to_bank(d["bank"]),
+                             to_shared(d["shared"]), spec.k)
+    out = layer(d["x"].to(DEV), idx=idx).cpu()
+    np.testing.assert_array_equal(idx.cpu().numpy(), r["idx"])
+    c, rel = assert_layer_close(out.float(), r["y_ref"])
+    print(f"cos={c:.9f} rel={rel:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_full_size_q3(T):
+    """hidden 4096, 256 q3 experts, top-8, inter 2048, bf16 shared 2048 (GPU-generated)."""
+    print(f"layer full-size q3 T={T}", flush=True)
+    layer = gsynth.make_layer(hidden=4096, n_experts=256, top_k=8, inter=2048,
+                              inter_shared=2048, quant="q3", seed=2, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(200 + T)
+    x = torch.randn((T, 4096), generator=g, device=DEV).to(torch.bfloat16)
+    idx = torch.empty((T, 8), dtype=torch.int32, device=DEV)
+    out = layer(x, idx=idx).cpu()
+    spec = L.LayerSpec(H=4096, E=256, k=8, I=2048, I_shared=2048, quant=L.QUANT_Q3)
+    shared = tuple(t.cpu() for t in (layer.shared.w1, layer.shared.w3, layer.shared.w2))
+    r = L.moe_forward(x.cpu(), layer.gate_w.cpu(), layer.gate_b.cpu(), _LazyBank(layer.bank), shared, spec)
+    np.testing.assert_array_equal(idx.cpu().numpy(), r["idx"])
+    c, rel = assert_layer_close(out.float(), r["y_ref"])
+    print(f"cos={c:.9f} rel={rel:.2e}", flush=True)

@@ -119,10 +119,10 @@ def test_q3_pack_roundtrip_and_geometry():
 
 
 def test_q3_pack_known_answer():
-    # one code at a time: code 32*m + 8*g + j = 7 lands in lane group g's words
+    # one code at a time: code 32*g + 8*m + j = 5 lands in lane group g's words
     for m, g, j in [(0, 0, 0), (0, 0, 1), (2, 1, 4), (3, 3, 6), (3, 3, 7), (1, 2, 3)]:
         q = np.zeros((1, 128), dtype=np.uint8)
-        q[0, 32 * m + 8 * g + j] = 5
+        q[0, 32 * g + 8 * m + j] = 5
         words = F.q3_pack(q).view("<u4").reshape(4, 3)
         p = 4 * m + j // 2
         expect = np.zeros((4, 3), dtype=np.uint32)
