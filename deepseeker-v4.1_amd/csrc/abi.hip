@@ -57,6 +57,7 @@ Workspace workspace_layout(const dsk_moe_desc& d) {
   L.hs_lo = take(T * Is * 2);
   L.y = take(N * H * 4);
   L.ys = take(T * H * 4);
+  L.pf_tiles = take(prefill_gemm(d) ? (2 + 2 * static_cast<size_t>(prefill_max_tiles(d))) * 4 : 0);
   L.total = o;
   return L;
 }

@@ -90,8 +90,8 @@ __device__ __forceinline__ void load_batch(UpBatch<G>& b, const uint8_t* W1, con
     for (int v = 0; v < G / 4; ++v) {
       const int kw = kb + 4 * v + g4;                 // K block whose scales this lane fetches
       const bool ok = rok && kw < k1;
-      b.w1[v] = ok ? *reinterpret_cast<const uint32_t*>(S1 + sb + 4 * kw) : 0u;
-      b.w3[v] = ok ? *reinterpret_cast<const uint32_t*>(S3 + sb + 4 * kw) : 0u;
+      b.w1[v] = ok ? ldg<uint32_t>(S1 + sb + 4 * kw) : 0u;
+      b.w3[v] = ok ? ldg<uint32_t>(S3 + sb + 4 * kw) : 0u;
     }
   }
 #pragma unroll
@@ -101,8 +101,8 @@ __device__ __forceinline__ void load_batch(UpBatch<G>& b, const uint8_t* W1, con
     b.c1[i] = ok ? ldg16(W1 + cb + kc / 2) : u32x4{0u, 0u, 0u, 0u};
     b.c3[i] = ok ? ldg16(W3 + cb + kc / 2) : u32x4{0u, 0u, 0u, 0u};
     if constexpr (!kWin) {
-      b.s1[i] = ok ? S1[sb + kc / 32] : 127u;
-      b.s3[i] = ok ? S3[sb + kc / 32] : 127u;
+      b.s1[i] = ok ? ldg<uint8_t>(S1 + sb + kc / 32) : 127u;
+      b.s3[i] = ok ? ldg<uint8_t>(S3 + sb + kc / 32) : 127u;
     }
   }
 }

@@ -78,6 +78,7 @@ struct Workspace {
   size_t hs_hi, hs_lo;      // shared intermediate      [T][Is]  (16-bit)
   size_t y;                 // routed outputs          [T*k][H] f32
   size_t ys;                // shared output           [T][H]   f32
+  size_t pf_tiles;          // prefill GEMM tile list  [2 + 2 * prefill_max_tiles]
   size_t total;
 };
 
@@ -92,6 +93,19 @@ constexpr int kDecodeMaxTokens = 16;
 constexpr int kDecodeMaxPositions = 64;
 constexpr size_t kMaxLds = 163840;          // LDS bytes one gfx950 workgroup may use
 constexpr size_t kUpLdsFixed = 2 * 4 * 2 * 64 * 4 * 4 + 8 * 640;   // decode gate/up: reduction + scale tiles
+// Prefill GEMM tiles: 256 weight rows x 256 dispatch rows per block.
+constexpr int kPfRows = 256;
+constexpr int kPfToks = 256;
+constexpr int kPrefillMinTokens = 256;
+
+// Large batches of bf16 tokens run the expert products as MFMA GEMM tiles
+// (gate/up tiles of 128 intermediate rows, down tiles of 256 output rows).
+inline bool prefill_gemm(const dsk_moe_desc& d) {
+  return d.x_dtype == DSK_DTYPE_BF16 && d.tokens >= kPrefillMinTokens && d.hidden % kPfRows == 0 &&
+         d.inter % 128 == 0 && d.inter_shared % 128 == 0;
+}
+int prefill_max_tiles(const dsk_moe_desc& d);
+
 inline bool decode_pipeline(const dsk_moe_desc& d) {
   // the gate/up kernel stages the tokens' activations (bf16 hi, and lo for
   // float32 x) plus its reduction and scale-exchange buffers in LDS
@@ -149,6 +163,16 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L,
                           const ExpertsArgs& a, hipStream_t s, const hipEvent_t* ev, int repeat);
 
 hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t s);
+
+// Prefill GEMM path (prefill_gemm(d)): tile list, gate/up, down; the caller
+// runs the combine.  ev (nullable): 2 events, after gate/up and after down.
+struct PrefillArgs {
+  const SlotDesc* desc; const int32_t* active; const int32_t* xrow; const float* wrow;
+  const void* x; const void* ws1; const void* ws3; const void* ws2;
+  char* ws;
+};
+hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, const PrefillArgs& a,
+                                  hipStream_t s, const hipEvent_t* ev, int repeat);
 
 // Decode pipeline (decode_pipeline(d)): routed and shared gate/up in one
 // kernel, then down + shared down + combine fused per 16 output rows.  Needs

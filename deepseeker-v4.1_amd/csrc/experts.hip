@@ -43,7 +43,7 @@ __device__ __forceinline__ RawFP4 load_fp4(const uint8_t* W, const uint8_t* S, i
   RawFP4 r;
   if (ok) {
     r.c = ldg16(W + row * (K / 2) + kc / 2);
-    r.s = S[row * (K / 32) + kc / 32];
+    r.s = ldg<uint8_t>(S + row * (K / 32) + kc / 32);
   } else {
     r.c = u32x4{0u, 0u, 0u, 0u};
     r.s = 127u;
@@ -505,6 +505,26 @@ hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t s) {
   return hipGetLastError();
 }
 
+// out[t] from the routed rows y and the shared output; ev (nullable): 1 event after it.
+hipError_t launch_combine(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
+                          const hipEvent_t* ev, int repeat) {
+  const int T = d.tokens, H = d.hidden, Is = d.inter_shared, k = d.top_k;
+  const float* y = reinterpret_cast<const float*>(a.ws + L.y);
+  const float* ys = reinterpret_cast<const float*>(a.ws + L.ys);
+  dim3 cg(static_cast<unsigned>(T), static_cast<unsigned>((H + 1023) / 1024));
+  const int mode = Is > 0 ? kSharedF32 : (a.shared_out ? kSharedExt : kNoShared);
+  hipError_t e = hipSuccess;
+  for (int r = 0; r < repeat; ++r) {
+    if (d.x_dtype == DSK_DTYPE_F32)
+      k_combine<false><<<cg, 256, 0, s>>>(y, ys, a.shared_out, a.rank, H, k, mode, a.out);
+    else
+      k_combine<true><<<cg, 256, 0, s>>>(y, ys, a.shared_out, a.rank, H, k, mode, a.out);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (ev) e = hipEventRecord(ev[0], s);
+  return e;
+}
+
 hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                           hipStream_t s, const hipEvent_t* ev, int repeat) {
   const int T = d.tokens, H = d.hidden, I = d.inter, Is = d.inter_shared, k = d.top_k;
@@ -527,6 +547,11 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
   }
   const uint16_t* xb_hi = static_cast<const uint16_t*>(a.x);
   const uint16_t* xb_lo = nullptr;
+  if (prefill_gemm(d)) {
+    PrefillArgs pa{desc, a.active, xrow, wrow, a.x, a.ws1, a.ws3, a.ws2, a.ws};
+    if ((e = launch_experts_prefill(d, L, pa, s, ev, repeat)) != hipSuccess) return e;
+    return launch_combine(d, L, a, s, ev ? ev + 2 : nullptr, repeat);
+  }
   if (x_f32) {
     uint16_t* hi = reinterpret_cast<uint16_t*>(a.ws + L.xb_hi);
     uint16_t* lo = reinterpret_cast<uint16_t*>(a.ws + L.xb_lo);
@@ -572,18 +597,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
     if (e != hipSuccess) return e;
   }
   if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
-
-  dim3 cg(static_cast<unsigned>(T), static_cast<unsigned>((H + 1023) / 1024));
-  const int mode = Is > 0 ? kSharedF32 : (a.shared_out ? kSharedExt : kNoShared);
-  for (int r = 0; r < repeat; ++r) {
-    if (x_f32)
-      k_combine<false><<<cg, 256, 0, s>>>(dn.y, dn.ys, a.shared_out, a.rank, H, k, mode, a.out);
-    else
-      k_combine<true><<<cg, 256, 0, s>>>(dn.y, dn.ys, a.shared_out, a.rank, H, k, mode, a.out);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  if (e == hipSuccess && ev) e = hipEventRecord(ev[2], s);
-  return e;
+  return launch_combine(d, L, a, s, ev ? ev + 2 : nullptr, repeat);
 }
 
 }  // namespace dsk

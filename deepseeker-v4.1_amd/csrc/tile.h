@@ -23,7 +23,19 @@ __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const 
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
 
-__device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// Loads through the global address space.  Weight pointers come from
+// descriptor tables, so the compiler cannot infer their address space; a
+// generic (flat) load would also count against the LDS wait counter and make
+// every LDS wait wait for it.
+template <typename T>
+__device__ __forceinline__ T ldg(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)(p);
+}
+__device__ __forceinline__ u32x4 ldg16(const void* p) { return ldg<u32x4>(p); }
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const void* p) {
+  return (const __attribute__((address_space(1))) T*)(p);
+}
 
 __device__ __forceinline__ bf16x8 fp4_word_to_bf16x8(uint32_t word, float scale) {
   bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
@@ -43,7 +55,7 @@ __device__ __forceinline__ void load_raw(RawFP4& r, const uint8_t* W, const uint
                                          int K, int kc, bool ok) {
   if (ok) {
     r.c = ldg16(W + row * (K / 2) + kc / 2);
-    r.s = S[row * (K / 32) + kc / 32];
+    r.s = ldg<uint8_t>(S + row * (K / 32) + kc / 32);
   } else {
     r.c = u32x4{0u, 0u, 0u, 0u};
     r.s = 127u;
@@ -67,10 +79,10 @@ struct RawQ3 { uint32_t w[3]; uint32_t sb; };   // sb: fp16 scale (low), fp16 bi
 __device__ __forceinline__ void load_raw(RawQ3& r, const uint8_t* W, const uint16_t* S, const uint16_t* B,
                                          int64_t row, int K, int kc, bool ok) {
   if (ok) {
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(W + row * (K / 8 * 3) + (kc >> 7) * 48 + ((kc >> 5) & 3) * 12);
+    const auto src = gptr<uint32_t>(W + row * (K / 8 * 3) + (kc >> 7) * 48 + ((kc >> 5) & 3) * 12);
     r.w[0] = src[0]; r.w[1] = src[1]; r.w[2] = src[2];
     const int64_t gi = row * (K / 64) + kc / 64;
-    r.sb = static_cast<uint32_t>(S[gi]) | (static_cast<uint32_t>(B[gi]) << 16);
+    r.sb = static_cast<uint32_t>(ldg<uint16_t>(S + gi)) | (static_cast<uint32_t>(ldg<uint16_t>(B + gi)) << 16);
   } else {
     r.w[0] = r.w[1] = r.w[2] = 0u;
     r.sb = 0u;
