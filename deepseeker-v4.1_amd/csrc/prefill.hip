@@ -149,21 +149,28 @@ struct Fp4Tile {
   }
 };
 
+// Operands of one K step: 4 weight fragments, 2 token fragments.
+struct KOps {
+  bf16x8 a[4], b[2];
+};
+
+template <class P>
+__device__ __forceinline__ void pf_operands(KOps& o, const typename P::Frag& fa, const uint16_t* B, int ks) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c) o.b[c] = lds16(B + c * 32 * kPfLd + 8 * ks);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o.a[i] = P::operand(fa, i, ks);
+}
+
 // 8 MFMAs of one K step: acc[i][c] += A(row tile i) x B(token tile c);
 // unless kFull, token tiles c >= n_ct are skipped (n_ct is wave-uniform).
-template <bool kFull, class P>
-__device__ __forceinline__ void pf_kstep(const typename P::Frag& fa, const uint16_t* B, int ks, int n_ct,
-                                         f32x16 (&acc)[4][2]) {
-  bf16x8 av[4], bv[2];
-#pragma unroll
-  for (int c = 0; c < 2; ++c) bv[c] = lds16(B + c * 32 * kPfLd + 8 * ks);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) av[i] = P::operand(fa, i, ks);
+template <bool kFull>
+__device__ __forceinline__ void pf_mma(const KOps& o, int n_ct, f32x16 (&acc)[4][2]) {
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     if (kFull || c < n_ct) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i][c] = mfma32(av[i], bv[c], acc[i][c]);
+      for (int i = 0; i < 4; ++i) acc[i][c] = mfma32(o.a[i], o.b[c], acc[i][c]);
     }
   }
 }
@@ -179,11 +186,15 @@ struct StageRegs {
 // Main loop of one block tile.  load_a(regs, st) fills this thread's half
 // weight row of stage st; brow[j] is the token row of LDS row (t >> 3) + 64 j.
 // An LDS stage buffer holds the weight tile (P) then the token tile
-// ([256][72] bf16).  Two buffers and two register sets: stage st + 2 is
-// loaded from global memory while stage st is multiplied, and stage st + 1
-// (loaded one stage earlier) goes to the other buffer in slices between the
-// K steps.  Wave w multiplies weight rows 128 (w & 1) + [0, 128) by tokens
-// 64 (w >> 1) + [0, 64).
+// ([256][72] bf16); two buffers alternate.  Per stage st (buffer st & 1):
+//   read the weight fragments of st; MFMAs of the previous stage's last K
+//   step (its operands were kept in registers, so they run while the LDS
+//   reads are in flight); K steps 0-2 of st; operands of K step 3, kept;
+//   store stage st + 1 (loaded during stage st - 1) into the other buffer;
+//   issue the global loads of stage st + 2; barrier.
+// The matrix pipe thus has work across the barrier, and a global load has a
+// whole stage to arrive.  Wave w multiplies weight rows 128 (w & 1) +
+// [0, 128) by tokens 64 (w >> 1) + [0, 64).
 template <bool kFull, class P, class Regs, class LoadA>
 __device__ __forceinline__ void pf_loop(LoadA load_a, const uint16_t* const (&brow)[4], int nst, int n_ct,
                                         char* lds, f32x16 (&acc)[4][2]) {
@@ -194,41 +205,42 @@ __device__ __forceinline__ void pf_loop(LoadA load_a, const uint16_t* const (&br
   const int b_st = (t >> 3) * kPfLd + ch;
   const int b_rd = (64 * wn + (lane & 31)) * kPfLd + 32 * (lane >> 5);
   auto btile = [&](int buf) { return reinterpret_cast<uint16_t*>(lds + buf * kBufBytes + P::kBytes); };
-  auto load = [&](StageRegs<Regs>& r, int st) {
+  StageRegs<Regs> r;
+  auto load = [&](int st) {
     load_a(r.a, st);
 #pragma unroll
     for (int j = 0; j < 4; ++j) r.b[j] = ldg16(brow[j] + st * kPfK + ch);
   };
-  auto store_slice = [&](const StageRegs<Regs>& r, int buf, int ks) {
-    P::store_slice(r.a, lds + buf * kBufBytes, t, ks);
-    sts16(btile(buf) + b_st + 64 * ks * kPfLd, r.b[ks]);
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int ks = 0; ks < kPfK / 16; ++ks) {
+      P::store_slice(r.a, lds + buf * kBufBytes, t, ks);
+      sts16(btile(buf) + b_st + 64 * ks * kPfLd, r.b[ks]);
+    }
   };
-  auto step = [&](int cur, const StageRegs<Regs>& next, int nxt, bool store) {
+  load(0);
+  store(0);
+  if (nst > 1) load(1);
+  __syncthreads();
+  KOps o, last;
+  for (int st = 0; st < nst; ++st) {
+    const int cur = st & 1;
     typename P::Frag fa;
     P::frag_begin(fa, lds + cur * kBufBytes, wm, lane);
     const uint16_t* B = btile(cur) + b_rd;
-#pragma unroll
-    for (int ks = 0; ks < kPfK / 16; ++ks) {
-      pf_kstep<kFull, P>(fa, B, ks, n_ct, acc);
-      if (store) store_slice(next, nxt, ks);
-    }
-  };
-  StageRegs<Regs> r0, r1;
-  load(r0, 0);
-  if (nst > 1) load(r1, 1);
-#pragma unroll
-  for (int ks = 0; ks < kPfK / 16; ++ks) store_slice(r0, 0, ks);
-  __syncthreads();
-  for (int st = 0; st < nst; st += 2) {
-    if (st + 2 < nst) load(r0, st + 2);
-    step(0, r1, 1, st + 1 < nst);
+    if (st > 0) pf_mma<kFull>(last, n_ct, acc);
+    pf_operands<P>(o, fa, B, 0);
+    pf_mma<kFull>(o, n_ct, acc);
+    pf_operands<P>(o, fa, B, 1);
+    pf_mma<kFull>(o, n_ct, acc);
+    pf_operands<P>(o, fa, B, 2);
+    pf_mma<kFull>(o, n_ct, acc);
+    pf_operands<P>(last, fa, B, 3);
+    if (st + 1 < nst) store(cur ^ 1);
+    if (st + 2 < nst) load(st + 2);
     __syncthreads();
-    if (st + 1 < nst) {
-      if (st + 3 < nst) load(r1, st + 3);
-      step(1, r0, 0, st + 2 < nst);
-      __syncthreads();
-    }
   }
+  pf_mma<kFull>(last, n_ct, acc);
 }
 
 template <class P, class Regs, class LoadA>

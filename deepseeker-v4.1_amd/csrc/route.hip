@@ -98,6 +98,148 @@ __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ scores,
              idx + static_cast<int64_t>(t) * k, weights + static_cast<int64_t>(t) * k);
 }
 
+// Wide gate for large batches.  Block = 8 waves and a 32-token x 16-expert
+// tile; wave w owns tokens 8 (w & 3) + [0, 8) and experts 8 (w >> 2) +
+// [0, 8), and lane l the partial l of each of its 64 (token, expert) pairs.
+// Each 256-element step m is staged through LDS (double-buffered: x [32][256],
+// W [16][256]) and every partial adds, for v = 0..3, the rounded product at
+// position 256m + 4l + v: the order of the definition above.  At the end of a
+// segment the 64 partials of each pair are combined by the same XOR tree,
+// computed as a reduce-scatter: at stride s a lane keeps the upper half of
+// its pairs if bit s of its lane id is set and adds the partner's (lane ^ s)
+// copy of them, so after strides 32..1 lane l holds the segment sum of pair l
+// -- the sum lane 0 of the full butterfly holds, at a sixth of the additions
+// and exchanges.
+constexpr int kGwThreads = 512;
+constexpr int kGwTok = 32, kGwExp = 16;
+constexpr int kGateWideMinTokens = 128;
+
+template <bool kBF16>
+__device__ __forceinline__ f32x4 lds_f32x4(const char* row, int lane) {
+  if constexpr (kBF16) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(row + 8 * lane);
+    return f32x4{__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                 __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
+  } else {
+    return *reinterpret_cast<const f32x4*>(row + 16 * lane);
+  }
+}
+
+// Reduce-scatter of N values per lane across the 64 lanes at stride S (then
+// S/2 .. 1); on return lane l holds in vals[0 .. N/64) the tree sums of
+// values l*N/64 .. of the full XOR butterfly.
+template <int N, int S>
+__device__ __forceinline__ void xor_reduce_scatter(float* vals, int lane) {
+#pragma clang fp contract(off)
+  if constexpr (S >= 1) {
+    const bool upper = (lane & S) != 0;
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+      const float send = upper ? vals[j] : vals[j + N / 2];
+      const float mine = upper ? vals[j + N / 2] : vals[j];
+      const float recv = __shfl_xor(send, S, 64);
+      vals[j] = mine + recv;
+    }
+    xor_reduce_scatter<N / 2, S / 2>(vals, lane);
+  }
+}
+
+template <bool kXBF16, bool kWBF16>
+__global__ __launch_bounds__(kGwThreads, 1) void k_gate_wide(GateArgs g) {
+#pragma clang fp contract(off)
+  constexpr int kSx = kXBF16 ? 2 : 4, kSw = kWBF16 ? 2 : 4;
+  constexpr int kXBytes = kGwTok * 256 * kSx, kWBytes = kGwExp * 256 * kSw;
+  constexpr int kBuf = kXBytes + kWBytes;
+  constexpr int kXChunks = kXBytes / 16 / kGwThreads, kWChunks = kWBytes / 16 / kGwThreads;
+  static_assert(kXChunks >= 1 && kWChunks >= 1, "staging chunks");
+  extern __shared__ __align__(16) char gw_lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wt = wave & 3, we = wave >> 2;
+  const int n_et = (g.E + kGwExp - 1) / kGwExp;
+  const int t0 = (blockIdx.x / n_et) * kGwTok, e0 = (blockIdx.x % n_et) * kGwExp;
+  const int H = g.H, steps = (H + 255) / 256, seg = (steps + kSegments - 1) / kSegments;
+  // staging: thread chunk c = tid + 512 q of the x tile ([32][256] elements,
+  // 16-byte chunks), the same for W; addresses recomputed per step
+  u32x4 xr[kXChunks], wr[kWChunks];
+  auto load = [&](int m) {
+#pragma unroll
+    for (int q = 0; q < kXChunks; ++q) {
+      constexpr int per_row = 256 * kSx / 16;
+      const int c = tid + kGwThreads * q;
+      const int col = 256 * m + (c % per_row) * (16 / kSx);
+      const int64_t row = min(t0 + c / per_row, g.T - 1);
+      xr[q] = col < H ? ldg16(static_cast<const char*>(g.x) + (row * H + col) * kSx) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int q = 0; q < kWChunks; ++q) {
+      constexpr int per_row = 256 * kSw / 16;
+      const int c = tid + kGwThreads * q;
+      const int col = 256 * m + (c % per_row) * (16 / kSw);
+      const int64_t row = min(e0 + c / per_row, g.E - 1);
+      wr[q] = col < H ? ldg16(static_cast<const char*>(g.gw) + (row * H + col) * kSw) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store = [&](int buf) {
+    char* b = gw_lds + buf * kBuf;
+#pragma unroll
+    for (int q = 0; q < kXChunks; ++q) *reinterpret_cast<u32x4*>(b + 16 * (tid + kGwThreads * q)) = xr[q];
+#pragma unroll
+    for (int q = 0; q < kWChunks; ++q)
+      *reinterpret_cast<u32x4*>(b + kXBytes + 16 * (tid + kGwThreads * q)) = wr[q];
+  };
+  float p[64];
+  float z = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) p[i] = 0.0f;
+  load(0);
+  store(0);
+  __syncthreads();
+  int done_segments = 0;
+  for (int m = 0; m < steps; ++m) {
+    if (m + 1 < steps) load(m + 1);
+    const char* b = gw_lds + (m & 1) * kBuf;
+    f32x4 xv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[i] = lds_f32x4<kXBF16>(b + (8 * wt + i) * 256 * kSx, lane);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const f32x4 wv = lds_f32x4<kWBF16>(b + kXBytes + (8 * we + j) * 256 * kSw, lane);
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float prod = xv[i][v] * wv[v];
+          p[8 * i + j] = p[8 * i + j] + prod;
+        }
+    }
+    if (m + 1 < steps) store((m + 1) & 1);
+    if (m + 1 == steps || (m + 1) % seg == 0) {
+      xor_reduce_scatter<64, 32>(p, lane);
+      z = done_segments == 0 ? p[0] : z + p[0];
+      ++done_segments;
+#pragma unroll
+      for (int i = 0; i < 64; ++i) p[i] = 0.0f;
+    }
+    __syncthreads();
+  }
+  for (int w = done_segments; w < kSegments; ++w) z = z + 0.0f;   // empty segments add +0
+  const int t = t0 + 8 * wt + lane / 8, e = e0 + 8 * we + lane % 8;
+  if (t < g.T && e < g.E) g.scores[static_cast<int64_t>(t) * g.E + e] = score_of(z, g.score_func);
+}
+
+hipError_t launch_gate_wide(const dsk_moe_desc& d, const GateArgs& g, hipStream_t s) {
+  const unsigned blocks = static_cast<unsigned>(((d.tokens + kGwTok - 1) / kGwTok) *
+                                                ((d.n_experts + kGwExp - 1) / kGwExp));
+  const bool xb = d.x_dtype == DSK_DTYPE_BF16, wb = d.gate_dtype == DSK_DTYPE_BF16;
+  const size_t lds = 2 * static_cast<size_t>(kGwTok * 256 * (xb ? 2 : 4) + kGwExp * 256 * (wb ? 2 : 4));
+  if (xb && wb) k_gate_wide<true, true><<<blocks, kGwThreads, lds, s>>>(g);
+  else if (xb) k_gate_wide<true, false><<<blocks, kGwThreads, lds, s>>>(g);
+  else if (wb) k_gate_wide<false, true><<<blocks, kGwThreads, lds, s>>>(g);
+  else k_gate_wide<false, false><<<blocks, kGwThreads, lds, s>>>(g);
+  return hipGetLastError();
+}
+
 template <int TW, int EW, bool kFused>
 hipError_t launch_gate(const dsk_moe_desc& d, const GateArgs& g, hipStream_t s) {
   const int n_et = (d.n_experts + EW - 1) / EW;
@@ -166,7 +308,9 @@ GateArgs make_gate_args(const dsk_moe_desc& d, const void* x, const void* gate_w
 }
 
 hipError_t launch_route_unfused(const dsk_moe_desc& d, const GateArgs& g, hipStream_t s) {
-  hipError_t e = (d.tokens >= 16) ? launch_gate<4, 4, false>(d, g, s) : launch_gate<1, 1, false>(d, g, s);
+  hipError_t e = (d.tokens >= kGateWideMinTokens) ? launch_gate_wide(d, g, s)
+                 : (d.tokens >= 16)              ? launch_gate<4, 4, false>(d, g, s)
+                                                 : launch_gate<1, 1, false>(d, g, s);
   if (e != hipSuccess) return e;
   const unsigned blocks = static_cast<unsigned>((d.tokens + 3) / 4);
   k_topk<<<blocks, 256, 0, s>>>(g.scores, g.bias, d.tokens, d.n_experts, d.top_k, d.route_scale,

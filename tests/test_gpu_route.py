@@ -85,3 +85,18 @@ def test_route_zipf_bias_skew():
     idx, _ = check(x, gate_w, gate_b, 8, "sigmoid", 2.5)
     counts = np.bincount(idx.ravel(), minlength=256)
     assert counts[0] > counts[-64:].mean()
+
+
+@pytest.mark.parametrize("T,H,E,k,score_func", [(128, 4096, 256, 8, "sigmoid"), (300, 1056, 100, 5, "sqrtsoftplus"),
+                                                (130, 64, 24, 3, "sigmoid"), (257, 2048, 384, 6, "sqrtsoftplus")])
+@pytest.mark.parametrize("xdt,gdt", [("bf16", "f32"), ("f32", "f32"), ("bf16", "bf16"), ("f32", "bf16")])
+def test_route_wide_gate_bit_exact(T, H, E, k, score_func, xdt, gdt):
+    """Batches of >= 128 tokens take the wide gate kernel (32x16 tiles staged through
+    LDS, segment sums by reduce-scatter); H = 64 and 1056 leave segments empty."""
+    g = torch.Generator().manual_seed(T + H + E)
+    x = torch.randn((T, H), generator=g)
+    x = x.to(torch.bfloat16) if xdt == "bf16" else x
+    gate_w = torch.randn((E, H), generator=g) / math.sqrt(H)
+    gate_w = gate_w.to(torch.bfloat16) if gdt == "bf16" else gate_w
+    gate_b = torch.rand((E,), generator=g) * 0.2 - 0.1
+    check(x, gate_w, gate_b, k, score_func, 2.5 if score_func == "sigmoid" else 1.5)
