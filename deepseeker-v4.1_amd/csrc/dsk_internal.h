@@ -85,9 +85,10 @@ struct Workspace {
 Workspace workspace_layout(const dsk_moe_desc& d);
 
 // Bytes reserved at the start of every workspace for the fused router's
-// arrival counters (one per token tile plus one; fused up to 64 tokens).
+// arrival counters (one per token tile plus one, for the fused router of up
+// to kFusedMaxTokens tokens).
 constexpr size_t kCounterBytes = 1024;
-constexpr int kFusedMaxTokens = 64;
+constexpr int kFusedMaxTokens = 8;
 // Decode pipeline limits and the shared expert's gate/up K split.
 constexpr int kDecodeMaxTokens = 16;
 constexpr int kDecodeMaxPositions = 64;
@@ -96,7 +97,7 @@ constexpr size_t kUpLdsFixed = 2 * 4 * 2 * 64 * 4 * 4 + 8 * 640;   // decode gat
 // Prefill GEMM tiles: 256 weight rows x 256 dispatch rows per block.
 constexpr int kPfRows = 256;
 constexpr int kPfToks = 256;
-constexpr int kPrefillMinTokens = 256;
+constexpr int kPrefillMinTokens = 64;
 
 // Large batches of bf16 tokens run the expert products as MFMA GEMM tiles
 // (gate/up tiles of 128 intermediate rows, down tiles of 256 output rows).
