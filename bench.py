@@ -107,19 +107,22 @@ def layer_bytes(u: int, t: int, quant: str = "fp4") -> int:
     return u * expert_bytes(quant) + 3 * IS * H * 2 + E * H * 4 + 2 * t * H * 2
 
 
+PREFILL_MIN_TOKENS = 64      # batches from this size run the expert products as MFMA GEMM tiles
+
+
 def layer_flops(t: int) -> int:
     return 2 * t * K_TOP * 3 * H * I + 2 * t * 3 * H * IS + 2 * t * H * E
 
 
-def measured_traffic(kernel: str, t: int):
+def measured_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
     measurement (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), or
-    None when no measurement for this kernel at this batch exists."""
+    None when no measurement for this kernel on this workload exists."""
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
         return None
     entry = json.loads(path.read_text()).get(kernel)
-    if not entry or entry.get("workload") != f"full-size FP4 MoE layer decode, B={t}":
+    if not entry or entry.get("workload") != workload:
         return None
     return int(entry["bytes_per_launch"])
 
@@ -256,6 +259,8 @@ def main() -> int:
     ap.add_argument("--inputs", type=int, default=16)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--zipf", type=float, default=None,
+                    help="gate bias = log Zipf(s) popularity (skewed routing, as in the prefill sweep)")
     ap.add_argument("--mode", choices=("layer", "copy"), default="layer")
     ap.add_argument("--bytes", type=int, default=1 << 30)
     args = ap.parse_args()
@@ -273,7 +278,7 @@ def main() -> int:
 
     t_gen = time.perf_counter()
     layers = [gsynth.make_layer(hidden=H, n_experts=E, top_k=K_TOP, inter=I, inter_shared=IS,
-                                seed=1000 + i, device="cuda:0") for i in range(args.layers)]
+                                seed=1000 + i, device="cuda:0", zipf_s=args.zipf) for i in range(args.layers)]
     torch.cuda.synchronize()
     print(f"# generated {args.layers} resident layers in {time.perf_counter() - t_gen:.1f} s", file=sys.stderr, flush=True)
 
@@ -287,6 +292,30 @@ def main() -> int:
     up_ms = np.maximum(st[:, 2] - marker_ms, 1e-6)
     up_bytes = np.array([up_kernel_bytes(int(x), T) for x in u])
     achieved = float(up_bytes.sum() / (up_ms.sum() * 1e-3))
+    prefill = T >= PREFILL_MIN_TOKENS
+    workload = (f"full-size FP4 MoE layer {'prefill' if prefill else 'decode'}, B={T}"
+                + (f", Zipf({args.zipf}) gate bias" if args.zipf else ""))
+    if prefill:
+        # gate/up GEMM of the prefill path: routed (T*k rows) and shared (T rows) w1, w3
+        up_flops = 2 * T * K_TOP * 2 * H * I + 2 * T * 2 * H * IS
+        achieved_f = up_flops / (float(up_ms.mean()) * 1e-3)
+        roofline = {"bound": "mfma", "achieved": round(achieved_f / 1e12, 1), "peak": PEAK_BF16 / 1e12,
+                    "unit": "TFLOP/s", "frac": round(achieved_f / PEAK_BF16, 4),
+                    "traffic": measured_traffic("k_pf_up", workload),
+                    "kernel": "k_pf_up (routed FP4 + shared bf16 w1/w3 GEMM tiles, SwiGLU epilogue)",
+                    "flops_per_launch": int(up_flops),
+                    "avg_launch_us": round(float(up_ms.mean()) * 1e3, 2),
+                    "timing": "HIP events around one launch per step, minus the GPU time of an "
+                              "empty event pair"}
+    else:
+        roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
+                    "traffic": measured_traffic("k_up_stream", workload),
+                    "kernel": "k_up_stream (routed FP4 w1/w3 + shared bf16 w1/w3, SwiGLU epilogue)",
+                    "bytes_per_launch": int(up_bytes.mean()),
+                    "avg_launch_us": round(float(up_ms.mean()) * 1e3, 2),
+                    "timing": "HIP events around one launch per step (cold weights), minus the "
+                              "GPU time of an empty event pair"}
     layer_b = np.array([layer_bytes(int(x), T) for x in u])
     stage_names = ["route", "dispatch", "gate_up", "down", "combine"]
     line = {
@@ -294,19 +323,12 @@ def main() -> int:
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"full-size FP4 MoE layer decode, B={T}", "hidden": H,
+        "config": {"workload": workload, "hidden": H,
                    "n_experts": E, "top_k": K_TOP, "inter": I, "shared_inter": IS,
                    "routed_format": "fp4-e2m1/e8m0-g32", "shared_format": "bf16",
                    "gate": "sigmoid, route_scale 2.5", "tokens": T,
                    "layers_rotated": args.layers, "inputs_rotated": args.inputs},
-        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
-                     "traffic": measured_traffic("k_up_stream", T),
-                     "kernel": "k_up_stream (routed FP4 w1/w3 + shared bf16 w1/w3, SwiGLU epilogue)",
-                     "bytes_per_launch": int(up_bytes.mean()),
-                     "avg_launch_us": round(float(up_ms.mean()) * 1e3, 2),
-                     "timing": "HIP events around one launch per step (cold weights), minus the "
-                               "GPU time of an empty event pair"},
+        "roofline": roofline,
         "stage_us": {n: round(max(float(st[:, i].mean()) - marker_ms, 0.0) * 1e3, 2)
                      for i, n in enumerate(stage_names)},
         "event_marker_us": round(marker_ms * 1e3, 2),
