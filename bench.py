@@ -96,10 +96,11 @@ def expert_bytes(quant: str = "fp4") -> int:
     return 2 * fp4_role_bytes(I, H) + fp4_role_bytes(H, I)      # 13,369,344 at the full shape
 
 
-def up_kernel_bytes(u: int, t: int) -> int:
+def up_kernel_bytes(u: int, t: int, quant: str = "fp4") -> int:
     """Algorithmic HBM bytes of one gate/up launch: routed w1+w3 of the u active
     experts, shared w1+w3 (bf16), x, and the h / hs planes written."""
-    return (u * 2 * fp4_role_bytes(I, H) + 2 * IS * H * 2 + t * H * 2
+    role = q3_role_bytes(I, H) if quant == "q3" else fp4_role_bytes(I, H)
+    return (u * 2 * role + 2 * IS * H * 2 + t * H * 2
             + t * K_TOP * I * 4 + t * IS * 4)
 
 
@@ -259,6 +260,7 @@ def main() -> int:
     ap.add_argument("--inputs", type=int, default=16)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quant", choices=("fp4", "q3"), default="fp4", help="routed expert format")
     ap.add_argument("--zipf", type=float, default=None,
                     help="gate bias = log Zipf(s) popularity (skewed routing, as in the prefill sweep)")
     ap.add_argument("--mode", choices=("layer", "copy"), default="layer")
@@ -278,7 +280,8 @@ def main() -> int:
 
     t_gen = time.perf_counter()
     layers = [gsynth.make_layer(hidden=H, n_experts=E, top_k=K_TOP, inter=I, inter_shared=IS,
-                                seed=1000 + i, device="cuda:0", zipf_s=args.zipf) for i in range(args.layers)]
+                                quant=args.quant, seed=1000 + i, device="cuda:0", zipf_s=args.zipf)
+              for i in range(args.layers)]
     torch.cuda.synchronize()
     print(f"# generated {args.layers} resident layers in {time.perf_counter() - t_gen:.1f} s", file=sys.stderr, flush=True)
 
@@ -290,10 +293,10 @@ def main() -> int:
     marker_ms = float(np.median(r["marker_ms"]))
     u = np.array(r["unique"])
     up_ms = np.maximum(st[:, 2] - marker_ms, 1e-6)
-    up_bytes = np.array([up_kernel_bytes(int(x), T) for x in u])
+    up_bytes = np.array([up_kernel_bytes(int(x), T, args.quant) for x in u])
     achieved = float(up_bytes.sum() / (up_ms.sum() * 1e-3))
     prefill = T >= PREFILL_MIN_TOKENS
-    workload = (f"full-size FP4 MoE layer {'prefill' if prefill else 'decode'}, B={T}"
+    workload = (f"full-size {args.quant.upper()} MoE layer {'prefill' if prefill else 'decode'}, B={T}"
                 + (f", Zipf({args.zipf}) gate bias" if args.zipf else ""))
     if prefill:
         # gate/up GEMM of the prefill path: routed (T*k rows) and shared (T rows) w1, w3
@@ -302,7 +305,7 @@ def main() -> int:
         roofline = {"bound": "mfma", "achieved": round(achieved_f / 1e12, 1), "peak": PEAK_BF16 / 1e12,
                     "unit": "TFLOP/s", "frac": round(achieved_f / PEAK_BF16, 4),
                     "traffic": measured_traffic("k_pf_up", workload),
-                    "kernel": "k_pf_up (routed FP4 + shared bf16 w1/w3 GEMM tiles, SwiGLU epilogue)",
+                    "kernel": f"k_pf_up (routed {args.quant.upper()} + shared bf16 w1/w3 GEMM tiles, SwiGLU epilogue)",
                     "flops_per_launch": int(up_flops),
                     "avg_launch_us": round(float(up_ms.mean()) * 1e3, 2),
                     "timing": "HIP events around one launch per step, minus the GPU time of an "
@@ -311,12 +314,12 @@ def main() -> int:
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
                     "traffic": measured_traffic("k_up_stream", workload),
-                    "kernel": "k_up_stream (routed FP4 w1/w3 + shared bf16 w1/w3, SwiGLU epilogue)",
+                    "kernel": f"k_up_stream (routed {args.quant.upper()} w1/w3 + shared bf16 w1/w3, SwiGLU epilogue)",
                     "bytes_per_launch": int(up_bytes.mean()),
                     "avg_launch_us": round(float(up_ms.mean()) * 1e3, 2),
                     "timing": "HIP events around one launch per step (cold weights), minus the "
                               "GPU time of an empty event pair"}
-    layer_b = np.array([layer_bytes(int(x), T) for x in u])
+    layer_b = np.array([layer_bytes(int(x), T, args.quant) for x in u])
     stage_names = ["route", "dispatch", "gate_up", "down", "combine"]
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1,
@@ -325,7 +328,8 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": workload, "hidden": H,
                    "n_experts": E, "top_k": K_TOP, "inter": I, "shared_inter": IS,
-                   "routed_format": "fp4-e2m1/e8m0-g32", "shared_format": "bf16",
+                   "routed_format": ("q3-affine-g64 (fp16 scale/bias)" if args.quant == "q3"
+                                     else "fp4-e2m1/e8m0-g32"), "shared_format": "bf16",
                    "gate": "sigmoid, route_scale 2.5", "tokens": T,
                    "layers_rotated": args.layers, "inputs_rotated": args.inputs},
         "roofline": roofline,

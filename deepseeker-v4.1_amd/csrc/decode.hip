@@ -283,19 +283,58 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
   float wr = 0.0f;
   if constexpr (kQ3) {
-    // weights: two batches of G K blocks in flight (q3 codes, scale and bias per lane)
+    // weights: two batches of G K blocks in flight (q3 codes, scale and bias
+    // per lane).  kWin: each batch's 2G (scale, bias) groups of a row come as
+    // one 16-byte window per role, and every lane picks its group's pair from
+    // it (the batch lies inside the row, see the launcher).
     RawQ3 a1[G], a3[G], b1[G], b3[G];
-    auto ld = [&](RawQ3 (&r1)[G], RawQ3 (&r3)[G], int kb) {
+    u32x4 aw[4], bw[4];   // windows: scales w1, biases w1, scales w3, biases w3
+    auto ld = [&](RawQ3 (&r1)[G], RawQ3 (&r3)[G], u32x4 (&win)[4], int kb) {
+      if constexpr (kWin) {
+        const uint8_t* W1 = static_cast<const uint8_t*>(d->p[0]);
+        const uint8_t* W3 = static_cast<const uint8_t*>(d->p[3]);
+        const int64_t code_row = static_cast<int64_t>(row) * (K / 8 * 3);
 #pragma unroll
-      for (int i = 0; i < G; ++i) {
-        const int kc = (kb + i) * 128 + g4 * 32;
-        const bool ok = rok && kb + i < k1 && kc < K;
-        load_role(r1[i], d->p, 0, row, K, kc, ok);
-        load_role(r3[i], d->p, 1, row, K, kc, ok);
+        for (int i = 0; i < G; ++i) {
+          const bool ok = rok && kb + i < k1;
+          const int64_t off = code_row + (kb + i) * 48 + g4 * 12;
+          const auto c1 = gptr<uint32_t>(W1 + off);
+          const auto c3 = gptr<uint32_t>(W3 + off);
+#pragma unroll
+          for (int q = 0; q < 3; ++q) {
+            r1[i].w[q] = ok ? c1[q] : 0u;
+            r3[i].w[q] = ok ? c3[q] : 0u;
+          }
+        }
+        const bool ok = rok && kb < k1;
+        const int64_t wo = (static_cast<int64_t>(row) * (K / 64) + 2 * kb) * 2;   // bytes
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          win[q] = ok ? ldg16(static_cast<const uint8_t*>(d->p[(q >> 1) * 3 + 1 + (q & 1)]) + wo)
+                      : u32x4{0u, 0u, 0u, 0u};
+      } else {
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+          const int kc = (kb + i) * 128 + g4 * 32;
+          const bool ok = rok && kb + i < k1 && kc < K;
+          load_role(r1[i], d->p, 0, row, K, kc, ok);
+          load_role(r3[i], d->p, 1, row, K, kc, ok);
+        }
       }
     };
-    ld(a1, a3, k0);
-    ld(b1, b3, k0 + G);
+    // (scale, bias) of K block i of a windowed batch: group 2i + (g4 >> 1)
+    auto win_sb = [&](RawQ3 (&r1)[G], RawQ3 (&r3)[G], const u32x4 (&win)[4]) {
+      if constexpr (kWin) {
+        const int sh = 16 * (g4 >> 1);
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+          r1[i].sb = ((win[0][i] >> sh) & 0xffffu) | (((win[1][i] >> sh) & 0xffffu) << 16);
+          r3[i].sb = ((win[2][i] >> sh) & 0xffffu) | (((win[3][i] >> sh) & 0xffffu) << 16);
+        }
+      }
+    };
+    ld(a1, a3, aw, k0);
+    ld(b1, b3, bw, k0 + G);
     if (xreg) {
 #pragma unroll
       for (int j = 0; j < kUpXRegChunks; ++j) {
@@ -307,7 +346,8 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
     __syncthreads();
     const uint16_t* bh = xh + (tv ? r16 : 0) * xs;
     const uint16_t* bl = xl + (tv ? r16 : 0) * xs;
-    auto mm = [&](const RawQ3 (&r1)[G], const RawQ3 (&r3)[G], int kb) {
+    auto mm = [&](RawQ3 (&r1)[G], RawQ3 (&r3)[G], const u32x4 (&win)[4], int kb) {
+      win_sb(r1, r3, win);
 #pragma unroll
       for (int i = 0; i < G; ++i) {
         const int kc = (kb + i) * 128 + g4 * 32;
@@ -317,10 +357,10 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
       }
     };
     for (int kb = k0; kb < k1; kb += 2 * G) {
-      mm(a1, a3, kb);
-      if (kb + 2 * G < k1) ld(a1, a3, kb + 2 * G);
-      if (kb + G < k1) mm(b1, b3, kb + G);
-      if (kb + 3 * G < k1) ld(b1, b3, kb + 3 * G);
+      mm(a1, a3, aw, kb);
+      if (kb + 2 * G < k1) ld(a1, a3, aw, kb + 2 * G);
+      if (kb + G < k1) mm(b1, b3, bw, kb + G);
+      if (kb + 3 * G < k1) ld(b1, b3, bw, kb + 3 * G);
     }
   } else {
     // weights: two batches in flight
@@ -672,8 +712,13 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   // scale windows need 4-byte aligned scale rows (H a multiple of 128)
   const bool win = d.hidden % 128 == 0;
   const bool q3 = d.quant == DSK_QUANT_Q3;
+  // q3 (scale, bias) windows: every wave's K range a whole number of G-block
+  // batches inside the row (so also 16-byte aligned windows)
+  const bool q3win = d.hidden % (kUpKS * kUpBatch * 128) == 0;
   for (int r = 0; r < repeat; ++r) {
-    if (q3 && !p.x_f32) k_up_stream<kUpBatch, false, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    if (q3 && q3win && !p.x_f32) k_up_stream<kUpBatch, true, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    else if (q3 && q3win) k_up_stream<kUpBatch, true, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+    else if (q3 && !p.x_f32) k_up_stream<kUpBatch, false, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
     else if (q3) k_up_stream<kUpBatch, false, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
     else if (win && !p.x_f32) k_up_stream<kUpBatch, true, false, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
     else if (win) k_up_stream<kUpBatch, true, true, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);

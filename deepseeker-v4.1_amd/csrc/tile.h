@@ -89,43 +89,79 @@ __device__ __forceinline__ void load_raw(RawQ3& r, const uint8_t* W, const uint1
   }
 }
 
-// Codes (lo, hi) of pair p of a lane's words.
-template <int P>
-__device__ __forceinline__ void q3_pair(const RawQ3& r, uint32_t& lo, uint32_t& hi) {
-  if constexpr (P < 15) {
-    const uint32_t t = r.w[P / 5] >> (3 * (P % 5));
-    lo = t & 7u;
-    hi = (t >> 16) & 7u;
-  } else {
-    lo = ((r.w[0] >> 15) & 1u) | ((r.w[1] >> 14) & 2u) | ((r.w[2] >> 13) & 4u);
-    hi = ((r.w[0] >> 31) & 1u) | ((r.w[1] >> 30) & 2u) | ((r.w[2] >> 29) & 4u);
+// Dequantised values of the code pair at bits [sh, sh+3) / [16+sh, 16+sh+3)
+// of word w: one mask, then each code is converted from the byte that holds
+// it (v_cvt_f32_ubyteN), which yields q * 2^k for a position-dependent k; the
+// matching s * 2^-k (exact: an fp16 scale has 11 significant bits) makes
+// fma(s * 2^-k, q * 2^k, b) = round(s*q + b) -- s*q is exact in float32, so
+// this is f32(s)*q + f32(b) with the format's rounding.
+struct Q3Scales { float s, s2, s8, s16, b; };   // s, s/2, s/8, s/16, bias
+
+__device__ __forceinline__ Q3Scales q3_scales(uint32_t sb) {
+  const float s = f16_bits_to_f32(static_cast<uint16_t>(sb & 0xffffu));
+  return Q3Scales{s, s * 0.5f, s * 0.125f, s * 0.0625f, f16_bits_to_f32(static_cast<uint16_t>(sb >> 16))};
+}
+
+// Byte k of v as float (v_cvt_f32_ubyteK: no shift or mask needed).
+template <int K>
+__device__ __forceinline__ float ubyte_f32(uint32_t v) {
+  float f;
+  if constexpr (K == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(v));
+  else if constexpr (K == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(v));
+  else if constexpr (K == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(v));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(v));
+  return f;
+}
+
+template <int SH>
+__device__ __forceinline__ void q3_pair_f(uint32_t w, const Q3Scales& c, float& lo, float& hi) {
+  const uint32_t m = w & ((7u << SH) | (7u << (16 + SH)));
+  if constexpr (SH == 0) {          // bytes 0 / 2 hold q
+    lo = __fmaf_rn(c.s, ubyte_f32<0>(m), c.b);
+    hi = __fmaf_rn(c.s, ubyte_f32<2>(m), c.b);
+  } else if constexpr (SH == 3) {   // bytes 0 / 2 hold 8q
+    lo = __fmaf_rn(c.s8, ubyte_f32<0>(m), c.b);
+    hi = __fmaf_rn(c.s8, ubyte_f32<2>(m), c.b);
+  } else if constexpr (SH == 6) {   // straddles a byte boundary: shift first
+    const uint32_t n = m >> 6;
+    lo = __fmaf_rn(c.s, ubyte_f32<0>(n), c.b);
+    hi = __fmaf_rn(c.s, ubyte_f32<2>(n), c.b);
+  } else if constexpr (SH == 9) {   // bytes 1 / 3 hold 2q
+    lo = __fmaf_rn(c.s2, ubyte_f32<1>(m), c.b);
+    hi = __fmaf_rn(c.s2, ubyte_f32<3>(m), c.b);
+  } else {                          // SH == 12: bytes 1 / 3 hold 16q
+    lo = __fmaf_rn(c.s16, ubyte_f32<1>(m), c.b);
+    hi = __fmaf_rn(c.s16, ubyte_f32<3>(m), c.b);
   }
 }
 
-// MFMA j's 8 dequantised weights: f32(s) * q + f32(b) (two roundings, as the
-// format defines), rounded to bf16.
+// Pair P of a lane's 32 codes (P < 15: word P/5, shift 3(P%5); P = 15: bits
+// 15 / 31 of the three words, gathered into bits 0-2 / 16-18).
+template <int P>
+__device__ __forceinline__ void q3_pair_val(const RawQ3& r, const Q3Scales& c, float& lo, float& hi) {
+  if constexpr (P < 15) {
+    q3_pair_f<3 * (P % 5)>(r.w[P / 5], c, lo, hi);
+  } else {
+    const uint32_t t = ((r.w[0] >> 15) & 0x00010001u) | ((r.w[1] >> 14) & 0x00020002u) |
+                       ((r.w[2] >> 13) & 0x00040004u);
+    q3_pair_f<0>(t, c, lo, hi);
+  }
+}
+
+// MFMA j's 8 dequantised weights: f32(s) * q + f32(b) (the format's two
+// roundings; s*q is exact), rounded to bf16.
 template <int J>
 __device__ __forceinline__ bf16x8 q3_operand(const RawQ3& r) {
-  const float s = f16_bits_to_f32(static_cast<uint16_t>(r.sb & 0xffffu));
-  const float b = f16_bits_to_f32(static_cast<uint16_t>(r.sb >> 16));
-  bf16x8 v;
+  const Q3Scales c = q3_scales(r.sb);
+  float v[8];
+  q3_pair_val<4 * J + 0>(r, c, v[0], v[1]);
+  q3_pair_val<4 * J + 1>(r, c, v[2], v[3]);
+  q3_pair_val<4 * J + 2>(r, c, v[4], v[5]);
+  q3_pair_val<4 * J + 3>(r, c, v[6], v[7]);
+  bf16x8 o;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t lo, hi;
-    switch (4 * J + i) {
-      case 0: q3_pair<0>(r, lo, hi); break;   case 1: q3_pair<1>(r, lo, hi); break;
-      case 2: q3_pair<2>(r, lo, hi); break;   case 3: q3_pair<3>(r, lo, hi); break;
-      case 4: q3_pair<4>(r, lo, hi); break;   case 5: q3_pair<5>(r, lo, hi); break;
-      case 6: q3_pair<6>(r, lo, hi); break;   case 7: q3_pair<7>(r, lo, hi); break;
-      case 8: q3_pair<8>(r, lo, hi); break;   case 9: q3_pair<9>(r, lo, hi); break;
-      case 10: q3_pair<10>(r, lo, hi); break; case 11: q3_pair<11>(r, lo, hi); break;
-      case 12: q3_pair<12>(r, lo, hi); break; case 13: q3_pair<13>(r, lo, hi); break;
-      case 14: q3_pair<14>(r, lo, hi); break; default: q3_pair<15>(r, lo, hi); break;
-    }
-    v[2 * i] = static_cast<__bf16>(__fadd_rn(__fmul_rn(s, static_cast<float>(lo)), b));
-    v[2 * i + 1] = static_cast<__bf16>(__fadd_rn(__fmul_rn(s, static_cast<float>(hi)), b));
-  }
-  return v;
+  for (int i = 0; i < 8; ++i) o[i] = static_cast<__bf16>(v[i]);
+  return o;
 }
 
 __device__ __forceinline__ bf16x8 a_operand(const RawQ3& r, int j) {
