@@ -321,4 +321,23 @@ int dsk_q3_dequant(const uint8_t* packed, const uint16_t* scales, const uint16_t
                    "dsk_q3_dequant launch");
 }
 
+int dsk_rmsnorm(const void* x, const void* residual, const float* gamma, int64_t rows, int32_t hidden,
+                float eps, int32_t dtype, void* h_out, void* out, void* stream) {
+  if (!x) return fail(DSK_EINVAL, "dsk_rmsnorm: x is NULL");
+  if (!out && !(residual && h_out))
+    return fail(DSK_EINVAL, "dsk_rmsnorm: nothing to write (out is NULL and no residual update)");
+  if (rows < 0 || hidden < 4 || hidden % 4)
+    return fail(DSK_EINVAL, "dsk_rmsnorm: rows=%lld, hidden=%d must be >= 0 and a positive multiple of 4",
+                (long long)rows, hidden);
+  if (dtype != DSK_DTYPE_F32 && dtype != DSK_DTYPE_BF16)
+    return fail(DSK_EINVAL, "dsk_rmsnorm: dtype %d must be F32 or BF16", dtype);
+  if (!(eps >= 0.0f)) return fail(DSK_EINVAL, "dsk_rmsnorm: eps must be >= 0");
+  if (!aligned(x, 16) || (residual && !aligned(residual, 16)) || (gamma && !aligned(gamma, 16)) ||
+      (h_out && !aligned(h_out, 16)) || (out && !aligned(out, 16)))
+    return fail(DSK_EALIGN, "dsk_rmsnorm: pointers must be 16-byte aligned");
+  return hip_check(launch_rmsnorm(x, residual, gamma, rows, hidden, eps, dtype, h_out, out,
+                                  static_cast<hipStream_t>(stream)),
+                   "dsk_rmsnorm launch");
+}
+
 }  // extern "C"

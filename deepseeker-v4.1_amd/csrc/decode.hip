@@ -30,6 +30,7 @@ constexpr int kStKB = 2;               // K blocks of each expert per wave (I = 
 constexpr int kStSlots = 2;            // experts per routed batch
 constexpr int kStMaxSlots = 16;        // active experts the staged kernel handles
 constexpr int kStRing = 4;             // routed batches in flight per wave
+constexpr int kStRedBytes = 2 * kStW * 64 * 4 * 4;   // wave partial sums, routed and shared
 constexpr int kStStage = 5;            // activation chunks per thread in flight while staging
 
 struct DecodeArgs {
@@ -523,8 +524,11 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
   uint16_t* hl = hh + N * is;
   uint16_t* sh_h = hl + N * is;
   uint16_t* sh_l = sh_h + p.T * iss;
-  float (*red)[kStW][64][4] = reinterpret_cast<float (*)[kStW][64][4]>(sh_l + p.T * iss);
-  int* ldrow = reinterpret_cast<int*>(red + 2);            // [U][T] dispatch rows (rowmap copy)
+  // the wave partial sums reuse the activation area once every wave is done with it
+  float (*red)[kStW][64][4] = reinterpret_cast<float (*)[kStW][64][4]>(lds_dn);
+  const int act_bytes = (N * is + p.T * iss) * 4;
+  int* ldrow = reinterpret_cast<int*>(reinterpret_cast<char*>(lds_dn) +   // [U][T] dispatch rows (rowmap copy)
+                                      (act_bytes > kStRedBytes ? act_bytes : kStRedBytes));
   const int kb0 = wave * kStKB;
   // 1. activations and dispatch rows, alone in flight (a short wait), into LDS
   const int hch = N * (I / 8), sch = p.T * (Is / 8);
@@ -600,6 +604,7 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
       }
     }
   }
+  __syncthreads();
   *reinterpret_cast<f32x4*>(&red[0][wave][lane][0]) = ((acc[0] + acc[1]) + acc[2]) + acc[3];
   *reinterpret_cast<f32x4*>(&red[1][wave][lane][0]) = ((accs[0] + accs[1]) + accs[2]) + accs[3];
   __syncthreads();
@@ -729,9 +734,9 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
   const int n_rows = d.tokens * d.top_k;
   const int max_u = d.n_experts < n_rows ? d.n_experts : n_rows;
-  const size_t dn_lds = static_cast<size_t>(n_rows) * (d.inter + 8) * 4 +
-                        static_cast<size_t>(d.tokens) * (d.inter_shared + 8) * 4 +
-                        2 * kStW * 64 * 4 * sizeof(float) + static_cast<size_t>(max_u) * d.tokens * 4;
+  const size_t act = static_cast<size_t>(n_rows) * (d.inter + 8) * 4 +
+                     static_cast<size_t>(d.tokens) * (d.inter_shared + 8) * 4;
+  const size_t dn_lds = (act > kStRedBytes ? act : kStRedBytes) + static_cast<size_t>(max_u) * d.tokens * 4;
   // staged: all activations fit in LDS, each wave's K blocks cover I (and
   // Is), few enough experts, and at most 8 tokens (two B columns each)
   const bool staged = dn_lds <= kMaxLds && max_u <= kStMaxSlots && d.tokens <= 8 &&

@@ -164,6 +164,8 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L,
                           const ExpertsArgs& a, hipStream_t s, const hipEvent_t* ev, int repeat);
 
 hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t s);
+hipError_t launch_rmsnorm(const void* x, const void* res, const float* gamma, int64_t rows, int H, float eps,
+                          int dtype, void* h_out, void* y, hipStream_t s);
 
 // Prefill GEMM path (prefill_gemm(d)): tile list, gate/up, down; the caller
 // runs the combine.  ev (nullable): 2 events, after gate/up and after down.

@@ -186,6 +186,18 @@ int dsk_q3_dequant(const uint8_t* packed, const uint16_t* scales,
                    const uint16_t* biases, int64_t rows, int64_t cols, void* out,
                    int32_t out_dtype, void* stream);
 
+/* RMSNorm on a residual stream: replaces rmsnorm (src/deepseeker/mlx_forward.py:45-59)
+ * together with the residual add that precedes it in a stack of layers.
+ * h = x (+ residual, rounded to dtype); h is written to h_out when given (h_out
+ * may be x itself); out = h * (1 / sqrt(mean(h^2) + eps)) * gamma, in float32
+ * with one rounding to dtype.  rows rows of `hidden` elements (dtype F32 or
+ * BF16); gamma [hidden] f32 or NULL (all ones); out may be NULL when only the
+ * residual update is wanted.  The sum of squares has one defined order (per
+ * thread over chunks t, t+256, ... of 4 elements, an XOR tree over each wave,
+ * the 4 waves in order), restated by the oracle.  16-byte aligned pointers. */
+int dsk_rmsnorm(const void* x, const void* residual, const float* gamma, int64_t rows,
+                int32_t hidden, float eps, int32_t dtype, void* h_out, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
