@@ -185,6 +185,63 @@ def run_workload(layers, t: int, steps: int, warmup: int, n_inputs: int, seed: i
     return {"wall_s": wall, "stage_ms": st, "marker_ms": marker, "unique": uniq}
 
 
+# ------------------------------------------------------------------ layer stack
+def run_stack(n_layers: int, batches, steps: int, warmup: int = 3, n_inputs: int = 8) -> dict:
+    """The resident stack: layers [0, n/2) FP4, [n/2, n) q3, each of the full
+    layer shape, on an RMSNorm residual stream (eps 1e-6, unit gamma), run as
+    one captured HIP graph per batch size.  A step copies the next input into
+    the graph's static buffer and replays the whole stack."""
+    from dsk_moe.stack import MoEStack
+
+    layers = [gsynth.make_layer(hidden=H, n_experts=E, top_k=K_TOP, inter=I, inter_shared=IS,
+                                quant="fp4" if l < n_layers // 2 else "q3", seed=4000 + l, device="cuda:0")
+              for l in range(n_layers)]
+    stack = MoEStack(layers, eps=1e-6)
+    resident = sum(t.numel() * t.element_size() for lay in layers
+                   for t in [p for parts in lay.bank.roles.values() for p in parts]
+                   + [lay.shared.w1, lay.shared.w3, lay.shared.w2, lay.gate_w])
+    out = {}
+    for b in batches:
+        g = torch.Generator(device="cuda:0").manual_seed(31 + b)
+        xs = [torch.randn((b, H), generator=g, device="cuda:0").to(torch.bfloat16) for _ in range(n_inputs)]
+        rec = []
+        stack(xs[0], record=rec)
+        quants = ["fp4" if l < n_layers // 2 else "q3" for l in range(n_layers)]
+        step_bytes = sum(layer_bytes(len(torch.unique(r[2]).tolist()), b, q) for r, q in zip(rec, quants))
+        del rec
+        stack.capture(b)
+        for i in range(warmup):
+            stack.replay(xs[i % n_inputs])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            stack.replay(xs[i % n_inputs])
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        # the same steps launched eagerly (per-kernel launches from the host)
+        bufs = stack._buffers(xs[0])
+        eo = torch.empty_like(xs[0])
+        for i in range(warmup):
+            stack(xs[i % n_inputs], out=eo, bufs=bufs)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for i in range(steps):
+            stack(xs[i % n_inputs], out=eo, bufs=bufs)
+        torch.cuda.synchronize()
+        wall_e = time.perf_counter() - t1
+        out[f"stack{n_layers}_B{b}"] = {
+            "tokens_per_s": round(b * steps / wall, 1), "ms_per_step": round(wall / steps * 1e3, 4),
+            "us_per_layer": round(wall / steps / n_layers * 1e6, 2),
+            "eager_ms_per_step": round(wall_e / steps * 1e3, 4),
+            "hbm_frac_wall": round(step_bytes / (wall / steps) / PEAK_HBM, 4),
+            "resident_GB": round(resident / 1e9, 1),
+            "layers": f"{n_layers // 2} FP4 + {n_layers - n_layers // 2} q3, RMSNorm residual, HIP graph replay"}
+        print(f"# stack{n_layers} B={b}: {out[f'stack{n_layers}_B{b}']}", file=sys.stderr, flush=True)
+    del stack, layers
+    torch.cuda.empty_cache()
+    return out
+
+
 # ------------------------------------------------------------------ CPU baseline
 def cpu_baseline(layer, n_tokens: int = 3):
     """The oracle (torch fp32 + numpy, the reference's algorithm restated) on
@@ -371,6 +428,7 @@ def main() -> int:
                                   "unique_experts_mean": float(us.mean()),
                                   "layer_hbm_frac": round(float(lb.mean() / (rs["wall_s"] / n_steps)) / PEAK_HBM, 4)}
         del q3_layers
+        sweep.update(run_stack(40, (1, 2), steps=30))
         line["sweep"] = sweep
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(layers[0])
