@@ -97,11 +97,11 @@ def expert_bytes(quant: str = "fp4") -> int:
 
 
 def up_kernel_bytes(u: int, t: int, quant: str = "fp4") -> int:
-    """Algorithmic HBM bytes of one gate/up launch: routed w1+w3 of the u active
-    experts, shared w1+w3 (bf16), x, and the h / hs planes written."""
+    """Algorithmic HBM bytes of one routed gate/up launch (the decode path's
+    k_up_stream): routed w1+w3 of the u active experts, x, and the h planes
+    written (bf16 hi and lo)."""
     role = q3_role_bytes(I, H) if quant == "q3" else fp4_role_bytes(I, H)
-    return (u * 2 * role + 2 * IS * H * 2 + t * H * 2
-            + t * K_TOP * I * 4 + t * IS * 4)
+    return u * 2 * role + t * H * 2 + t * K_TOP * I * 4
 
 
 def layer_bytes(u: int, t: int, quant: str = "fp4") -> int:
@@ -371,7 +371,7 @@ def main() -> int:
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
                     "traffic": measured_traffic("k_up_stream", workload),
-                    "kernel": f"k_up_stream (routed {args.quant.upper()} w1/w3 + shared bf16 w1/w3, SwiGLU epilogue)",
+                    "kernel": f"k_up_stream (routed {args.quant.upper()} w1/w3, SwiGLU and route weight epilogue)",
                     "bytes_per_launch": int(up_bytes.mean()),
                     "avg_launch_us": round(float(up_ms.mean()) * 1e3, 2),
                     "timing": "HIP events around one launch per step (cold weights), minus the "

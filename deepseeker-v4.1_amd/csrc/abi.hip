@@ -225,33 +225,34 @@ static int forward_impl(const dsk_moe_desc* d, const void* x, const void* gate_w
                        reinterpret_cast<int32_t*>(ws + L.xrow),
                        reinterpret_cast<float*>(ws + L.wrow)};
   ra.ctr = reinterpret_cast<unsigned int*>(ws + L.ctr);
-  const bool decode = decode_pipeline(*d);
-  if (ev && (rc = hip_check(hipEventRecord(ev[0], s), "event record"))) return rc;
-  if (decode) {
-    // gate kernel, then top-k + one-wave dispatch in one block
-    ra.rowmap = reinterpret_cast<int32_t*>(ws + L.rowmap);
-    for (int r = 0; r < repeat && !rc; ++r) rc = hip_check(launch_gate_scores(*d, ra, s), "gate launch");
-    if (rc) return rc;
-    if (ev && (rc = hip_check(hipEventRecord(ev[1], s), "event record"))) return rc;
-    for (int r = 0; r < repeat && !rc; ++r) rc = hip_check(launch_route_tail(*d, ra, s), "route tail launch");
-    if (rc) return rc;
-  } else {
-    for (int r = 0; r < repeat && !rc; ++r)
-      rc = hip_check(launch_route_dispatch(*d, ra, s), "route launch");
-    if (rc) return rc;
-    // the fused router also dispatches: both stage events mark its end
-    if (ev && (rc = hip_check(hipEventRecord(ev[1], s), "event record"))) return rc;
-  }
-  if (ev && (rc = hip_check(hipEventRecord(ev[2], s), "event record"))) return rc;
+  ra.rowmap = reinterpret_cast<int32_t*>(ws + L.rowmap);
   ExpertsArgs a{};
   a.table = table; a.desc = ra.out.desc; a.xrow = ra.out.xrow; a.wrow = ra.out.wrow;
   a.ws1 = ws1; a.ws3 = ws3; a.ws2 = ws2; a.shared_out = shared_out; a.x = x;
   a.weights = w_buf; a.counts = counts; a.offsets = offsets; a.perm = perm; a.rank = rank;
   a.active = active; a.out = out; a.ws = ws;
   a.rowmap = ra.rowmap;
-  if (decode)
+  a.scores = scores; a.bias = gate_b;
+  a.route = DecodeRoute{idx_buf, w_buf, ra.out.desc, active, ra.rowmap, ra.out.wrow};
+  const bool decode = decode_pipeline(*d);
+  if (ev && (rc = hip_check(hipEventRecord(ev[0], s), "event record"))) return rc;
+  if (decode) {
+    // gate scores; then the top-k and the slot map beside the shared expert's gate/up
+    for (int r = 0; r < repeat && !rc; ++r) rc = hip_check(launch_gate_scores(*d, ra, s), "gate launch");
+    if (rc) return rc;
+    if (ev && (rc = hip_check(hipEventRecord(ev[1], s), "event record"))) return rc;
+    rc = hip_check(launch_route_shared(*d, L, a, s, repeat), "route / shared gate-up launch");
+    if (rc) return rc;
+    if (ev && (rc = hip_check(hipEventRecord(ev[2], s), "event record"))) return rc;
     return hip_check(launch_experts_decode(*d, L, a, s, ev ? ev + 3 : nullptr, repeat),
                      "decode experts launch");
+  }
+  for (int r = 0; r < repeat && !rc; ++r)
+    rc = hip_check(launch_route_dispatch(*d, ra, s), "route launch");
+  if (rc) return rc;
+  // the fused router also dispatches: both stage events mark its end
+  if (ev && (rc = hip_check(hipEventRecord(ev[1], s), "event record"))) return rc;
+  if (ev && (rc = hip_check(hipEventRecord(ev[2], s), "event record"))) return rc;
   return hip_check(launch_experts(*d, L, a, s, ev ? ev + 3 : nullptr, repeat), "experts launch");
 }
 

@@ -1,16 +1,18 @@
 // Decode pipeline of the expert products (up to 16 tokens and 64 routed
-// positions): after the fused router (which also ran the shared expert's
-// gate/up partial products),
-//   k_up_stream    routed gate/up tiles of the active experts (FP4) -> h, and
-//                  the shared expert's SwiGLU from its partials -> hs;
-//   k_down_decode[_staged]  per 16 output rows: every active expert's w2 rows (FP4) in
-//                  ascending expert id, then the shared expert's w2 rows
-//                  (bf16), and the final add and cast -- no separate combine.
+// positions), after the gate kernel has written the scores:
+//   k_route_shared  block 0: top-k and slot map (descriptors, token ->
+//                   dispatch-row map, row weights); the other blocks: the
+//                   shared expert's gate/up -> hs;
+//   k_up_stream     routed gate/up tiles of the active experts (FP4 or q3) -> h;
+//   k_down_decode[_staged]  per 16 output rows: every active expert's w2 rows in
+//                   ascending expert id, then the shared expert's w2 rows
+//                   (bf16), and the final add and cast -- no separate combine.
 // Token slot of the MFMA tiles = token index (T <= 16), so the products of
 // all experts accumulate into one tile; tokens not routed to an expert get a
 // zero B operand.  Replaces the per-expert loop, the shared expert and the
 // combine of the reference's moe_layer (src/deepseeker/mlx_forward.py:388-419,
 // src/deepseeker/mlx_runner.py:765-783).
+#include "block_route.h"
 #include "tile.h"
 
 namespace dsk {
@@ -37,6 +39,10 @@ struct DecodeArgs {
   int T, H, I, Is, k;
   float limit;
   const SlotDesc* desc; const int32_t* active; const int32_t* rowmap; const float* wrow;
+  // routing block of k_route_shared: gate scores and selection bias in, routing out
+  float* scores; const float* bias; const dsk_expert_ptrs* table;
+  int E; float route_scale;
+  DecodeRoute route;
   const void* x; int x_f32;
   const uint16_t* ws1; const uint16_t* ws3;   // shared w1, w3 [Is][H] bf16
   uint16_t* hs_hi; uint16_t* hs_lo;    // [T][Is]
@@ -45,7 +51,6 @@ struct DecodeArgs {
   const void* shared_out;              // precomputed shared output [T][H] (x dtype) or null
   void* out;                           // [T][H] x dtype
   int up_tiles;                        // I / 16
-  int shared_blocks;                   // leading gate/up blocks that run shared-expert tiles
 };
 
 __device__ __forceinline__ u32x4 pack_bf16x8(const uint16_t* v) {
@@ -144,17 +149,60 @@ __device__ __forceinline__ void mma_batch(const UpBatch<G>& b, const uint16_t* x
   }
 }
 
-// Shared-expert gate/up tile (block = 16 rows of w1 and w3, all K; wave w
-// takes the w-th K range).  Called after the block's x chunks have been
+// The tokens' activations x [T][H] of a gate/up block: into registers xv when
+// they fit (returns true; put_staged_x writes them to the LDS planes later,
+// once the block's weight loads are in flight), else straight into the LDS
+// planes xh / xl (row stride xs).
+template <bool kF32, int NT>
+__device__ __forceinline__ bool load_x(const DecodeArgs& p, uint16_t* xh, uint16_t* xl, int xs, int tid,
+                                       u32x4 (&xv)[kUpXRegChunks][2]) {
+  const int K = p.H, cpr = K / 8, xchunks = p.T * cpr;
+  if (xchunks <= kUpXRegChunks * NT) {
+#pragma unroll
+    for (int j = 0; j < kUpXRegChunks; ++j) {
+      const int c = tid + j * NT;
+      if (c < xchunks) {
+        const int64_t e = static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8;
+        if (!kF32) {
+          xv[j][0] = ldg16(static_cast<const uint16_t*>(p.x) + e);
+        } else {
+          xv[j][0] = ldg16(static_cast<const float*>(p.x) + e);
+          xv[j][1] = ldg16(static_cast<const float*>(p.x) + e + 4);
+        }
+      }
+    }
+    return true;
+  }
+  for (int c = tid; c < xchunks; c += NT) {
+    const int64_t e = static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8;
+    const int off = (c / cpr) * xs + (c % cpr) * 8;
+    if (!kF32) put_x_chunk(xh, xl, off, ldg16(static_cast<const uint16_t*>(p.x) + e), u32x4{}, false);
+    else put_x_chunk(xh, xl, off, ldg16(static_cast<const float*>(p.x) + e),
+                     ldg16(static_cast<const float*>(p.x) + e + 4), true);
+  }
+  return false;
+}
+
+template <bool kF32, int NT>
+__device__ __forceinline__ void put_staged_x(const DecodeArgs& p, uint16_t* xh, uint16_t* xl, int xs, int tid,
+                                             const u32x4 (&xv)[kUpXRegChunks][2]) {
+  const int cpr = p.H / 8, xchunks = p.T * cpr;
+#pragma unroll
+  for (int j = 0; j < kUpXRegChunks; ++j) {
+    const int c = tid + j * NT;
+    if (c < xchunks) put_x_chunk(xh, xl, (c / cpr) * xs + (c % cpr) * 8, xv[j][0], xv[j][1], kF32);
+  }
+}
+
+// Shared-expert gate/up tile rt (block = kUpW waves, 16 rows of w1 and w3,
+// all K; wave w takes the w-th K range, two K blocks in flight).  Called after the block's x chunks have been
 // loaded into registers; writes them to LDS once its own weight loads are in
 // flight.
 template <bool kF32>
-__device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, uint16_t* xh, uint16_t* xl, int xs,
-                                               bool xreg, const u32x4 (&xv)[kUpXRegChunks][2], int cpr,
-                                               int xchunks, uint16_t* lds, int tid, int lane, int wave,
-                                               int r16, int g4) {
+__device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint16_t* xh, uint16_t* xl, int xs,
+                                               bool xreg, const u32x4 (&xv)[kUpXRegChunks][2], uint16_t* lds,
+                                               int tid, int lane, int wave, int r16, int g4) {
   const int T = p.T, K = p.H;
-  const int rt = blockIdx.x;
   const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
   const int nblk = (K + 127) / 128;
   const int per = (nblk + kUpW - 1) / kUpW;
@@ -169,13 +217,7 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, uint16_t* xh
   };
   ld(a1, a3, k0);
   ld(b1, b3, k0 + 1);
-  if (xreg) {
-#pragma unroll
-    for (int j = 0; j < kUpXRegChunks; ++j) {
-      const int c = tid + j * kUpW * 64;
-      if (c < xchunks) put_x_chunk(xh, xl, (c / cpr) * xs + (c % cpr) * 8, xv[j][0], xv[j][1], kF32);
-    }
-  }
+  if (xreg) put_staged_x<kF32, kUpW * 64>(p, xh, xl, xs, tid, xv);
   __syncthreads();
   const uint16_t* bh = xh + (tv ? r16 : 0) * xs;
   const uint16_t* bl = xl + (tv ? r16 : 0) * xs;
@@ -212,15 +254,38 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, uint16_t* xh
   }
 }
 
-// Gate/up of the decode pipeline.  Blocks [0, shared_blocks) each take one
-// 16-row tile of the shared expert (bf16 w1/w3, K split over the block's
-// waves, one K block per batch); hs = SwiGLU(gate, up) as bf16 hi/lo planes.
-// The other blocks take kUpItems row tiles of one active expert, kUpKS waves
-// per tile, each streaming one K range of its FP4 w1/w3 rows in batches of G
-// K blocks; h[drow] = SwiGLU(gate, up) * route weight.  Two batches are in
-// flight per wave; the tokens' activations are loaded before the weights and
-// written to LDS after the weight loads have been issued; K ranges are added
-// in wave order.
+// Routing and the shared expert's gate/up, one kernel: block 0 runs the
+// top-k of every token and the slot map of the routed kernels
+// (block_route); blocks 1 .. Is/16 each take one 16-row tile of the shared
+// expert (bf16 w1/w3, K split over the block's waves); hs = SwiGLU(gate, up)
+// as bf16 hi/lo planes.  The routing block's dependent loads and wave
+// reductions overlap the shared expert's weight stream.
+template <bool kF32>
+__global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 ? 3 : 4))) void k_route_shared(
+    DecodeArgs p) {
+  extern __shared__ __align__(16) uint16_t lds_up[];
+  if (blockIdx.x == 0) {
+    block_route(*reinterpret_cast<BlockRoute*>(lds_up), p.scores, p.bias, p.T, p.E, p.k, p.route_scale,
+                p.table, true, p.route);
+    return;
+  }
+  const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int xs = p.H + 8;
+  uint16_t* xh = lds_up;
+  uint16_t* xl = lds_up + p.T * xs;
+  u32x4 xv[kUpXRegChunks][2];
+  const bool xreg = load_x<kF32, kUpW * 64>(p, xh, xl, xs, tid, xv);
+  shared_up_tile<kF32>(p, static_cast<int>(blockIdx.x) - 1, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave, r16, g4);
+}
+
+// Routed gate/up of the decode pipeline.  Each block takes kUpItems row
+// tiles of one active expert, kUpKS waves per tile, each streaming one K
+// range of its FP4 (or q3) w1/w3 rows in batches of G K blocks;
+// h[drow] = SwiGLU(gate, up) * route weight.  Two batches are in flight per
+// wave; the tokens' activations are loaded before the weights and written to
+// LDS after the weight loads have been issued; K ranges are added in wave
+// order.
 template <int G, bool kWin, bool kF32, bool kQ3>
 __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 ? 3 : 4))) void k_up_stream(DecodeArgs p) {
   extern __shared__ __align__(16) uint16_t lds_up[];
@@ -228,52 +293,21 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
   const int groups = (p.up_tiles + kUpItems - 1) / kUpItems;
-  const bool shared_tile = static_cast<int>(blockIdx.x) < p.shared_blocks;
-  const int rb = static_cast<int>(blockIdx.x) - p.shared_blocks;
-  const int slot = shared_tile ? 0 : rb / groups;
-  if (!shared_tile && slot >= p.active[0]) return;
+  const int rb = static_cast<int>(blockIdx.x);
+  const int slot = rb / groups;
+  if (slot >= p.active[0]) return;
   const int T = p.T, K = p.H;
   const int item = wave / kUpKS, ks = wave % kUpKS;
   const int rt = (rb % groups) * kUpItems + item;
   const bool rok = rt < p.up_tiles;
-  const int drow = shared_tile ? -1 : (r16 < T ? p.rowmap[slot * T + r16] : -1);
-  const bool tv = shared_tile ? r16 < T : drow >= 0;
-  // x chunks through registers (or straight to LDS when there are many)
+  const int drow = r16 < T ? p.rowmap[slot * T + r16] : -1;
+  const bool tv = drow >= 0;
   const int xs = K + 8;                       // padded LDS row stride (elements)
   constexpr bool f32 = kF32;
   uint16_t* xh = lds_up;
   uint16_t* xl = lds_up + T * xs;
-  const int cpr = K / 8;                      // chunks per row
-  const int xchunks = T * cpr;
-  const bool xreg = xchunks <= kUpXRegChunks * kUpW * 64;
   u32x4 xv[kUpXRegChunks][2];
-  if (xreg) {
-#pragma unroll
-    for (int j = 0; j < kUpXRegChunks; ++j) {
-      const int c = tid + j * kUpW * 64;
-      if (c < xchunks) {
-        const int64_t e = static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8;
-        if (!f32) {
-          xv[j][0] = ldg16(static_cast<const uint16_t*>(p.x) + e);
-        } else {
-          xv[j][0] = ldg16(static_cast<const float*>(p.x) + e);
-          xv[j][1] = ldg16(static_cast<const float*>(p.x) + e + 4);
-        }
-      }
-    }
-  } else {
-    for (int c = tid; c < xchunks; c += kUpW * 64) {
-      const int64_t e = static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8;
-      const int off = (c / cpr) * xs + (c % cpr) * 8;
-      if (!f32) put_x_chunk(xh, xl, off, ldg16(static_cast<const uint16_t*>(p.x) + e), u32x4{}, false);
-      else put_x_chunk(xh, xl, off, ldg16(static_cast<const float*>(p.x) + e),
-                       ldg16(static_cast<const float*>(p.x) + e + 4), true);
-    }
-  }
-  if (shared_tile) {
-    shared_up_tile<kF32>(p, xh, xl, xs, xreg, xv, cpr, xchunks, lds_up, tid, lane, wave, r16, g4);
-    return;
-  }
+  const bool xreg = load_x<kF32, kUpW * 64>(p, xh, xl, xs, tid, xv);
   const SlotDesc* d = p.desc + slot;
   const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
   const int nblk = (K + 127) / 128;
@@ -336,13 +370,7 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
     };
     ld(a1, a3, aw, k0);
     ld(b1, b3, bw, k0 + G);
-    if (xreg) {
-#pragma unroll
-      for (int j = 0; j < kUpXRegChunks; ++j) {
-        const int c = tid + j * kUpW * 64;
-        if (c < xchunks) put_x_chunk(xh, xl, (c / cpr) * xs + (c % cpr) * 8, xv[j][0], xv[j][1], f32);
-      }
-    }
+    if (xreg) put_staged_x<kF32, kUpW * 64>(p, xh, xl, xs, tid, xv);
     wr = tv ? p.wrow[drow] : 0.0f;
     __syncthreads();
     const uint16_t* bh = xh + (tv ? r16 : 0) * xs;
@@ -372,13 +400,7 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
     UpBatch<G> A, B;
     load_batch<G, kWin>(A, W1, S1, W3, S3, row, K, k0, k1, g4, rok);
     load_batch<G, kWin>(B, W1, S1, W3, S3, row, K, k0 + G, k1, g4, rok);
-    if (xreg) {
-#pragma unroll
-      for (int j = 0; j < kUpXRegChunks; ++j) {
-        const int c = tid + j * kUpW * 64;
-        if (c < xchunks) put_x_chunk(xh, xl, (c / cpr) * xs + (c % cpr) * 8, xv[j][0], xv[j][1], f32);
-      }
-    }
+    if (xreg) put_staged_x<kF32, kUpW * 64>(p, xh, xl, xs, tid, xv);
     wr = tv ? p.wrow[drow] : 0.0f;
     uint8_t* xch = reinterpret_cast<uint8_t*>(red + kUpItems) + wave * 640;
     __syncthreads();
@@ -689,10 +711,7 @@ __global__ __launch_bounds__(kDownW * 64) void k_down_decode(DecodeArgs p) {
   }
 }
 
-}  // namespace
-
-hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
-                                 hipStream_t s, const hipEvent_t* ev, int repeat) {
+DecodeArgs decode_args(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a) {
   DecodeArgs p{};
   p.T = d.tokens; p.H = d.hidden; p.I = d.inter; p.Is = d.inter_shared; p.k = d.top_k;
   p.limit = d.limit;
@@ -708,12 +727,42 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   p.shared_out = a.shared_out;
   p.out = a.out;
   p.up_tiles = d.inter / 16;
+  p.scores = a.scores; p.bias = a.bias; p.table = a.table;
+  p.E = d.n_experts; p.route_scale = d.route_scale;
+  p.route = a.route;
+  return p;
+}
+
+size_t up_lds_bytes(const DecodeArgs& p) {
+  return static_cast<size_t>(p.x_f32 ? 2 : 1) * p.T * (p.H + 8) * 2 + kUpLdsFixed;
+}
+
+static_assert(sizeof(BlockRoute) <= kUpLdsFixed, "routing block state must fit the gate/up LDS");
+
+}  // namespace
+
+hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                               hipStream_t s, int repeat) {
+  const DecodeArgs p = decode_args(d, L, a);
+  const unsigned blocks = static_cast<unsigned>(1 + p.Is / 16);
+  const size_t lds = up_lds_bytes(p);
+  for (int r = 0; r < repeat; ++r) {
+    if (p.x_f32) k_route_shared<true><<<blocks, kUpW * 64, lds, s>>>(p);
+    else k_route_shared<false><<<blocks, kUpW * 64, lds, s>>>(p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                                 hipStream_t s, const hipEvent_t* ev, int repeat) {
+  const DecodeArgs p = decode_args(d, L, a);
   const int groups = (p.up_tiles + kUpItems - 1) / kUpItems;
   const int max_slots = d.n_experts < d.tokens * d.top_k ? d.n_experts : d.tokens * d.top_k;
-  p.shared_blocks = p.Is / 16;
-  const unsigned up_blocks = static_cast<unsigned>(p.shared_blocks + max_slots * groups);
+  const unsigned up_blocks = static_cast<unsigned>(max_slots * groups);
   hipError_t e;
-  const size_t up_lds = static_cast<size_t>(p.x_f32 ? 2 : 1) * p.T * (p.H + 8) * 2 + kUpLdsFixed;
+  const size_t up_lds = up_lds_bytes(p);
   // scale windows need 4-byte aligned scale rows (H a multiple of 128)
   const bool win = d.hidden % 128 == 0;
   const bool q3 = d.quant == DSK_QUANT_Q3;

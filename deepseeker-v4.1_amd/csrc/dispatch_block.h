@@ -165,103 +165,6 @@ __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ idx, 
   }
 }
 
-// One-wave dispatch for N = T*k <= 64 positions (lane i holds position i),
-// same outputs as dispatch_block, plus rowmap[slot * T + t] = the dispatch
-// row of token t for active expert `slot` (-1 if the token is not routed to
-// it).  A position's sorted place is the number of positions with a smaller
-// (expert, position) key, counted over the wave with uniform readlanes;
-// counts come from an LDS histogram and offsets from its exclusive scan.
-// idx / wflat may point to LDS.  LDS needed: 64 + 64 * ceil(E / 64) +
-// min(E, 64) * T int32.
-__device__ __forceinline__ void dispatch_wave(const int32_t* idx, int N, int E, int k, int T,
-                                              const float* wflat,
-                                              const dsk_expert_ptrs* __restrict__ table,
-                                              const DispatchOut& o, int32_t* rowmap_out,
-                                              int32_t* lds) {
-  const int lane = threadIdx.x & 63;
-  const int per = (E + 63) / 64;         // experts per lane in the histogram
-  int32_t* sorted = lds;                 // [64] expert id at each sorted position
-  int32_t* hist = lds + 64;              // [64 * per]
-  int32_t* rmap = hist + 64 * per;       // [slots][T]
-  const int e_in = lane < N ? idx[lane] : -1;
-  const bool ok = lane < N && e_in >= 0 && e_in < E;
-  const int key = ok ? e_in : E;         // dropped positions sort last
-  for (int i = 0; i < per; ++i) hist[lane * per + i] = 0;
-  int pos = 0;
-  for (int j = 0; j < N; ++j) {
-    const int kj = __builtin_amdgcn_readlane(key, j);
-    pos += (kj < key) || (kj == key && j < lane);
-  }
-  const int n_valid = __popcll(__ballot(ok));
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  if (lane < N) sorted[pos] = key;
-  if (lane >= N) sorted[lane] = E;
-  if (ok) atomicAdd(&hist[e_in], 1);
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  // dense counts / offsets: lane handles experts [lane*per, lane*per + per)
-  int run = 0;
-  for (int i = 0; i < per; ++i) run += hist[lane * per + i];
-  int xo = wave_incl_scan(run, lane) - run;
-  for (int i = 0; i < per; ++i) {
-    const int e = lane * per + i;
-    if (e < E) {
-      const int c = hist[e];
-      o.counts[e] = c;
-      o.offsets[e] = xo;
-      xo += c;
-    }
-  }
-  // position q = lane: first position of its expert?
-  const int se = sorted[lane];
-  const bool first = lane < n_valid && (lane == 0 || sorted[lane - 1] != se);
-  const uint64_t firsts = __ballot(first);
-  const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
-  const int n_act = __popcll(firsts);
-  const int slot_here = __popcll(firsts & (lt | (1ull << lane))) - 1;   // slot of position q
-  if (lane == 0) { o.offsets[E] = n_valid; o.active[0] = n_act; }
-  if (first) {
-    const int slot = slot_here;
-    o.active[1 + slot] = se;
-    if (o.desc) {
-      const int cnt = hist[se];
-      SlotDesc d;
-      d.e = se; d.n_tok = cnt; d.tok_base = lane; d.pad = 0;
-      const dsk_expert_ptrs t = table[se];
-      d.p[0] = t.w1; d.p[1] = t.s1; d.p[2] = t.b1;
-      d.p[3] = t.w3; d.p[4] = t.s3; d.p[5] = t.b3;
-      d.p[6] = t.w2; d.p[7] = t.s2; d.p[8] = t.b2;
-      d.pad2 = nullptr;
-      o.desc[slot] = d;
-    }
-  }
-  const int n_map = n_act * T;
-  for (int i = lane; i < n_map; i += 64) rmap[i] = -1;
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  const int my_slot = __shfl(slot_here, pos & 63, 64);
-  if (ok) {
-    o.perm[pos] = lane;
-    o.rank[lane] = pos;
-    if (o.xrow) {
-      o.xrow[pos] = lane / k;
-      o.wrow[pos] = wflat[lane];
-    }
-    rmap[my_slot * T + lane / k] = pos;
-  } else if (lane < N) {
-    o.rank[lane] = -1;
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  if (rowmap_out)
-    for (int i = lane; i < n_map; i += 64) rowmap_out[i] = rmap[i];
-}
-
 __host__ __device__ inline int bits_for(int E) {
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;

@@ -130,18 +130,22 @@ struct RouteArgs {
   const dsk_expert_ptrs* table;
   DispatchOut out;
   unsigned int* ctr;        // [tokens + 1] arrival counters (fused path), zero between calls
-  // decode pipeline (tokens * top_k <= 64 and tokens <= 16): one-wave dispatch
-  // with a token -> dispatch-row map
-  int32_t* rowmap;          // [min(E, 64)][tokens] or null
+  int32_t* rowmap;          // decode pipeline: [slot][tokens] token -> dispatch row map
 };
 // Fused router + dispatch (general path).
 hipError_t launch_route_dispatch(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
-// Decode pipeline: gate scores only, then one block of top-k + one-wave dispatch.
-hipError_t launch_gate_scores(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
-hipError_t launch_route_tail(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
 
 hipError_t launch_dispatch(const dsk_moe_desc& d, const int32_t* idx, const float* wflat,
                            const dsk_expert_ptrs* table, const DispatchOut& o, hipStream_t s);
+
+// Routing of the decode pipeline: the layer's idx / weights [T][k], and for
+// the decode kernels active (count, then the expert of each slot), one
+// descriptor per slot, rowmap [slot][T] (-1: token not routed to the slot)
+// and the route weight of each dispatch row.
+struct DecodeRoute {
+  int32_t* idx; float* weights;
+  SlotDesc* desc; int32_t* active; int32_t* rowmap; float* wrow;
+};
 
 struct ExpertsArgs {
   const dsk_expert_ptrs* table;
@@ -155,6 +159,9 @@ struct ExpertsArgs {
   void* out;
   char* ws;                  // workspace base
   const int32_t* rowmap;     // decode pipeline: [slot][T] dispatch row of token t, -1 if none
+  // decode pipeline: gate scores and selection bias in, routing out
+  float* scores; const float* bias;
+  DecodeRoute route;
 };
 
 // ev (nullable): 3 events recorded after the gate/up kernel, the down kernel
@@ -177,9 +184,16 @@ struct PrefillArgs {
 hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, const PrefillArgs& a,
                                   hipStream_t s, const hipEvent_t* ev, int repeat);
 
-// Decode pipeline (decode_pipeline(d)): routed and shared gate/up in one
-// kernel, then down + shared down + combine fused per 16 output rows.  Needs
-// a.desc, a.active, a.rowmap, a.wrow from the route tail.
+// Decode pipeline (decode_pipeline(d)), four kernels:
+//   launch_gate_scores    gate scores (a.scores);
+//   launch_route_shared   top-k and slot map (a.route) in one block beside the shared
+//                         expert's gate/up (hs);
+//   launch_experts_decode the routed gate/up, then the routed and shared down and the
+//                         combine in one kernel.  ev (nullable): 3 events as for
+//                         launch_experts.
+hipError_t launch_gate_scores(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
+hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                               hipStream_t s, int repeat);
 hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L,
                                  const ExpertsArgs& a, hipStream_t s, const hipEvent_t* ev,
                                  int repeat);

@@ -161,8 +161,8 @@ __device__ __forceinline__ void gate_tile(const void* x, const void* gw, int T, 
 // the keys of experts l + 64*i, i < S.  Each round every lane takes its best
 // remaining key (lowest id among equal keys), the wave maximum key is found
 // with DPP, and among the lanes holding it the lowest expert id wins.
-// Results go to idx_row / w_row and, when given, to the LDS copies lidx / lw
-// (used by the dispatch that follows).
+// Results go to idx_row / w_row and to the LDS copies lidx / lw, each pair
+// when given (the LDS copies feed the dispatch that follows).
 template <int S>
 __device__ __forceinline__ void topk_token_s(const float* __restrict__ srow, const float* __restrict__ bias,
                                              int E, int k, float route_scale, int32_t* __restrict__ idx_row,
@@ -205,8 +205,7 @@ __device__ __forceinline__ void topk_token_s(const float* __restrict__ srow, con
   const float denom = acc + 1e-20f;
   if (lane < k) {
     const float w = (my_s / denom) * route_scale;
-    idx_row[lane] = my_e;
-    w_row[lane] = w;
+    if (idx_row) { idx_row[lane] = my_e; w_row[lane] = w; }
     if (lidx) { lidx[lane] = my_e; lw[lane] = w; }
   }
 }

@@ -255,47 +255,6 @@ hipError_t launch_gate(const dsk_moe_desc& d, const GateArgs& g, hipStream_t s) 
   return hipGetLastError();
 }
 
-// Top-k of T <= 16 tokens (wave t: token t) and the one-wave dispatch of the
-// decode pipeline, in one block after the gate kernel.  The other waves (and
-// the top-k waves once done) copy the expert table into LDS meanwhile, so the
-// dispatch's descriptor writes do not wait on global loads.
-__global__ __launch_bounds__(1024) void k_route_tail(GateArgs g, int32_t* rowmap) {
-  extern __shared__ __align__(16) int32_t tail_lds[];
-  const int wave = threadIdx.x >> 6;
-  const int N = g.T * g.k;
-  int32_t* lidx = tail_lds;                                  // [64]
-  float* lw = reinterpret_cast<float*>(tail_lds + 64);       // [64]
-  uint64_t* ltab = reinterpret_cast<uint64_t*>(tail_lds + 128);   // [E * 9]
-  int32_t* ldisp = tail_lds + 128 + 2 * 9 * g.E;
-  if (wave < g.T)
-    topk_token(g.scores + static_cast<int64_t>(wave) * g.E, g.bias, g.E, g.k, g.route_scale,
-               g.idx + static_cast<int64_t>(wave) * g.k, g.weights + static_cast<int64_t>(wave) * g.k,
-               lidx + wave * g.k, lw + wave * g.k);
-  {
-    constexpr int kWords = sizeof(dsk_expert_ptrs) / 8;
-    const uint64_t* src = reinterpret_cast<const uint64_t*>(g.table);
-    const int n = g.E * kWords;
-    constexpr int kU = 8;
-    for (int i0 = threadIdx.x; i0 < n; i0 += kU * blockDim.x) {
-      uint64_t v[kU];
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int i = i0 + u * blockDim.x;
-        v[u] = i < n ? src[i] : 0ull;
-      }
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int i = i0 + u * blockDim.x;
-        if (i < n) ltab[i] = v[u];
-      }
-    }
-  }
-  __syncthreads();
-  if (wave == 0)
-    dispatch_wave(lidx, N, g.E, g.k, g.T, lw, reinterpret_cast<const dsk_expert_ptrs*>(ltab), g.out,
-                  rowmap, ldisp);
-}
-
 GateArgs make_gate_args(const dsk_moe_desc& d, const void* x, const void* gate_w,
                         const float* gate_b, float* scores, int32_t* idx, float* weights) {
   GateArgs g{};
@@ -347,18 +306,6 @@ hipError_t launch_route_dispatch(const dsk_moe_desc& d, const RouteArgs& a, hipS
 hipError_t launch_gate_scores(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s) {
   const GateArgs g = route_gate_args(d, a);
   return d.tokens >= 16 ? launch_gate<4, 4, false>(d, g, s) : launch_gate<1, 1, false>(d, g, s);
-}
-
-hipError_t launch_route_tail(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s) {
-  const GateArgs g = route_gate_args(d, a);
-  const int per = (d.n_experts + 63) / 64;
-  const size_t lds = static_cast<size_t>(128 + 2 * 9 * d.n_experts + 64 + 64 * per + 64 * d.tokens) *
-                     sizeof(int32_t);
-  // top-k waves plus at least three copy waves
-  const int waves = d.tokens + 3 < 16 ? d.tokens + 3 : 16;
-  const unsigned threads = static_cast<unsigned>(64 * waves);
-  k_route_tail<<<1, threads, lds, s>>>(g, a.rowmap);
-  return hipGetLastError();
 }
 
 }  // namespace dsk
