@@ -184,6 +184,16 @@ struct PrefillArgs {
 hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, const PrefillArgs& a,
                                   hipStream_t s, const hipEvent_t* ev, int repeat);
 
+// Grouped path for batches below the prefill size (bf16 x, shapes that
+// tile): per slot, column tiles of its dispatch rows with only their
+// activation rows staged; the shared expert as a pseudo-slot.  Writes the
+// routed rows y and the shared output ys for launch_combine.  ev (nullable):
+// 2 events, after gate/up and after down.
+bool grouped_path(const dsk_moe_desc& d);
+hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                                  const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
+                                  const hipEvent_t* ev, int repeat);
+
 // Decode pipeline (decode_pipeline(d)), four kernels:
 //   launch_gate_scores    gate scores (a.scores);
 //   launch_route_shared   top-k and slot map (a.route) in one block beside the shared

@@ -552,6 +552,10 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
     if ((e = launch_experts_prefill(d, L, pa, s, ev, repeat)) != hipSuccess) return e;
     return launch_combine(d, L, a, s, ev ? ev + 2 : nullptr, repeat);
   }
+  if (grouped_path(d)) {
+    if ((e = launch_experts_grouped(d, L, a, desc, xrow, wrow, s, ev, repeat)) != hipSuccess) return e;
+    return launch_combine(d, L, a, s, ev ? ev + 2 : nullptr, repeat);
+  }
   if (x_f32) {
     uint16_t* hi = reinterpret_cast<uint16_t*>(a.ws + L.xb_hi);
     uint16_t* lo = reinterpret_cast<uint16_t*>(a.ws + L.xb_lo);

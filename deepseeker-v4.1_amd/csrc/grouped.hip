@@ -1,0 +1,324 @@
+// Grouped expert products for medium batches (a few to a few dozen tokens).
+//
+// Replaces the per-expert gate/up and w2 products of the reference's
+// moe_layer (src/deepseeker/mlx_forward.py:388-406) and its shared expert
+// (src/deepseeker/mlx_runner.py:765-783) when each active expert sees only a
+// handful of tokens: every expert's weights must be streamed from HBM once,
+// and the MFMA B operand (16 columns) is mostly empty.  A block takes one
+// slot (an active expert, or the shared expert as a pseudo-slot over all T
+// tokens) and a group of row tiles; it walks the slot's dispatch rows in
+// column tiles of kGNC.  For each column tile the waves issue their weight
+// loads first, the block gathers only that tile's activation rows into LDS
+// (x for gate/up, the h planes for down) while the weights are in flight,
+// and each wave then multiplies its K range; K ranges are added in a fixed
+// order through LDS.  Gate/up writes h = SwiGLU(gate, up) * route weight by
+// dispatch row (hs by token for the shared expert); down writes one float32
+// output row per dispatch row (ys per token for the shared expert), which
+// the combine kernel adds in ascending expert id.
+#include "tile.h"
+
+namespace dsk {
+namespace {
+
+constexpr int kGI = 2;              // gate/up: row tiles of a block
+constexpr int kGKS = 4;             // gate/up: K ranges of a row tile (one wave each)
+constexpr int kGW = kGI * kGKS;     // waves of a gate/up block
+constexpr int kDI = 4;              // down: row tiles of a block
+constexpr int kDKS = 2;             // down: K ranges of a row tile
+constexpr int kDW = kDI * kDKS;     // waves of a down block
+constexpr int kGNC = 8;             // dispatch rows (B columns) of a column tile
+constexpr int kStageQ = 2;          // 16-byte activation chunks per thread per staging pass
+
+static_assert(kGW == kDW, "both kernels use the same block size");
+
+struct GroupedArgs {
+  int T, H, I, Is, k;
+  float limit;
+  const SlotDesc* desc; const int32_t* active;   // active[0] = number of descriptors
+  const int32_t* xrow; const float* wrow;        // per dispatch row: token, route weight
+  const uint16_t* x;                             // [T][H] bf16
+  const uint16_t* ws1; const uint16_t* ws3;      // shared [Is][H] bf16
+  const uint16_t* ws2;                           // shared [H][Is] bf16
+  uint16_t* h_hi; uint16_t* h_lo;                // [T*k][I] by dispatch row
+  uint16_t* hs_hi; uint16_t* hs_lo;              // [T][Is]
+  float* y;                                      // [T*k][H]
+  float* ys;                                     // [T][H]
+  int up_groups, up_shared;                      // gate/up: row-tile groups per slot, shared blocks
+  int dn_groups, dn_shared;                      // down: the same
+};
+
+// K blocks per weight batch, two batches in flight per wave, within the
+// register budget of four waves per SIMD: one for bf16 rows (64 bytes per
+// lane and K block), two for FP4 and q3 (20 and 16).
+template <typename Raw>
+constexpr int batch_blocks() { return sizeof(Raw) > 32 ? 1 : 2; }
+
+// Rows [c0, c0 + cols) of the slot's activations (row r comes from source row
+// src(r) of `base`, row stride `ld` elements, K elements) into LDS rows of
+// stride K + 8, issued kStageQ chunks per thread at a time.
+template <typename Src>
+__device__ __forceinline__ void stage_rows(uint16_t* dst, const uint16_t* base, int ld, int K, int cols,
+                                           Src src) {
+  const int cpr = K / 8, chunks = cols * cpr, nt = blockDim.x;
+  for (int c = threadIdx.x; c < chunks; c += kStageQ * nt) {
+    u32x4 v[kStageQ];
+#pragma unroll
+    for (int q = 0; q < kStageQ; ++q) {
+      const int cc = c + q * nt;
+      if (cc < chunks) v[q] = ldg16(base + static_cast<int64_t>(src(cc / cpr)) * ld + (cc % cpr) * 8);
+    }
+#pragma unroll
+    for (int q = 0; q < kStageQ; ++q) {
+      const int cc = c + q * nt;
+      if (cc < chunks) *reinterpret_cast<u32x4*>(dst + (cc / cpr) * (K + 8) + (cc % cpr) * 8) = v[q];
+    }
+  }
+}
+
+// Gate/up of one block: row tile rt (rows 16 rt ..) of w1 and w3 for the n
+// dispatch rows base .. base + n - 1 (shared: tokens 0 .. n - 1).
+template <typename Raw, typename LoadW>
+__device__ __forceinline__ void up_block(const GroupedArgs& p, LoadW load_w, int rt, bool rok, int n, int base,
+                                         bool shared, uint16_t* lds) {
+  constexpr int G = batch_blocks<Raw>();
+  const int lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int item = wave / kGKS, ks = wave % kGKS;
+  const int K = p.H, nblk = K / 128;
+  const int per = (nblk + kGKS - 1) / kGKS;
+  const int k0 = min(ks * per, nblk), k1 = min(k0 + per, nblk);
+  const int xs = K + 8;
+  const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
+  float (*red)[kGKS][2][64][4] = reinterpret_cast<float (*)[kGKS][2][64][4]>(lds);   // over the x tile
+  for (int c0 = 0; c0 < n; c0 += kGNC) {
+    const int cols = min(kGNC, n - c0);
+    Raw a1[G], a3[G], b1[G], b3[G];
+    auto ld = [&](Raw (&r1)[G], Raw (&r3)[G], int kb) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const int kc = (kb + i) * 128 + g4 * 32;
+        const bool ok = rok && kb + i < k1;
+        load_w(r1[i], 0, row, kc, ok);
+        load_w(r3[i], 1, row, kc, ok);
+      }
+    };
+    ld(a1, a3, k0);
+    ld(b1, b3, k0 + G);
+    if (shared) stage_rows(lds, p.x, K, K, cols, [&](int r) { return c0 + r; });
+    else stage_rows(lds, p.x, K, K, cols, [&](int r) { return p.xrow[base + c0 + r]; });
+    __syncthreads();
+    const bool tv = r16 < cols;
+    const uint16_t* brow = lds + (tv ? r16 : 0) * xs;
+    f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
+    auto mm = [&](const Raw (&r1)[G], const Raw (&r3)[G], int kb) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const int kc = (kb + i) * 128 + g4 * 32;
+        mma_block2(r1[i], r3[i], brow, kc, tv && kb + i < k1, ag, au);
+      }
+    };
+    for (int kb = k0; kb < k1; kb += 2 * G) {
+      mm(a1, a3, kb);
+      if (kb + 2 * G < k1) ld(a1, a3, kb + 2 * G);
+      if (kb + G < k1) mm(b1, b3, kb + G);
+      if (kb + 3 * G < k1) ld(b1, b3, kb + 3 * G);
+    }
+    __syncthreads();   // every wave is done with the x tile
+    *reinterpret_cast<f32x4*>(&red[item][ks][0][lane][0]) = ag;
+    *reinterpret_cast<f32x4*>(&red[item][ks][1][lane][0]) = au;
+    __syncthreads();
+    if (ks == 0 && rok && tv) {
+#pragma unroll
+      for (int w = 1; w < kGKS; ++w) {
+        ag += *reinterpret_cast<const f32x4*>(&red[item][w][0][lane][0]);
+        au += *reinterpret_cast<const f32x4*>(&red[item][w][1][lane][0]);
+      }
+      const int r = base + c0 + r16;              // dispatch row (shared: token)
+      const float wr = shared ? 1.0f : p.wrow[r];
+      uint16_t hh[4], hl[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) split_bf16(silu_clamped(ag[q], au[q], p.limit) * wr, hh[q], hl[q]);
+      const int ldh = shared ? p.Is : p.I;
+      const int64_t off = static_cast<int64_t>(r) * ldh + rt * 16 + 4 * g4;
+      uint16_t* dh = shared ? p.hs_hi : p.h_hi;
+      uint16_t* dl = shared ? p.hs_lo : p.h_lo;
+      *reinterpret_cast<uint2*>(dh + off) = uint2{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16)};
+      *reinterpret_cast<uint2*>(dl + off) = uint2{hl[0] | (uint32_t(hl[1]) << 16), hl[2] | (uint32_t(hl[3]) << 16)};
+    }
+    __syncthreads();   // the next column tile reuses the LDS
+  }
+}
+
+// Blocks [0, up_shared): the shared expert (bf16 w1/w3, all T tokens); the
+// others: up_groups blocks per slot.
+template <typename Raw>
+__global__ __launch_bounds__(kGW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_up_grouped(GroupedArgs p) {
+  extern __shared__ __align__(16) uint16_t lds_g[];
+  const int b = static_cast<int>(blockIdx.x);
+  const int item = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / kGKS;
+  if (b < p.up_shared) {
+    const int rt = b * kGI + item;
+    auto load_w = [&](RawBF16& r, int role, uint32_t row, int kc, bool ok) {
+      load_raw(r, role ? p.ws3 : p.ws1, row, p.H, kc, ok);
+    };
+    up_block<RawBF16>(p, load_w, rt, rt < p.Is / 16, p.T, 0, true, lds_g);
+    return;
+  }
+  const int rb = b - p.up_shared;
+  const int slot = rb / p.up_groups;
+  if (slot >= p.active[0]) return;
+  const SlotDesc* d = p.desc + slot;
+  const int rt = (rb % p.up_groups) * kGI + item;
+  auto load_w = [&](Raw& r, int role, uint32_t row, int kc, bool ok) { load_role(r, d->p, role, row, p.H, kc, ok); };
+  up_block<Raw>(p, load_w, rt, rt < p.I / 16, d->n_tok, d->tok_base, false, lds_g);
+}
+
+// Down of one block: row tile rt (output rows 16 rt ..) of w2 for the n
+// dispatch rows base .. base + n - 1 (shared: tokens 0 .. n - 1), K = I (Is).
+template <typename Raw, typename LoadW>
+__device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, int rt, int n, int base,
+                                           bool shared, uint16_t* lds) {
+  constexpr int G = batch_blocks<Raw>();
+  const int lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int item = wave / kDKS, ks = wave % kDKS;
+  const int K = shared ? p.Is : p.I, nblk = K / 128;
+  const int per = (nblk + kDKS - 1) / kDKS;
+  const int k0 = min(ks * per, nblk), k1 = min(k0 + per, nblk);
+  const int hs = K + 8;
+  const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
+  const uint16_t* src_hi = shared ? p.hs_hi : p.h_hi;
+  const uint16_t* src_lo = shared ? p.hs_lo : p.h_lo;
+  uint16_t* thi = lds;                      // [kGNC][K + 8] hi plane
+  uint16_t* tlo = lds + kGNC * hs;          // [kGNC][K + 8] lo plane
+  float (*red)[kDKS][64][4] = reinterpret_cast<float (*)[kDKS][64][4]>(lds);   // over the h tile
+  for (int c0 = 0; c0 < n; c0 += kGNC) {
+    const int cols = min(kGNC, n - c0);
+    Raw a[G], b[G];
+    auto ld = [&](Raw (&r)[G], int kb) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) load_w(r[i], row, (kb + i) * 128 + g4 * 32, kb + i < k1);
+    };
+    ld(a, k0);
+    ld(b, k0 + G);
+    stage_rows(thi, src_hi, K, K, cols, [&](int r) { return base + c0 + r; });
+    stage_rows(tlo, src_lo, K, K, cols, [&](int r) { return base + c0 + r; });
+    __syncthreads();
+    const bool tv = r16 < cols;
+    const uint16_t* bh = thi + (tv ? r16 : 0) * hs;
+    const uint16_t* bl = tlo + (tv ? r16 : 0) * hs;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    auto mm = [&](const Raw (&r)[G], int kb) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const int kc = (kb + i) * 128 + g4 * 32;
+        const bool ok = tv && kb + i < k1;
+        mma_block(r[i], bh, kc, ok, acc);
+        mma_block(r[i], bl, kc, ok, acc);
+      }
+    };
+    for (int kb = k0; kb < k1; kb += 2 * G) {
+      mm(a, kb);
+      if (kb + 2 * G < k1) ld(a, kb + 2 * G);
+      if (kb + G < k1) mm(b, kb + G);
+      if (kb + 3 * G < k1) ld(b, kb + 3 * G);
+    }
+    __syncthreads();   // every wave is done with the h tile
+    *reinterpret_cast<f32x4*>(&red[item][ks][lane][0]) = acc;
+    __syncthreads();
+    if (ks == 0 && tv) {
+#pragma unroll
+      for (int w = 1; w < kDKS; ++w) acc += *reinterpret_cast<const f32x4*>(&red[item][w][lane][0]);
+      float* out = shared ? p.ys : p.y;
+      *reinterpret_cast<f32x4*>(out + static_cast<int64_t>(base + c0 + r16) * p.H + rt * 16 + 4 * g4) = acc;
+    }
+    __syncthreads();   // the next column tile reuses the LDS
+  }
+}
+
+// Blocks [0, dn_shared): the shared expert's w2 (bf16, all T tokens); the
+// others: dn_groups blocks per slot.
+template <typename Raw>
+__global__ __launch_bounds__(kDW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_down_grouped(GroupedArgs p) {
+  extern __shared__ __align__(16) uint16_t lds_g[];
+  const int b = static_cast<int>(blockIdx.x);
+  const int item = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / kDKS;
+  if (b < p.dn_shared) {
+    const int rt = b * kDI + item;
+    auto load_w = [&](RawBF16& r, uint32_t row, int kc, bool ok) { load_raw(r, p.ws2, row, p.Is, kc, ok); };
+    down_block<RawBF16>(p, load_w, rt, p.T, 0, true, lds_g);
+    return;
+  }
+  const int rb = b - p.dn_shared;
+  const int slot = rb / p.dn_groups;
+  if (slot >= p.active[0]) return;
+  const SlotDesc* d = p.desc + slot;
+  const int rt = (rb % p.dn_groups) * kDI + item;
+  auto load_w = [&](Raw& r, uint32_t row, int kc, bool ok) { load_role(r, d->p, 2, row, p.I, kc, ok); };
+  down_block<Raw>(p, load_w, rt, d->n_tok, d->tok_base, false, lds_g);
+}
+
+size_t up_lds(const dsk_moe_desc& d) {
+  const size_t x_tile = static_cast<size_t>(kGNC) * (d.hidden + 8) * 2;
+  const size_t red = static_cast<size_t>(kGI) * kGKS * 2 * 64 * 4 * sizeof(float);
+  return x_tile > red ? x_tile : red;
+}
+
+size_t down_lds(const dsk_moe_desc& d) {
+  const int K = d.inter > d.inter_shared ? d.inter : d.inter_shared;
+  const size_t h_tile = 2 * static_cast<size_t>(kGNC) * (K + 8) * 2;
+  const size_t red = static_cast<size_t>(kDI) * kDKS * 64 * 4 * sizeof(float);
+  return h_tile > red ? h_tile : red;
+}
+
+}  // namespace
+
+bool grouped_path(const dsk_moe_desc& d) {
+  return d.x_dtype == DSK_DTYPE_BF16 && d.hidden % (kGI * 16) == 0 && d.hidden % (kDI * 16) == 0 &&
+         d.hidden % 128 == 0 && d.inter % 128 == 0 && d.inter % (kGI * 16) == 0 &&
+         d.inter_shared % 128 == 0 && d.inter_shared % (kGI * 16) == 0 &&
+         up_lds(d) <= kMaxLds && down_lds(d) <= kMaxLds;
+}
+
+hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                                  const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
+                                  const hipEvent_t* ev, int repeat) {
+  GroupedArgs p{};
+  p.T = d.tokens; p.H = d.hidden; p.I = d.inter; p.Is = d.inter_shared; p.k = d.top_k; p.limit = d.limit;
+  p.desc = desc; p.active = a.active; p.xrow = xrow; p.wrow = wrow;
+  p.x = static_cast<const uint16_t*>(a.x);
+  p.ws1 = static_cast<const uint16_t*>(a.ws1);
+  p.ws3 = static_cast<const uint16_t*>(a.ws3);
+  p.ws2 = static_cast<const uint16_t*>(a.ws2);
+  p.h_hi = reinterpret_cast<uint16_t*>(a.ws + L.h_hi);
+  p.h_lo = reinterpret_cast<uint16_t*>(a.ws + L.h_lo);
+  p.hs_hi = reinterpret_cast<uint16_t*>(a.ws + L.hs_hi);
+  p.hs_lo = reinterpret_cast<uint16_t*>(a.ws + L.hs_lo);
+  p.y = reinterpret_cast<float*>(a.ws + L.y);
+  p.ys = reinterpret_cast<float*>(a.ws + L.ys);
+  p.up_groups = d.inter / 16 / kGI;
+  p.up_shared = d.inter_shared / 16 / kGI;
+  p.dn_groups = d.hidden / 16 / kDI;
+  p.dn_shared = d.inter_shared > 0 ? p.dn_groups : 0;
+  const int max_slots = d.n_experts < d.tokens * d.top_k ? d.n_experts : d.tokens * d.top_k;
+  const bool q3 = d.quant == DSK_QUANT_Q3;
+  const unsigned up_blocks = static_cast<unsigned>(p.up_shared + max_slots * p.up_groups);
+  const unsigned dn_blocks = static_cast<unsigned>(p.dn_shared + max_slots * p.dn_groups);
+  const size_t ul = up_lds(d), dl = down_lds(d);
+  hipError_t e;
+  for (int r = 0; r < repeat; ++r) {
+    if (q3) k_up_grouped<RawQ3><<<up_blocks, kGW * 64, ul, s>>>(p);
+    else k_up_grouped<RawFP4><<<up_blocks, kGW * 64, ul, s>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
+  for (int r = 0; r < repeat; ++r) {
+    if (q3) k_down_grouped<RawQ3><<<dn_blocks, kDW * 64, dl, s>>>(p);
+    else k_down_grouped<RawFP4><<<dn_blocks, kDW * 64, dl, s>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
+  return hipSuccess;
+}
+
+}  // namespace dsk
