@@ -108,7 +108,7 @@ def layer_bytes(u: int, t: int, quant: str = "fp4") -> int:
     return u * expert_bytes(quant) + 3 * IS * H * 2 + E * H * 4 + 2 * t * H * 2
 
 
-PREFILL_MIN_TOKENS = 64      # batches from this size run the expert products as MFMA GEMM tiles
+PREFILL_MIN_TOKENS = 128     # batches from this size run the expert products as MFMA GEMM tiles
 
 
 def layer_flops(t: int) -> int:

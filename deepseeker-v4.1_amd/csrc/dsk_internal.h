@@ -97,7 +97,7 @@ constexpr size_t kUpLdsFixed = 2 * 4 * 2 * 64 * 4 * 4 + 8 * 640;   // decode gat
 // Prefill GEMM tiles: 256 weight rows x 256 dispatch rows per block.
 constexpr int kPfRows = 256;
 constexpr int kPfToks = 256;
-constexpr int kPrefillMinTokens = 64;
+constexpr int kPrefillMinTokens = 128;
 
 // Large batches of bf16 tokens run the expert products as MFMA GEMM tiles
 // (gate/up tiles of 128 intermediate rows, down tiles of 256 output rows).

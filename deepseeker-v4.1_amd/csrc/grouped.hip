@@ -23,8 +23,8 @@ namespace {
 constexpr int kGI = 2;              // gate/up: row tiles of a block
 constexpr int kGKS = 4;             // gate/up: K ranges of a row tile (one wave each)
 constexpr int kGW = kGI * kGKS;     // waves of a gate/up block
-constexpr int kDI = 4;              // down: row tiles of a block
-constexpr int kDKS = 2;             // down: K ranges of a row tile
+constexpr int kDI = 8;              // down: row tiles of a block
+constexpr int kDKS = 1;             // down: K ranges of a row tile
 constexpr int kDW = kDI * kDKS;     // waves of a down block
 constexpr int kGNC = 8;             // dispatch rows (B columns) of a column tile
 constexpr int kStageQ = 2;          // 16-byte activation chunks per thread per staging pass
@@ -123,10 +123,12 @@ __device__ __forceinline__ void up_block(const GroupedArgs& p, LoadW load_w, int
       if (kb + G < k1) mm(b1, b3, kb + G);
       if (kb + 3 * G < k1) ld(b1, b3, kb + 3 * G);
     }
-    __syncthreads();   // every wave is done with the x tile
-    *reinterpret_cast<f32x4*>(&red[item][ks][0][lane][0]) = ag;
-    *reinterpret_cast<f32x4*>(&red[item][ks][1][lane][0]) = au;
-    __syncthreads();
+    if constexpr (kGKS > 1) {
+      __syncthreads();   // every wave is done with the x tile
+      *reinterpret_cast<f32x4*>(&red[item][ks][0][lane][0]) = ag;
+      *reinterpret_cast<f32x4*>(&red[item][ks][1][lane][0]) = au;
+      __syncthreads();
+    }
     if (ks == 0 && rok && tv) {
 #pragma unroll
       for (int w = 1; w < kGKS; ++w) {
@@ -223,9 +225,11 @@ __device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, i
       if (kb + G < k1) mm(b, kb + G);
       if (kb + 3 * G < k1) ld(b, kb + 3 * G);
     }
-    __syncthreads();   // every wave is done with the h tile
-    *reinterpret_cast<f32x4*>(&red[item][ks][lane][0]) = acc;
-    __syncthreads();
+    if constexpr (kDKS > 1) {
+      __syncthreads();   // every wave is done with the h tile
+      *reinterpret_cast<f32x4*>(&red[item][ks][lane][0]) = acc;
+      __syncthreads();
+    }
     if (ks == 0 && tv) {
 #pragma unroll
       for (int w = 1; w < kDKS; ++w) acc += *reinterpret_cast<const f32x4*>(&red[item][w][lane][0]);

@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ scores,
 // and exchanges.
 constexpr int kGwThreads = 512;
 constexpr int kGwTok = 32, kGwExp = 16;
-constexpr int kGateWideMinTokens = 32;
+constexpr int kGateWideMinTokens = 128;
 
 template <bool kBF16>
 __device__ __forceinline__ f32x4 lds_f32x4(const char* row, int lane) {
