@@ -233,7 +233,7 @@ static int forward_impl(const dsk_moe_desc* d, const void* x, const void* gate_w
   a.active = active; a.out = out; a.ws = ws;
   a.rowmap = ra.rowmap;
   a.scores = scores; a.bias = gate_b;
-  a.route = DecodeRoute{idx_buf, w_buf, ra.out.desc, active, ra.rowmap, ra.out.wrow};
+  a.route = DecodeRoute{idx_buf, w_buf, ra.out.desc, active, ra.rowmap, ra.out.xrow, ra.out.wrow, rank};
   const bool decode = decode_pipeline(*d);
   if (ev && (rc = hip_check(hipEventRecord(ev[0], s), "event record"))) return rc;
   if (decode) {

@@ -27,8 +27,8 @@ struct BlockRoute {
 // Top-k of the T tokens (wave w: tokens w, w + waves, ...) from the gate
 // scores, then the slot map in wave 0, into r.  With `publish` the block also
 // writes the routing outputs of the layer (o): idx / weights, and for the
-// down kernel active, one descriptor per slot and rowmap.  Contains two block
-// barriers.
+// expert kernels active, one descriptor per slot, rowmap, the row weights
+// and rank.  Contains two block barriers.
 __device__ __forceinline__ void block_route(BlockRoute& r, const float* scores, const float* bias, int T,
                                             int E, int k, float route_scale, const dsk_expert_ptrs* table,
                                             bool publish, const DecodeRoute& o) {
@@ -90,8 +90,12 @@ __device__ __forceinline__ void block_route(BlockRoute& r, const float* scores, 
     if (ok) {
       r.rmap[my_slot * T + lane / k] = pos;
       r.row_w[pos] = r.w[lane];
-      if (publish) o.wrow[pos] = r.w[lane];
+      if (publish) {
+        o.wrow[pos] = r.w[lane];
+        o.xrow[pos] = lane / k;
+      }
     }
+    if (publish && lane < N) o.rank[lane] = ok ? pos : -1;
     if (publish) {
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_s_waitcnt(0);

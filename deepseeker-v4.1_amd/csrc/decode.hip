@@ -769,18 +769,29 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   // q3 (scale, bias) windows: every wave's K range a whole number of G-block
   // batches inside the row (so also 16-byte aligned windows)
   const bool q3win = d.hidden % (kUpKS * kUpBatch * 128) == 0;
-  for (int r = 0; r < repeat; ++r) {
-    if (q3 && q3win && !p.x_f32) k_up_stream<kUpBatch, true, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-    else if (q3 && q3win) k_up_stream<kUpBatch, true, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-    else if (q3 && !p.x_f32) k_up_stream<kUpBatch, false, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-    else if (q3) k_up_stream<kUpBatch, false, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-    else if (win && !p.x_f32) k_up_stream<kUpBatch, true, false, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-    else if (win) k_up_stream<kUpBatch, true, true, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-    else if (!p.x_f32) k_up_stream<kUpBatch, false, false, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-    else k_up_stream<kUpBatch, false, true, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (d.tokens >= kDecodeGroupedUpMin && grouped_path(d)) {
+    e = launch_grouped_up_routed(d, L, a, a.route.desc, a.route.xrow, a.route.wrow, s, repeat);
+    if (e != hipSuccess) return e;
+  } else {
+    for (int r = 0; r < repeat; ++r) {
+      if (q3 && q3win && !p.x_f32) k_up_stream<kUpBatch, true, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+      else if (q3 && q3win) k_up_stream<kUpBatch, true, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+      else if (q3 && !p.x_f32) k_up_stream<kUpBatch, false, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+      else if (q3) k_up_stream<kUpBatch, false, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+      else if (win && !p.x_f32) k_up_stream<kUpBatch, true, false, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+      else if (win) k_up_stream<kUpBatch, true, true, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+      else if (!p.x_f32) k_up_stream<kUpBatch, false, false, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+      else k_up_stream<kUpBatch, false, true, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
   }
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
+  if (d.tokens >= kDecodeGroupedDownMin && grouped_path(d)) {
+    // routed and shared down per slot (one output row per dispatch row), then the combine
+    if ((e = launch_grouped_down(d, L, a, a.route.desc, s, repeat)) != hipSuccess) return e;
+    if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
+    return launch_combine(d, L, a, s, ev ? ev + 2 : nullptr, repeat);
+  }
   const int n_rows = d.tokens * d.top_k;
   const int max_u = d.n_experts < n_rows ? d.n_experts : n_rows;
   const size_t act = static_cast<size_t>(n_rows) * (d.inter + 8) * 4 +

@@ -91,6 +91,11 @@ constexpr size_t kCounterBytes = 1024;
 constexpr int kFusedMaxTokens = 8;
 // Decode pipeline limits and the shared expert's gate/up K split.
 constexpr int kDecodeMaxTokens = 16;
+// From this many tokens the decode pipeline runs the grouped down kernel and
+// the combine instead of its fused down + combine kernel.
+constexpr int kDecodeGroupedDownMin = 3;
+// ... and from this many its routed gate/up in the grouped kernel.
+constexpr int kDecodeGroupedUpMin = 8;
 constexpr int kDecodeMaxPositions = 64;
 constexpr size_t kMaxLds = 163840;          // LDS bytes one gfx950 workgroup may use
 constexpr size_t kUpLdsFixed = 2 * 4 * 2 * 64 * 4 * 4 + 8 * 640;   // decode gate/up: reduction + scale tiles
@@ -140,11 +145,12 @@ hipError_t launch_dispatch(const dsk_moe_desc& d, const int32_t* idx, const floa
 
 // Routing of the decode pipeline: the layer's idx / weights [T][k], and for
 // the decode kernels active (count, then the expert of each slot), one
-// descriptor per slot, rowmap [slot][T] (-1: token not routed to the slot)
-// and the route weight of each dispatch row.
+// descriptor per slot, rowmap [slot][T] (-1: token not routed to the slot),
+// the token and route weight of each dispatch row (xrow, wrow) and, for the
+// combine, the dispatch row of each flat position (rank, -1 if dropped).
 struct DecodeRoute {
   int32_t* idx; float* weights;
-  SlotDesc* desc; int32_t* active; int32_t* rowmap; float* wrow;
+  SlotDesc* desc; int32_t* active; int32_t* rowmap; int32_t* xrow; float* wrow; int32_t* rank;
 };
 
 struct ExpertsArgs {
@@ -193,6 +199,18 @@ bool grouped_path(const dsk_moe_desc& d);
 hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                   const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
                                   const hipEvent_t* ev, int repeat);
+// Its kernels one at a time, for the decode pipeline: the routed gate/up
+// alone (from kDecodeGroupedUpMin tokens) and the down (routed rows from h,
+// shared from hs; from kDecodeGroupedDownMin tokens).
+hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                                    const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
+                                    int repeat);
+hipError_t launch_grouped_down(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                               const SlotDesc* desc, hipStream_t s, int repeat);
+// out[t] = cast(sum of the token's routed rows y in ascending expert id +
+// shared); ev (nullable): 1 event after it.
+hipError_t launch_combine(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
+                          const hipEvent_t* ev, int repeat);
 
 // Decode pipeline (decode_pipeline(d)), four kernels:
 //   launch_gate_scores    gate scores (a.scores);

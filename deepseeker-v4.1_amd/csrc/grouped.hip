@@ -284,9 +284,10 @@ bool grouped_path(const dsk_moe_desc& d) {
          up_lds(d) <= kMaxLds && down_lds(d) <= kMaxLds;
 }
 
-hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
-                                  const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
-                                  const hipEvent_t* ev, int repeat) {
+namespace {
+
+GroupedArgs grouped_args(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, const SlotDesc* desc,
+                         const int32_t* xrow, const float* wrow) {
   GroupedArgs p{};
   p.T = d.tokens; p.H = d.hidden; p.I = d.inter; p.Is = d.inter_shared; p.k = d.top_k; p.limit = d.limit;
   p.desc = desc; p.active = a.active; p.xrow = xrow; p.wrow = wrow;
@@ -304,25 +305,62 @@ hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, con
   p.up_shared = d.inter_shared / 16 / kGI;
   p.dn_groups = d.hidden / 16 / kDI;
   p.dn_shared = d.inter_shared > 0 ? p.dn_groups : 0;
-  const int max_slots = d.n_experts < d.tokens * d.top_k ? d.n_experts : d.tokens * d.top_k;
-  const bool q3 = d.quant == DSK_QUANT_Q3;
-  const unsigned up_blocks = static_cast<unsigned>(p.up_shared + max_slots * p.up_groups);
-  const unsigned dn_blocks = static_cast<unsigned>(p.dn_shared + max_slots * p.dn_groups);
-  const size_t ul = up_lds(d), dl = down_lds(d);
+  return p;
+}
+
+int max_slots(const dsk_moe_desc& d) { return d.n_experts < d.tokens * d.top_k ? d.n_experts : d.tokens * d.top_k; }
+
+hipError_t grouped_down(const dsk_moe_desc& d, const GroupedArgs& p, hipStream_t s, int repeat) {
+  const unsigned blocks = static_cast<unsigned>(p.dn_shared + max_slots(d) * p.dn_groups);
+  const size_t lds = down_lds(d);
+  for (int r = 0; r < repeat; ++r) {
+    if (d.quant == DSK_QUANT_Q3) k_down_grouped<RawQ3><<<blocks, kDW * 64, lds, s>>>(p);
+    else k_down_grouped<RawFP4><<<blocks, kDW * 64, lds, s>>>(p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                                  const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
+                                  const hipEvent_t* ev, int repeat) {
+  const GroupedArgs p = grouped_args(d, L, a, desc, xrow, wrow);
+  const unsigned up_blocks = static_cast<unsigned>(p.up_shared + max_slots(d) * p.up_groups);
+  const size_t ul = up_lds(d);
   hipError_t e;
   for (int r = 0; r < repeat; ++r) {
-    if (q3) k_up_grouped<RawQ3><<<up_blocks, kGW * 64, ul, s>>>(p);
+    if (d.quant == DSK_QUANT_Q3) k_up_grouped<RawQ3><<<up_blocks, kGW * 64, ul, s>>>(p);
     else k_up_grouped<RawFP4><<<up_blocks, kGW * 64, ul, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
-  for (int r = 0; r < repeat; ++r) {
-    if (q3) k_down_grouped<RawQ3><<<dn_blocks, kDW * 64, dl, s>>>(p);
-    else k_down_grouped<RawFP4><<<dn_blocks, kDW * 64, dl, s>>>(p);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
+  if ((e = grouped_down(d, p, s, repeat)) != hipSuccess) return e;
   if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
   return hipSuccess;
+}
+
+hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                                    const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
+                                    int repeat) {
+  GroupedArgs p = grouped_args(d, L, a, desc, xrow, wrow);
+  p.up_shared = 0;
+  const unsigned blocks = static_cast<unsigned>(max_slots(d) * p.up_groups);
+  const size_t lds = up_lds(d);
+  for (int r = 0; r < repeat; ++r) {
+    if (d.quant == DSK_QUANT_Q3) k_up_grouped<RawQ3><<<blocks, kGW * 64, lds, s>>>(p);
+    else k_up_grouped<RawFP4><<<blocks, kGW * 64, lds, s>>>(p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_grouped_down(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
+                               const SlotDesc* desc, hipStream_t s, int repeat) {
+  return grouped_down(d, grouped_args(d, L, a, desc, nullptr, nullptr), s, repeat);
 }
 
 }  // namespace dsk
