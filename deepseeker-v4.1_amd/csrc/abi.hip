@@ -288,6 +288,20 @@ int dsk_fp4_dequant(const uint8_t* packed, const uint8_t* scales, int64_t rows, 
                    "dsk_fp4_dequant launch");
 }
 
+int dsk_fp8_block_dequant(const uint8_t* codes, const uint8_t* scales, int64_t rows, int64_t cols, void* out,
+                          int32_t out_dtype, void* stream) {
+  if (!codes || !scales || !out) return fail(DSK_EINVAL, "dsk_fp8_block_dequant: NULL pointer argument");
+  if (rows < 0 || cols < 0 || rows % 32 || cols % 32)
+    return fail(DSK_EINVAL, "rows=%lld and cols=%lld must be multiples of 32", (long long)rows, (long long)cols);
+  if (out_dtype != DSK_DTYPE_F32 && out_dtype != DSK_DTYPE_BF16)
+    return fail(DSK_EINVAL, "out_dtype %d must be F32 or BF16", out_dtype);
+  if (!aligned(codes, 16) || !aligned(out, 16))
+    return fail(DSK_EALIGN, "dsk_fp8_block_dequant: codes and out must be 16-byte aligned");
+  return hip_check(launch_fp8_block_dequant(codes, scales, rows, cols, out, out_dtype,
+                                            static_cast<hipStream_t>(stream)),
+                   "dsk_fp8_block_dequant launch");
+}
+
 int dsk_fp4_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* packed, uint8_t* scales,
                      void* stream) {
   if (!w || !packed || !scales) return fail(DSK_EINVAL, "dsk_fp4_quantize: NULL pointer argument");

@@ -226,6 +226,8 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L,
                                  const ExpertsArgs& a, hipStream_t s, const hipEvent_t* ev,
                                  int repeat);
 
+hipError_t launch_fp8_block_dequant(const uint8_t* codes, const uint8_t* scales, int64_t rows, int64_t cols,
+                                    void* out, int out_dtype, hipStream_t s);
 hipError_t launch_fp4_dequant(const uint8_t* packed, const uint8_t* scales,
                               int64_t rows, int64_t cols, void* out, int out_dtype,
                               hipStream_t s);

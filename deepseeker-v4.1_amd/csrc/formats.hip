@@ -78,6 +78,49 @@ __global__ __launch_bounds__(kThreads) void k_fp4_dequant_bf16(
   for (int q = 0; q < 4; ++q) o[q] = res[q];
 }
 
+// OCP FP8 E4M3 (e4m3fn): sign, 4 exponent bits (bias 7), 3 mantissa bits; no
+// infinities, exponent 15 with mantissa 7 is NaN, exponent 0 is subnormal
+// (m/8 * 2^-6).  Every value times a power of two stays exact in float32.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+  const uint32_t e = (b >> 3) & 0xFu, m = b & 7u;
+  float v;
+  if (e == 15u && m == 7u) v = __builtin_nanf("");
+  else if (e == 0u) v = ldexpf(static_cast<float>(m), -9);
+  else v = ldexpf(static_cast<float>(8u + m), static_cast<int>(e) - 10);
+  return (b & 0x80u) ? -v : v;
+}
+
+// FP8 block dequant: codes [rows, cols] (one byte each) with one E8M0 scale
+// per 32 x 32 block (scales [rows/32, cols/32]); thread = 16 consecutive codes.
+template <bool kBF16>
+__global__ __launch_bounds__(kThreads) void k_fp8_block_dequant(const uint8_t* __restrict__ codes,
+                                                                const uint8_t* __restrict__ scales,
+                                                                int64_t rows, int64_t cols, void* out) {
+  const int64_t chunks = rows * (cols / 16);
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= chunks) return;
+  const int64_t r = i / (cols / 16), c0 = (i % (cols / 16)) * 16;
+  const u32x4 w = *reinterpret_cast<const u32x4*>(codes + r * cols + c0);
+  const float sc = e8m0_to_f32(scales[(r / 32) * (cols / 32) + c0 / 32]);
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+  float v[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) v[q] = e4m3_to_f32((words[q / 4] >> (8 * (q % 4))) & 0xFFu) * sc;
+  if constexpr (kBF16) {
+    uint32_t packed[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      packed[q] = f32_to_bf16_bits(v[2 * q]) | (uint32_t(f32_to_bf16_bits(v[2 * q + 1])) << 16);
+    u32x4* o = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + r * cols + c0);
+    o[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+    o[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
+  } else {
+    f32x4* o = reinterpret_cast<f32x4*>(static_cast<float*>(out) + r * cols + c0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+  }
+}
+
 // Spec quantiser: per 32-group scale 2^ceil(log2(amax/6)), nearest-even e2m1
 // code, saturating at 6, no negative zero.
 __global__ __launch_bounds__(kThreads) void k_fp4_quantize(
@@ -224,6 +267,15 @@ __global__ __launch_bounds__(kThreads) void k_q3_dequant(
 inline unsigned grid_for(int64_t n) { return static_cast<unsigned>((n + kThreads - 1) / kThreads); }
 
 }  // namespace
+
+hipError_t launch_fp8_block_dequant(const uint8_t* codes, const uint8_t* scales, int64_t rows, int64_t cols,
+                                    void* out, int out_dtype, hipStream_t s) {
+  const int64_t chunks = rows * (cols / 16);
+  if (chunks == 0) return hipSuccess;
+  if (out_dtype == DSK_DTYPE_F32) k_fp8_block_dequant<false><<<grid_for(chunks), kThreads, 0, s>>>(codes, scales, rows, cols, out);
+  else k_fp8_block_dequant<true><<<grid_for(chunks), kThreads, 0, s>>>(codes, scales, rows, cols, out);
+  return hipGetLastError();
+}
 
 hipError_t launch_fp4_dequant(const uint8_t* packed, const uint8_t* scales, int64_t rows,
                               int64_t cols, void* out, int out_dtype, hipStream_t s) {

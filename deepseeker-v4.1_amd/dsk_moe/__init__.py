@@ -12,11 +12,12 @@ ctypes on the current HIP stream.
 
 from ._lib import DskError, load as load_library
 from .bank import ResidentBank, SharedExpert
+from .checkpoint import Checkpoint, build_manifest, fp8_block_dequant
 from .layer import MoELayer, moe_layer
 from .stack import MoEStack, rmsnorm
 from .ops import (align_block_size, dispatch, fp4_dequant, fp4_quantize, q3_dequant,
                   q3_quantize, route, workspace_size)
 
-__all__ = ["DskError", "MoELayer", "MoEStack", "ResidentBank", "SharedExpert", "align_block_size",
-           "dispatch", "fp4_dequant", "fp4_quantize", "load_library", "moe_layer",
+__all__ = ["Checkpoint", "DskError", "MoELayer", "MoEStack", "ResidentBank", "SharedExpert", "align_block_size",
+           "build_manifest", "dispatch", "fp4_dequant", "fp8_block_dequant", "fp4_quantize", "load_library", "moe_layer",
            "q3_dequant", "q3_quantize", "rmsnorm", "route", "workspace_size"]

@@ -68,6 +68,7 @@ SIGNATURES = {
     "dsk_fp4_quantize": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "dsk_q3_quantize": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "dsk_q3_dequant": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp]),
+    "dsk_fp8_block_dequant": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _i32, _vp]),
     "dsk_rmsnorm": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, ctypes.c_float, _i32, _vp, _vp, _vp]),
 }
 

@@ -168,6 +168,15 @@ int dsk_moe_forward_timed(const dsk_moe_desc* d, const void* x, const void* gate
 int dsk_fp4_dequant(const uint8_t* packed, const uint8_t* scales, int64_t rows,
                     int64_t cols, void* out, int32_t out_dtype, void* stream);
 
+/* FP8 block dequant of the checkpoint's dense weights (the shared expert):
+ * replaces dequant_fp8_block and E4M3_TABLE (src/deepseeker/mlx_weights.py:29-41,
+ * 82-89).  codes [rows, cols] OCP E4M3 bytes, scales [rows/32, cols/32] E8M0
+ * (one per 32 x 32 block; 0xFF -> NaN) -> out [rows, cols] in out_dtype (f32 or
+ * bf16; exact unless the scaled value leaves the bf16 range).  rows % 32 == 0,
+ * cols % 32 == 0. */
+int dsk_fp8_block_dequant(const uint8_t* codes, const uint8_t* scales, int64_t rows,
+                          int64_t cols, void* out, int32_t out_dtype, void* stream);
+
 /* FP4 quantise (spec rule: scale 2^ceil(log2(amax/6)) per 32, nearest-even
  * e2m1, saturate at 6): stands in for mx.quantize(mode="mxfp4") used by the
  * reference's tests and loaders.  w [rows, cols] f32. */

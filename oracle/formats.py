@@ -31,6 +31,17 @@ Q3 affine (group 64, fp16 scale and bias)
     Parity with MLX's packing and its quantiser rounding is unpinned; the
     layout is pinned by a pack/unpack round trip and a hand-built
     known-answer vector in the tests.
+
+FP8 E4M3 with 32 x 32 block scales (the checkpoint's dense weights, e.g. the
+shared expert)
+    OCP e4m3fn: sign, 4 exponent bits (bias 7), 3 mantissa bits; exponent 15
+    with mantissa 7 is NaN (no infinities, the rest of that row is
+    256 * (1 + m/8)); exponent 0 is subnormal, m/8 * 2**-6.  One E8M0 scale
+    per 32 x 32 block: ``w[i, j] = E4M3[codes[i, j]] * 2**(scales[i//32, j//32] - 127)``.
+    Follows ``src/deepseeker/mlx_weights.py:29-41`` (table) and ``:82-89``
+    (``dequant_fp8_block``).  Pinned by torch's ``float8_e4m3fn`` decode of all
+    256 bytes, the reference's spot values (``tests/test_mlx_weights.py:47-57``)
+    and its seeded block test (``:64-74``, regenerated with numpy).
 """
 
 from __future__ import annotations
@@ -253,3 +264,27 @@ def q3_dequant(packed: np.ndarray, scales: np.ndarray, biases: np.ndarray) -> np
     k = groups * Q3_GROUP
     q = q3_unpack(packed, k).astype(np.float32).reshape(n, groups, Q3_GROUP)
     return ((s[..., None] * q) + b[..., None]).astype(np.float32).reshape(n, k)
+
+
+def _e4m3_table() -> np.ndarray:
+    b = np.arange(256)
+    sign = np.where(b & 0x80, -1.0, 1.0)
+    e = (b >> 3) & 0xF
+    m = (b & 7).astype(np.float64)
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    t = (sign * mag).astype(np.float32)
+    t[(e == 15) & ((b & 7) == 7)] = np.nan
+    return t
+
+
+E4M3_TABLE = _e4m3_table()
+
+
+def fp8_block_dequant(codes: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """[R, C] E4M3 bytes + [R/32, C/32] E8M0 block scales -> float32 [R, C]."""
+    codes = np.asarray(codes, dtype=np.uint8)
+    rows, cols = codes.shape
+    if rows % 32 or cols % 32 or scales.shape != (rows // 32, cols // 32):
+        raise ValueError(f"codes {codes.shape} / scales {scales.shape} do not tile in 32 x 32 blocks")
+    gain = np.repeat(np.repeat(e8m0_to_f32(np.asarray(scales, dtype=np.uint8)), 32, axis=0), 32, axis=1)
+    return (E4M3_TABLE[codes] * gain).astype(np.float32)
