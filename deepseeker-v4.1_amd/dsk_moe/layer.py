@@ -182,6 +182,38 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
     return out
 
 
+def experts_forward(x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor, bank: ResidentBank,
+                    shared: SharedExpert | None = None, *, limit: float = 10.0,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Expert products for a given routing (``dsk_dispatch`` + ``dsk_experts``): the
+    part of ``moe_layer`` after ``route_topk`` (``src/deepseeker/mlx_forward.py:294-419``)
+    with ``idx [T, k]`` int32 expert ids and ``w [T, k]`` float32 route weights
+    supplied by the caller -- e.g. a recorded trace replayed.  Entries of ``idx``
+    outside [0, E) are dropped."""
+    dev = require_device(x, idx, w)
+    t, h = x.shape
+    if idx.dtype != torch.int32 or w.dtype != torch.float32 or idx.shape != w.shape or idx.shape[0] != t:
+        raise ValueError("idx must be int32 [T, k] and w float32 [T, k], with T = x.shape[0]")
+    if bank.hidden != h or (shared is not None and shared.hidden != h):
+        raise ValueError("bank / shared hidden size does not match x")
+    idx, w = idx.contiguous(), w.contiguous()
+    k = idx.shape[1]
+    desc = make_desc(tokens=t, hidden=h, n_experts=bank.n_experts, top_k=k, inter=bank.inter,
+                     inter_shared=shared.inter if shared else 0, quant=bank.quant, x_dtype=x.dtype,
+                     limit=limit)
+    if out is None:
+        out = torch.empty_like(x)
+    from .ops import dispatch as _dispatch
+    d = _dispatch(idx, bank.n_experts)
+    ws = workspace(desc, dev)
+    _lib.call("dsk_experts", ctypes.byref(desc), ptr(bank.table), ptr(shared.w1 if shared else None),
+              ptr(shared.w3 if shared else None), ptr(shared.w2 if shared else None), ptr(None), ptr(x),
+              ptr(w), ptr(d["counts"]), ptr(d["offsets"]), ptr(d["perm"]), ptr(d["rank"]),
+              ptr(d["active"]), ptr(out), ptr(ws), ws.numel(), stream_of(dev))
+    torch.cuda.current_stream(dev).synchronize()   # d's buffers are referenced by raw pointer
+    return out
+
+
 class MoELayer:
     """One resident layer: gate, bank, shared expert and configuration."""
 
@@ -192,9 +224,15 @@ class MoELayer:
         self.top_k, self.score_func, self.route_scale, self.limit = top_k, score_func, route_scale, limit
 
     def __call__(self, x: torch.Tensor, out: torch.Tensor | None = None,
-                 idx: torch.Tensor | None = None, w: torch.Tensor | None = None) -> torch.Tensor:
+                 idx: torch.Tensor | None = None, w: torch.Tensor | None = None,
+                 trace=None, layer_id: int = 0) -> torch.Tensor:
+        """``trace(layer_id, idx, weights)`` (optional, e.g. a ``TraceSink``) receives the
+        routing on the host, in ascending key order like the reference's trace_hook."""
         dev = require_device(x, self.gate_w)
         t, h = x.shape
+        if trace is not None:
+            idx = idx if idx is not None else torch.empty((t, self.top_k), dtype=torch.int32, device=dev)
+            w = w if w is not None else torch.empty((t, self.top_k), dtype=torch.float32, device=dev)
         desc = make_desc(tokens=t, hidden=h, n_experts=self.bank.n_experts, top_k=self.top_k,
                          inter=self.bank.inter, inter_shared=self.shared.inter if self.shared else 0,
                          score_func=self.score_func, quant=self.bank.quant, x_dtype=x.dtype,
@@ -208,4 +246,6 @@ class MoELayer:
                   ptr(self.bank.table), ptr(s.w1 if s else None), ptr(s.w3 if s else None),
                   ptr(s.w2 if s else None), ptr(None), ptr(out), ptr(idx), ptr(w), ptr(ws),
                   ws.numel(), stream_of(dev))
+        if trace is not None:
+            trace(layer_id, idx.flip(1).tolist(), w.flip(1).tolist())
         return out

@@ -61,9 +61,11 @@ class MoEStack:
         return torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)   # h, y, d
 
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None, bufs=None,
-                record: list | None = None) -> torch.Tensor:
+                record: list | None = None, trace=None) -> torch.Tensor:
         """h_L for input rows x [T, H].  ``record`` (optional list) receives, per
-        layer, copies of (h_l, rmsnorm(h_l), idx_l, layer output)."""
+        layer, copies of (h_l, rmsnorm(h_l), idx_l, layer output); ``trace``
+        (optional, e.g. a ``TraceSink``) receives every layer's routing as
+        ``trace(layer, idx, weights)`` on the host."""
         h, y, d = bufs if bufs is not None else self._buffers(x)
         if out is None:
             out = torch.empty_like(x)
@@ -77,7 +79,7 @@ class MoEStack:
                 prev = h
             if record is not None:
                 idx = torch.empty((x.shape[0], layer.top_k), dtype=torch.int32, device=x.device)
-            layer(y, out=d, idx=idx)
+            layer(y, out=d, idx=idx, trace=trace, layer_id=l)
             if record is not None:
                 record.append((prev.clone(), y.clone(), idx, d.clone()))
         rmsnorm(prev, self.eps, residual=d, h_out=out, out=False)
