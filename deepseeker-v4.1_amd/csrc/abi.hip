@@ -315,7 +315,8 @@ int dsk_fp4_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* packed
 int dsk_q3_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* packed, uint16_t* scales,
                     uint16_t* biases, void* stream) {
   if (!w || !packed || !scales || !biases) return fail(DSK_EINVAL, "dsk_q3_quantize: NULL pointer argument");
-  if (rows < 0 || cols < 0 || cols % 128) return fail(DSK_EINVAL, "cols=%lld must be a multiple of 128", (long long)cols);
+  if (rows < 0 || cols < 0 || cols % 128 || cols > INT32_MAX)
+    return fail(DSK_EINVAL, "cols=%lld must be a multiple of 128 below 2^31", (long long)cols);
   if (!aligned(w, 4) || !aligned(packed, 4) || !aligned(scales, 2) || !aligned(biases, 2))
     return fail(DSK_EALIGN, "dsk_q3_quantize: misaligned pointer");
   return hip_check(launch_q3_quantize(w, rows, cols, packed, scales, biases,
@@ -326,7 +327,8 @@ int dsk_q3_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* packed,
 int dsk_q3_dequant(const uint8_t* packed, const uint16_t* scales, const uint16_t* biases,
                    int64_t rows, int64_t cols, void* out, int32_t out_dtype, void* stream) {
   if (!packed || !scales || !biases || !out) return fail(DSK_EINVAL, "dsk_q3_dequant: NULL pointer argument");
-  if (rows < 0 || cols < 0 || cols % 128) return fail(DSK_EINVAL, "cols=%lld must be a multiple of 128", (long long)cols);
+  if (rows < 0 || cols < 0 || cols % 128 || cols > INT32_MAX)
+    return fail(DSK_EINVAL, "cols=%lld must be a multiple of 128 below 2^31", (long long)cols);
   if (out_dtype != DSK_DTYPE_F32 && out_dtype != DSK_DTYPE_BF16)
     return fail(DSK_EINVAL, "out_dtype %d must be F32 or BF16", out_dtype);
   if (!aligned(packed, 4) || !aligned(out, 4))

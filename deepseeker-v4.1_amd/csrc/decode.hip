@@ -332,7 +332,7 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
 #pragma unroll
         for (int i = 0; i < G; ++i) {
           const bool ok = rok && kb + i < k1;
-          const int64_t off = code_row + (kb + i) * 48 + g4 * 12;
+          const int64_t off = code_row + q3_chunk_offset(K, kb + i, g4);
           const auto c1 = gptr<uint32_t>(W1 + off);
           const auto c3 = gptr<uint32_t>(W3 + off);
 #pragma unroll
@@ -433,6 +433,290 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
     const int64_t off = static_cast<int64_t>(drow) * p.I + rt * 16 + 4 * g4;
     *reinterpret_cast<uint2*>(p.h_hi + off) = uint2{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16)};
     *reinterpret_cast<uint2*>(p.h_lo + off) = uint2{hl[0] | (uint32_t(hl[1]) << 16), hl[2] | (uint32_t(hl[3]) << 16)};
+  }
+}
+
+// ---------------------------------------------------------------- q3 gate/up, factored
+// Tokens of the factored q3 gate/up (A operand row 2t + h for t < 8).
+constexpr int kQ3fMaxTokens = 8;
+
+// One activation chunk (8 values of token t, chunk cc of its row) for the
+// factored q3 product: the values at 8q code positions divided by 8 (exact),
+// as bf16 plane(s); the chunk's sum(x) and sum(x / m) are reduced over the 8
+// lanes of its 64-group (fixed order) and written to xsum[kb][t][h] =
+// {sum x, sum x / m}.  All lanes of an aligned 8-lane group call it together.
+template <bool kF32>
+__device__ __forceinline__ void stage_chunk_q3(uint16_t* xh, uint16_t* xl, float* xsum, int xs, int cpr, int c,
+                                               const u32x4& v0, const u32x4& v1) {
+  const int t = c / cpr, cc = c % cpr;
+  const uint32_t div8 = q3m_div8_pairs(cc & 3);
+  float f[8];
+  if constexpr (!kF32) {
+    const uint32_t w[4] = {v0.x, v0.y, v0.z, v0.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else {
+    const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = __uint_as_float(w[i]);
+  }
+  uint16_t h[8], l[8];
+  float sx = 0.0f, sxm = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const bool d8 = (div8 >> (e >> 1)) & 1u;
+    const float sc = d8 ? 0.125f : 1.0f, m = d8 ? 8.0f : 1.0f;
+    if constexpr (!kF32) {
+      h[e] = f32_to_bf16_bits(f[e] * sc);
+      sx += f[e];
+      sxm += f[e] * sc;
+    } else {
+      split_bf16(f[e] * sc, h[e], l[e]);
+      const float v = bf16_bits_to_f32(h[e]) + bf16_bits_to_f32(l[e]);   // what the MFMA sees
+      sx += v * m;
+      sxm += v;
+    }
+  }
+  const int off = t * xs + cc * 8;
+  *reinterpret_cast<u32x4*>(xh + off) = pack_bf16x8(h);
+  if constexpr (kF32) *reinterpret_cast<u32x4*>(xl + off) = pack_bf16x8(l);
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) {
+    sx += __shfl_xor(sx, o, 8);
+    sxm += __shfl_xor(sxm, o, 8);
+  }
+  if ((cc & 7) == 0) {
+    const int gi = cc >> 3;
+    *reinterpret_cast<float2*>(xsum + (((gi >> 1) * kQ3fMaxTokens + t) * 2 + (gi & 1)) * 2) = float2{sx, sxm};
+  }
+}
+
+// One batch of G K blocks of a wave's q3 gate and up rows: three code words
+// per lane, block and role, and the (scale, bias) pairs of the block's two
+// 64-groups per role (sb: S1, B1, S3, B3; low half = first group).
+template <int G>
+struct Q3Batch {
+  uint32_t c1[G][3], c3[G][3];
+  uint32_t sb[4][G];
+};
+
+// acc[t] += s * (d - 128 * sum(x / m)) + b * sum(x) over the block's two
+// groups h = 0, 1: d[2t' + h] is the MFMA output of token row 2t' + h of this
+// lane, xa / xb = xsum of its two tokens {sum x, sum x / m} x {h = 0, 1}.
+__device__ __forceinline__ void q3_factor(const f32x4& d, uint32_t s, uint32_t b, const f32x4& xa,
+                                          const f32x4& xb, float (&acc)[2]) {
+  acc[0] = fmaf(f16_half<0>(s), fmaf(-128.0f, xa.y, d[0]), acc[0]);
+  acc[0] = fmaf(f16_half<0>(b), xa.x, acc[0]);
+  acc[0] = fmaf(f16_half<1>(s), fmaf(-128.0f, xa.w, d[1]), acc[0]);
+  acc[0] = fmaf(f16_half<1>(b), xa.z, acc[0]);
+  acc[1] = fmaf(f16_half<0>(s), fmaf(-128.0f, xb.y, d[2]), acc[1]);
+  acc[1] = fmaf(f16_half<0>(b), xb.x, acc[1]);
+  acc[1] = fmaf(f16_half<1>(s), fmaf(-128.0f, xb.w, d[3]), acc[1]);
+  acc[1] = fmaf(f16_half<1>(b), xb.z, acc[1]);
+}
+
+// Routed gate/up of the decode pipeline for q3 experts (T <= 8), factored
+// (see q3m_pair): the codes go into the MFMA as exact bf16 integers and each
+// 64-group's scale and bias are applied once per K block to the MFMA output,
+// about a fifth of the vector instructions of dequantising every weight.  The
+// activations are the A operand (row 2t + h: token t restricted to the K
+// block's h-th 64-group, zero elsewhere -- lane groups 0, 1 of a block hold
+// group 0, lane groups 2, 3 group 1), the weights the B operand (column =
+// weight row), so a 16x16x32 MFMA covers both groups of a block for up to 8
+// tokens and a lane's outputs are one weight row of tokens 2g, 2g + 1.
+// Block shape, K split, batches in flight and the K-range reduction order
+// are those of k_up_stream.
+template <bool kWin, bool kF32>
+__global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 || !kWin ? 3 : 4))) void k_up_q3(DecodeArgs p) {
+  constexpr int G = kUpBatch;
+  extern __shared__ __align__(16) uint16_t lds_up[];
+  const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int groups = (p.up_tiles + kUpItems - 1) / kUpItems;
+  const int rb = static_cast<int>(blockIdx.x);
+  const int slot = rb / groups;
+  if (slot >= p.active[0]) return;
+  const int T = p.T, K = p.H;
+  const int item = wave / kUpKS, ks = wave % kUpKS;
+  const int rt = (rb % groups) * kUpItems + item;
+  const bool rok = rt < p.up_tiles;
+  // this lane's A operand row: token ta, group half ha
+  const int ta = r16 >> 1;
+  const int drow_a = ta < T ? p.rowmap[slot * T + ta] : -1;
+  const bool av = drow_a >= 0 && (r16 & 1) == (g4 >> 1);
+  // this lane's output tokens
+  const int t0 = 2 * g4;
+  const int drow0 = t0 < T ? p.rowmap[slot * T + t0] : -1;
+  const int drow1 = t0 + 1 < T ? p.rowmap[slot * T + t0 + 1] : -1;
+  const int xs = K + 8, nblk = K / 128, cpr = K / 8, xchunks = T * cpr;
+  constexpr int NT = kUpW * 64;
+  uint16_t* xh = lds_up;
+  uint16_t* xl = lds_up + T * xs;
+  float* xsum = reinterpret_cast<float*>(lds_up + (kF32 ? 2 : 1) * T * xs);   // [nblk][8][2][2]
+  float (*red)[kUpKS][2][64][2] = reinterpret_cast<float (*)[kUpKS][2][64][2]>(xsum + nblk * kQ3fMaxTokens * 4);
+  const uint16_t* zero = reinterpret_cast<const uint16_t*>(red + kUpItems);   // 64 zero bytes
+  if (tid < 4) reinterpret_cast<u32x4*>(red + kUpItems)[tid] = u32x4{0u, 0u, 0u, 0u};
+  // activations: into registers when they fit (staged after the weight loads are issued)
+  const bool xreg = xchunks <= NT;
+  u32x4 xv0{}, xv1{};
+  if (xreg) {
+    if (tid < xchunks) {
+      const int64_t e = static_cast<int64_t>(tid / cpr) * K + (tid % cpr) * 8;
+      if constexpr (!kF32) {
+        xv0 = ldg16(static_cast<const uint16_t*>(p.x) + e);
+      } else {
+        xv0 = ldg16(static_cast<const float*>(p.x) + e);
+        xv1 = ldg16(static_cast<const float*>(p.x) + e + 4);
+      }
+    }
+  } else {
+    for (int c0 = 0; c0 < xchunks; c0 += NT) {   // xchunks is a multiple of 8: whole lane groups
+      const int c = c0 + tid;
+      if (c < xchunks) {
+        const int64_t e = static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8;
+        u32x4 v0, v1{};
+        if constexpr (!kF32) {
+          v0 = ldg16(static_cast<const uint16_t*>(p.x) + e);
+        } else {
+          v0 = ldg16(static_cast<const float*>(p.x) + e);
+          v1 = ldg16(static_cast<const float*>(p.x) + e + 4);
+        }
+        stage_chunk_q3<kF32>(xh, xl, xsum, xs, cpr, c, v0, v1);
+      }
+    }
+  }
+  const SlotDesc* d = p.desc + slot;
+  const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
+  const int per = (nblk + kUpKS - 1) / kUpKS;
+  const int k0 = min(ks * per, nblk), k1 = min(k0 + per, nblk);
+  const uint8_t* W1 = static_cast<const uint8_t*>(d->p[0]);
+  const uint8_t* W3 = static_cast<const uint8_t*>(d->p[3]);
+  const uint8_t* SB[4] = {static_cast<const uint8_t*>(d->p[1]), static_cast<const uint8_t*>(d->p[2]),
+                          static_cast<const uint8_t*>(d->p[4]), static_cast<const uint8_t*>(d->p[5])};
+  const uint32_t code_row = row * static_cast<uint32_t>(K / 8 * 3);
+  const uint32_t sb_row = row * static_cast<uint32_t>(K / 64) * 2;   // bytes
+  auto ld = [&](Q3Batch<G>& b, int kb0) {
+    if constexpr (kWin) {
+      // a batch is one 512-code superblock: this lane group's chunks of its
+      // 4 blocks are 48 contiguous bytes
+      const bool ok = rok && kb0 < k1;
+      const uint32_t off = code_row + (kb0 >> 2) * 192 + 48 * g4;
+      const auto c1 = gptr<u32x4>(W1 + off);
+      const auto c3 = gptr<u32x4>(W3 + off);
+#pragma unroll
+      for (int v = 0; v < 3; ++v) {
+        const u32x4 a = ok ? c1[v] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 e = ok ? c3[v] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          b.c1[(4 * v + j) / 3][(4 * v + j) % 3] = a[j];
+          b.c3[(4 * v + j) / 3][(4 * v + j) % 3] = e[j];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const bool ok = rok && kb0 + i < k1;
+        const uint32_t off = code_row + q3_chunk_offset(K, kb0 + i, g4);
+        const auto c1 = gptr<uint32_t>(W1 + off);
+        const auto c3 = gptr<uint32_t>(W3 + off);
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+          b.c1[i][q] = ok ? c1[q] : 0u;
+          b.c3[i][q] = ok ? c3[q] : 0u;
+        }
+      }
+    }
+    if constexpr (kWin) {
+      // one 16-byte window per array: the 8 groups of the batch's 4 blocks
+      const bool ok = rok && kb0 < k1;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const u32x4 w = ok ? ldg16(SB[a] + sb_row + kb0 * 4) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < G; ++i) b.sb[a][i] = w[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const bool ok = rok && kb0 + i < k1;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) b.sb[a][i] = ok ? ldg<uint32_t>(SB[a] + sb_row + (kb0 + i) * 4) : 0u;
+      }
+    }
+  };
+  Q3Batch<G> A, B;
+  ld(A, k0);
+  ld(B, k0 + G);
+  if (xreg && tid < xchunks) stage_chunk_q3<kF32>(xh, xl, xsum, xs, cpr, tid, xv0, xv1);   // whole lane groups
+  const float wr0 = drow0 >= 0 ? p.wrow[drow0] : 0.0f;
+  const float wr1 = drow1 >= 0 ? p.wrow[drow1] : 0.0f;
+  __syncthreads();
+  float acc1[2] = {0.0f, 0.0f}, acc3[2] = {0.0f, 0.0f};
+  const Q3Masks km = q3_masks();
+  auto mm = [&](const Q3Batch<G>& b, int kb0) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int kb = kb0 + i;
+      if (kb >= k1) break;   // wave-uniform; blocks past the range must add nothing
+      const int ao = ta * xs + kb * 128 + 32 * g4;
+      const uint16_t* ah = av ? xh + ao : zero;
+      f32x4 d1 = {0.0f, 0.0f, 0.0f, 0.0f}, d3 = d1;
+#define DSK_Q3F_STEP(M)                                                             \
+      {                                                                            \
+        const bf16x8 xa = as_bf16x8(*reinterpret_cast<const u32x4*>(ah + 8 * M)); \
+        d1 = mfma16(xa, q3m_operand<M>(b.c1[i], km), d1);                              \
+        d3 = mfma16(xa, q3m_operand<M>(b.c3[i], km), d3);                              \
+        if constexpr (kF32) {                                                      \
+          const uint16_t* al = av ? xl + ao : zero;                                \
+          const bf16x8 xb = as_bf16x8(*reinterpret_cast<const u32x4*>(al + 8 * M)); \
+          d1 = mfma16(xb, q3m_operand<M>(b.c1[i], km), d1);                            \
+          d3 = mfma16(xb, q3m_operand<M>(b.c3[i], km), d3);                            \
+        }                                                                          \
+      }
+      DSK_Q3F_STEP(0) DSK_Q3F_STEP(1) DSK_Q3F_STEP(2) DSK_Q3F_STEP(3)
+#undef DSK_Q3F_STEP
+      const float* xg = xsum + (kb * kQ3fMaxTokens + t0) * 4;
+      const f32x4 xa = *reinterpret_cast<const f32x4*>(xg);
+      const f32x4 xb = *reinterpret_cast<const f32x4*>(xg + 4);
+      q3_factor(d1, b.sb[0][i], b.sb[1][i], xa, xb, acc1);
+      q3_factor(d3, b.sb[2][i], b.sb[3][i], xa, xb, acc3);
+    }
+  };
+  for (int kb = k0; kb < k1; kb += 2 * G) {
+    mm(A, kb);
+    if (kb + 2 * G < k1) ld(A, kb + 2 * G);
+    if (kb + G < k1) mm(B, kb + G);
+    if (kb + 3 * G < k1) ld(B, kb + 3 * G);
+  }
+  // K ranges added in order: ((r0 + r1) + r2) + r3
+  *reinterpret_cast<float2*>(&red[item][ks][0][lane][0]) = float2{acc1[0], acc1[1]};
+  *reinterpret_cast<float2*>(&red[item][ks][1][lane][0]) = float2{acc3[0], acc3[1]};
+  __syncthreads();
+  if (ks == 0 && rok && (drow0 >= 0 || drow1 >= 0)) {
+#pragma unroll
+    for (int w = 1; w < kUpKS; ++w) {
+      const float2 g = *reinterpret_cast<const float2*>(&red[item][w][0][lane][0]);
+      const float2 u = *reinterpret_cast<const float2*>(&red[item][w][1][lane][0]);
+      acc1[0] += g.x; acc1[1] += g.y;
+      acc3[0] += u.x; acc3[1] += u.y;
+    }
+    const int n = rt * 16 + r16;
+    if (drow0 >= 0) {
+      uint16_t hh, hl;
+      split_bf16(silu_clamped(acc1[0], acc3[0], p.limit) * wr0, hh, hl);
+      p.h_hi[static_cast<int64_t>(drow0) * p.I + n] = hh;
+      p.h_lo[static_cast<int64_t>(drow0) * p.I + n] = hl;
+    }
+    if (drow1 >= 0) {
+      uint16_t hh, hl;
+      split_bf16(silu_clamped(acc1[1], acc3[1], p.limit) * wr1, hh, hl);
+      p.h_hi[static_cast<int64_t>(drow1) * p.I + n] = hh;
+      p.h_lo[static_cast<int64_t>(drow1) * p.I + n] = hl;
+    }
   }
 }
 
@@ -737,6 +1021,13 @@ size_t up_lds_bytes(const DecodeArgs& p) {
   return static_cast<size_t>(p.x_f32 ? 2 : 1) * p.T * (p.H + 8) * 2 + kUpLdsFixed;
 }
 
+// k_up_q3: activation plane(s), xsum [H/128][8][2][2] f32, K-range partial
+// sums [kUpItems][kUpKS][2][64][2] f32, 64 zero bytes.
+size_t up_q3_lds_bytes(const DecodeArgs& p) {
+  return static_cast<size_t>(p.x_f32 ? 2 : 1) * p.T * (p.H + 8) * 2 +
+         static_cast<size_t>(p.H / 128) * kQ3fMaxTokens * 16 + kUpItems * kUpKS * 2 * 64 * 2 * 4 + 64;
+}
+
 static_assert(sizeof(BlockRoute) <= kUpLdsFixed, "routing block state must fit the gate/up LDS");
 
 }  // namespace
@@ -773,8 +1064,15 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
     e = launch_grouped_up_routed(d, L, a, a.route.desc, a.route.xrow, a.route.wrow, s, repeat);
     if (e != hipSuccess) return e;
   } else {
+    // q3 up to 8 tokens: the factored kernel
+    const size_t q3f_lds = up_q3_lds_bytes(p);
+    const bool q3f = q3 && d.tokens <= kQ3fMaxTokens && q3f_lds <= kMaxLds;
     for (int r = 0; r < repeat; ++r) {
-      if (q3 && q3win && !p.x_f32) k_up_stream<kUpBatch, true, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+      if (q3f && q3win && !p.x_f32) k_up_q3<true, false><<<up_blocks, kUpW * 64, q3f_lds, s>>>(p);
+      else if (q3f && q3win) k_up_q3<true, true><<<up_blocks, kUpW * 64, q3f_lds, s>>>(p);
+      else if (q3f && !p.x_f32) k_up_q3<false, false><<<up_blocks, kUpW * 64, q3f_lds, s>>>(p);
+      else if (q3f) k_up_q3<false, true><<<up_blocks, kUpW * 64, q3f_lds, s>>>(p);
+      else if (q3 && q3win && !p.x_f32) k_up_stream<kUpBatch, true, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
       else if (q3 && q3win) k_up_stream<kUpBatch, true, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
       else if (q3 && !p.x_f32) k_up_stream<kUpBatch, false, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
       else if (q3) k_up_stream<kUpBatch, false, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);

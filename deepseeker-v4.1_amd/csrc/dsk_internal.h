@@ -50,6 +50,17 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t b) {
   return __uint_as_float(bits);
 }
 
+// Byte offset, within a row of a q3 role, of lane group g's 12 bytes (its 32
+// codes 128*kb + 32*g + [0, 32)) of 128-code block kb.  Every full 512-code
+// superblock (4 blocks, 192 bytes) holds lane group g's chunks of its 4 blocks
+// contiguously at byte 48*g, in block order, so one lane reads 4 blocks as
+// three 16-byte words; blocks after the last full superblock are plain
+// 48-byte blocks (chunk g at byte 12*g).
+__host__ __device__ __forceinline__ uint32_t q3_chunk_offset(int K, int kb, int g) {
+  return (kb >> 2) < (K >> 9) ? static_cast<uint32_t>((kb >> 2) * 192 + 48 * g + 12 * (kb & 3))
+                              : static_cast<uint32_t>(kb * 48 + 12 * g);
+}
+
 // ---------------------------------------------------------------- dispatch
 // One active expert, written by the dispatch for the expert kernels.
 struct SlotDesc {

@@ -190,7 +190,7 @@ __device__ __forceinline__ void q3_block_codes(const uint32_t* wds /*[4][3]*/, u
 
 // One thread per 128-code block of one row.
 __global__ __launch_bounds__(kThreads) void k_q3_quantize(
-    const float* __restrict__ w, int64_t blocks, uint8_t* __restrict__ packed,
+    const float* __restrict__ w, int64_t blocks, int cols, uint8_t* __restrict__ packed,
     uint16_t* __restrict__ scales, uint16_t* __restrict__ biases) {
   int64_t b = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (b >= blocks) return;
@@ -235,21 +235,31 @@ __global__ __launch_bounds__(kThreads) void k_q3_quantize(
       }
     }
   }
-  uint32_t* dst = reinterpret_cast<uint32_t*>(packed + b * 48);
+  const int nbk = cols / 128;
+  uint8_t* row = packed + (b / nbk) * (cols / 8 * 3);
 #pragma unroll
-  for (int i = 0; i < 12; ++i) dst[i] = wds[i];
+  for (int g = 0; g < 4; ++g) {
+    uint32_t* dst = reinterpret_cast<uint32_t*>(row + q3_chunk_offset(cols, static_cast<int>(b % nbk), g));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) dst[i] = wds[3 * g + i];
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void k_q3_dequant(
     const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scales,
-    const uint16_t* __restrict__ biases, int64_t blocks, int out_bf16,
+    const uint16_t* __restrict__ biases, int64_t blocks, int cols, int out_bf16,
     void* __restrict__ out) {
   int64_t b = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (b >= blocks) return;
   uint32_t wds[12];
-  const uint32_t* src = reinterpret_cast<const uint32_t*>(packed + b * 48);
+  const int nbk = cols / 128;
+  const uint8_t* row = packed + (b / nbk) * (cols / 8 * 3);
 #pragma unroll
-  for (int i = 0; i < 12; ++i) wds[i] = src[i];
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(row + q3_chunk_offset(cols, static_cast<int>(b % nbk), g));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) wds[3 * g + i] = src[i];
+  }
   uint8_t q[128];
   q3_block_codes(wds, q);
   float s[2] = {f16_bits_to_f32(scales[2 * b]), f16_bits_to_f32(scales[2 * b + 1])};
@@ -302,7 +312,7 @@ hipError_t launch_q3_quantize(const float* w, int64_t rows, int64_t cols, uint8_
                               uint16_t* scales, uint16_t* biases, hipStream_t s) {
   int64_t blocks = rows * (cols / 128);
   if (blocks == 0) return hipSuccess;
-  k_q3_quantize<<<grid_for(blocks), kThreads, 0, s>>>(w, blocks, packed, scales, biases);
+  k_q3_quantize<<<grid_for(blocks), kThreads, 0, s>>>(w, blocks, static_cast<int>(cols), packed, scales, biases);
   return hipGetLastError();
 }
 
@@ -311,7 +321,7 @@ hipError_t launch_q3_dequant(const uint8_t* packed, const uint16_t* scales,
                              int out_dtype, hipStream_t s) {
   int64_t blocks = rows * (cols / 128);
   if (blocks == 0) return hipSuccess;
-  k_q3_dequant<<<grid_for(blocks), kThreads, 0, s>>>(packed, scales, biases, blocks,
+  k_q3_dequant<<<grid_for(blocks), kThreads, 0, s>>>(packed, scales, biases, blocks, static_cast<int>(cols),
                                                      out_dtype == DSK_DTYPE_BF16, out);
   return hipGetLastError();
 }

@@ -79,12 +79,12 @@ struct StageBF16 {
 };
 
 // q3: a stage is half of a 128-code block and exactly one 64-group; half hf
-// of it is lane group 2 (st & 1) + hf of the canonical layout (12 bytes).
+// of it is lane group 2 (st & 1) + hf of the block (12 bytes).
 struct StageQ3 {
   RawQ3 r;
   __device__ __forceinline__ void load(const uint8_t* W, const uint16_t* S, const uint16_t* B,
                                        int64_t row, int K, int st, int hf) {
-    const auto src = gptr<uint32_t>(W + row * (K / 8 * 3) + (st >> 1) * 48 + (2 * (st & 1) + hf) * 12);
+    const auto src = gptr<uint32_t>(W + row * (K / 8 * 3) + q3_chunk_offset(K, st >> 1, 2 * (st & 1) + hf));
     r.w[0] = src[0]; r.w[1] = src[1]; r.w[2] = src[2];
     const int64_t gi = row * (K / 64) + st;
     r.sb = static_cast<uint32_t>(ldg<uint16_t>(S + gi)) | (static_cast<uint32_t>(ldg<uint16_t>(B + gi)) << 16);

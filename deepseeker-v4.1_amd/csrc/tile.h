@@ -68,18 +68,18 @@ __device__ __forceinline__ void load_raw(RawBF16& r, const uint16_t* W, int64_t 
   for (int j = 0; j < 4; ++j) r.v[j] = ok ? ldg16(W + row * K + kc + 8 * j) : u32x4{0u, 0u, 0u, 0u};
 }
 
-// q3 affine (group 64, fp16 scale / bias) in the canonical layout: a
-// 128-code block of a row is 48 bytes, lane group g's 12 bytes (three LE
-// words) hold its 32 codes 32g + 8m + j as pairs P = 4m + j/2 -- P < 15 at
-// bits 3(P%5) / 16 + 3(P%5) of word P/5, pair 15 in bits 15 / 31 of the
-// three words.  A lane's 32 codes lie in one 64-group, so one scale and one
-// bias per lane and block.
+// q3 affine (group 64, fp16 scale / bias) in the canonical layout: lane group
+// g's 12 bytes (three LE words, placed by q3_chunk_offset) of a 128-code block
+// hold its 32 codes 32g + 8m + j as pairs P = 4m + j/2 -- P < 15 at bits
+// 3(P%5) / 16 + 3(P%5) of word P/5, pair 15 in bits 15 / 31 of the three
+// words.  A lane's 32 codes lie in one 64-group, so one scale and one bias per
+// lane and block.
 struct RawQ3 { uint32_t w[3]; uint32_t sb; };   // sb: fp16 scale (low), fp16 bias (high)
 
 __device__ __forceinline__ void load_raw(RawQ3& r, const uint8_t* W, const uint16_t* S, const uint16_t* B,
                                          int64_t row, int K, int kc, bool ok) {
   if (ok) {
-    const auto src = gptr<uint32_t>(W + row * (K / 8 * 3) + (kc >> 7) * 48 + ((kc >> 5) & 3) * 12);
+    const auto src = gptr<uint32_t>(W + row * (K / 8 * 3) + q3_chunk_offset(K, kc >> 7, (kc >> 5) & 3));
     r.w[0] = src[0]; r.w[1] = src[1]; r.w[2] = src[2];
     const int64_t gi = row * (K / 64) + kc / 64;
     r.sb = static_cast<uint32_t>(ldg<uint16_t>(S + gi)) | (static_cast<uint32_t>(ldg<uint16_t>(B + gi)) << 16);
@@ -166,6 +166,68 @@ __device__ __forceinline__ bf16x8 q3_operand(const RawQ3& r) {
 
 __device__ __forceinline__ bf16x8 a_operand(const RawQ3& r, int j) {
   return j == 0 ? q3_operand<0>(r) : (j == 1 ? q3_operand<1>(r) : (j == 2 ? q3_operand<2>(r) : q3_operand<3>(r)));
+}
+
+// Factored q3 product.  Per 64-group, x . W = s * sum(q x) + b * sum(x), so
+// the MFMA can take the raw codes and the group's scale and bias are applied
+// to its output.  A code pair masked into the low mantissa bits of 128.0
+// (bf16 0x4300, ulp 1) is an exact bf16 integer: 128 + q for a code at bits
+// 0..2 of its half, 128 + 8q for one at bits 3..5 (pairs with P % 5 == 1 or 3
+// are used unshifted).  The activations at the 8q positions are staged
+// divided by 8, so every product is (128 + m q) * (x / m), exact, and the
+// MFMA sum over a group is sum(q x) + 128 * sum(x / m).
+
+// Masks of the code pairs at bits 0..2 / 16..18 and 3..5 / 19..21 in VGPRs
+// and the magic in an SGPR, as values the compiler cannot see through: with a
+// literal mask and a literal magic it splits every (d & m) | magic into two
+// instructions (a VOP3 encoding holds no literal here), with these it emits
+// one v_and_or_b32.  (Writing v_and_or_b32 as inline assembly instead would
+// hide a VALU write from the hazard checks, and an MFMA reading its result
+// needs wait states the compiler then does not insert.)
+struct Q3Masks { uint32_t m7, m38, magic; };
+
+__device__ __forceinline__ Q3Masks q3_masks() {
+  Q3Masks k;
+  asm volatile("v_mov_b32 %0, 0x70007" : "=v"(k.m7));
+  asm volatile("v_mov_b32 %0, 0x380038" : "=v"(k.m38));
+  asm volatile("s_mov_b32 %0, 0x43004300" : "=s"(k.magic));
+  return k;
+}
+
+template <int P>
+__device__ __forceinline__ uint32_t q3m_pair(const uint32_t (&w)[3], const Q3Masks& k) {
+  if constexpr (P < 15) {
+    constexpr int s = P % 5;
+    const uint32_t d = w[P / 5];
+    if constexpr (s == 0) return (d & k.m7) | k.magic;
+    else if constexpr (s == 1) return (d & k.m38) | k.magic;
+    else if constexpr (s == 2) return ((d >> 6) & k.m7) | k.magic;
+    else if constexpr (s == 3) return ((d >> 6) & k.m38) | k.magic;
+    else return ((d >> 12) & k.m7) | k.magic;
+  } else {
+    // bit t of pair 15's codes is bit 15 / 31 of word t
+    const uint32_t a = w[0] >> 15, b = w[1] >> 14, c = w[2] >> 13;
+    const uint32_t ab = (a & 0x00010001u) | (b & ~0x00010001u);
+    const uint32_t abc = (ab & 0x00030003u) | (c & ~0x00030003u);
+    return (abc & k.m7) | k.magic;
+  }
+}
+
+// MFMA step m's operand (pairs 4m .. 4m+3) of a lane's 32 codes.
+template <int M>
+__device__ __forceinline__ bf16x8 q3m_operand(const uint32_t (&w)[3], const Q3Masks& k) {
+  return as_bf16x8(u32x4{q3m_pair<4 * M>(w, k), q3m_pair<4 * M + 1>(w, k), q3m_pair<4 * M + 2>(w, k),
+                         q3m_pair<4 * M + 3>(w, k)});
+}
+
+// Bit i set: pair 4m + i of MFMA step m comes out as 128 + 8q (its two
+// activations are staged divided by 8).  Steps 0..3: pairs {1,3}, {6}, {8,11}, {13}.
+__device__ __forceinline__ uint32_t q3m_div8_pairs(int m) { return (0x294Au >> (4 * m)) & 0xFu; }
+
+// Half h of a packed fp16 pair as float (folds into v_fma_mix_f32).
+template <int H>
+__device__ __forceinline__ float f16_half(uint32_t v) {
+  return static_cast<float>(__builtin_bit_cast(f16x2, v)[H]);
 }
 
 // Load one role (0: w1, 1: w3, 2: w2) of an expert from its 9 descriptor

@@ -27,7 +27,8 @@ Q3 affine (group 64, fp16 scale and bias)
     ``[N, K/64] f16`` as in the reference (``src/deepseeker/mlx_weights.py:119-145``;
     ``scripts/requant_experts_3bit.py:69-83``).  The reference's code packing is
     MLX-internal and not visible, so the codes use this build's canonical
-    layout (3 bits per code, 48 bytes per 128 codes): see ``q3_pack``.
+    layout (3 bits per code, 48 bytes per 128 codes, lane-group chunks of 4
+    blocks interleaved per 512 codes): see ``q3_pack``.
     Parity with MLX's packing and its quantiser rounding is unpinned; the
     layout is pinned by a pack/unpack round trip and a hand-built
     known-answer vector in the tests.
@@ -56,8 +57,10 @@ FP4_TABLE = np.array(
 FP4_GROUP = 32
 Q3_GROUP = 64
 Q3_BITS = 3
-Q3_SUPERBLOCK = 128          # codes per 48-byte block of the canonical layout
-Q3_SUPERBLOCK_BYTES = 48
+Q3_BLOCK = 128               # codes per 48-byte block (four 12-byte lane-group chunks)
+Q3_BLOCK_BYTES = 48
+Q3_SUPERBLOCK = 512          # four blocks whose lane-group chunks are interleaved
+Q3_SUPERBLOCK_BYTES = 192
 
 
 def e8m0_to_f32(scales: np.ndarray) -> np.ndarray:
@@ -181,19 +184,39 @@ def _q3_pair_table():
     return [(p // 4, p % 4) for p in range(16)]
 
 
+def q3_chunk_offset(k: int, kb: int, g: int) -> int:
+    """Byte offset, within a row of K codes, of lane group g's 12 bytes of
+    128-code block kb: in a full 512-code superblock the chunks of one lane
+    group are contiguous (``192 * (kb // 4) + 48 * g + 12 * (kb % 4)``); blocks
+    after the last full superblock are plain 48-byte blocks (``48 * kb + 12 * g``)."""
+    if kb // 4 < k // Q3_SUPERBLOCK:
+        return (kb // 4) * Q3_SUPERBLOCK_BYTES + 48 * g + 12 * (kb % 4)
+    return kb * Q3_BLOCK_BYTES + 12 * g
+
+
+def _q3_byte_index(k: int) -> np.ndarray:
+    """[K/128, 4, 12] row byte index of each block's lane-group chunks."""
+    nb = k // Q3_BLOCK
+    off = np.array([[q3_chunk_offset(k, kb, g) for g in range(4)] for kb in range(nb)], dtype=np.int64)
+    return off[:, :, None] + np.arange(12)
+
+
 def q3_pack(q: np.ndarray) -> np.ndarray:
     """Codes [N, K] (0..7) -> canonical packed bytes [N, 3K/8] u8.
 
-    Canonical layout (this build's; K must be a multiple of 128):
-    a row is a sequence of 128-code blocks of 48 bytes.  Within a block,
-    lane group g (0..3) owns the 12 bytes at 12*g, read as three
-    little-endian u32 words d0, d1, d2.  Lane group g holds the 32
-    consecutive codes ``32*g + 8*m + j`` (m = 0..3, j = 0..7) of the block,
-    as 16 pairs P = 4*m + j//2 with the even-j code in the low half and the
-    odd-j code in the high half.  Pair P < 15 sits in word P // 5: low code at
-    bit 3*(P % 5), high code at bit 16 + 3*(P % 5).  Pair 15 uses the spare
-    bits: bit t of its low code is bit 15 of word t, bit t of its high code
-    is bit 31 of word t.
+    Canonical layout (this build's; K must be a multiple of 128): a row is a
+    sequence of 128-code blocks.  Lane group g (0..3) of a block owns 12
+    bytes, read as three little-endian u32 words d0, d1, d2, holding the 32
+    consecutive codes ``32*g + 8*m + j`` (m = 0..3, j = 0..7) of the block as
+    16 pairs P = 4*m + j//2, the even-j code in the low half and the odd-j
+    code in the high half.  Pair P < 15 sits in word P // 5: low code at bit
+    3*(P % 5), high code at bit 16 + 3*(P % 5).  Pair 15 uses the spare bits:
+    bit t of its low code is bit 15 of word t, bit t of its high code is bit
+    31 of word t.  The chunks are placed by ``q3_chunk_offset``: within each
+    full 512-code superblock (192 bytes) lane group g's chunks of the four
+    blocks are the 48 contiguous bytes at 48*g, so a lane reads four blocks
+    as three aligned 16-byte words; a tail of fewer than four blocks keeps
+    plain 48-byte blocks.
     A lane group's 32 codes are the same K range an FP4 lane group reads
     (one 16-byte word of 32 codes), all in one 64-group (g < 2: the block's
     first group), and every pair is one shift-and-mask away from a packed
@@ -201,11 +224,11 @@ def q3_pack(q: np.ndarray) -> np.ndarray:
     """
     q = np.asarray(q, dtype=np.uint32)
     n, k = q.shape
-    if k % Q3_SUPERBLOCK:
-        raise ValueError(f"K={k} is not a multiple of {Q3_SUPERBLOCK}")
+    if k % Q3_BLOCK:
+        raise ValueError(f"K={k} is not a multiple of {Q3_BLOCK}")
     if q.size and q.max() > 7:
         raise ValueError("q3 codes must be in 0..7")
-    nb = k // Q3_SUPERBLOCK
+    nb = k // Q3_BLOCK
     # code index within block = 32*g + 8*m + j  -> axes [N, nb, g, m, j]
     c = q.reshape(n, nb, 4, 4, 8)
     words = np.zeros((n, nb, 4, 3), dtype=np.uint32)   # [.., g, d]
@@ -218,17 +241,21 @@ def q3_pack(q: np.ndarray) -> np.ndarray:
         else:
             for t in range(3):
                 words[:, :, :, t] |= (((lo >> t) & 1) << 15) | (((hi >> t) & 1) << 31)
-    return words.astype("<u4").view(np.uint8).reshape(n, nb * Q3_SUPERBLOCK_BYTES)
+    chunks = words.astype("<u4").view(np.uint8).reshape(n, nb, 4, 12)
+    out = np.zeros((n, k * 3 // 8), dtype=np.uint8)
+    out[:, _q3_byte_index(k)] = chunks
+    return out
 
 
 def q3_unpack(packed: np.ndarray, k: int) -> np.ndarray:
     """Canonical packed bytes [N, 3K/8] -> codes [N, K] u8 (inverse of ``q3_pack``)."""
     p = np.ascontiguousarray(packed, dtype=np.uint8)
     n = p.shape[0]
-    if k % Q3_SUPERBLOCK or p.shape[1] != k * 3 // 8:
+    if k % Q3_BLOCK or p.shape[1] != k * 3 // 8:
         raise ValueError(f"packed {p.shape} does not hold K={k} q3 codes")
-    nb = k // Q3_SUPERBLOCK
-    words = p.reshape(n, nb, 4, 12).copy().view("<u4").reshape(n, nb, 4, 3).astype(np.uint32)
+    nb = k // Q3_BLOCK
+    chunks = np.ascontiguousarray(p[:, _q3_byte_index(k)])           # [N, nb, 4, 12]
+    words = chunks.view("<u4").reshape(n, nb, 4, 3).astype(np.uint32)
     c = np.zeros((n, nb, 4, 4, 8), dtype=np.uint32)    # [.., g, m, j]
     for pidx, (m, i) in enumerate(_q3_pair_table()):
         if pidx < 15:

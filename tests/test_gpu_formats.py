@@ -61,9 +61,11 @@ def test_fp4_quantize_bit_exact(scale):
     np.testing.assert_array_equal(p_got.cpu().numpy(), p_want)
 
 
-def test_q3_quantize_and_dequant_bit_exact():
+@pytest.mark.parametrize("cols", [512, 640, 1408])
+def test_q3_quantize_and_dequant_bit_exact(cols):
+    """Full 512-code superblocks and a tail of plain 128-code blocks."""
     g = torch.Generator().manual_seed(5)
-    w = (torch.randn((64, 512), generator=g) * 0.02).float()
+    w = (torch.randn((64, cols), generator=g) * 0.02).float()
     w[3, :64] = 0.0          # zero range group
     p_want, s_want, b_want = F.q3_quantize(w.numpy())
     p_got, s_got, b_got = dsk_moe.q3_quantize(w.to(DEV))

@@ -112,10 +112,11 @@ def test_fp4_quantize_nearest_even_brute_force():
 # ------------------------------------------------------------------ Q3
 def test_q3_pack_roundtrip_and_geometry():
     rng = np.random.default_rng(11)
-    q = rng.integers(0, 8, size=(5, 384), dtype=np.uint8)
-    packed = F.q3_pack(q)
-    assert packed.shape == (5, 384 * 3 // 8)
-    np.testing.assert_array_equal(F.q3_unpack(packed, 384), q)
+    for k in (384, 1024, 1152):
+        q = rng.integers(0, 8, size=(5, k), dtype=np.uint8)
+        packed = F.q3_pack(q)
+        assert packed.shape == (5, k * 3 // 8)
+        np.testing.assert_array_equal(F.q3_unpack(packed, k), q)
 
 
 def test_q3_pack_known_answer():
@@ -132,6 +133,28 @@ def test_q3_pack_known_answer():
             for t in range(3):
                 expect[g, t] = ((5 >> t) & 1) << (31 if j % 2 else 15)
         np.testing.assert_array_equal(words, expect)
+
+
+def test_q3_pack_superblock_placement():
+    # K = 640: one 512-code superblock (lane group g's chunks of blocks 0..3 at
+    # bytes 48g + 12b) and one plain 48-byte tail block at byte 192
+    for b, g, m, j in [(0, 0, 0, 0), (1, 2, 1, 3), (3, 3, 3, 7), (2, 1, 0, 2), (4, 0, 0, 1), (4, 3, 2, 5)]:
+        q = np.zeros((1, 640), dtype=np.uint8)
+        q[0, 128 * b + 32 * g + 8 * m + j] = 6
+        packed = F.q3_pack(q)
+        off = 48 * g + 12 * b if b < 4 else 192 + 12 * g
+        nz = np.flatnonzero(packed[0])
+        assert nz.size and nz.min() >= off and nz.max() < off + 12, (b, g, nz)
+        words = packed[0, off:off + 12].copy().view("<u4")
+        p = 4 * m + j // 2
+        expect = np.zeros(3, dtype=np.uint32)
+        if p < 15:
+            expect[p // 5] = 6 << (3 * (p % 5) + (16 if j % 2 else 0))
+        else:
+            for t in range(3):
+                expect[t] = ((6 >> t) & 1) << (31 if j % 2 else 15)
+        np.testing.assert_array_equal(words, expect)
+        np.testing.assert_array_equal(F.q3_unpack(packed, 640), q)
 
 
 def test_q3_quantize_error_bound():
