@@ -931,6 +931,223 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
   }
 }
 
+// ---------------------------------------------------------------- q3 down, factored
+constexpr int kDqW = 8;             // waves: 0..3 routed, 4..7 shared
+constexpr int kDqRouted = 4;        // routed waves: one 512-code superblock of I each (I = 2048)
+constexpr int kDqMaxTokens = 4;     // A operand row 4t + 2h + plane
+constexpr int kDqRing = 8;          // routed experts in flight per wave
+constexpr int kDqSharedKB = 4;      // shared K blocks per shared wave (Is <= 2048)
+
+// One routed expert's w2 data of a routed wave: this lane's chunks of the
+// superblock's 4 blocks (3 x 16 bytes) and the (scale, bias) windows of its 8
+// groups (word j: groups 2j, 2j + 1 of block j).
+struct DqSlot {
+  uint32_t c[4][3];
+  u32x4 s, b;
+};
+
+__device__ __forceinline__ void load_dq_slot(DqSlot& r, const DecodeArgs& p, int u, int U, uint32_t row,
+                                             int sbk, int g4) {
+  const bool in = u < U;
+  const SlotDesc* d = p.desc + (in ? u : 0);
+  const int I = p.I;
+  const auto c = gptr<u32x4>(static_cast<const uint8_t*>(d->p[6]) + row * static_cast<uint32_t>(I / 8 * 3) +
+                             sbk * 192 + 48 * g4);
+#pragma unroll
+  for (int v = 0; v < 3; ++v) {
+    const u32x4 a = in ? c[v] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.c[(4 * v + j) / 3][(4 * v + j) % 3] = a[j];
+  }
+  const uint32_t wo = (row * static_cast<uint32_t>(I / 64) + 8 * sbk) * 2;   // bytes
+  r.s = in ? ldg16(static_cast<const uint8_t*>(d->p[7]) + wo) : u32x4{0u, 0u, 0u, 0u};
+  r.b = in ? ldg16(static_cast<const uint8_t*>(d->p[8]) + wo) : u32x4{0u, 0u, 0u, 0u};
+}
+
+// Final add and cast of one output element (token t, column n).
+__device__ __forceinline__ void down_epilogue1(const DecodeArgs& p, float a, float sh, int n, int t) {
+  const int64_t o = static_cast<int64_t>(t) * p.H + n;
+  if (!p.x_f32) {
+    // the shared output is rounded to x's dtype before it is added
+    if (p.Is > 0) a += bf16_bits_to_f32(f32_to_bf16_bits(sh));
+    else if (p.shared_out) a += bf16_bits_to_f32(static_cast<const uint16_t*>(p.shared_out)[o]);
+    static_cast<uint16_t*>(p.out)[o] = f32_to_bf16_bits(a);
+  } else {
+    if (p.Is > 0) a += sh;
+    else if (p.shared_out) a += static_cast<const float*>(p.shared_out)[o];
+    static_cast<float*>(p.out)[o] = a;
+  }
+}
+
+// Down + combine of the decode pipeline for q3 experts (T <= 4, I = 2048),
+// factored like k_up_q3: the h activations are the A operand (row 4t + 2h +
+// plane: token t's hi or lo plane restricted to a K block's h-th 64-group),
+// the raw w2 codes the B operand (column = output row), and each group's
+// scale and bias are applied once per block: acc += s (D_hi + D_lo - 128 *
+// sum(h / m)) + b * sum(h).  Block = 16 output rows, kDqW waves: routed wave
+// w streams superblock w (4 K blocks, 48 contiguous bytes per lane) of every
+// active expert's w2 rows, kDqRing experts in flight; shared wave 4 + s takes
+// K quarter s of the shared expert's bf16 w2 rows.  Routed h rows are staged
+// in LDS with the 8q positions divided by 8 and their group sums, the shared
+// hs rows as they are.  A token's routed sum runs over its experts in slot
+// (ascending id) order, then the routed waves and the shared waves are each
+// added in order: no term depends on the other tokens of the batch.
+__global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
+  extern __shared__ __align__(16) uint16_t lds_dq[];
+  const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int row0 = blockIdx.x * 16;
+  const uint32_t row = static_cast<uint32_t>(row0 + r16);
+  const int U = p.active[0];
+  const int T = p.T, N = T * p.k;
+  const int I = p.I, Is = p.Is;
+  const int is = I + 8, iss = Is + 8;       // padded LDS row strides
+  const int ng = I / 64;                    // 64-groups per h row
+  uint16_t* hh = lds_dq;
+  uint16_t* hl = hh + N * is;
+  uint16_t* sh_h = hl + N * is;
+  uint16_t* sh_l = sh_h + T * iss;
+  float* hsum = reinterpret_cast<float*>(sh_l + T * iss);            // [N][ng][2]: sum h, sum h / m
+  float (*red)[kDqRouted][kDqMaxTokens][16] =
+      reinterpret_cast<float (*)[kDqRouted][kDqMaxTokens][16]>(hsum + N * ng * 2);   // [routed, shared]
+  const uint16_t* zero = reinterpret_cast<const uint16_t*>(red + 2);                // 64 zero bytes
+  int* ldrow = reinterpret_cast<int*>(red + 2) + 16;                                // [U][T]
+  if (tid < 4) reinterpret_cast<u32x4*>(red + 2)[tid] = u32x4{0u, 0u, 0u, 0u};
+  // 1. activations (routed rows scaled and summed per group) and dispatch rows into LDS
+  {
+    constexpr int NT = kDqW * 64;
+    const int cpr = I / 8, hch = N * cpr, sch = T * (Is / 8);
+    for (int c0 = 0; c0 < hch + sch; c0 += NT) {   // hch, sch: multiples of 8 (whole lane groups)
+      const int c = c0 + tid;
+      if (c < hch) {
+        const int r = c / cpr, cc = c % cpr;
+        const int64_t e = static_cast<int64_t>(r) * I + cc * 8;
+        const u32x4 vh = ldg16(p.h_hi + e), vl = ldg16(p.h_lo + e);
+        const uint32_t div8 = q3m_div8_pairs(cc & 3);
+        const uint32_t wh[4] = {vh.x, vh.y, vh.z, vh.w}, wl[4] = {vl.x, vl.y, vl.z, vl.w};
+        uint16_t oh[8], ol[8];
+        float sx = 0.0f, sxm = 0.0f;
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) {
+          const float fh = __uint_as_float((e2 & 1) ? (wh[e2 >> 1] & 0xffff0000u) : (wh[e2 >> 1] << 16));
+          const float fl = __uint_as_float((e2 & 1) ? (wl[e2 >> 1] & 0xffff0000u) : (wl[e2 >> 1] << 16));
+          const float sc = ((div8 >> (e2 >> 1)) & 1u) ? 0.125f : 1.0f;
+          oh[e2] = f32_to_bf16_bits(fh * sc);
+          ol[e2] = f32_to_bf16_bits(fl * sc);
+          const float v = fh + fl;
+          sx += v;
+          sxm += v * sc;
+        }
+        *reinterpret_cast<u32x4*>(hh + r * is + cc * 8) = pack_bf16x8(oh);
+        *reinterpret_cast<u32x4*>(hl + r * is + cc * 8) = pack_bf16x8(ol);
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+          sx += __shfl_xor(sx, o, 8);
+          sxm += __shfl_xor(sxm, o, 8);
+        }
+        if ((cc & 7) == 0) *reinterpret_cast<float2*>(hsum + (r * ng + (cc >> 3)) * 2) = float2{sx, sxm};
+      } else if (c < hch + sch) {
+        const int cs = c - hch;
+        const int64_t e = static_cast<int64_t>(cs / (Is / 8)) * Is + (cs % (Is / 8)) * 8;
+        const int off = (cs / (Is / 8)) * iss + (cs % (Is / 8)) * 8;
+        *reinterpret_cast<u32x4*>(sh_h + off) = ldg16(p.hs_hi + e);
+        *reinterpret_cast<u32x4*>(sh_l + off) = ldg16(p.hs_lo + e);
+      }
+    }
+  }
+  if (wave == 0)
+    for (int i = lane; i < U * T; i += 64) ldrow[i] = p.rowmap[i];
+  const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (wave < kDqRouted) {
+    // 2. routed: superblock `wave` of every active expert's w2 rows
+    const int sbk = wave;
+    DqSlot ring[kDqRing];
+#pragma unroll
+    for (int q = 0; q < kDqRing; ++q)
+      if (q < U) load_dq_slot(ring[q], p, q, U, row, sbk, g4);
+    __syncthreads();
+    // A operand row of this lane: token ta, group half ha, plane pa
+    const int ta = r16 >> 2, ha = (r16 >> 1) & 1;
+    const uint16_t* aplane = (r16 & 1) ? hl : hh;
+    const bool arow = ta < T && ha == (g4 >> 1);
+    const int to = g4;                         // this lane's output token
+    const Q3Masks km = q3_masks();
+    float acc = 0.0f;
+    auto mm = [&](const DqSlot& r, int u) {
+      const int dra = arow ? ldrow[u * T + ta] : -1;
+      const int dro = to < T ? ldrow[u * T + to] : -1;
+      const uint32_t sw[4] = {r.s.x, r.s.y, r.s.z, r.s.w}, bw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int kb = 4 * sbk + j;
+        const uint16_t* ah = dra >= 0 ? aplane + dra * is + kb * 128 + 32 * g4 : zero;
+        f32x4 d = z;
+        d = mfma16(as_bf16x8(*reinterpret_cast<const u32x4*>(ah)), q3m_operand<0>(r.c[j], km), d);
+        d = mfma16(as_bf16x8(*reinterpret_cast<const u32x4*>(ah + 8)), q3m_operand<1>(r.c[j], km), d);
+        d = mfma16(as_bf16x8(*reinterpret_cast<const u32x4*>(ah + 16)), q3m_operand<2>(r.c[j], km), d);
+        d = mfma16(as_bf16x8(*reinterpret_cast<const u32x4*>(ah + 24)), q3m_operand<3>(r.c[j], km), d);
+        if (dro >= 0) {
+          const f32x4 xs = *reinterpret_cast<const f32x4*>(hsum + (dro * ng + 2 * kb) * 2);
+          acc = fmaf(f16_half<0>(sw[j]), fmaf(-128.0f, xs.y, d[0] + d[1]), acc);
+          acc = fmaf(f16_half<0>(bw[j]), xs.x, acc);
+          acc = fmaf(f16_half<1>(sw[j]), fmaf(-128.0f, xs.w, d[2] + d[3]), acc);
+          acc = fmaf(f16_half<1>(bw[j]), xs.z, acc);
+        }
+      }
+    };
+    for (int u0 = 0; u0 < U; u0 += kDqRing) {
+#pragma unroll
+      for (int q = 0; q < kDqRing; ++q) {
+        const int u = u0 + q;
+        if (u < U) {
+          mm(ring[q], u);
+          if (u + kDqRing < U) load_dq_slot(ring[q], p, u + kDqRing, U, row, sbk, g4);
+        }
+      }
+    }
+    if (to < T) red[0][wave][to][r16] = acc;
+  } else {
+    // 2'. shared: K quarter `s` of the shared expert's bf16 w2 rows
+    const int s = wave - kDqRouted;
+    const int nbs = Is / 128, per = (nbs + 3) / 4;
+    const int k0 = min(s * per, nbs), k1 = min(k0 + per, nbs);
+    RawBF16 rs[kDqSharedKB];
+#pragma unroll
+    for (int j = 0; j < kDqSharedKB; ++j) {
+      const int kc = (k0 + j) * 128 + g4 * 32;
+      load_raw(rs[j], p.ws2, row, Is, kc, k0 + j < k1);
+    }
+    __syncthreads();
+    // A operand row 2t + plane
+    const int ta = r16 >> 1;
+    const uint16_t* sbase = ta < T ? ((r16 & 1) ? sh_l : sh_h) + ta * iss + 32 * g4 : zero;
+    f32x4 d = z;
+#pragma unroll
+    for (int j = 0; j < kDqSharedKB; ++j) {
+      if (k0 + j < k1) {
+        const uint16_t* a = ta < T ? sbase + (k0 + j) * 128 : zero;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          d = mfma16(as_bf16x8(*reinterpret_cast<const u32x4*>(a + 8 * m)), as_bf16x8(rs[j].v[m]), d);
+      }
+    }
+    // rows 4 g4 + q: token 2 g4 + (q >> 1), plane q & 1
+    const int t0 = 2 * g4;
+    if (t0 < T) red[1][s][t0][r16] = d[0] + d[1];
+    if (t0 + 1 < T) red[1][s][t0 + 1][r16] = d[2] + d[3];
+  }
+  __syncthreads();
+  if (wave == 0 && g4 < T) {
+    float a = 0.0f, sh = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kDqRouted; ++w) {
+      a += red[0][w][g4][r16];
+      sh += red[1][w][g4][r16];
+    }
+    down_epilogue1(p, a, sh, row0 + r16, g4);
+  }
+}
+
 template <typename Raw>
 __global__ __launch_bounds__(kDownW * 64) void k_down_decode(DecodeArgs p) {
   __shared__ float red[2][kDownW][64][4];
@@ -1092,6 +1309,23 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   }
   const int n_rows = d.tokens * d.top_k;
   const int max_u = d.n_experts < n_rows ? d.n_experts : n_rows;
+  if (q3 && d.tokens <= kDqMaxTokens && d.inter == kDqRouted * 512 && d.inter_shared <= 2048 &&
+      d.inter_shared % 128 == 0) {
+    // factored q3 down: h planes, hs planes, group sums, partial sums, zeros, dispatch rows
+    const size_t dq_lds = static_cast<size_t>(n_rows) * (d.inter + 8) * 4 +
+                          static_cast<size_t>(d.tokens) * (d.inter_shared + 8) * 4 +
+                          static_cast<size_t>(n_rows) * (d.inter / 64) * 8 + 2 * kDqRouted * kDqMaxTokens * 16 * 4 +
+                          64 + static_cast<size_t>(max_u) * d.tokens * 4;
+    if (dq_lds <= kMaxLds) {
+      for (int r = 0; r < repeat; ++r) {
+        k_down_q3<<<static_cast<unsigned>(d.hidden / 16), kDqW * 64, dq_lds, s>>>(p);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+      }
+      if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
+      if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return e;
+      return hipSuccess;
+    }
+  }
   const size_t act = static_cast<size_t>(n_rows) * (d.inter + 8) * 4 +
                      static_cast<size_t>(d.tokens) * (d.inter_shared + 8) * 4;
   const size_t dn_lds = (act > kStRedBytes ? act : kStRedBytes) + static_cast<size_t>(max_u) * d.tokens * 4;
