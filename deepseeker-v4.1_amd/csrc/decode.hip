@@ -85,30 +85,32 @@ struct UpBatch {
   uint32_t w1[G / 4], w3[G / 4];
 };
 
+// Loads without conditions (see load_raw_nc): blocks past the wave's range
+// re-read its last block and rows past the tile read row 0; mma_batch gives
+// them a zero B operand and their rows are not stored.  k1 >= 1.
 template <int G, bool kWin>
 __device__ __forceinline__ void load_batch(UpBatch<G>& b, const uint8_t* W1, const uint8_t* S1,
                                            const uint8_t* W3, const uint8_t* S3, uint32_t row, int K,
                                            int kb, int k1, int g4, bool rok) {
   // 32-bit offsets from the (uniform) role base pointers: one expert role is < 4 GB
-  const uint32_t cb = row * static_cast<uint32_t>(K / 2), sb = row * static_cast<uint32_t>(K / 32);
+  const uint32_t rowc = rok ? row : 0u;
+  const uint32_t cb = rowc * static_cast<uint32_t>(K / 2), sb = rowc * static_cast<uint32_t>(K / 32);
   if constexpr (kWin) {
 #pragma unroll
     for (int v = 0; v < G / 4; ++v) {
-      const int kw = kb + 4 * v + g4;                 // K block whose scales this lane fetches
-      const bool ok = rok && kw < k1;
-      b.w1[v] = ok ? ldg<uint32_t>(S1 + sb + 4 * kw) : 0u;
-      b.w3[v] = ok ? ldg<uint32_t>(S3 + sb + 4 * kw) : 0u;
+      const int kw = min(kb + 4 * v + g4, k1 - 1);    // K block whose scales this lane fetches
+      b.w1[v] = ldg<uint32_t>(S1 + sb + 4 * kw);
+      b.w3[v] = ldg<uint32_t>(S3 + sb + 4 * kw);
     }
   }
 #pragma unroll
   for (int i = 0; i < G; ++i) {
-    const int kc = (kb + i) * 128 + g4 * 32;
-    const bool ok = rok && kb + i < k1 && kc < K;
-    b.c1[i] = ok ? ldg16(W1 + cb + kc / 2) : u32x4{0u, 0u, 0u, 0u};
-    b.c3[i] = ok ? ldg16(W3 + cb + kc / 2) : u32x4{0u, 0u, 0u, 0u};
+    const int kc = min(min(kb + i, k1 - 1) * 128 + g4 * 32, K - 32);
+    b.c1[i] = ldg16(W1 + cb + kc / 2);
+    b.c3[i] = ldg16(W3 + cb + kc / 2);
     if constexpr (!kWin) {
-      b.s1[i] = ok ? ldg<uint8_t>(S1 + sb + kc / 32) : 127u;
-      b.s3[i] = ok ? ldg<uint8_t>(S3 + sb + kc / 32) : 127u;
+      b.s1[i] = ldg<uint8_t>(S1 + sb + kc / 32);
+      b.s3[i] = ldg<uint8_t>(S3 + sb + kc / 32);
     }
   }
 }
@@ -160,15 +162,13 @@ __device__ __forceinline__ bool load_x(const DecodeArgs& p, uint16_t* xh, uint16
   if (xchunks <= kUpXRegChunks * NT) {
 #pragma unroll
     for (int j = 0; j < kUpXRegChunks; ++j) {
-      const int c = tid + j * NT;
-      if (c < xchunks) {
-        const int64_t e = static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8;
-        if (!kF32) {
-          xv[j][0] = ldg16(static_cast<const uint16_t*>(p.x) + e);
-        } else {
-          xv[j][0] = ldg16(static_cast<const float*>(p.x) + e);
-          xv[j][1] = ldg16(static_cast<const float*>(p.x) + e + 4);
-        }
+      const int c = min(tid + j * NT, xchunks - 1);   // no condition on the load (see load_raw_nc)
+      const int64_t e = static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8;
+      if (!kF32) {
+        xv[j][0] = ldg16(static_cast<const uint16_t*>(p.x) + e);
+      } else {
+        xv[j][0] = ldg16(static_cast<const float*>(p.x) + e);
+        xv[j][1] = ldg16(static_cast<const float*>(p.x) + e + 4);
       }
     }
     return true;
@@ -210,10 +210,10 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint
   const bool tv = r16 < T;
   RawBF16 a1, a3, b1, b3;
   auto ld = [&](RawBF16& r1, RawBF16& r3, int kb) {
-    const int kc = kb * 128 + g4 * 32;
-    const bool ok = kb < k1 && kc < K;
-    load_raw(r1, p.ws1, row, K, kc, ok);
-    load_raw(r3, p.ws3, row, K, kc, ok);
+    // no condition (see load_raw_nc): past the range, the last block again
+    const int kc = min(min(kb, k1 - 1) * 128 + g4 * 32, K - 32);
+    load_raw_nc(r1, p.ws1, row, K, kc);
+    load_raw_nc(r3, p.ws3, row, K, kc);
   };
   ld(a1, a3, k0);
   ld(b1, b3, k0 + 1);
@@ -439,6 +439,9 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
 // ---------------------------------------------------------------- q3 gate/up, factored
 // Tokens of the factored q3 gate/up (A operand row 2t + h for t < 8).
 constexpr int kQ3fMaxTokens = 8;
+constexpr int kQ3fItems = 1;                      // row tiles of a block
+constexpr int kQ3fKS = 8;                         // K ranges of a row tile (one wave each)
+constexpr int kQ3fW = kQ3fItems * kQ3fKS;
 
 // One activation chunk (8 values of token t, chunk cc of its row) for the
 // factored q3 product: the values at 8q code positions divided by 8 (exact),
@@ -527,21 +530,23 @@ __device__ __forceinline__ void q3_factor(const f32x4& d, uint32_t s, uint32_t b
 // group 0, lane groups 2, 3 group 1), the weights the B operand (column =
 // weight row), so a 16x16x32 MFMA covers both groups of a block for up to 8
 // tokens and a lane's outputs are one weight row of tokens 2g, 2g + 1.
-// Block shape, K split, batches in flight and the K-range reduction order
-// are those of k_up_stream.
-template <bool kWin, bool kF32>
-__global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 || !kWin ? 3 : 4))) void k_up_q3(DecodeArgs p) {
+// Block = kQ3fItems row tiles x kQ3fKS K ranges (one wave each; at hidden
+// 4096 a wave's range is one 512-code superblock, so one batch per wave),
+// kTwo: two batches in flight where a range is longer (a separate variant,
+// so that the one-batch kernel keeps its registers); K ranges added in order.
+template <bool kWin, bool kF32, bool kTwo>
+__global__ __launch_bounds__(kQ3fW * 64) __attribute__((amdgpu_waves_per_eu(kF32 || !kWin || kTwo ? 3 : 4))) void k_up_q3(DecodeArgs p) {
   constexpr int G = kUpBatch;
   extern __shared__ __align__(16) uint16_t lds_up[];
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
-  const int groups = (p.up_tiles + kUpItems - 1) / kUpItems;
+  const int groups = (p.up_tiles + kQ3fItems - 1) / kQ3fItems;
   const int rb = static_cast<int>(blockIdx.x);
   const int slot = rb / groups;
   if (slot >= p.active[0]) return;
   const int T = p.T, K = p.H;
-  const int item = wave / kUpKS, ks = wave % kUpKS;
-  const int rt = (rb % groups) * kUpItems + item;
+  const int item = wave / kQ3fKS, ks = wave % kQ3fKS;
+  const int rt = (rb % groups) * kQ3fItems + item;
   const bool rok = rt < p.up_tiles;
   // this lane's A operand row: token ta, group half ha
   const int ta = r16 >> 1;
@@ -552,25 +557,24 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
   const int drow0 = t0 < T ? p.rowmap[slot * T + t0] : -1;
   const int drow1 = t0 + 1 < T ? p.rowmap[slot * T + t0 + 1] : -1;
   const int xs = K + 8, nblk = K / 128, cpr = K / 8, xchunks = T * cpr;
-  constexpr int NT = kUpW * 64;
+  constexpr int NT = kQ3fW * 64;
   uint16_t* xh = lds_up;
   uint16_t* xl = lds_up + T * xs;
   float* xsum = reinterpret_cast<float*>(lds_up + (kF32 ? 2 : 1) * T * xs);   // [nblk][8][2][2]
-  float (*red)[kUpKS][2][64][2] = reinterpret_cast<float (*)[kUpKS][2][64][2]>(xsum + nblk * kQ3fMaxTokens * 4);
-  const uint16_t* zero = reinterpret_cast<const uint16_t*>(red + kUpItems);   // 64 zero bytes
-  if (tid < 4) reinterpret_cast<u32x4*>(red + kUpItems)[tid] = u32x4{0u, 0u, 0u, 0u};
+  float (*red)[kQ3fKS][2][64][2] = reinterpret_cast<float (*)[kQ3fKS][2][64][2]>(xsum + nblk * kQ3fMaxTokens * 4);
+  const uint16_t* zero = reinterpret_cast<const uint16_t*>(red + kQ3fItems);   // 64 zero bytes
+  if (tid < 4) reinterpret_cast<u32x4*>(red + kQ3fItems)[tid] = u32x4{0u, 0u, 0u, 0u};
   // activations: into registers when they fit (staged after the weight loads are issued)
   const bool xreg = xchunks <= NT;
   u32x4 xv0{}, xv1{};
   if (xreg) {
-    if (tid < xchunks) {
-      const int64_t e = static_cast<int64_t>(tid / cpr) * K + (tid % cpr) * 8;
-      if constexpr (!kF32) {
-        xv0 = ldg16(static_cast<const uint16_t*>(p.x) + e);
-      } else {
-        xv0 = ldg16(static_cast<const float*>(p.x) + e);
-        xv1 = ldg16(static_cast<const float*>(p.x) + e + 4);
-      }
+    const int c = min(tid, xchunks - 1);   // no condition on the load (see load_raw_nc)
+    const int64_t e = static_cast<int64_t>(c) * 8;   // the rows are contiguous: chunk c at 8c
+    if constexpr (!kF32) {
+      xv0 = ldg16(static_cast<const uint16_t*>(p.x) + e);
+    } else {
+      xv0 = ldg16(static_cast<const float*>(p.x) + e);
+      xv1 = ldg16(static_cast<const float*>(p.x) + e + 4);
     }
   } else {
     for (int c0 = 0; c0 < xchunks; c0 += NT) {   // xchunks is a multiple of 8: whole lane groups
@@ -590,68 +594,66 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
   }
   const SlotDesc* d = p.desc + slot;
   const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
-  const int per = (nblk + kUpKS - 1) / kUpKS;
+  const int per = (nblk + kQ3fKS - 1) / kQ3fKS;
   const int k0 = min(ks * per, nblk), k1 = min(k0 + per, nblk);
   const uint8_t* W1 = static_cast<const uint8_t*>(d->p[0]);
   const uint8_t* W3 = static_cast<const uint8_t*>(d->p[3]);
   const uint8_t* SB[4] = {static_cast<const uint8_t*>(d->p[1]), static_cast<const uint8_t*>(d->p[2]),
                           static_cast<const uint8_t*>(d->p[4]), static_cast<const uint8_t*>(d->p[5])};
-  const uint32_t code_row = row * static_cast<uint32_t>(K / 8 * 3);
-  const uint32_t sb_row = row * static_cast<uint32_t>(K / 64) * 2;   // bytes
+  // loads without conditions (see load_raw_nc): rows past the tile read row
+  // 0 (not stored), blocks past the wave's range re-read its last ones (not
+  // computed: mm stops at k1); every wave has k1 > k0 here except the ones
+  // past a short row, which clamp to the row's last block
+  const uint32_t rowc = rok ? row : 0u;
+  const uint32_t code_row = rowc * static_cast<uint32_t>(K / 8 * 3);
+  const uint32_t sb_row = rowc * static_cast<uint32_t>(K / 64) * 2;   // bytes
   auto ld = [&](Q3Batch<G>& b, int kb0) {
     if constexpr (kWin) {
       // a batch is one 512-code superblock: this lane group's chunks of its
-      // 4 blocks are 48 contiguous bytes
-      const bool ok = rok && kb0 < k1;
-      const uint32_t off = code_row + (kb0 >> 2) * 192 + 48 * g4;
+      // 4 blocks are 48 contiguous bytes (windowed: k1 - k0 is a multiple of 4, >= 4)
+      const int kbc = kb0 < k1 ? kb0 : k1 - G;
+      const uint32_t off = code_row + (kbc >> 2) * 192 + 48 * g4;
       const auto c1 = gptr<u32x4>(W1 + off);
       const auto c3 = gptr<u32x4>(W3 + off);
 #pragma unroll
       for (int v = 0; v < 3; ++v) {
-        const u32x4 a = ok ? c1[v] : u32x4{0u, 0u, 0u, 0u};
-        const u32x4 e = ok ? c3[v] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 a = c1[v];
+        const u32x4 e = c3[v];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           b.c1[(4 * v + j) / 3][(4 * v + j) % 3] = a[j];
           b.c3[(4 * v + j) / 3][(4 * v + j) % 3] = e[j];
         }
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < G; ++i) {
-        const bool ok = rok && kb0 + i < k1;
-        const uint32_t off = code_row + q3_chunk_offset(K, kb0 + i, g4);
-        const auto c1 = gptr<uint32_t>(W1 + off);
-        const auto c3 = gptr<uint32_t>(W3 + off);
-#pragma unroll
-        for (int q = 0; q < 3; ++q) {
-          b.c1[i][q] = ok ? c1[q] : 0u;
-          b.c3[i][q] = ok ? c3[q] : 0u;
-        }
-      }
-    }
-    if constexpr (kWin) {
       // one 16-byte window per array: the 8 groups of the batch's 4 blocks
-      const bool ok = rok && kb0 < k1;
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        const u32x4 w = ok ? ldg16(SB[a] + sb_row + kb0 * 4) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 w = ldg16(SB[a] + sb_row + kbc * 4);
 #pragma unroll
         for (int i = 0; i < G; ++i) b.sb[a][i] = w[i];
       }
     } else {
 #pragma unroll
       for (int i = 0; i < G; ++i) {
-        const bool ok = rok && kb0 + i < k1;
+        const int kb = min(kb0 + i, nblk - 1);
+        const uint32_t off = code_row + q3_chunk_offset(K, kb, g4);
+        const auto c1 = gptr<uint32_t>(W1 + off);
+        const auto c3 = gptr<uint32_t>(W3 + off);
 #pragma unroll
-        for (int a = 0; a < 4; ++a) b.sb[a][i] = ok ? ldg<uint32_t>(SB[a] + sb_row + (kb0 + i) * 4) : 0u;
+        for (int q = 0; q < 3; ++q) {
+          b.c1[i][q] = c1[q];
+          b.c3[i][q] = c3[q];
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a) b.sb[a][i] = ldg<uint32_t>(SB[a] + sb_row + kb * 4);
       }
     }
   };
+  // batch A streams while the activations are staged, then batch B
   Q3Batch<G> A, B;
   ld(A, k0);
-  ld(B, k0 + G);
   if (xreg && tid < xchunks) stage_chunk_q3<kF32>(xh, xl, xsum, xs, cpr, tid, xv0, xv1);   // whole lane groups
+  if (kTwo) ld(B, k0 + G);
   const float wr0 = drow0 >= 0 ? p.wrow[drow0] : 0.0f;
   const float wr1 = drow1 >= 0 ? p.wrow[drow1] : 0.0f;
   __syncthreads();
@@ -686,19 +688,23 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
       q3_factor(d3, b.sb[2][i], b.sb[3][i], xa, xb, acc3);
     }
   };
-  for (int kb = k0; kb < k1; kb += 2 * G) {
-    mm(A, kb);
-    if (kb + 2 * G < k1) ld(A, kb + 2 * G);
-    if (kb + G < k1) mm(B, kb + G);
-    if (kb + 3 * G < k1) ld(B, kb + 3 * G);
+  if constexpr (kTwo) {
+    for (int kb = k0; kb < k1; kb += 2 * G) {
+      mm(A, kb);
+      if (kb + 2 * G < k1) ld(A, kb + 2 * G);
+      if (kb + G < k1) mm(B, kb + G);
+      if (kb + 3 * G < k1) ld(B, kb + 3 * G);
+    }
+  } else {
+    mm(A, k0);   // the range is one batch
   }
-  // K ranges added in order: ((r0 + r1) + r2) + r3
+  // K ranges added in order: ((r0 + r1) + r2) + ...
   *reinterpret_cast<float2*>(&red[item][ks][0][lane][0]) = float2{acc1[0], acc1[1]};
   *reinterpret_cast<float2*>(&red[item][ks][1][lane][0]) = float2{acc3[0], acc3[1]};
   __syncthreads();
   if (ks == 0 && rok && (drow0 >= 0 || drow1 >= 0)) {
 #pragma unroll
-    for (int w = 1; w < kUpKS; ++w) {
+    for (int w = 1; w < kQ3fKS; ++w) {
       const float2 g = *reinterpret_cast<const float2*>(&red[item][w][0][lane][0]);
       const float2 u = *reinterpret_cast<const float2*>(&red[item][w][1][lane][0]);
       acc1[0] += g.x; acc1[1] += g.y;
@@ -783,8 +789,8 @@ __device__ __forceinline__ void load_down_batch(DownBatch<Raw>& b, const DecodeA
     const SlotDesc* d = p.desc + (in ? u0 + i : 0);
 #pragma unroll
     for (int j = 0; j < kStKB; ++j) {
-      const int kc = (kb0 + j) * 128 + g4 * 32;
-      load_role(b.r[i][j], d->p, 2, row, I, kc, in && kc < I);
+      // no condition (see load_raw_nc): slots past U re-read slot 0 and are not computed
+      load_role_nc(b.r[i][j], d->p, 2, row, I, min((kb0 + j) * 128 + g4 * 32, I - 32));
     }
   }
 }
@@ -843,17 +849,19 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
     u32x4 vh[kStStage], vl[kStStage];
 #pragma unroll
     for (int j = 0; j < kStStage; ++j) {
-      const int c = c0 + j * kStW * 64;
-      if (c < hch) {
-        const int64_t e = static_cast<int64_t>(c / (I / 8)) * I + (c % (I / 8)) * 8;
-        vh[j] = ldg16(p.h_hi + e);
-        vl[j] = ldg16(p.h_lo + e);
-      } else if (c < hch + sch) {
+      // no condition on the loads (see load_raw_nc): chunks past the end re-read the last one
+      const int c = min(c0 + j * kStW * 64, hch + sch - 1);
+      const uint16_t* ph = p.h_hi;
+      const uint16_t* pl = p.h_lo;
+      int64_t e = static_cast<int64_t>(c / (I / 8)) * I + (c % (I / 8)) * 8;
+      if (c >= hch) {
         const int cs = c - hch;
-        const int64_t e = static_cast<int64_t>(cs / (Is / 8)) * Is + (cs % (Is / 8)) * 8;
-        vh[j] = ldg16(p.hs_hi + e);
-        vl[j] = ldg16(p.hs_lo + e);
+        ph = p.hs_hi;
+        pl = p.hs_lo;
+        e = static_cast<int64_t>(cs / (Is / 8)) * Is + (cs % (Is / 8)) * 8;
       }
+      vh[j] = ldg16(ph + e);
+      vl[j] = ldg16(pl + e);
     }
 #pragma unroll
     for (int j = 0; j < kStStage; ++j) {
@@ -874,10 +882,9 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
     for (int i = lane; i < U * p.T; i += 64) ldrow[i] = p.rowmap[i];
   // 2. every weight of the block in flight: the shared batch and kStRing routed batches
   RawBF16 rs[kStKB];
+  if (Is > 0) {
 #pragma unroll
-  for (int j = 0; j < kStKB; ++j) {
-    const int kc = (kb0 + j) * 128 + g4 * 32;
-    load_raw(rs[j], p.ws2, row, Is, kc, Is > 0 && kc < Is);
+    for (int j = 0; j < kStKB; ++j) load_raw_nc(rs[j], p.ws2, row, Is, min((kb0 + j) * 128 + g4 * 32, Is - 32));
   }
   DownBatch<Raw> ring[kStRing];
 #pragma unroll
@@ -891,7 +898,7 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
   const uint16_t* splane = (r16 & 1) ? sh_l : sh_h;
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
   f32x4 acc[4] = {z, z, z, z}, accs[4] = {z, z, z, z};
-  {
+  if (Is > 0) {
     const uint16_t* brow = splane + (tcol ? t : 0) * iss;
 #pragma unroll
     for (int j = 0; j < kStKB; ++j) {
@@ -948,20 +955,20 @@ struct DqSlot {
 
 __device__ __forceinline__ void load_dq_slot(DqSlot& r, const DecodeArgs& p, int u, int U, uint32_t row,
                                              int sbk, int g4) {
-  const bool in = u < U;
-  const SlotDesc* d = p.desc + (in ? u : 0);
+  // no condition on the loads (see load_raw_nc): slots past U re-read slot 0 and are not computed
+  const SlotDesc* d = p.desc + (u < U ? u : 0);
   const int I = p.I;
   const auto c = gptr<u32x4>(static_cast<const uint8_t*>(d->p[6]) + row * static_cast<uint32_t>(I / 8 * 3) +
                              sbk * 192 + 48 * g4);
 #pragma unroll
   for (int v = 0; v < 3; ++v) {
-    const u32x4 a = in ? c[v] : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 a = c[v];
 #pragma unroll
     for (int j = 0; j < 4; ++j) r.c[(4 * v + j) / 3][(4 * v + j) % 3] = a[j];
   }
   const uint32_t wo = (row * static_cast<uint32_t>(I / 64) + 8 * sbk) * 2;   // bytes
-  r.s = in ? ldg16(static_cast<const uint8_t*>(d->p[7]) + wo) : u32x4{0u, 0u, 0u, 0u};
-  r.b = in ? ldg16(static_cast<const uint8_t*>(d->p[8]) + wo) : u32x4{0u, 0u, 0u, 0u};
+  r.s = ldg16(static_cast<const uint8_t*>(d->p[7]) + wo);
+  r.b = ldg16(static_cast<const uint8_t*>(d->p[8]) + wo);
 }
 
 // Final add and cast of one output element (token t, column n).
@@ -1016,13 +1023,32 @@ __global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
   // 1. activations (routed rows scaled and summed per group) and dispatch rows into LDS
   {
     constexpr int NT = kDqW * 64;
+    constexpr int kStg = 6;                     // chunks per thread in flight (T = 1, k = 8: 4.5)
     const int cpr = I / 8, hch = N * cpr, sch = T * (Is / 8);
-    for (int c0 = 0; c0 < hch + sch; c0 += NT) {   // hch, sch: multiples of 8 (whole lane groups)
-      const int c = c0 + tid;
+    for (int c1 = 0; c1 < hch + sch; c1 += kStg * NT) {
+      u32x4 lh[kStg], ll[kStg];
+#pragma unroll
+      for (int j = 0; j < kStg; ++j) {
+        // no condition on the loads (see load_raw_nc): chunks past the end re-read the last one
+        const int c = min(c1 + j * NT + tid, hch + sch - 1);
+        const uint16_t* ph = p.h_hi;
+        const uint16_t* pl = p.h_lo;
+        int64_t e = static_cast<int64_t>(c / cpr) * I + (c % cpr) * 8;
+        if (c >= hch) {
+          const int cs = c - hch;
+          ph = p.hs_hi;
+          pl = p.hs_lo;
+          e = static_cast<int64_t>(cs / (Is / 8)) * Is + (cs % (Is / 8)) * 8;
+        }
+        lh[j] = ldg16(ph + e);
+        ll[j] = ldg16(pl + e);
+      }
+#pragma unroll
+    for (int j = 0; j < kStg; ++j) {   // hch, sch: multiples of 8 (whole lane groups)
+      const int c = c1 + j * NT + tid;
       if (c < hch) {
         const int r = c / cpr, cc = c % cpr;
-        const int64_t e = static_cast<int64_t>(r) * I + cc * 8;
-        const u32x4 vh = ldg16(p.h_hi + e), vl = ldg16(p.h_lo + e);
+        const u32x4 vh = lh[j], vl = ll[j];
         const uint32_t div8 = q3m_div8_pairs(cc & 3);
         const uint32_t wh[4] = {vh.x, vh.y, vh.z, vh.w}, wl[4] = {vl.x, vl.y, vl.z, vl.w};
         uint16_t oh[8], ol[8];
@@ -1048,11 +1074,11 @@ __global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
         if ((cc & 7) == 0) *reinterpret_cast<float2*>(hsum + (r * ng + (cc >> 3)) * 2) = float2{sx, sxm};
       } else if (c < hch + sch) {
         const int cs = c - hch;
-        const int64_t e = static_cast<int64_t>(cs / (Is / 8)) * Is + (cs % (Is / 8)) * 8;
         const int off = (cs / (Is / 8)) * iss + (cs % (Is / 8)) * 8;
-        *reinterpret_cast<u32x4*>(sh_h + off) = ldg16(p.hs_hi + e);
-        *reinterpret_cast<u32x4*>(sh_l + off) = ldg16(p.hs_lo + e);
+        *reinterpret_cast<u32x4*>(sh_h + off) = lh[j];
+        *reinterpret_cast<u32x4*>(sh_l + off) = ll[j];
       }
+    }
     }
   }
   if (wave == 0)
@@ -1112,10 +1138,10 @@ __global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
     const int nbs = Is / 128, per = (nbs + 3) / 4;
     const int k0 = min(s * per, nbs), k1 = min(k0 + per, nbs);
     RawBF16 rs[kDqSharedKB];
+    if (k0 < k1) {
+      // no condition on the loads (see load_raw_nc): past k1, the last block again (not computed)
 #pragma unroll
-    for (int j = 0; j < kDqSharedKB; ++j) {
-      const int kc = (k0 + j) * 128 + g4 * 32;
-      load_raw(rs[j], p.ws2, row, Is, kc, k0 + j < k1);
+      for (int j = 0; j < kDqSharedKB; ++j) load_raw_nc(rs[j], p.ws2, row, Is, min(k0 + j, k1 - 1) * 128 + g4 * 32);
     }
     __syncthreads();
     // A operand row 2t + plane
@@ -1239,10 +1265,10 @@ size_t up_lds_bytes(const DecodeArgs& p) {
 }
 
 // k_up_q3: activation plane(s), xsum [H/128][8][2][2] f32, K-range partial
-// sums [kUpItems][kUpKS][2][64][2] f32, 64 zero bytes.
+// sums [kQ3fItems][kQ3fKS][2][64][2] f32, 64 zero bytes.
 size_t up_q3_lds_bytes(const DecodeArgs& p) {
   return static_cast<size_t>(p.x_f32 ? 2 : 1) * p.T * (p.H + 8) * 2 +
-         static_cast<size_t>(p.H / 128) * kQ3fMaxTokens * 16 + kUpItems * kUpKS * 2 * 64 * 2 * 4 + 64;
+         static_cast<size_t>(p.H / 128) * kQ3fMaxTokens * 16 + kQ3fItems * kQ3fKS * 2 * 64 * 2 * 4 + 64;
 }
 
 static_assert(sizeof(BlockRoute) <= kUpLdsFixed, "routing block state must fit the gate/up LDS");
@@ -1277,6 +1303,9 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   // q3 (scale, bias) windows: every wave's K range a whole number of G-block
   // batches inside the row (so also 16-byte aligned windows)
   const bool q3win = d.hidden % (kUpKS * kUpBatch * 128) == 0;
+  const bool q3fwin = d.hidden % (kQ3fKS * kUpBatch * 128) == 0;
+  const bool q3f2 = (d.hidden / 128 + kQ3fKS - 1) / kQ3fKS > kUpBatch;   // a wave's range is two or more batches
+  const unsigned q3f_blocks = static_cast<unsigned>(max_slots * ((p.up_tiles + kQ3fItems - 1) / kQ3fItems));
   if (d.tokens >= kDecodeGroupedUpMin && grouped_path(d)) {
     e = launch_grouped_up_routed(d, L, a, a.route.desc, a.route.xrow, a.route.wrow, s, repeat);
     if (e != hipSuccess) return e;
@@ -1285,10 +1314,17 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
     const size_t q3f_lds = up_q3_lds_bytes(p);
     const bool q3f = q3 && d.tokens <= kQ3fMaxTokens && q3f_lds <= kMaxLds;
     for (int r = 0; r < repeat; ++r) {
-      if (q3f && q3win && !p.x_f32) k_up_q3<true, false><<<up_blocks, kUpW * 64, q3f_lds, s>>>(p);
-      else if (q3f && q3win) k_up_q3<true, true><<<up_blocks, kUpW * 64, q3f_lds, s>>>(p);
-      else if (q3f && !p.x_f32) k_up_q3<false, false><<<up_blocks, kUpW * 64, q3f_lds, s>>>(p);
-      else if (q3f) k_up_q3<false, true><<<up_blocks, kUpW * 64, q3f_lds, s>>>(p);
+      if (q3f && !q3f2) {
+        if (q3fwin && !p.x_f32) k_up_q3<true, false, false><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
+        else if (q3fwin) k_up_q3<true, true, false><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
+        else if (!p.x_f32) k_up_q3<false, false, false><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
+        else k_up_q3<false, true, false><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
+      } else if (q3f) {
+        if (q3fwin && !p.x_f32) k_up_q3<true, false, true><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
+        else if (q3fwin) k_up_q3<true, true, true><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
+        else if (!p.x_f32) k_up_q3<false, false, true><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
+        else k_up_q3<false, true, true><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
+      }
       else if (q3 && q3win && !p.x_f32) k_up_stream<kUpBatch, true, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
       else if (q3 && q3win) k_up_stream<kUpBatch, true, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
       else if (q3 && !p.x_f32) k_up_stream<kUpBatch, false, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);

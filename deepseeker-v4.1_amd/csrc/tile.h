@@ -68,6 +68,23 @@ __device__ __forceinline__ void load_raw(RawBF16& r, const uint16_t* W, int64_t 
   for (int j = 0; j < 4; ++j) r.v[j] = ok ? ldg16(W + row * K + kc + 8 * j) : u32x4{0u, 0u, 0u, 0u};
 }
 
+// Loads without a condition: the caller passes an in-range row and K offset.
+// The data of a block outside the wave's range is then loaded from a valid
+// place and cancelled by a zero activation operand.  (A load under a per-lane
+// condition compiles to a branch whose merge copies the loaded registers, and
+// every copy waits for its load: a batch's loads then go out one memory
+// latency at a time.)
+__device__ __forceinline__ void load_raw_nc(RawFP4& r, const uint8_t* W, const uint8_t* S, int64_t row, int K,
+                                            int kc) {
+  r.c = ldg16(W + row * (K / 2) + kc / 2);
+  r.s = ldg<uint8_t>(S + row * (K / 32) + kc / 32);
+}
+
+__device__ __forceinline__ void load_raw_nc(RawBF16& r, const uint16_t* W, int64_t row, int K, int kc) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r.v[j] = ldg16(W + row * K + kc + 8 * j);
+}
+
 // q3 affine (group 64, fp16 scale / bias) in the canonical layout: lane group
 // g's 12 bytes (three LE words, placed by q3_chunk_offset) of a 128-code block
 // hold its 32 codes 32g + 8m + j as pairs P = 4m + j/2 -- P < 15 at bits
@@ -241,6 +258,25 @@ __device__ __forceinline__ void load_role(RawQ3& r, const void* const* ptr, int 
                                           int kc, bool ok) {
   load_raw(r, static_cast<const uint8_t*>(ptr[3 * role]), static_cast<const uint16_t*>(ptr[3 * role + 1]),
            static_cast<const uint16_t*>(ptr[3 * role + 2]), row, K, kc, ok);
+}
+
+__device__ __forceinline__ void load_raw_nc(RawQ3& r, const uint8_t* W, const uint16_t* S, const uint16_t* B,
+                                            int64_t row, int K, int kc) {
+  const auto src = gptr<uint32_t>(W + row * (K / 8 * 3) + q3_chunk_offset(K, kc >> 7, (kc >> 5) & 3));
+  r.w[0] = src[0]; r.w[1] = src[1]; r.w[2] = src[2];
+  const int64_t gi = row * (K / 64) + kc / 64;
+  r.sb = static_cast<uint32_t>(ldg<uint16_t>(S + gi)) | (static_cast<uint32_t>(ldg<uint16_t>(B + gi)) << 16);
+}
+
+__device__ __forceinline__ void load_role_nc(RawFP4& r, const void* const* ptr, int role, int64_t row, int K,
+                                             int kc) {
+  load_raw_nc(r, static_cast<const uint8_t*>(ptr[3 * role]), static_cast<const uint8_t*>(ptr[3 * role + 1]),
+              row, K, kc);
+}
+__device__ __forceinline__ void load_role_nc(RawQ3& r, const void* const* ptr, int role, int64_t row, int K,
+                                             int kc) {
+  load_raw_nc(r, static_cast<const uint8_t*>(ptr[3 * role]), static_cast<const uint16_t*>(ptr[3 * role + 1]),
+              static_cast<const uint16_t*>(ptr[3 * role + 2]), row, K, kc);
 }
 
 __device__ __forceinline__ bf16x8 a_operand(const RawFP4& r, int j) {

@@ -8,7 +8,7 @@ b * sum(x)); the oracle dequantises W first.  Both are exact up to float32
 summation and the final bf16 roundings, so the layer tolerance applies.
 Cases: every token count of the gate/up kernel (1..8) with bf16 and float32
 activations, the scale/bias-window variant (hidden a multiple of 2048) and the
-per-block variant (hidden 1024), activations with a large common offset (the
+per-block variant (hidden 1024; windows need hidden 4096), activations with a large common offset (the
 MFMA sums carry 128 * sum(x / m), removed afterwards), the down kernel
 (intermediate 2048) with a shared expert of 2048 or 1024 rows, none, or a
 callable one, and batch invariance (a token's row does not depend on the
@@ -30,7 +30,7 @@ from test_gpu_layer import run_layer, to_bank, to_shared
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 MID = L.LayerSpec(H=1024, E=64, k=8, I=512, I_shared=512, quant=L.QUANT_Q3)      # per-block scales
-WIN = L.LayerSpec(H=2048, E=32, k=4, I=256, I_shared=256, quant=L.QUANT_Q3)      # scale windows
+WIN = L.LayerSpec(H=4096, E=8, k=4, I=256, I_shared=256, quant=L.QUANT_Q3)       # scale windows
 DN = L.LayerSpec(H=512, E=8, k=4, I=2048, I_shared=1024, quant=L.QUANT_Q3)        # factored down
 
 
