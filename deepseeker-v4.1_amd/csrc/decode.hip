@@ -194,18 +194,21 @@ __device__ __forceinline__ void put_staged_x(const DecodeArgs& p, uint16_t* xh, 
   }
 }
 
-// Shared-expert gate/up tile rt (block = kUpW waves, 16 rows of w1 and w3,
-// all K; wave w takes the w-th K range, two K blocks in flight).  Called after the block's x chunks have been
+// Shared-expert gate/up tile rt (block = NW waves, ROWS (8 or 16) rows of w1
+// and w3, all K; wave w takes the w-th K range, two K blocks in flight).  With
+// 8 rows the MFMA's rows 8..15 repeat rows 0..7 (the same addresses, so no
+// extra traffic) and are not stored: twice the tiles, so the shared stream is
+// spread over twice the CUs.  Called after the block's x chunks have been
 // loaded into registers; writes them to LDS once its own weight loads are in
 // flight.
-template <bool kF32>
+template <bool kF32, int NW, int ROWS>
 __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint16_t* xh, uint16_t* xl, int xs,
                                                bool xreg, const u32x4 (&xv)[kUpXRegChunks][2], uint16_t* lds,
                                                int tid, int lane, int wave, int r16, int g4) {
   const int T = p.T, K = p.H;
-  const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
+  const uint32_t row = static_cast<uint32_t>(rt * ROWS + (r16 & (ROWS - 1)));
   const int nblk = (K + 127) / 128;
-  const int per = (nblk + kUpW - 1) / kUpW;
+  const int per = (nblk + NW - 1) / NW;
   const int k0 = min(wave * per, nblk), k1 = min(k0 + per, nblk);
   const bool tv = r16 < T;
   RawBF16 a1, a3, b1, b3;
@@ -217,7 +220,7 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint
   };
   ld(a1, a3, k0);
   ld(b1, b3, k0 + 1);
-  if (xreg) put_staged_x<kF32, kUpW * 64>(p, xh, xl, xs, tid, xv);
+  if (xreg) put_staged_x<kF32, NW * 64>(p, xh, xl, xs, tid, xv);
   __syncthreads();
   const uint16_t* bh = xh + (tv ? r16 : 0) * xs;
   const uint16_t* bl = xl + (tv ? r16 : 0) * xs;
@@ -234,21 +237,23 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint
     if (kb + 1 < k1) mm(b1, b3, kb + 1);
     if (kb + 3 < k1) ld(b1, b3, kb + 3);
   }
-  // K ranges added in wave order
-  float (*red)[2][64][4] = reinterpret_cast<float (*)[2][64][4]>(lds + (kF32 ? 2 : 1) * T * xs);
+  // K ranges added in wave order; the partial sums reuse the activation area
+  // once every wave is done with it
+  float (*red)[2][64][4] = reinterpret_cast<float (*)[2][64][4]>(lds);
+  __syncthreads();
   *reinterpret_cast<f32x4*>(&red[wave][0][lane][0]) = ag;
   *reinterpret_cast<f32x4*>(&red[wave][1][lane][0]) = au;
   __syncthreads();
-  if (wave == 0 && tv) {
+  if (wave == 0 && tv && g4 < ROWS / 4) {
 #pragma unroll
-    for (int w = 1; w < kUpW; ++w) {
+    for (int w = 1; w < NW; ++w) {
       ag += *reinterpret_cast<const f32x4*>(&red[w][0][lane][0]);
       au += *reinterpret_cast<const f32x4*>(&red[w][1][lane][0]);
     }
     uint16_t hh[4], hl[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) split_bf16(silu_clamped(ag[q], au[q], p.limit), hh[q], hl[q]);
-    const int64_t off = static_cast<int64_t>(r16) * p.Is + rt * 16 + 4 * g4;
+    const int64_t off = static_cast<int64_t>(r16) * p.Is + rt * ROWS + 4 * g4;
     *reinterpret_cast<uint2*>(p.hs_hi + off) = uint2{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16)};
     *reinterpret_cast<uint2*>(p.hs_lo + off) = uint2{hl[0] | (uint32_t(hl[1]) << 16), hl[2] | (uint32_t(hl[3]) << 16)};
   }
@@ -260,8 +265,13 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint
 // expert (bf16 w1/w3, K split over the block's waves); hs = SwiGLU(gate, up)
 // as bf16 hi/lo planes.  The routing block's dependent loads and wave
 // reductions overlap the shared expert's weight stream.
+// 8-row shared tiles (a 2048-row shared expert: 256 tiles, one per CU) and
+// 16 waves per block, so each wave takes two K blocks, all in flight at once.
+constexpr int kRsW = 8;
+constexpr int kRsRows = 8;
+
 template <bool kF32>
-__global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 ? 3 : 4))) void k_route_shared(
+__global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_route_shared(
     DecodeArgs p) {
   extern __shared__ __align__(16) uint16_t lds_up[];
   if (blockIdx.x == 0) {
@@ -275,8 +285,9 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
   uint16_t* xh = lds_up;
   uint16_t* xl = lds_up + p.T * xs;
   u32x4 xv[kUpXRegChunks][2];
-  const bool xreg = load_x<kF32, kUpW * 64>(p, xh, xl, xs, tid, xv);
-  shared_up_tile<kF32>(p, static_cast<int>(blockIdx.x) - 1, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave, r16, g4);
+  const bool xreg = load_x<kF32, kRsW * 64>(p, xh, xl, xs, tid, xv);
+  shared_up_tile<kF32, kRsW, kRsRows>(p, static_cast<int>(blockIdx.x) - 1, xh, xl, xs, xreg, xv, lds_up, tid, lane,
+                                      wave, r16, g4);
 }
 
 // Routed gate/up of the decode pipeline.  Each block takes kUpItems row
@@ -779,18 +790,34 @@ struct DownBatch {
   Raw r[kStSlots][kStKB];
 };
 
+// FP4: the codes of each slot's kStKB blocks and, instead of one scale byte
+// per block and lane (a wave instruction touching 16 cache lines per block),
+// one 8-byte window per slot holding the scales of both blocks for all four
+// lane groups (byte 4j + g of block kb0 + j); the byte is picked at use.
+template <>
+struct DownBatch<RawFP4> {
+  u32x4 c[kStSlots][kStKB];
+  u32x2 sw[kStSlots];
+};
+static_assert(kStKB == 2, "the FP4 scale window holds two blocks");
+
 template <typename Raw>
 __device__ __forceinline__ void load_down_batch(DownBatch<Raw>& b, const DecodeArgs& p, int u0, int U,
                                                 uint32_t row, int kb0, int g4) {
   const int I = p.I;
 #pragma unroll
   for (int i = 0; i < kStSlots; ++i) {
-    const bool in = u0 + i < U;
-    const SlotDesc* d = p.desc + (in ? u0 + i : 0);
+    const int su = u0 + i < U ? u0 + i : 0;   // slots past U re-read slot 0 and are not computed
+    if constexpr (std::is_same_v<Raw, RawFP4>) {
+      // the staged kernel's K blocks cover I exactly (I = kStW * kStKB * 128)
+      const uint8_t* W = static_cast<const uint8_t*>(desc_ptr(p.desc, su, 6));
+      const uint8_t* S = static_cast<const uint8_t*>(desc_ptr(p.desc, su, 7));
 #pragma unroll
-    for (int j = 0; j < kStKB; ++j) {
-      // no condition (see load_raw_nc): slots past U re-read slot 0 and are not computed
-      load_role_nc(b.r[i][j], d->p, 2, row, I, min((kb0 + j) * 128 + g4 * 32, I - 32));
+      for (int j = 0; j < kStKB; ++j) b.c[i][j] = ldg16(W + row * static_cast<uint32_t>(I / 2) + (kb0 + j) * 64 + g4 * 16);
+      b.sw[i] = ldg<u32x2>(S + row * static_cast<uint32_t>(I / 32) + kb0 * 4);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kStKB; ++j) load_w2_nc(b.r[i][j], p.desc, su, row, I, min((kb0 + j) * 128 + g4 * 32, I - 32));
     }
   }
 }
@@ -816,7 +843,12 @@ __device__ __forceinline__ void mma_down_batch(const DownBatch<Raw>& b, int u0, 
 #pragma unroll
     for (int j = 0; j < kStKB; ++j) {
       const int kc = (kb0 + j) * 128 + g4 * 32;
-      mma_cols(b.r[i][j], brow, kc, tok && kc < I, acc);
+      if constexpr (std::is_same_v<Raw, RawFP4>) {
+        const uint32_t w = j == 0 ? b.sw[i].x : b.sw[i].y;
+        mma_cols(RawFP4{b.c[i][j], (w >> (8 * g4)) & 0xffu}, brow, kc, tok && kc < I, acc);
+      } else {
+        mma_cols(b.r[i][j], brow, kc, tok && kc < I, acc);
+      }
     }
   }
 }
@@ -842,7 +874,9 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
   int* ldrow = reinterpret_cast<int*>(reinterpret_cast<char*>(lds_dn) +   // [U][T] dispatch rows (rowmap copy)
                                       (act_bytes > kStRedBytes ? act_bytes : kStRedBytes));
   const int kb0 = wave * kStKB;
-  // 1. activations and dispatch rows, alone in flight (a short wait), into LDS
+  // 1. activations and dispatch rows, alone in flight (a short wait), into LDS;
+  // one dispatch-row entry per thread (U * T <= kStMaxSlots * 8 <= kStW * 64)
+  const int rm = p.rowmap[min(tid, U * p.T - 1)];
   const int hch = N * (I / 8), sch = p.T * (Is / 8);
   // chunk c < hch: h row c / (I/8); c >= hch: hs row; kStStage chunks per thread in flight at once
   for (int c0 = tid; c0 < hch + sch; c0 += kStStage * kStW * 64) {
@@ -878,8 +912,8 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
       }
     }
   }
-  if (wave == 0)
-    for (int i = lane; i < U * p.T; i += 64) ldrow[i] = p.rowmap[i];
+  wait_vm_all();   // only staging loads outstanding (see wait_vm_all)
+  if (tid < U * p.T) ldrow[tid] = rm;
   // 2. every weight of the block in flight: the shared batch and kStRing routed batches
   RawBF16 rs[kStKB];
   if (Is > 0) {
@@ -955,11 +989,12 @@ struct DqSlot {
 
 __device__ __forceinline__ void load_dq_slot(DqSlot& r, const DecodeArgs& p, int u, int U, uint32_t row,
                                              int sbk, int g4) {
-  // no condition on the loads (see load_raw_nc): slots past U re-read slot 0 and are not computed
-  const SlotDesc* d = p.desc + (u < U ? u : 0);
+  // no condition on the loads (see load_raw_nc): slots past U re-read slot 0
+  // and are not computed; descriptors through the scalar cache (desc_ptr)
+  const int su = u < U ? u : 0;
   const int I = p.I;
-  const auto c = gptr<u32x4>(static_cast<const uint8_t*>(d->p[6]) + row * static_cast<uint32_t>(I / 8 * 3) +
-                             sbk * 192 + 48 * g4);
+  const auto c = gptr<u32x4>(static_cast<const uint8_t*>(desc_ptr(p.desc, su, 6)) +
+                             row * static_cast<uint32_t>(I / 8 * 3) + sbk * 192 + 48 * g4);
 #pragma unroll
   for (int v = 0; v < 3; ++v) {
     const u32x4 a = c[v];
@@ -967,8 +1002,8 @@ __device__ __forceinline__ void load_dq_slot(DqSlot& r, const DecodeArgs& p, int
     for (int j = 0; j < 4; ++j) r.c[(4 * v + j) / 3][(4 * v + j) % 3] = a[j];
   }
   const uint32_t wo = (row * static_cast<uint32_t>(I / 64) + 8 * sbk) * 2;   // bytes
-  r.s = ldg16(static_cast<const uint8_t*>(d->p[7]) + wo);
-  r.b = ldg16(static_cast<const uint8_t*>(d->p[8]) + wo);
+  r.s = ldg16(static_cast<const uint8_t*>(desc_ptr(p.desc, su, 7)) + wo);
+  r.b = ldg16(static_cast<const uint8_t*>(desc_ptr(p.desc, su, 8)) + wo);
 }
 
 // Final add and cast of one output element (token t, column n).
@@ -1020,7 +1055,9 @@ __global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
   const uint16_t* zero = reinterpret_cast<const uint16_t*>(red + 2);                // 64 zero bytes
   int* ldrow = reinterpret_cast<int*>(red + 2) + 16;                                // [U][T]
   if (tid < 4) reinterpret_cast<u32x4*>(red + 2)[tid] = u32x4{0u, 0u, 0u, 0u};
-  // 1. activations (routed rows scaled and summed per group) and dispatch rows into LDS
+  // 1. activations (routed rows scaled and summed per group) and dispatch rows
+  // into LDS; one dispatch-row entry per thread (U * T <= 16 * 4 * 4 <= kDqW * 64)
+  const int rm = p.rowmap[min(tid, U * T - 1)];
   {
     constexpr int NT = kDqW * 64;
     constexpr int kStg = 6;                     // chunks per thread in flight (T = 1, k = 8: 4.5)
@@ -1081,8 +1118,8 @@ __global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
     }
     }
   }
-  if (wave == 0)
-    for (int i = lane; i < U * T; i += 64) ldrow[i] = p.rowmap[i];
+  wait_vm_all();   // only staging loads outstanding (see wait_vm_all)
+  if (tid < U * T) ldrow[tid] = rm;
   const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
   if (wave < kDqRouted) {
     // 2. routed: superblock `wave` of every active expert's w2 rows
@@ -1271,18 +1308,25 @@ size_t up_q3_lds_bytes(const DecodeArgs& p) {
          static_cast<size_t>(p.H / 128) * kQ3fMaxTokens * 16 + kQ3fItems * kQ3fKS * 2 * 64 * 2 * 4 + 64;
 }
 
-static_assert(sizeof(BlockRoute) <= kUpLdsFixed, "routing block state must fit the gate/up LDS");
+// k_route_shared: the routing block's state, or a shared tile's activation
+// planes and then (over them) its wave partial sums [kRsW][2][64][4] f32.
+constexpr size_t kRsRedBytes = kRsW * 2 * 64 * 4 * 4;
+static_assert(sizeof(BlockRoute) <= kRsRedBytes, "routing block state must fit the route/shared LDS");
+size_t rs_lds_bytes(const DecodeArgs& p) {
+  const size_t planes = static_cast<size_t>(p.x_f32 ? 2 : 1) * p.T * (p.H + 8) * 2;
+  return planes > kRsRedBytes ? planes : kRsRedBytes;
+}
 
 }  // namespace
 
 hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                hipStream_t s, int repeat) {
   const DecodeArgs p = decode_args(d, L, a);
-  const unsigned blocks = static_cast<unsigned>(1 + p.Is / 16);
-  const size_t lds = up_lds_bytes(p);
+  const unsigned blocks = static_cast<unsigned>(1 + p.Is / kRsRows);
+  const size_t lds = rs_lds_bytes(p);
   for (int r = 0; r < repeat; ++r) {
-    if (p.x_f32) k_route_shared<true><<<blocks, kUpW * 64, lds, s>>>(p);
-    else k_route_shared<false><<<blocks, kUpW * 64, lds, s>>>(p);
+    if (p.x_f32) k_route_shared<true><<<blocks, kRsW * 64, lds, s>>>(p);
+    else k_route_shared<false><<<blocks, kRsW * 64, lds, s>>>(p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

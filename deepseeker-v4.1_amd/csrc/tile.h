@@ -68,6 +68,14 @@ __device__ __forceinline__ void load_raw(RawBF16& r, const uint16_t* W, int64_t 
   for (int j = 0; j < 4; ++j) r.v[j] = ok ? ldg16(W + row * K + kc + 8 * j) : u32x4{0u, 0u, 0u, 0u};
 }
 
+// Wait for every outstanding vector memory load (s_waitcnt vmcnt(0); expcnt
+// and lgkmcnt left alone).  After a staging loop whose stores are guarded,
+// the loaded registers stay "pending" on the path that skipped the store, and
+// the compiler's wait before their next use would also wait for every weight
+// load issued in between; an explicit wait while only the staging loads are
+// outstanding costs nothing and clears that state.
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Loads without a condition: the caller passes an in-range row and K offset.
 // The data of a block outside the wave's range is then loaded from a valid
 // place and cancelled by a zero activation operand.  (A load under a per-lane
@@ -277,6 +285,25 @@ __device__ __forceinline__ void load_role_nc(RawQ3& r, const void* const* ptr, i
                                              int kc) {
   load_raw_nc(r, static_cast<const uint8_t*>(ptr[3 * role]), static_cast<const uint16_t*>(ptr[3 * role + 1]),
               static_cast<const uint16_t*>(ptr[3 * role + 2]), row, K, kc);
+}
+
+// Pointer i of slot u's descriptor (u wave-uniform) through the constant
+// address space, i.e. a scalar load: the descriptors are written by an earlier
+// kernel and only read here (the scalar cache starts empty at every launch).
+// A vector load of a pointer would wait behind the weight loads already in
+// flight before the next batch could be addressed.
+__device__ __forceinline__ const void* desc_ptr(const SlotDesc* desc, int u, int i) {
+  return ((const __attribute__((address_space(4))) SlotDesc*)desc)[u].p[i];
+}
+
+// Role 2 (w2) of slot u without conditions (see load_raw_nc).
+__device__ __forceinline__ void load_w2_nc(RawFP4& r, const SlotDesc* desc, int u, int64_t row, int K, int kc) {
+  load_raw_nc(r, static_cast<const uint8_t*>(desc_ptr(desc, u, 6)), static_cast<const uint8_t*>(desc_ptr(desc, u, 7)),
+              row, K, kc);
+}
+__device__ __forceinline__ void load_w2_nc(RawQ3& r, const SlotDesc* desc, int u, int64_t row, int K, int kc) {
+  load_raw_nc(r, static_cast<const uint8_t*>(desc_ptr(desc, u, 6)), static_cast<const uint16_t*>(desc_ptr(desc, u, 7)),
+              static_cast<const uint16_t*>(desc_ptr(desc, u, 8)), row, K, kc);
 }
 
 __device__ __forceinline__ bf16x8 a_operand(const RawFP4& r, int j) {
