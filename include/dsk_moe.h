@@ -12,9 +12,11 @@
  * Layouts (row-major, the reference's expert weight layout):
  *   FP4 role [N, K]:  packed [N, K/2] u8 (two e2m1 codes per byte, low nibble
  *                     first) + scales [N, K/32] u8 (E8M0, 2^(b-127), 0xFF = NaN)
- *   Q3 role [N, K]:   packed [N, 3K/8] u8 (canonical 48-byte blocks of 128
- *                     codes) + scales [N, K/64] f16 + biases [N, K/64] f16,
- *                     W = s*q + b
+ *   Q3 role [N, K]:   packed [N, 3K/8] u8 (canonical packing: 128-code blocks
+ *                     of four 12-byte lane-group chunks; in every full 512-code
+ *                     superblock, chunk g of its 4 blocks sits at byte 48g,
+ *                     block order; a tail block is plain 48 bytes) + scales
+ *                     [N, K/64] f16 + biases [N, K/64] f16, W = s*q + b
  *   roles: w1, w3 [I, H]; w2 [H, I]; used as x @ W^T.
  *   shared expert: bf16 w1, w3 [Is, H]; w2 [H, Is].
  */
