@@ -374,8 +374,10 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
         const int sh = 16 * (g4 >> 1);
 #pragma unroll
         for (int i = 0; i < G; ++i) {
-          r1[i].sb = ((win[0][i] >> sh) & 0xffffu) | (((win[1][i] >> sh) & 0xffffu) << 16);
-          r3[i].sb = ((win[2][i] >> sh) & 0xffffu) | (((win[3][i] >> sh) & 0xffffu) << 16);
+          r1[i].s = (win[0][i] >> sh) & 0xffffu;
+          r1[i].b = (win[1][i] >> sh) & 0xffffu;
+          r3[i].s = (win[2][i] >> sh) & 0xffffu;
+          r3[i].b = (win[3][i] >> sh) & 0xffffu;
         }
       }
     };

@@ -49,9 +49,10 @@ struct GroupedArgs {
 
 // K blocks per weight batch, two batches in flight per wave, within the
 // register budget of four waves per SIMD: one for bf16 rows (64 bytes per
-// lane and K block), two for FP4 and q3 (20 and 16).
+// lane and K block) and for q3 (20 bytes, but its dequantisation needs many
+// temporaries), two for FP4 (20 bytes).
 template <typename Raw>
-constexpr int batch_blocks() { return sizeof(Raw) > 32 ? 1 : 2; }
+constexpr int batch_blocks() { return std::is_same_v<Raw, RawFP4> ? 2 : 1; }
 
 // Rows [c0, c0 + cols) of the slot's activations (row r comes from source row
 // src(r) of `base`, row stride `ld` elements, K elements) into LDS rows of
@@ -64,8 +65,8 @@ __device__ __forceinline__ void stage_rows(uint16_t* dst, const uint16_t* base, 
     u32x4 v[kStageQ];
 #pragma unroll
     for (int q = 0; q < kStageQ; ++q) {
-      const int cc = c + q * nt;
-      if (cc < chunks) v[q] = ldg16(base + static_cast<int64_t>(src(cc / cpr)) * ld + (cc % cpr) * 8);
+      const int cc = min(c + q * nt, chunks - 1);   // no condition on the load (see load_raw_nc)
+      v[q] = ldg16(base + static_cast<int64_t>(src(cc / cpr)) * ld + (cc % cpr) * 8);
     }
 #pragma unroll
     for (int q = 0; q < kStageQ; ++q) {
@@ -93,13 +94,14 @@ __device__ __forceinline__ void up_block(const GroupedArgs& p, LoadW load_w, int
   for (int c0 = 0; c0 < n; c0 += kGNC) {
     const int cols = min(kGNC, n - c0);
     Raw a1[G], a3[G], b1[G], b3[G];
+    // no condition on the loads (see load_raw_nc): rows past the tile read
+    // row 0, blocks past the range the range's last block (not computed)
     auto ld = [&](Raw (&r1)[G], Raw (&r3)[G], int kb) {
 #pragma unroll
       for (int i = 0; i < G; ++i) {
-        const int kc = (kb + i) * 128 + g4 * 32;
-        const bool ok = rok && kb + i < k1;
-        load_w(r1[i], 0, row, kc, ok);
-        load_w(r3[i], 1, row, kc, ok);
+        const int kc = min(kb + i, k1 - 1) * 128 + g4 * 32;
+        load_w(r1[i], 0, rok ? row : 0u, kc);
+        load_w(r3[i], 1, rok ? row : 0u, kc);
       }
     };
     ld(a1, a3, k0);
@@ -160,9 +162,7 @@ __global__ __launch_bounds__(kGW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   const int item = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / kGKS;
   if (b < p.up_shared) {
     const int rt = b * kGI + item;
-    auto load_w = [&](RawBF16& r, int role, uint32_t row, int kc, bool ok) {
-      load_raw(r, role ? p.ws3 : p.ws1, row, p.H, kc, ok);
-    };
+    auto load_w = [&](RawBF16& r, int role, uint32_t row, int kc) { load_raw_nc(r, role ? p.ws3 : p.ws1, row, p.H, kc); };
     up_block<RawBF16>(p, load_w, rt, rt < p.Is / 16, p.T, 0, true, lds_g);
     return;
   }
@@ -171,7 +171,9 @@ __global__ __launch_bounds__(kGW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   if (slot >= p.active[0]) return;
   const SlotDesc* d = p.desc + slot;
   const int rt = (rb % p.up_groups) * kGI + item;
-  auto load_w = [&](Raw& r, int role, uint32_t row, int kc, bool ok) { load_role(r, d->p, role, row, p.H, kc, ok); };
+  const void* const wp[6] = {desc_ptr(p.desc, slot, 0), desc_ptr(p.desc, slot, 1), desc_ptr(p.desc, slot, 2),
+                             desc_ptr(p.desc, slot, 3), desc_ptr(p.desc, slot, 4), desc_ptr(p.desc, slot, 5)};
+  auto load_w = [&](Raw& r, int role, uint32_t row, int kc) { load_role_nc(r, wp, role, row, p.H, kc); };
   up_block<Raw>(p, load_w, rt, rt < p.I / 16, d->n_tok, d->tok_base, false, lds_g);
 }
 
@@ -197,9 +199,11 @@ __device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, i
   for (int c0 = 0; c0 < n; c0 += kGNC) {
     const int cols = min(kGNC, n - c0);
     Raw a[G], b[G];
+    // no condition on the loads (see load_raw_nc): blocks past the range
+    // re-read its last block (not computed)
     auto ld = [&](Raw (&r)[G], int kb) {
 #pragma unroll
-      for (int i = 0; i < G; ++i) load_w(r[i], row, (kb + i) * 128 + g4 * 32, kb + i < k1);
+      for (int i = 0; i < G; ++i) load_w(r[i], row, min(kb + i, k1 - 1) * 128 + g4 * 32);
     };
     ld(a, k0);
     ld(b, k0 + G);
@@ -249,7 +253,7 @@ __global__ __launch_bounds__(kDW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   const int item = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / kDKS;
   if (b < p.dn_shared) {
     const int rt = b * kDI + item;
-    auto load_w = [&](RawBF16& r, uint32_t row, int kc, bool ok) { load_raw(r, p.ws2, row, p.Is, kc, ok); };
+    auto load_w = [&](RawBF16& r, uint32_t row, int kc) { load_raw_nc(r, p.ws2, row, p.Is, kc); };
     down_block<RawBF16>(p, load_w, rt, p.T, 0, true, lds_g);
     return;
   }
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(kDW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   if (slot >= p.active[0]) return;
   const SlotDesc* d = p.desc + slot;
   const int rt = (rb % p.dn_groups) * kDI + item;
-  auto load_w = [&](Raw& r, uint32_t row, int kc, bool ok) { load_role(r, d->p, 2, row, p.I, kc, ok); };
+  auto load_w = [&](Raw& r, uint32_t row, int kc) { load_w2_nc(r, p.desc, slot, row, p.I, kc); };
   down_block<Raw>(p, load_w, rt, d->n_tok, d->tok_base, false, lds_g);
 }
 

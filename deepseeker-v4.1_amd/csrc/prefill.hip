@@ -87,7 +87,8 @@ struct StageQ3 {
     const auto src = gptr<uint32_t>(W + row * (K / 8 * 3) + q3_chunk_offset(K, st >> 1, 2 * (st & 1) + hf));
     r.w[0] = src[0]; r.w[1] = src[1]; r.w[2] = src[2];
     const int64_t gi = row * (K / 64) + st;
-    r.sb = static_cast<uint32_t>(ldg<uint16_t>(S + gi)) | (static_cast<uint32_t>(ldg<uint16_t>(B + gi)) << 16);
+    r.s = ldg<uint16_t>(S + gi);
+    r.b = ldg<uint16_t>(B + gi);
   }
   __device__ __forceinline__ bf16x8 chunk(int q) const {
     return q == 0 ? q3_operand<0>(r) : (q == 1 ? q3_operand<1>(r) : (q == 2 ? q3_operand<2>(r) : q3_operand<3>(r)));

@@ -99,7 +99,8 @@ __device__ __forceinline__ void load_raw_nc(RawBF16& r, const uint16_t* W, int64
 // 3(P%5) / 16 + 3(P%5) of word P/5, pair 15 in bits 15 / 31 of the three
 // words.  A lane's 32 codes lie in one 64-group, so one scale and one bias per
 // lane and block.
-struct RawQ3 { uint32_t w[3]; uint32_t sb; };   // sb: fp16 scale (low), fp16 bias (high)
+// s, b: fp16 scale and bias bits (low halves), loaded separately and combined at use
+struct RawQ3 { uint32_t w[3]; uint32_t s, b; };
 
 __device__ __forceinline__ void load_raw(RawQ3& r, const uint8_t* W, const uint16_t* S, const uint16_t* B,
                                          int64_t row, int K, int kc, bool ok) {
@@ -107,10 +108,11 @@ __device__ __forceinline__ void load_raw(RawQ3& r, const uint8_t* W, const uint1
     const auto src = gptr<uint32_t>(W + row * (K / 8 * 3) + q3_chunk_offset(K, kc >> 7, (kc >> 5) & 3));
     r.w[0] = src[0]; r.w[1] = src[1]; r.w[2] = src[2];
     const int64_t gi = row * (K / 64) + kc / 64;
-    r.sb = static_cast<uint32_t>(ldg<uint16_t>(S + gi)) | (static_cast<uint32_t>(ldg<uint16_t>(B + gi)) << 16);
+    r.s = ldg<uint16_t>(S + gi);
+    r.b = ldg<uint16_t>(B + gi);
   } else {
     r.w[0] = r.w[1] = r.w[2] = 0u;
-    r.sb = 0u;
+    r.s = r.b = 0u;
   }
 }
 
@@ -122,9 +124,9 @@ __device__ __forceinline__ void load_raw(RawQ3& r, const uint8_t* W, const uint1
 // this is f32(s)*q + f32(b) with the format's rounding.
 struct Q3Scales { float s, s2, s8, s16, b; };   // s, s/2, s/8, s/16, bias
 
-__device__ __forceinline__ Q3Scales q3_scales(uint32_t sb) {
-  const float s = f16_bits_to_f32(static_cast<uint16_t>(sb & 0xffffu));
-  return Q3Scales{s, s * 0.5f, s * 0.125f, s * 0.0625f, f16_bits_to_f32(static_cast<uint16_t>(sb >> 16))};
+__device__ __forceinline__ Q3Scales q3_scales(uint32_t sbits, uint32_t bbits) {
+  const float s = f16_bits_to_f32(static_cast<uint16_t>(sbits));
+  return Q3Scales{s, s * 0.5f, s * 0.125f, s * 0.0625f, f16_bits_to_f32(static_cast<uint16_t>(bbits))};
 }
 
 // Byte k of v as float (v_cvt_f32_ubyteK: no shift or mask needed).
@@ -177,7 +179,7 @@ __device__ __forceinline__ void q3_pair_val(const RawQ3& r, const Q3Scales& c, f
 // roundings; s*q is exact), rounded to bf16.
 template <int J>
 __device__ __forceinline__ bf16x8 q3_operand(const RawQ3& r) {
-  const Q3Scales c = q3_scales(r.sb);
+  const Q3Scales c = q3_scales(r.s, r.b);
   float v[8];
   q3_pair_val<4 * J + 0>(r, c, v[0], v[1]);
   q3_pair_val<4 * J + 1>(r, c, v[2], v[3]);
@@ -273,7 +275,8 @@ __device__ __forceinline__ void load_raw_nc(RawQ3& r, const uint8_t* W, const ui
   const auto src = gptr<uint32_t>(W + row * (K / 8 * 3) + q3_chunk_offset(K, kc >> 7, (kc >> 5) & 3));
   r.w[0] = src[0]; r.w[1] = src[1]; r.w[2] = src[2];
   const int64_t gi = row * (K / 64) + kc / 64;
-  r.sb = static_cast<uint32_t>(ldg<uint16_t>(S + gi)) | (static_cast<uint32_t>(ldg<uint16_t>(B + gi)) << 16);
+  r.s = ldg<uint16_t>(S + gi);
+  r.b = ldg<uint16_t>(B + gi);
 }
 
 __device__ __forceinline__ void load_role_nc(RawFP4& r, const void* const* ptr, int role, int64_t row, int K,
