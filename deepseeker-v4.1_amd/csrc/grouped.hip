@@ -78,9 +78,9 @@ __device__ __forceinline__ void stage_rows(uint16_t* dst, const uint16_t* base, 
 
 // Gate/up of one block: row tile rt (rows 16 rt ..) of w1 and w3 for the n
 // dispatch rows base .. base + n - 1 (shared: tokens 0 .. n - 1).
-template <typename Raw, typename LoadW>
-__device__ __forceinline__ void up_block(const GroupedArgs& p, LoadW load_w, int rt, bool rok, int n, int base,
-                                         bool shared, uint16_t* lds) {
+template <typename Raw, typename LoadW, typename WPtr>
+__device__ __forceinline__ void up_block(const GroupedArgs& p, LoadW load_w, WPtr wptr, int rt, bool rok, int n,
+                                         int base, bool shared, uint16_t* lds) {
   constexpr int G = batch_blocks<Raw>();
   const int lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
@@ -94,36 +94,56 @@ __device__ __forceinline__ void up_block(const GroupedArgs& p, LoadW load_w, int
   for (int c0 = 0; c0 < n; c0 += kGNC) {
     const int cols = min(kGNC, n - c0);
     Raw a1[G], a3[G], b1[G], b3[G];
+    // FP4: each role's scales of a batch's 2 blocks (all lane groups) as one
+    // 8-byte window instead of one byte per lane and block (picked at use)
+    u32x2 wa1{}, wa3{}, wb1{}, wb3{};
     // no condition on the loads (see load_raw_nc): rows past the tile read
     // row 0, blocks past the range the range's last block (not computed)
-    auto ld = [&](Raw (&r1)[G], Raw (&r3)[G], int kb) {
+    auto ld = [&](Raw (&r1)[G], Raw (&r3)[G], u32x2& w1, u32x2& w3, int kb) {
+      const uint32_t rw = rok ? row : 0u;
+      if constexpr (std::is_same_v<Raw, RawFP4> && G == 2) {
+        const int kbc = min(kb, k1 - 2);   // every range has an even number of blocks
+        const uint32_t co = rw * static_cast<uint32_t>(K / 2) + g4 * 16, so = rw * static_cast<uint32_t>(K / 32) + kbc * 4;
 #pragma unroll
-      for (int i = 0; i < G; ++i) {
-        const int kc = min(kb + i, k1 - 1) * 128 + g4 * 32;
-        load_w(r1[i], 0, rok ? row : 0u, kc);
-        load_w(r3[i], 1, rok ? row : 0u, kc);
+        for (int i = 0; i < G; ++i) {
+          r1[i].c = ldg16(static_cast<const uint8_t*>(wptr(0)) + co + (kbc + i) * 64);
+          r3[i].c = ldg16(static_cast<const uint8_t*>(wptr(3)) + co + (kbc + i) * 64);
+        }
+        w1 = ldg<u32x2>(static_cast<const uint8_t*>(wptr(1)) + so);
+        w3 = ldg<u32x2>(static_cast<const uint8_t*>(wptr(4)) + so);
+      } else {
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+          const int kc = min(kb + i, k1 - 1) * 128 + g4 * 32;
+          load_w(r1[i], 0, rw, kc);
+          load_w(r3[i], 1, rw, kc);
+        }
       }
     };
-    ld(a1, a3, k0);
-    ld(b1, b3, k0 + G);
+    ld(a1, a3, wa1, wa3, k0);
+    ld(b1, b3, wb1, wb3, k0 + G);
     if (shared) stage_rows(lds, p.x, K, K, cols, [&](int r) { return c0 + r; });
     else stage_rows(lds, p.x, K, K, cols, [&](int r) { return p.xrow[base + c0 + r]; });
     __syncthreads();
     const bool tv = r16 < cols;
     const uint16_t* brow = lds + (tv ? r16 : 0) * xs;
     f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
-    auto mm = [&](const Raw (&r1)[G], const Raw (&r3)[G], int kb) {
+    auto mm = [&](Raw (&r1)[G], Raw (&r3)[G], const u32x2& w1, const u32x2& w3, int kb) {
 #pragma unroll
       for (int i = 0; i < G; ++i) {
         const int kc = (kb + i) * 128 + g4 * 32;
+        if constexpr (std::is_same_v<Raw, RawFP4> && G == 2) {
+          r1[i].s = ((i == 0 ? w1.x : w1.y) >> (8 * g4)) & 0xffu;
+          r3[i].s = ((i == 0 ? w3.x : w3.y) >> (8 * g4)) & 0xffu;
+        }
         mma_block2(r1[i], r3[i], brow, kc, tv && kb + i < k1, ag, au);
       }
     };
     for (int kb = k0; kb < k1; kb += 2 * G) {
-      mm(a1, a3, kb);
-      if (kb + 2 * G < k1) ld(a1, a3, kb + 2 * G);
-      if (kb + G < k1) mm(b1, b3, kb + G);
-      if (kb + 3 * G < k1) ld(b1, b3, kb + 3 * G);
+      mm(a1, a3, wa1, wa3, kb);
+      if (kb + 2 * G < k1) ld(a1, a3, wa1, wa3, kb + 2 * G);
+      if (kb + G < k1) mm(b1, b3, wb1, wb3, kb + G);
+      if (kb + 3 * G < k1) ld(b1, b3, wb1, wb3, kb + 3 * G);
     }
     if constexpr (kGKS > 1) {
       __syncthreads();   // every wave is done with the x tile
@@ -163,7 +183,7 @@ __global__ __launch_bounds__(kGW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   if (b < p.up_shared) {
     const int rt = b * kGI + item;
     auto load_w = [&](RawBF16& r, int role, uint32_t row, int kc) { load_raw_nc(r, role ? p.ws3 : p.ws1, row, p.H, kc); };
-    up_block<RawBF16>(p, load_w, rt, rt < p.Is / 16, p.T, 0, true, lds_g);
+    up_block<RawBF16>(p, load_w, [&](int) -> const void* { return p.ws1; }, rt, rt < p.Is / 16, p.T, 0, true, lds_g);
     return;
   }
   const int rb = b - p.up_shared;
@@ -174,13 +194,13 @@ __global__ __launch_bounds__(kGW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   const void* const wp[6] = {desc_ptr(p.desc, slot, 0), desc_ptr(p.desc, slot, 1), desc_ptr(p.desc, slot, 2),
                              desc_ptr(p.desc, slot, 3), desc_ptr(p.desc, slot, 4), desc_ptr(p.desc, slot, 5)};
   auto load_w = [&](Raw& r, int role, uint32_t row, int kc) { load_role_nc(r, wp, role, row, p.H, kc); };
-  up_block<Raw>(p, load_w, rt, rt < p.I / 16, d->n_tok, d->tok_base, false, lds_g);
+  up_block<Raw>(p, load_w, [&](int i) { return wp[i]; }, rt, rt < p.I / 16, d->n_tok, d->tok_base, false, lds_g);
 }
 
 // Down of one block: row tile rt (output rows 16 rt ..) of w2 for the n
 // dispatch rows base .. base + n - 1 (shared: tokens 0 .. n - 1), K = I (Is).
-template <typename Raw, typename LoadW>
-__device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, int rt, int n, int base,
+template <typename Raw, typename LoadW, typename WPtr>
+__device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, WPtr wptr, int rt, int n, int base,
                                            bool shared, uint16_t* lds) {
   constexpr int G = batch_blocks<Raw>();
   const int lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -199,14 +219,24 @@ __device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, i
   for (int c0 = 0; c0 < n; c0 += kGNC) {
     const int cols = min(kGNC, n - c0);
     Raw a[G], b[G];
+    // FP4: the scales of a batch's 2 blocks (all lane groups) as one 8-byte
+    // window instead of one byte per lane and block; the byte is picked at use
+    u32x2 wa{}, wb{};
     // no condition on the loads (see load_raw_nc): blocks past the range
     // re-read its last block (not computed)
-    auto ld = [&](Raw (&r)[G], int kb) {
+    auto ld = [&](Raw (&r)[G], u32x2& w, int kb) {
+      if constexpr (std::is_same_v<Raw, RawFP4> && G == 2) {
+        const int kbc = min(kb, k1 - 2);   // the range has an even number of blocks
 #pragma unroll
-      for (int i = 0; i < G; ++i) load_w(r[i], row, min(kb + i, k1 - 1) * 128 + g4 * 32);
+        for (int i = 0; i < G; ++i) r[i].c = ldg16(static_cast<const uint8_t*>(wptr(0)) + row * static_cast<uint32_t>(K / 2) + (kbc + i) * 64 + g4 * 16);
+        w = ldg<u32x2>(static_cast<const uint8_t*>(wptr(1)) + row * static_cast<uint32_t>(K / 32) + kbc * 4);
+      } else {
+#pragma unroll
+        for (int i = 0; i < G; ++i) load_w(r[i], row, min(kb + i, k1 - 1) * 128 + g4 * 32);
+      }
     };
-    ld(a, k0);
-    ld(b, k0 + G);
+    ld(a, wa, k0);
+    ld(b, wb, k0 + G);
     stage_rows(thi, src_hi, K, K, cols, [&](int r) { return base + c0 + r; });
     stage_rows(tlo, src_lo, K, K, cols, [&](int r) { return base + c0 + r; });
     __syncthreads();
@@ -214,20 +244,21 @@ __device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, i
     const uint16_t* bh = thi + (tv ? r16 : 0) * hs;
     const uint16_t* bl = tlo + (tv ? r16 : 0) * hs;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    auto mm = [&](const Raw (&r)[G], int kb) {
+    auto mm = [&](Raw (&r)[G], const u32x2& w, int kb) {
 #pragma unroll
       for (int i = 0; i < G; ++i) {
         const int kc = (kb + i) * 128 + g4 * 32;
         const bool ok = tv && kb + i < k1;
+        if constexpr (std::is_same_v<Raw, RawFP4> && G == 2) r[i].s = ((i == 0 ? w.x : w.y) >> (8 * g4)) & 0xffu;
         mma_block(r[i], bh, kc, ok, acc);
         mma_block(r[i], bl, kc, ok, acc);
       }
     };
     for (int kb = k0; kb < k1; kb += 2 * G) {
-      mm(a, kb);
-      if (kb + 2 * G < k1) ld(a, kb + 2 * G);
-      if (kb + G < k1) mm(b, kb + G);
-      if (kb + 3 * G < k1) ld(b, kb + 3 * G);
+      mm(a, wa, kb);
+      if (kb + 2 * G < k1) ld(a, wa, kb + 2 * G);
+      if (kb + G < k1) mm(b, wb, kb + G);
+      if (kb + 3 * G < k1) ld(b, wb, kb + 3 * G);
     }
     if constexpr (kDKS > 1) {
       __syncthreads();   // every wave is done with the h tile
@@ -254,7 +285,7 @@ __global__ __launch_bounds__(kDW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   if (b < p.dn_shared) {
     const int rt = b * kDI + item;
     auto load_w = [&](RawBF16& r, uint32_t row, int kc) { load_raw_nc(r, p.ws2, row, p.Is, kc); };
-    down_block<RawBF16>(p, load_w, rt, p.T, 0, true, lds_g);
+    down_block<RawBF16>(p, load_w, [&](int) -> const void* { return p.ws2; }, rt, p.T, 0, true, lds_g);
     return;
   }
   const int rb = b - p.dn_shared;
@@ -263,7 +294,8 @@ __global__ __launch_bounds__(kDW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   const SlotDesc* d = p.desc + slot;
   const int rt = (rb % p.dn_groups) * kDI + item;
   auto load_w = [&](Raw& r, uint32_t row, int kc) { load_w2_nc(r, p.desc, slot, row, p.I, kc); };
-  down_block<Raw>(p, load_w, rt, d->n_tok, d->tok_base, false, lds_g);
+  auto wptr = [&](int i) { return desc_ptr(p.desc, slot, 6 + i); };   // 0: w2 codes, 1: w2 scales
+  down_block<Raw>(p, load_w, wptr, rt, d->n_tok, d->tok_base, false, lds_g);
 }
 
 size_t up_lds(const dsk_moe_desc& d) {
@@ -282,7 +314,10 @@ size_t down_lds(const dsk_moe_desc& d) {
 }  // namespace
 
 bool grouped_path(const dsk_moe_desc& d) {
+  // FP4 reads 2-block scale windows: an even number of K blocks in every
+  // wave's range (down: I % 256 == 0; gate/up, 4 ranges: H % 1024 == 0)
   return d.x_dtype == DSK_DTYPE_BF16 && d.hidden % (kGI * 16) == 0 && d.hidden % (kDI * 16) == 0 &&
+         (d.quant != DSK_QUANT_FP4 || (d.inter % 256 == 0 && d.hidden % (kGKS * 256) == 0)) &&
          d.hidden % 128 == 0 && d.inter % 128 == 0 && d.inter % (kGI * 16) == 0 &&
          d.inter_shared % 128 == 0 && d.inter_shared % (kGI * 16) == 0 &&
          up_lds(d) <= kMaxLds && down_lds(d) <= kMaxLds;
