@@ -53,11 +53,6 @@ struct DecodeArgs {
   int up_tiles;                        // I / 16
 };
 
-__device__ __forceinline__ u32x4 pack_bf16x8(const uint16_t* v) {
-  return u32x4{v[0] | (uint32_t(v[1]) << 16), v[2] | (uint32_t(v[3]) << 16),
-               v[4] | (uint32_t(v[5]) << 16), v[6] | (uint32_t(v[7]) << 16)};
-}
-
 // One x chunk (8 values at column `col` of token row t) into the LDS planes.
 __device__ __forceinline__ void put_x_chunk(uint16_t* xh, uint16_t* xl, int off, const u32x4& v0,
                                             const u32x4& v1, bool f32) {
@@ -450,89 +445,10 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
 }
 
 // ---------------------------------------------------------------- q3 gate/up, factored
-// Tokens of the factored q3 gate/up (A operand row 2t + h for t < 8).
-constexpr int kQ3fMaxTokens = 8;
+// ---------------------------------------------------------------- q3 gate/up, factored
 constexpr int kQ3fItems = 1;                      // row tiles of a block
 constexpr int kQ3fKS = 8;                         // K ranges of a row tile (one wave each)
 constexpr int kQ3fW = kQ3fItems * kQ3fKS;
-
-// One activation chunk (8 values of token t, chunk cc of its row) for the
-// factored q3 product: the values at 8q code positions divided by 8 (exact),
-// as bf16 plane(s); the chunk's sum(x) and sum(x / m) are reduced over the 8
-// lanes of its 64-group (fixed order) and written to xsum[kb][t][h] =
-// {sum x, sum x / m}.  All lanes of an aligned 8-lane group call it together.
-template <bool kF32>
-__device__ __forceinline__ void stage_chunk_q3(uint16_t* xh, uint16_t* xl, float* xsum, int xs, int cpr, int c,
-                                               const u32x4& v0, const u32x4& v1) {
-  const int t = c / cpr, cc = c % cpr;
-  const uint32_t div8 = q3m_div8_pairs(cc & 3);
-  float f[8];
-  if constexpr (!kF32) {
-    const uint32_t w[4] = {v0.x, v0.y, v0.z, v0.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[2 * i] = __uint_as_float(w[i] << 16);
-      f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-    }
-  } else {
-    const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = __uint_as_float(w[i]);
-  }
-  uint16_t h[8], l[8];
-  float sx = 0.0f, sxm = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const bool d8 = (div8 >> (e >> 1)) & 1u;
-    const float sc = d8 ? 0.125f : 1.0f, m = d8 ? 8.0f : 1.0f;
-    if constexpr (!kF32) {
-      h[e] = f32_to_bf16_bits(f[e] * sc);
-      sx += f[e];
-      sxm += f[e] * sc;
-    } else {
-      split_bf16(f[e] * sc, h[e], l[e]);
-      const float v = bf16_bits_to_f32(h[e]) + bf16_bits_to_f32(l[e]);   // what the MFMA sees
-      sx += v * m;
-      sxm += v;
-    }
-  }
-  const int off = t * xs + cc * 8;
-  *reinterpret_cast<u32x4*>(xh + off) = pack_bf16x8(h);
-  if constexpr (kF32) *reinterpret_cast<u32x4*>(xl + off) = pack_bf16x8(l);
-#pragma unroll
-  for (int o = 1; o < 8; o <<= 1) {
-    sx += __shfl_xor(sx, o, 8);
-    sxm += __shfl_xor(sxm, o, 8);
-  }
-  if ((cc & 7) == 0) {
-    const int gi = cc >> 3;
-    *reinterpret_cast<float2*>(xsum + (((gi >> 1) * kQ3fMaxTokens + t) * 2 + (gi & 1)) * 2) = float2{sx, sxm};
-  }
-}
-
-// One batch of G K blocks of a wave's q3 gate and up rows: three code words
-// per lane, block and role, and the (scale, bias) pairs of the block's two
-// 64-groups per role (sb: S1, B1, S3, B3; low half = first group).
-template <int G>
-struct Q3Batch {
-  uint32_t c1[G][3], c3[G][3];
-  uint32_t sb[4][G];
-};
-
-// acc[t] += s * (d - 128 * sum(x / m)) + b * sum(x) over the block's two
-// groups h = 0, 1: d[2t' + h] is the MFMA output of token row 2t' + h of this
-// lane, xa / xb = xsum of its two tokens {sum x, sum x / m} x {h = 0, 1}.
-__device__ __forceinline__ void q3_factor(const f32x4& d, uint32_t s, uint32_t b, const f32x4& xa,
-                                          const f32x4& xb, float (&acc)[2]) {
-  acc[0] = fmaf(f16_half<0>(s), fmaf(-128.0f, xa.y, d[0]), acc[0]);
-  acc[0] = fmaf(f16_half<0>(b), xa.x, acc[0]);
-  acc[0] = fmaf(f16_half<1>(s), fmaf(-128.0f, xa.w, d[1]), acc[0]);
-  acc[0] = fmaf(f16_half<1>(b), xa.z, acc[0]);
-  acc[1] = fmaf(f16_half<0>(s), fmaf(-128.0f, xb.y, d[2]), acc[1]);
-  acc[1] = fmaf(f16_half<0>(b), xb.x, acc[1]);
-  acc[1] = fmaf(f16_half<1>(s), fmaf(-128.0f, xb.w, d[3]), acc[1]);
-  acc[1] = fmaf(f16_half<1>(b), xb.z, acc[1]);
-}
 
 // Routed gate/up of the decode pipeline for q3 experts (T <= 8), factored
 // (see q3m_pair): the codes go into the MFMA as exact bf16 integers and each

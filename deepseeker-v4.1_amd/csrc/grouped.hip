@@ -45,6 +45,7 @@ struct GroupedArgs {
   float* ys;                                     // [T][H]
   int up_groups, up_shared;                      // gate/up: row-tile groups per slot, shared blocks
   int dn_groups, dn_shared;                      // down: the same
+  int q3f;                                       // q3 gate/up in the factored form (up_block_q3f)
 };
 
 // K blocks per weight batch, two batches in flight per wave, within the
@@ -173,6 +174,145 @@ __device__ __forceinline__ void up_block(const GroupedArgs& p, LoadW load_w, WPt
   }
 }
 
+// Gate/up of one q3 block in the factored form (x . W = s * sum(q x) + b *
+// sum(x) per 64-group, see q3m_pair): row tile rt of w1 / w3 for the n
+// dispatch rows base .. in column tiles of kGNC; the A operand is the
+// activations (row 2t + h: dispatch row c0 + t of the tile on the K block's
+// h-th 64-group), the B operand the raw codes.  Block = one row tile x kQ3gKS
+// K ranges (one wave each); every wave's range is whole 512-code superblocks
+// (hidden % (kQ3gKS * 512) == 0), one batch (superblock) in flight.  The
+// tile's x rows are staged first, divided by 8 at the 8q positions and with
+// their group sums; then the weights are issued.
+constexpr int kQ3gKS = kGW;
+__device__ __forceinline__ void up_block_q3f(const GroupedArgs& p, const void* const* wp, int rt, bool rok, int n,
+                                             int base, uint16_t* lds) {
+  constexpr int G = 4;                       // K blocks per batch: one superblock
+  constexpr int kStg = 4;                    // x chunks per thread in flight while staging
+  constexpr int NT = kGW * 64;
+  const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int ks = wave;
+  const int K = p.H, nblk = K / 128, cpr = K / 8;
+  const int per = nblk / kQ3gKS;
+  const int k0 = ks * per, k1 = k0 + per;
+  const int xs = K + 8;
+  uint16_t* xh = lds;                                                        // [kGNC][K + 8]
+  float* xsum = reinterpret_cast<float*>(lds + kGNC * xs);                   // [nblk][8][2][2]
+  u32x4* zero4 = reinterpret_cast<u32x4*>(xsum + nblk * kQ3fMaxTokens * 4);  // 64 zero bytes
+  const uint16_t* zero = reinterpret_cast<const uint16_t*>(zero4);
+  float (*red)[2][64][2] = reinterpret_cast<float (*)[2][64][2]>(lds);       // [wave][role], over the x tile
+  if (tid < 4) zero4[tid] = u32x4{0u, 0u, 0u, 0u};
+  const uint32_t rowc = rok ? static_cast<uint32_t>(rt * 16 + r16) : 0u;   // rows past the tile: row 0, not stored
+  const uint32_t code_row = rowc * static_cast<uint32_t>(K / 8 * 3);
+  const uint32_t sb_row = rowc * static_cast<uint32_t>(K / 64) * 2;        // bytes
+  const uint8_t* W1 = static_cast<const uint8_t*>(wp[0]);
+  const uint8_t* W3 = static_cast<const uint8_t*>(wp[3]);
+  const uint8_t* SB[4] = {static_cast<const uint8_t*>(wp[1]), static_cast<const uint8_t*>(wp[2]),
+                          static_cast<const uint8_t*>(wp[4]), static_cast<const uint8_t*>(wp[5])};
+  // loads without conditions (see load_raw_nc): a batch past the range re-reads its last superblock
+  auto ld = [&](Q3Batch<G>& b, int kb0) {
+    const int kbc = min(kb0, k1 - G);
+    const uint32_t off = code_row + (kbc >> 2) * 192 + 48 * g4;
+    const auto c1 = gptr<u32x4>(W1 + off);
+    const auto c3 = gptr<u32x4>(W3 + off);
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+      const u32x4 a = c1[v];
+      const u32x4 e = c3[v];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        b.c1[(4 * v + j) / 3][(4 * v + j) % 3] = a[j];
+        b.c3[(4 * v + j) / 3][(4 * v + j) % 3] = e[j];
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const u32x4 w = ldg16(SB[a] + sb_row + kbc * 4);
+#pragma unroll
+      for (int i = 0; i < G; ++i) b.sb[a][i] = w[i];
+    }
+  };
+  const int ta = r16 >> 1;
+  const Q3Masks km = q3_masks();
+  for (int c0 = 0; c0 < n; c0 += kGNC) {
+    const int cols = min(kGNC, n - c0);
+    // the tile's x rows first (their registers are free again before the
+    // weights land), kStg chunks per thread in flight (cols * cpr is a
+    // multiple of 8: whole lane groups)
+    const int xch = cols * cpr;
+    for (int cb = 0; cb < xch; cb += kStg * NT) {
+      u32x4 v[kStg];
+#pragma unroll
+      for (int j = 0; j < kStg; ++j) {
+        const int c = min(cb + j * NT + tid, xch - 1);
+        v[j] = ldg16(p.x + static_cast<int64_t>(p.xrow[base + c0 + c / cpr]) * K + (c % cpr) * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < kStg; ++j) {
+        const int c = cb + j * NT + tid;
+        if (c < xch) stage_chunk_q3<false>(xh, nullptr, xsum, xs, cpr, c, v[j], u32x4{});
+      }
+    }
+    Q3Batch<G> A;
+    ld(A, k0);
+    __syncthreads();
+    const bool av = ta < cols && (r16 & 1) == (g4 >> 1);
+    const int t0 = 2 * g4;
+    float acc1[2] = {0.0f, 0.0f}, acc3[2] = {0.0f, 0.0f};
+    auto mm = [&](const Q3Batch<G>& b, int kb0) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const int kb = kb0 + i;
+        const uint16_t* ah = av ? xh + ta * xs + kb * 128 + 32 * g4 : zero;
+        f32x4 d1 = {0.0f, 0.0f, 0.0f, 0.0f}, d3 = d1;
+#define DSK_Q3G_STEP(M)                                                              \
+        {                                                                            \
+          const bf16x8 xa = as_bf16x8(*reinterpret_cast<const u32x4*>(ah + 8 * M)); \
+          d1 = mfma16(xa, q3m_operand<M>(b.c1[i], km), d1);                          \
+          d3 = mfma16(xa, q3m_operand<M>(b.c3[i], km), d3);                          \
+        }
+        DSK_Q3G_STEP(0) DSK_Q3G_STEP(1) DSK_Q3G_STEP(2) DSK_Q3G_STEP(3)
+#undef DSK_Q3G_STEP
+        const float* xg = xsum + (kb * kQ3fMaxTokens + t0) * 4;
+        const f32x4 xa = *reinterpret_cast<const f32x4*>(xg);
+        const f32x4 xb = *reinterpret_cast<const f32x4*>(xg + 4);
+        q3_factor(d1, b.sb[0][i], b.sb[1][i], xa, xb, acc1);
+        q3_factor(d3, b.sb[2][i], b.sb[3][i], xa, xb, acc3);
+      }
+    };
+    for (int kb = k0; kb < k1; kb += G) {   // one batch at hidden 4096
+      if (kb > k0) ld(A, kb);
+      mm(A, kb);
+    }
+    // K ranges added in order, through LDS over the x tile
+    __syncthreads();
+    *reinterpret_cast<float2*>(&red[ks][0][lane][0]) = float2{acc1[0], acc1[1]};
+    *reinterpret_cast<float2*>(&red[ks][1][lane][0]) = float2{acc3[0], acc3[1]};
+    __syncthreads();
+    if (ks == 0 && rok && t0 < cols) {
+#pragma unroll
+      for (int w = 1; w < kQ3gKS; ++w) {
+        const float2 g = *reinterpret_cast<const float2*>(&red[w][0][lane][0]);
+        const float2 u = *reinterpret_cast<const float2*>(&red[w][1][lane][0]);
+        acc1[0] += g.x; acc1[1] += g.y;
+        acc3[0] += u.x; acc3[1] += u.y;
+      }
+      const int n16 = rt * 16 + r16;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        if (t0 + q < cols) {
+          const int r = base + c0 + t0 + q;   // dispatch row
+          uint16_t hh, hl;
+          split_bf16(silu_clamped(acc1[q], acc3[q], p.limit) * p.wrow[r], hh, hl);
+          p.h_hi[static_cast<int64_t>(r) * p.I + n16] = hh;
+          p.h_lo[static_cast<int64_t>(r) * p.I + n16] = hl;
+        }
+      }
+    }
+    __syncthreads();   // the next column tile reuses the LDS
+  }
+}
+
 // Blocks [0, up_shared): the shared expert (bf16 w1/w3, all T tokens); the
 // others: up_groups blocks per slot.
 template <typename Raw>
@@ -193,6 +333,13 @@ __global__ __launch_bounds__(kGW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   const int rt = (rb % p.up_groups) * kGI + item;
   const void* const wp[6] = {desc_ptr(p.desc, slot, 0), desc_ptr(p.desc, slot, 1), desc_ptr(p.desc, slot, 2),
                              desc_ptr(p.desc, slot, 3), desc_ptr(p.desc, slot, 4), desc_ptr(p.desc, slot, 5)};
+  if constexpr (std::is_same_v<Raw, RawQ3>) {
+    if (p.q3f) {   // one row tile per block (up_groups = I / 16)
+      const int rt1 = rb % p.up_groups;
+      up_block_q3f(p, wp, rt1, rt1 < p.I / 16, d->n_tok, d->tok_base, lds_g);
+      return;
+    }
+  }
   auto load_w = [&](Raw& r, int role, uint32_t row, int kc) { load_role_nc(r, wp, role, row, p.H, kc); };
   up_block<Raw>(p, load_w, [&](int i) { return wp[i]; }, rt, rt < p.I / 16, d->n_tok, d->tok_base, false, lds_g);
 }
@@ -298,10 +445,16 @@ __global__ __launch_bounds__(kDW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   down_block<Raw>(p, load_w, wptr, rt, d->n_tok, d->tok_base, false, lds_g);
 }
 
+// The factored q3 gate/up: every wave's K range whole superblocks.
+bool up_q3f(const dsk_moe_desc& d) { return d.quant == DSK_QUANT_Q3 && d.hidden % (kQ3gKS * 512) == 0; }
+
 size_t up_lds(const dsk_moe_desc& d) {
   const size_t x_tile = static_cast<size_t>(kGNC) * (d.hidden + 8) * 2;
   const size_t red = static_cast<size_t>(kGI) * kGKS * 2 * 64 * 4 * sizeof(float);
-  return x_tile > red ? x_tile : red;
+  // factored q3: the x tile, its group sums [H/128][8][2][2] f32, 64 zero bytes
+  const size_t q3f = x_tile + static_cast<size_t>(d.hidden / 128) * kQ3fMaxTokens * 16 + 64;
+  const size_t base = x_tile > red ? x_tile : red;
+  return up_q3f(d) && q3f > base ? q3f : base;
 }
 
 size_t down_lds(const dsk_moe_desc& d) {
@@ -340,7 +493,8 @@ GroupedArgs grouped_args(const dsk_moe_desc& d, const Workspace& L, const Expert
   p.hs_lo = reinterpret_cast<uint16_t*>(a.ws + L.hs_lo);
   p.y = reinterpret_cast<float*>(a.ws + L.y);
   p.ys = reinterpret_cast<float*>(a.ws + L.ys);
-  p.up_groups = d.inter / 16 / kGI;
+  p.q3f = up_q3f(d) ? 1 : 0;
+  p.up_groups = p.q3f ? d.inter / 16 : d.inter / 16 / kGI;   // factored q3: one row tile per block
   p.up_shared = d.inter_shared / 16 / kGI;
   p.dn_groups = d.hidden / 16 / kDI;
   p.dn_shared = d.inter_shared > 0 ? p.dn_groups : 0;

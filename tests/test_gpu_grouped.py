@@ -4,9 +4,9 @@ and the prefill GEMM, bf16 activations) against the oracle.
 Routing indices bit-exact; outputs within the layer tolerance.  Cases: the
 full-size FP4 layer at T=20; mid-size layers with skewed routing (every
 token to the same few experts, so each slot spans several column tiles of
-dispatch rows), q3 experts, no shared expert, a callable shared expert, and
-the host-dispatch entry point (dsk_experts) reached through a callable
-expert_fn.
+dispatch rows), q3 experts, no shared expert, a callable shared expert, the
+host-dispatch entry point (dsk_experts) reached through a callable
+expert_fn, and the factored q3 gate/up at hidden 4096.
 """
 
 from __future__ import annotations
@@ -46,6 +46,26 @@ def test_grouped_mid(quant, T, hot):
     r = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], d["shared"], spec)
     if hot:
         assert (r["idx"] < hot).all()          # each hot expert holds every token: T rows, several tiles
+    idx = torch.empty((T, spec.k), dtype=torch.int32, device=DEV)
+    layer = dsk_moe.MoELayer(d["gate_w"].to(DEV), d["gate_b"].to(DEV), to_bank(d["bank"]),
+                             to_shared(d["shared"]), spec.k)
+    out = layer(d["x"].to(DEV), idx=idx).cpu()
+    np.testing.assert_array_equal(idx.cpu().numpy(), r["idx"])
+    c, rel = assert_layer_close(out.float(), r["y_ref"])
+    print(f"cos={c:.9f} rel={rel:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("T,hot", [(12, 0), (30, 4), (40, 0)])
+def test_grouped_q3_factored(T, hot):
+    """Hidden 4096: the factored q3 gate/up (one row tile x 8 K ranges per block,
+    one 512-code superblock per wave); hot = 4 sends every token to experts
+    0..3, so each of their slots spans several column tiles."""
+    spec = L.LayerSpec(H=4096, E=16, k=4, I=256, I_shared=256, quant=L.QUANT_Q3)
+    print(f"grouped q3 factored H=4096 T={T} hot={hot}", flush=True)
+    d = synth.make_layer(spec, 70 + T, T)
+    if hot:
+        d["gate_b"] = _skewed(d, hot)
+    r = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], d["shared"], spec)
     idx = torch.empty((T, spec.k), dtype=torch.int32, device=DEV)
     layer = dsk_moe.MoELayer(d["gate_w"].to(DEV), d["gate_b"].to(DEV), to_bank(d["bank"]),
                              to_shared(d["shared"]), spec.k)
