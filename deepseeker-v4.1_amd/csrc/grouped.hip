@@ -46,6 +46,7 @@ struct GroupedArgs {
   int up_groups, up_shared;                      // gate/up: row-tile groups per slot, shared blocks
   int dn_groups, dn_shared;                      // down: the same
   int q3f;                                       // q3 gate/up in the factored form (up_block_q3f)
+  int q3fd;                                      // q3 down in the factored form (down_block_q3f)
 };
 
 // K blocks per weight batch, two batches in flight per wave, within the
@@ -422,10 +423,126 @@ __device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, W
   }
 }
 
+// Down of one q3 block in the factored form (as up_block_q3f): output row
+// tile rt (one wave) over all of K = I in 512-code superblocks (I % 512 ==
+// 0), two in flight; A operand row 2t + h on the hi plane and then the lo
+// plane of dispatch row c0 + t's h (both into one accumulator), B operand the
+// raw w2 codes; the tile's h rows are staged divided by 8 at the 8q positions
+// with the group sums of hi + lo.  Writes one float32 row per dispatch row.
+struct Q3Sb { uint32_t c[4][3]; u32x4 s, b; };   // one superblock of a lane's w2 row: codes, windows
+
+__device__ __forceinline__ void down_block_q3f(const GroupedArgs& p, int slot, int rt, int n, int base,
+                                               uint16_t* lds) {
+  constexpr int kStg = 2;                    // h chunks per thread in flight while staging
+  constexpr int NT = kDW * 64;
+  const int tid = threadIdx.x, lane = __lane_id();
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int K = p.I, nblk = K / 128, nsb = K / 512, cpr = K / 8;
+  const int hs = K + 8;
+  uint16_t* thi = lds;                                                       // [kGNC][K + 8]
+  uint16_t* tlo = lds + kGNC * hs;                                           // [kGNC][K + 8]
+  float* hsum = reinterpret_cast<float*>(lds + 2 * kGNC * hs);               // [nblk][8][2][2]
+  u32x4* zero4 = reinterpret_cast<u32x4*>(hsum + nblk * kQ3fMaxTokens * 4);  // 64 zero bytes
+  const uint16_t* zero = reinterpret_cast<const uint16_t*>(zero4);
+  if (tid < 4) zero4[tid] = u32x4{0u, 0u, 0u, 0u};
+  const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
+  const uint8_t* W = static_cast<const uint8_t*>(desc_ptr(p.desc, slot, 6));
+  const uint8_t* S = static_cast<const uint8_t*>(desc_ptr(p.desc, slot, 7));
+  const uint8_t* B = static_cast<const uint8_t*>(desc_ptr(p.desc, slot, 8));
+  const uint32_t code_row = row * static_cast<uint32_t>(K / 8 * 3), sb_row = row * static_cast<uint32_t>(K / 64) * 2;
+  // no condition on the loads (see load_raw_nc): past the last superblock, the last again (not computed)
+  auto ld = [&](Q3Sb& r, int sb) {
+    const int sbc = min(sb, nsb - 1);
+    const auto c = gptr<u32x4>(W + code_row + sbc * 192 + 48 * g4);
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+      const u32x4 a = c[v];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r.c[(4 * v + j) / 3][(4 * v + j) % 3] = a[j];
+    }
+    r.s = ldg16(S + sb_row + sbc * 16);
+    r.b = ldg16(B + sb_row + sbc * 16);
+  };
+  const int ta = r16 >> 1;
+  const Q3Masks km = q3_masks();
+  for (int c0 = 0; c0 < n; c0 += kGNC) {
+    const int cols = min(kGNC, n - c0);
+    // the tile's h rows (hi + lo), kStg chunks per thread in flight (whole lane groups)
+    const int xch = cols * cpr;
+    for (int cb = 0; cb < xch; cb += kStg * NT) {
+      u32x4 vh[kStg], vl[kStg];
+#pragma unroll
+      for (int j = 0; j < kStg; ++j) {
+        const int c = min(cb + j * NT + tid, xch - 1);
+        const int64_t e = static_cast<int64_t>(base + c0 + c / cpr) * K + (c % cpr) * 8;
+        vh[j] = ldg16(p.h_hi + e);
+        vl[j] = ldg16(p.h_lo + e);
+      }
+#pragma unroll
+      for (int j = 0; j < kStg; ++j) {
+        const int c = cb + j * NT + tid;
+        if (c < xch) {
+          // hi + lo is exact in float32; staged again as a (hi, lo) pair of the scaled value
+          const uint32_t wh[4] = {vh[j].x, vh[j].y, vh[j].z, vh[j].w}, wl[4] = {vl[j].x, vl[j].y, vl[j].z, vl[j].w};
+          uint32_t f[8];
+#pragma unroll
+          for (int e2 = 0; e2 < 8; ++e2) {
+            const uint32_t sh = (e2 & 1) ? 0u : 16u;
+            const float v = __uint_as_float(((wh[e2 >> 1] << sh) & 0xffff0000u)) +
+                            __uint_as_float(((wl[e2 >> 1] << sh) & 0xffff0000u));
+            f[e2] = __float_as_uint(v);
+          }
+          stage_chunk_q3<true>(thi, tlo, hsum, hs, cpr, c, u32x4{f[0], f[1], f[2], f[3]}, u32x4{f[4], f[5], f[6], f[7]});
+        }
+      }
+    }
+    // keep the weight loads below the staging (their registers would overlap)
+    __builtin_amdgcn_sched_barrier(0);
+    Q3Sb ra, rb;
+    ld(ra, 0);
+    ld(rb, 1);
+    __syncthreads();
+    const bool av = ta < cols && (r16 & 1) == (g4 >> 1);
+    const int t0 = 2 * g4;
+    float acc[2] = {0.0f, 0.0f};
+    auto mm = [&](const Q3Sb& r, int sb) {
+      const uint32_t sw[4] = {r.s.x, r.s.y, r.s.z, r.s.w}, bw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kb = 4 * sb + i;
+        const int ao = ta * hs + kb * 128 + 32 * g4;
+        const uint16_t* ah = av ? thi + ao : zero;
+        const uint16_t* al = av ? tlo + ao : zero;
+        f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#define DSK_Q3D_STEP(M)                                                                                \
+        d = mfma16(as_bf16x8(*reinterpret_cast<const u32x4*>(ah + 8 * M)), q3m_operand<M>(r.c[i], km), d); \
+        d = mfma16(as_bf16x8(*reinterpret_cast<const u32x4*>(al + 8 * M)), q3m_operand<M>(r.c[i], km), d);
+        DSK_Q3D_STEP(0) DSK_Q3D_STEP(1) DSK_Q3D_STEP(2) DSK_Q3D_STEP(3)
+#undef DSK_Q3D_STEP
+        const float* xg = hsum + (kb * kQ3fMaxTokens + t0) * 4;
+        q3_factor(d, sw[i], bw[i], *reinterpret_cast<const f32x4*>(xg), *reinterpret_cast<const f32x4*>(xg + 4), acc);
+      }
+    };
+    for (int sb = 0; sb < nsb; sb += 2) {
+      mm(ra, sb);
+      if (sb + 2 < nsb) ld(ra, sb + 2);
+      if (sb + 1 < nsb) mm(rb, sb + 1);
+      if (sb + 3 < nsb) ld(rb, sb + 3);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      if (t0 + q < cols) p.y[static_cast<int64_t>(base + c0 + t0 + q) * p.H + rt * 16 + r16] = acc[q];
+    __syncthreads();   // the next column tile reuses the LDS
+  }
+}
+
 // Blocks [0, dn_shared): the shared expert's w2 (bf16, all T tokens); the
 // others: dn_groups blocks per slot.
+// q3: three waves per SIMD (the factored product keeps two superblocks of w2
+// in flight per wave)
 template <typename Raw>
-__global__ __launch_bounds__(kDW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_down_grouped(GroupedArgs p) {
+__global__ __launch_bounds__(kDW * 64) __attribute__((amdgpu_waves_per_eu(std::is_same_v<Raw, RawQ3> ? 3 : 4))) void
+k_down_grouped(GroupedArgs p) {
   extern __shared__ __align__(16) uint16_t lds_g[];
   const int b = static_cast<int>(blockIdx.x);
   const int item = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / kDKS;
@@ -440,6 +557,12 @@ __global__ __launch_bounds__(kDW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   if (slot >= p.active[0]) return;
   const SlotDesc* d = p.desc + slot;
   const int rt = (rb % p.dn_groups) * kDI + item;
+  if constexpr (std::is_same_v<Raw, RawQ3>) {
+    if (p.q3fd) {
+      down_block_q3f(p, slot, rt, d->n_tok, d->tok_base, lds_g);
+      return;
+    }
+  }
   auto load_w = [&](Raw& r, uint32_t row, int kc) { load_w2_nc(r, p.desc, slot, row, p.I, kc); };
   auto wptr = [&](int i) { return desc_ptr(p.desc, slot, 6 + i); };   // 0: w2 codes, 1: w2 scales
   down_block<Raw>(p, load_w, wptr, rt, d->n_tok, d->tok_base, false, lds_g);
@@ -457,11 +580,18 @@ size_t up_lds(const dsk_moe_desc& d) {
   return up_q3f(d) && q3f > base ? q3f : base;
 }
 
+// The factored q3 down: K = I whole superblocks.
+bool down_q3f(const dsk_moe_desc& d) { return d.quant == DSK_QUANT_Q3 && d.inter % 512 == 0; }
+
 size_t down_lds(const dsk_moe_desc& d) {
   const int K = d.inter > d.inter_shared ? d.inter : d.inter_shared;
   const size_t h_tile = 2 * static_cast<size_t>(kGNC) * (K + 8) * 2;
   const size_t red = static_cast<size_t>(kDI) * kDKS * 64 * 4 * sizeof(float);
-  return h_tile > red ? h_tile : red;
+  const size_t base = h_tile > red ? h_tile : red;
+  // factored q3: the h tile of I, its group sums [I/128][8][2][2] f32, 64 zero bytes
+  const size_t q3f = 2 * static_cast<size_t>(kGNC) * (d.inter + 8) * 2 +
+                     static_cast<size_t>(d.inter / 128) * kQ3fMaxTokens * 16 + 64;
+  return down_q3f(d) && q3f > base ? q3f : base;
 }
 
 }  // namespace
@@ -494,6 +624,7 @@ GroupedArgs grouped_args(const dsk_moe_desc& d, const Workspace& L, const Expert
   p.y = reinterpret_cast<float*>(a.ws + L.y);
   p.ys = reinterpret_cast<float*>(a.ws + L.ys);
   p.q3f = up_q3f(d) ? 1 : 0;
+  p.q3fd = down_q3f(d) ? 1 : 0;
   p.up_groups = p.q3f ? d.inter / 16 : d.inter / 16 / kGI;   // factored q3: one row tile per block
   p.up_shared = d.inter_shared / 16 / kGI;
   p.dn_groups = d.hidden / 16 / kDI;
