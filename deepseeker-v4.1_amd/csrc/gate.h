@@ -110,30 +110,36 @@ __device__ __forceinline__ void gate_tile(const void* x, const void* gw, int T, 
   const int steps = (H + 255) / 256;
   const int seg = (steps + kSegments - 1) / kSegments;
   const int m0 = wave * seg, m1 = active ? min(m0 + seg, steps) : m0;
-#pragma unroll 4
-  for (int m = m0; m < m1; ++m) {
-    const int c = 256 * m + 4 * lane;
-    const bool ok = c < H;
-    f32x4 xv[TW], wv[EW];
+  // The loads of kC steps are issued together and without conditions (a load
+  // under a per-lane condition compiles to a branch whose merge waits for
+  // it): out-of-range elements are read from an in-range place and zeroed
+  // before the product, and steps past the segment add +0, which leaves a
+  // partial that starts at +0 unchanged -- the sums are those of the plain
+  // loop, in the same order.
+  constexpr int kC = TW * EW == 1 ? 4 : 1;
+  for (int mb = m0; mb < m1; mb += kC) {
+    f32x4 xv[kC][TW], wv[kC][EW];
 #pragma unroll
-    for (int i = 0; i < TW; ++i) {
-      const int t = min(t0 + i, T - 1);
-      xv[i] = ok ? load4<kXBF16>(x, static_cast<int64_t>(t) * H + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < kC; ++q) {
+      const int c = min(256 * min(mb + q, m1 - 1) + 4 * lane, H - 4);
+#pragma unroll
+      for (int i = 0; i < TW; ++i) xv[q][i] = load4<kXBF16>(x, static_cast<int64_t>(min(t0 + i, T - 1)) * H + c);
+#pragma unroll
+      for (int j = 0; j < EW; ++j) wv[q][j] = load4<kWBF16>(gw, static_cast<int64_t>(min(e0 + j, E - 1)) * H + c);
     }
 #pragma unroll
-    for (int j = 0; j < EW; ++j) {
-      const int e = min(e0 + j, E - 1);
-      wv[j] = ok ? load4<kWBF16>(gw, static_cast<int64_t>(e) * H + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < kC; ++q) {
+      const bool ok = mb + q < m1 && 256 * (mb + q) + 4 * lane < H;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int i = 0; i < TW; ++i)
+#pragma unroll
+          for (int j = 0; j < EW; ++j) {
+            const float prod = (ok ? xv[q][i][v] : 0.0f) * (ok ? wv[q][j][v] : 0.0f);
+            p[i][j] = p[i][j] + prod;
+          }
     }
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-#pragma unroll
-      for (int i = 0; i < TW; ++i)
-#pragma unroll
-        for (int j = 0; j < EW; ++j) {
-          const float prod = xv[i][v] * wv[j][v];
-          p[i][j] = p[i][j] + prod;
-        }
   }
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1)
