@@ -190,12 +190,15 @@ __device__ __forceinline__ void put_staged_x(const DecodeArgs& p, uint16_t* xh, 
 }
 
 // Shared-expert gate/up tile rt (block = NW waves, ROWS (8 or 16) rows of w1
-// and w3, all K; wave w takes the w-th K range, two K blocks in flight).  With
-// 8 rows the MFMA's rows 8..15 repeat rows 0..7 (the same addresses, so no
-// extra traffic) and are not stored: twice the tiles, so the shared stream is
-// spread over twice the CUs.  Called after the block's x chunks have been
-// loaded into registers; writes them to LDS once its own weight loads are in
-// flight.
+// and w3, all K; wave w takes the w-th K range).  16 rows: two K blocks in
+// flight.  8 rows (T <= 8): the MFMA's A rows 8..15 hold the same 8 weight
+// rows at the next K block and its B columns 8..15 the tokens' activations
+// there, so one MFMA covers a pair of K blocks (D rows 0..7 x columns 0..7
+// and rows 8..15 x columns 8..15 are added once at the end); the wave's four
+// K blocks are then all in flight in the registers of two, and twice the
+// tiles spread the shared stream over twice the CUs.  Called after the
+// block's x chunks have been loaded into registers; writes them to LDS once
+// its own weight loads are in flight.
 template <bool kF32, int NW, int ROWS>
 __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint16_t* xh, uint16_t* xl, int xs,
                                                bool xreg, const u32x4 (&xv)[kUpXRegChunks][2], uint16_t* lds,
@@ -205,32 +208,46 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint
   const int nblk = (K + 127) / 128;
   const int per = (nblk + NW - 1) / NW;
   const int k0 = min(wave * per, nblk), k1 = min(k0 + per, nblk);
-  const bool tv = r16 < T;
+  // 8 rows: this lane's half of a K-block pair (A row r16 and B column r16 agree)
+  constexpr int kStep = ROWS == 8 ? 2 : 1;            // K blocks per MFMA group
+  const int half = ROWS == 8 ? (r16 >> 3) : 0;
+  const int tok = ROWS == 8 ? (r16 & 7) : r16;        // this lane's B column token
+  const bool tv = tok < T;
   RawBF16 a1, a3, b1, b3;
   auto ld = [&](RawBF16& r1, RawBF16& r3, int kb) {
     // no condition (see load_raw_nc): past the range, the last block again
-    const int kc = min(min(kb, k1 - 1) * 128 + g4 * 32, K - 32);
+    const int kc = min(min(kb + half, k1 - 1) * 128 + g4 * 32, K - 32);
     load_raw_nc(r1, p.ws1, row, K, kc);
     load_raw_nc(r3, p.ws3, row, K, kc);
   };
   ld(a1, a3, k0);
-  ld(b1, b3, k0 + 1);
+  ld(b1, b3, k0 + kStep);
   if (xreg) put_staged_x<kF32, NW * 64>(p, xh, xl, xs, tid, xv);
   __syncthreads();
-  const uint16_t* bh = xh + (tv ? r16 : 0) * xs;
-  const uint16_t* bl = xl + (tv ? r16 : 0) * xs;
+  const uint16_t* bh = xh + (tv ? tok : 0) * xs;
+  const uint16_t* bl = xl + (tv ? tok : 0) * xs;
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
   auto mm = [&](const RawBF16& r1, const RawBF16& r3, int kb) {
-    const int kc = kb * 128 + g4 * 32;
-    const bool ok = tv && kb < k1 && kc < K;
+    const int kbl = kb + half;
+    const int kc = kbl * 128 + g4 * 32;
+    const bool ok = tv && kbl < k1 && kc < K;
     mma_block2(r1, r3, bh, kc, ok, ag, au);
     if (kF32) mma_block2(r1, r3, bl, kc, ok, ag, au);
   };
-  for (int kb = k0; kb < k1; kb += 2) {
+  for (int kb = k0; kb < k1; kb += 2 * kStep) {
     mm(a1, a3, kb);
-    if (kb + 2 < k1) ld(a1, a3, kb + 2);
-    if (kb + 1 < k1) mm(b1, b3, kb + 1);
-    if (kb + 3 < k1) ld(b1, b3, kb + 3);
+    if (kb + 2 * kStep < k1) ld(a1, a3, kb + 2 * kStep);
+    if (kb + kStep < k1) mm(b1, b3, kb + kStep);
+    if (kb + 3 * kStep < k1) ld(b1, b3, kb + 3 * kStep);
+  }
+  if constexpr (ROWS == 8) {
+    // D[r][t] (K blocks of the first halves) + D[8 + r][8 + t] (second halves):
+    // lane l (rows 4 g4 .., column r16) and lane l + 40
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ag[q] += __shfl_down(ag[q], 40, 64);
+      au[q] += __shfl_down(au[q], 40, 64);
+    }
   }
   // K ranges added in wave order; the partial sums reuse the activation area
   // once every wave is done with it
@@ -239,7 +256,7 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint
   *reinterpret_cast<f32x4*>(&red[wave][0][lane][0]) = ag;
   *reinterpret_cast<f32x4*>(&red[wave][1][lane][0]) = au;
   __syncthreads();
-  if (wave == 0 && tv && g4 < ROWS / 4) {
+  if (wave == 0 && tv && g4 < ROWS / 4 && (ROWS == 16 || r16 < 8)) {
 #pragma unroll
     for (int w = 1; w < NW; ++w) {
       ag += *reinterpret_cast<const f32x4*>(&red[w][0][lane][0]);
@@ -248,7 +265,7 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint
     uint16_t hh[4], hl[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) split_bf16(silu_clamped(ag[q], au[q], p.limit), hh[q], hl[q]);
-    const int64_t off = static_cast<int64_t>(r16) * p.Is + rt * ROWS + 4 * g4;
+    const int64_t off = static_cast<int64_t>(tok) * p.Is + rt * ROWS + 4 * g4;
     *reinterpret_cast<uint2*>(p.hs_hi + off) = uint2{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16)};
     *reinterpret_cast<uint2*>(p.hs_lo + off) = uint2{hl[0] | (uint32_t(hl[1]) << 16), hl[2] | (uint32_t(hl[3]) << 16)};
   }
@@ -260,10 +277,9 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint
 // expert (bf16 w1/w3, K split over the block's waves); hs = SwiGLU(gate, up)
 // as bf16 hi/lo planes.  The routing block's dependent loads and wave
 // reductions overlap the shared expert's weight stream.
-// 8-row shared tiles (a 2048-row shared expert: 256 tiles, one per CU) and
-// 16 waves per block, so each wave takes two K blocks, all in flight at once.
+// Shared tiles of 8 rows up to 8 tokens (a 2048-row shared expert: 256
+// tiles, one per CU; K-block pairs per MFMA, see shared_up_tile), else 16.
 constexpr int kRsW = 8;
-constexpr int kRsRows = 8;
 
 template <bool kF32>
 __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_route_shared(
@@ -281,8 +297,12 @@ __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
   uint16_t* xl = lds_up + p.T * xs;
   u32x4 xv[kUpXRegChunks][2];
   const bool xreg = load_x<kF32, kRsW * 64>(p, xh, xl, xs, tid, xv);
-  shared_up_tile<kF32, kRsW, kRsRows>(p, static_cast<int>(blockIdx.x) - 1, xh, xl, xs, xreg, xv, lds_up, tid, lane,
-                                      wave, r16, g4);
+  if (p.T <= 8)
+    shared_up_tile<kF32, kRsW, 8>(p, static_cast<int>(blockIdx.x) - 1, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave,
+                                  r16, g4);
+  else
+    shared_up_tile<kF32, kRsW, 16>(p, static_cast<int>(blockIdx.x) - 1, xh, xl, xs, xreg, xv, lds_up, tid, lane,
+                                   wave, r16, g4);
 }
 
 // Routed gate/up of the decode pipeline.  Each block takes kUpItems row
@@ -1240,7 +1260,7 @@ size_t rs_lds_bytes(const DecodeArgs& p) {
 hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                hipStream_t s, int repeat) {
   const DecodeArgs p = decode_args(d, L, a);
-  const unsigned blocks = static_cast<unsigned>(1 + p.Is / kRsRows);
+  const unsigned blocks = static_cast<unsigned>(1 + p.Is / (p.T <= 8 ? 8 : 16));
   const size_t lds = rs_lds_bytes(p);
   for (int r = 0; r < repeat; ++r) {
     if (p.x_f32) k_route_shared<true><<<blocks, kRsW * 64, lds, s>>>(p);
