@@ -116,7 +116,7 @@ __device__ __forceinline__ void gate_tile(const void* x, const void* gw, int T, 
   // before the product, and steps past the segment add +0, which leaves a
   // partial that starts at +0 unchanged -- the sums are those of the plain
   // loop, in the same order.
-  constexpr int kC = TW * EW == 1 ? 4 : 1;
+  constexpr int kC = TW * EW == 1 ? 4 : 2;
   for (int mb = m0; mb < m1; mb += kC) {
     f32x4 xv[kC][TW], wv[kC][EW];
 #pragma unroll
