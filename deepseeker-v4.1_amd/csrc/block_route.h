@@ -24,21 +24,51 @@ struct BlockRoute {
   int32_t rmap[kDecodeMaxPositions * kDecodeMaxTokens];   // [slot][token] dispatch row, -1 if none
 };
 
+// 8-byte words of the expert pointer table each thread prefetches into LDS.
+constexpr int kRouteTabWords = 5;
+constexpr int kTabWordsPerExpert = static_cast<int>(sizeof(dsk_expert_ptrs) / 8);
+static_assert(sizeof(dsk_expert_ptrs) % 8 == 0, "pointer table entries are whole 8-byte words");
+
+// Wait for the wave's LDS operations only (s_waitcnt lgkmcnt(0); vmcnt and
+// expcnt at their maxima), so LDS hand-offs inside wave 0 do not also wait
+// for the acknowledgement of the global stores issued before them.
+__device__ __forceinline__ void wait_lds_only() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 // Top-k of the T tokens (wave w: tokens w, w + waves, ...) from the gate
 // scores, then the slot map in wave 0, into r.  With `publish` the block also
 // writes the routing outputs of the layer (o): idx / weights, and for the
 // expert kernels active, one descriptor per slot, rowmap, the row weights
-// and rank.  Contains two block barriers.
+// and rank.  ltab (ltab_words 8-byte words of LDS, or null) receives the
+// whole pointer table, loaded together with the scores, when it fits there
+// and in the block's registers; the descriptors then read it from LDS
+// instead of making a dependent global load.  Contains two block barriers.
 __device__ __forceinline__ void block_route(BlockRoute& r, const float* scores, const float* bias, int T,
                                             int E, int k, float route_scale, const dsk_expert_ptrs* table,
-                                            bool publish, const DecodeRoute& o) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+                                            bool publish, const DecodeRoute& o, uint64_t* ltab,
+                                            int ltab_words) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int waves = blockDim.x >> 6;
+  const int nthr = static_cast<int>(blockDim.x);
+  const int nq = E * kTabWordsPerExpert;
+  const bool tab = publish && ltab != nullptr && nq <= ltab_words && nq <= kRouteTabWords * nthr;
+  uint64_t tq[kRouteTabWords];
+  if (tab) {
+    // no conditions on the loads: words past the table re-read its last word
+    const uint64_t* tg = reinterpret_cast<const uint64_t*>(table);
+#pragma unroll
+    for (int i = 0; i < kRouteTabWords; ++i) tq[i] = tg[min(tid + i * nthr, nq - 1)];
+  }
   for (int t = wave; t < T; t += waves)
     topk_token(scores + static_cast<int64_t>(t) * E, bias, E, k, route_scale,
                publish ? o.idx + static_cast<int64_t>(t) * k : nullptr,
                publish ? o.weights + static_cast<int64_t>(t) * k : nullptr, r.key + t * k, r.w + t * k);
+  if (tab) {
+#pragma unroll
+    for (int i = 0; i < kRouteTabWords; ++i)
+      if (tid + i * nthr < nq) ltab[tid + i * nthr] = tq[i];
+  }
   __syncthreads();
   if (wave == 0) {
     const int N = T * k;
@@ -54,7 +84,7 @@ __device__ __forceinline__ void block_route(BlockRoute& r, const float* scores, 
     if (lane < N) r.sorted[pos] = key;
     else r.sorted[lane] = E;
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_s_waitcnt(0);
+    wait_lds_only();
     __builtin_amdgcn_wave_barrier();
     const int se = r.sorted[lane];
     const bool first = lane < n_valid && (lane == 0 || r.sorted[lane - 1] != se);
@@ -69,7 +99,9 @@ __device__ __forceinline__ void block_route(BlockRoute& r, const float* scores, 
         const int next = above ? __builtin_ctzll(above) : n_valid;
         SlotDesc d;
         d.e = se; d.n_tok = next - lane; d.tok_base = lane; d.pad = 0;
-        const dsk_expert_ptrs t = table[se];
+        dsk_expert_ptrs t;
+        if (tab) t = reinterpret_cast<const dsk_expert_ptrs*>(ltab)[se];
+        else t = table[se];
         d.p[0] = t.w1; d.p[1] = t.s1; d.p[2] = t.b1;
         d.p[3] = t.w3; d.p[4] = t.s3; d.p[5] = t.b3;
         d.p[6] = t.w2; d.p[7] = t.s2; d.p[8] = t.b2;
@@ -84,7 +116,7 @@ __device__ __forceinline__ void block_route(BlockRoute& r, const float* scores, 
     }
     for (int i = lane; i < n_act * T; i += 64) r.rmap[i] = -1;
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_s_waitcnt(0);
+    wait_lds_only();
     __builtin_amdgcn_wave_barrier();
     const int my_slot = __shfl(slot_here, pos & 63, 64);
     if (ok) {
@@ -98,7 +130,7 @@ __device__ __forceinline__ void block_route(BlockRoute& r, const float* scores, 
     if (publish && lane < N) o.rank[lane] = ok ? pos : -1;
     if (publish) {
       __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_s_waitcnt(0);
+      wait_lds_only();
       __builtin_amdgcn_wave_barrier();
       for (int i = lane; i < n_act * T; i += 64) o.rowmap[i] = r.rmap[i];
     }

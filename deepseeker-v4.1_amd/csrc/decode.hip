@@ -280,6 +280,12 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint
 // Shared tiles of 8 rows up to 8 tokens (a 2048-row shared expert: 256
 // tiles, one per CU; K-block pairs per MFMA, see shared_up_tile), else 16.
 constexpr int kRsW = 8;
+// LDS of k_route_shared: the routing block's state and after it the expert
+// pointer table, or a shared tile's activation planes and then (over them)
+// its wave partial sums [kRsW][2][64][4] f32.
+constexpr size_t kRsRedBytes = kRsW * 2 * 64 * 4 * 4;
+constexpr size_t kRsTabOffset = (sizeof(BlockRoute) + 15) / 16 * 16;
+static_assert(kRsTabOffset < kRsRedBytes, "routing block state must fit the route/shared LDS");
 
 template <bool kF32>
 __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_route_shared(
@@ -287,7 +293,8 @@ __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
   extern __shared__ __align__(16) uint16_t lds_up[];
   if (blockIdx.x == 0) {
     block_route(*reinterpret_cast<BlockRoute*>(lds_up), p.scores, p.bias, p.T, p.E, p.k, p.route_scale,
-                p.table, true, p.route);
+                p.table, true, p.route, reinterpret_cast<uint64_t*>(lds_up + kRsTabOffset / 2),
+                static_cast<int>((kRsRedBytes - kRsTabOffset) / 8));
     return;
   }
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1246,10 +1253,6 @@ size_t up_q3_lds_bytes(const DecodeArgs& p) {
          static_cast<size_t>(p.H / 128) * kQ3fMaxTokens * 16 + kQ3fItems * kQ3fKS * 2 * 64 * 2 * 4 + 64;
 }
 
-// k_route_shared: the routing block's state, or a shared tile's activation
-// planes and then (over them) its wave partial sums [kRsW][2][64][4] f32.
-constexpr size_t kRsRedBytes = kRsW * 2 * 64 * 4 * 4;
-static_assert(sizeof(BlockRoute) <= kRsRedBytes, "routing block state must fit the route/shared LDS");
 size_t rs_lds_bytes(const DecodeArgs& p) {
   const size_t planes = static_cast<size_t>(p.x_f32 ? 2 : 1) * p.T * (p.H + 8) * 2;
   return planes > kRsRedBytes ? planes : kRsRedBytes;

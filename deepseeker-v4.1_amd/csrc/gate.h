@@ -176,19 +176,25 @@ __device__ __forceinline__ void topk_token_s(const float* __restrict__ srow, con
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   // ord[i]: order-preserving bits of the key of expert lane + 64*i; 0 = taken or absent.
+  // sv[i]: the score itself, kept for the weights (no second load).
   uint32_t ord[S];
+  float sv[S];
 #pragma unroll
   for (int i = 0; i < S; ++i) {
     const int e = lane + 64 * i;
     uint32_t o = 0u;
+    float s = 0.0f;
     if (e < E) {
-      const float key = (srow[e] + bias[e]) + 0.0f;
+      s = srow[e];
+      const float key = (s + bias[e]) + 0.0f;
       const uint32_t u = __float_as_uint(key);
       o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     }
     ord[i] = o;
+    sv[i] = s;
   }
   int my_e = 0;                         // lane j keeps the j-th selected expert
+  float my_s = 0.0f;                    // and its score
   for (int j = 0; j < k; ++j) {
     uint32_t bk = ord[0];
     int bi = 0;
@@ -198,14 +204,21 @@ __device__ __forceinline__ void topk_token_s(const float* __restrict__ srow, con
     const uint32_t m = wave_max_u32(bk);
     int e = -1;   // only if every remaining key has the bit pattern of -NaN with all payload bits set
     if (m != 0u) e = static_cast<int>(wave_min_u32(bk == m ? static_cast<uint32_t>(lane + 64 * bi) : ~0u));
-    if (lane == j) my_e = e;
+    float se = 0.0f;                    // score of expert e (wave-uniform e: a lane read)
+    if (e >= 0) {
+      float v = sv[0];
+#pragma unroll
+      for (int i = 1; i < S; ++i)
+        if (i == (e >> 6)) v = sv[i];
+      se = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), e & 63));
+    }
+    if (lane == j) { my_e = e; my_s = se; }
     if (e >= 0 && (e & 63) == lane) {
 #pragma unroll
       for (int i = 0; i < S; ++i)
         if (i == (e >> 6)) ord[i] = 0u;
     }
   }
-  const float my_s = (lane < k && my_e >= 0) ? srow[my_e] : 0.0f;
   float acc = 0.0f;                     // every lane forms the same sum, in selection order
   for (int j = 0; j < k; ++j) acc = acc + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_s), j));
   const float denom = acc + 1e-20f;
