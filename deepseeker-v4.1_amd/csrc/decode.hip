@@ -298,6 +298,11 @@ __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
     return;
   }
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // At one or two tokens the routing block ends the kernel: its score loads
+  // wait for whatever the tile block beside it on the same CU requested
+  // first.  The tile blocks wait ~0.5 us (19 x 64 clocks) before their first
+  // loads, so the routing block's go out ahead of them.
+  if (p.T <= 2) __builtin_amdgcn_s_sleep(19);
   const int r16 = lane & 15, g4 = lane >> 4;
   const int xs = p.H + 8;
   uint16_t* xh = lds_up;
