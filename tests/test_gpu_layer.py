@@ -180,6 +180,27 @@ def test_full_size_fp4_decode(T):
     print(f"cos={c:.9f} rel={rel:.2e}", flush=True)
 
 
+@pytest.mark.parametrize("E,T", [(384, 1), (384, 4), (256, 2)])
+def test_decode_expert_table_sizes(E, T):
+    """Decode pipeline with 384 experts (top-6): the routing block's copy of the
+    expert pointer table (72 bytes per expert) does not fit its LDS area, so the
+    descriptors read the table from global memory; 256 experts take the LDS
+    copy.  Two tokens also take the shared tiles' start delay."""
+    print(f"layer decode E={E} k=6 T={T}", flush=True)
+    layer = gsynth.make_layer(hidden=512, n_experts=E, top_k=6, inter=256,
+                              inter_shared=256, seed=30 + E + T, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(300 + E + T)
+    x = torch.randn((T, 512), generator=g, device=DEV).to(torch.bfloat16)
+    idx = torch.empty((T, 6), dtype=torch.int32, device=DEV)
+    out = layer(x, idx=idx).cpu()
+    spec = L.LayerSpec(H=512, E=E, k=6, I=256, I_shared=256)
+    shared = tuple(t.cpu() for t in (layer.shared.w1, layer.shared.w3, layer.shared.w2))
+    r = L.moe_forward(x.cpu(), layer.gate_w.cpu(), layer.gate_b.cpu(), _LazyBank(layer.bank), shared, spec)
+    np.testing.assert_array_equal(idx.cpu().numpy(), r["idx"])
+    c, rel = assert_layer_close(out.float(), r["y_ref"])
+    print(f"cos={c:.9f} rel={rel:.2e}", flush=True)
+
+
 def test_mid_size_batch64():
     """B=64 exercises 4 token tiles per weight tile (hidden 1024, 64 experts, top-8)."""
     spec = L.LayerSpec(H=1024, E=64, k=8, I=512, I_shared=512)
