@@ -62,6 +62,9 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   return min(min(readlane_u32(v, 0), readlane_u32(v, 16)), min(readlane_u32(v, 32), readlane_u32(v, 48)));
 }
 
+// Chunks of 64 positions whose loads a wave issues together.
+constexpr int kDispBatch = 8;
+
 // LDS needed: (S * E + E + 32) int32.
 __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ idx, int N, int E, int k,
                                                int nbits, const float* __restrict__ wflat,
@@ -80,9 +83,17 @@ __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ idx, 
 
   const int seg = ((N + S - 1) / S + 63) & ~63;
   const int beg = min(wave * seg, N), end = min(beg + seg, N);
-  for (int p = beg + lane; p < end; p += 64) {
-    const int e = idx[p];
-    if (e >= 0 && e < E) atomicAdd(&hist[wave * E + e], 1);
+  // the segment is read kDispBatch chunks of 64 positions at a time, the loads
+  // of a batch issued together (clamped into the segment, no conditions)
+  for (int c0 = beg; c0 < end; c0 += 64 * kDispBatch) {
+    int ev[kDispBatch];
+#pragma unroll
+    for (int j = 0; j < kDispBatch; ++j) ev[j] = idx[min(c0 + 64 * j + lane, end - 1)];
+#pragma unroll
+    for (int j = 0; j < kDispBatch; ++j) {
+      const int e = ev[j];
+      if (c0 + 64 * j + lane < end && e >= 0 && e < E) atomicAdd(&hist[wave * E + e], 1);
+    }
   }
   __syncthreads();
 
@@ -135,33 +146,46 @@ __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ idx, 
   __syncthreads();
 
   const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
-  for (int c0 = beg; c0 < end; c0 += 64) {
-    const int p = c0 + lane;
-    const bool in = p < end;
-    const int e = in ? idx[p] : -1;
-    const bool ok = in && e >= 0 && e < E;
-    uint64_t mask = __ballot(ok);
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = ok && ((e >> b) & 1);
-      const uint64_t bb = __ballot(bit);
-      mask &= bit ? bb : ~bb;
+  for (int cb = beg; cb < end; cb += 64 * kDispBatch) {
+    int ev[kDispBatch];
+    float wv[kDispBatch];
+#pragma unroll
+    for (int j = 0; j < kDispBatch; ++j) {
+      const int pc = min(cb + 64 * j + lane, end - 1);
+      ev[j] = idx[pc];
+      wv[j] = o.xrow ? wflat[pc] : 0.0f;
     }
-    if (ok) {
-      const int rk = __popcll(mask & lt);
-      const int pos = base[e] + hist[wave * E + e] + rk;
-      o.perm[pos] = p;
-      o.rank[p] = pos;
-      if (o.xrow) {
-        o.xrow[pos] = p / k;
-        o.wrow[pos] = wflat[p];
+#pragma unroll
+    for (int j = 0; j < kDispBatch; ++j) {
+      const int c0 = cb + 64 * j;
+      if (c0 >= end) break;
+      const int p = c0 + lane;
+      const bool in = p < end;
+      const int e = in ? ev[j] : -1;
+      const bool ok = in && e >= 0 && e < E;
+      uint64_t mask = __ballot(ok);
+      for (int b = 0; b < nbits; ++b) {
+        const bool bit = ok && ((e >> b) & 1);
+        const uint64_t bb = __ballot(bit);
+        mask &= bit ? bb : ~bb;
       }
-    } else if (in) {
-      o.rank[p] = -1;
+      if (ok) {
+        const int rk = __popcll(mask & lt);
+        const int pos = base[e] + hist[wave * E + e] + rk;
+        o.perm[pos] = p;
+        o.rank[p] = pos;
+        if (o.xrow) {
+          o.xrow[pos] = p / k;
+          o.wrow[pos] = wv[j];
+        }
+      } else if (in) {
+        o.rank[p] = -1;
+      }
+      // the highest lane of each group advances the cursor (after every lane read it)
+      __builtin_amdgcn_wave_barrier();
+      if (ok && lane == 63 - __clzll(mask)) hist[wave * E + e] += __popcll(mask);
+      __builtin_amdgcn_wave_barrier();
     }
-    // the highest lane of each group advances the cursor (after every lane read it)
-    __builtin_amdgcn_wave_barrier();
-    if (ok && lane == 63 - __clzll(mask)) hist[wave * E + e] += __popcll(mask);
-    __builtin_amdgcn_wave_barrier();
   }
 }
 
