@@ -427,6 +427,8 @@ __global__ __launch_bounds__(256) void k_prepare(const int32_t* __restrict__ cou
 // precomputed x-dtype shared output.
 enum SharedMode { kNoShared = 0, kSharedF32 = 1, kSharedExt = 2 };
 
+constexpr int kCombineMaxK = 16;     // top-k the combine handles (validated on the host)
+constexpr int kCombineBatch = 8;     // rows of a token whose loads are issued together
 template <bool XBF16>
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, const float* __restrict__ ys,
                                                  const void* __restrict__ shared_ext,
@@ -435,17 +437,34 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, co
   const int t = blockIdx.x;
   const int f = (blockIdx.y * 256 + threadIdx.x) * 4;
   if (f >= H) return;
-  int rows[16];
+  // The token's k ranks, then its first kCombineBatch rows, are each loaded
+  // together (no chain of dependent loads): ranks past k re-read rank k - 1,
+  // rows past n read row 0 and are not added.  Rows are added in ascending
+  // dispatch-row order.
+  int rk[kCombineMaxK];
+#pragma unroll
+  for (int j = 0; j < kCombineMaxK; ++j) rk[j] = rank[static_cast<int64_t>(t) * k + min(j, k - 1)];
+  int rows[kCombineMaxK];
+#pragma unroll
+  for (int j = 0; j < kCombineMaxK; ++j) rows[j] = 0;
   int n = 0;
-  for (int j = 0; j < k; ++j) {
-    const int r = rank[static_cast<int64_t>(t) * k + j];
+#pragma unroll
+  for (int j = 0; j < kCombineMaxK; ++j) {
+    if (j >= k) break;
+    const int r = rk[j];
     if (r < 0) continue;
     int i = n++;
     while (i > 0 && rows[i - 1] > r) { rows[i] = rows[i - 1]; --i; }
     rows[i] = r;
   }
+  f32x4 v[kCombineBatch];
+#pragma unroll
+  for (int q = 0; q < kCombineBatch; ++q) v[q] = *reinterpret_cast<const f32x4*>(y + static_cast<int64_t>(rows[q]) * H + f);
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int i = 0; i < n; ++i) acc += *reinterpret_cast<const f32x4*>(y + static_cast<int64_t>(rows[i]) * H + f);
+#pragma unroll
+  for (int q = 0; q < kCombineBatch; ++q)
+    if (q < n) acc += v[q];
+  for (int i = kCombineBatch; i < n; ++i) acc += *reinterpret_cast<const f32x4*>(y + static_cast<int64_t>(rows[i]) * H + f);
   const int64_t o = static_cast<int64_t>(t) * H + f;
   if (shared_mode == kSharedF32) {
     f32x4 s = *reinterpret_cast<const f32x4*>(ys + o);
