@@ -15,10 +15,10 @@ from .bank import ResidentBank, SharedExpert
 from .checkpoint import Checkpoint, build_manifest, fp8_block_dequant
 from .layer import MoELayer, moe_layer
 from .stack import MoEStack, rmsnorm
-from .trace import TraceSink, read_trace, write_trace
+from .trace import Geometry, Trace, TraceSink
 from .ops import (align_block_size, dispatch, fp4_dequant, fp4_quantize, q3_dequant,
                   q3_quantize, route, workspace_size)
 
 __all__ = ["Checkpoint", "DskError", "MoELayer", "MoEStack", "ResidentBank", "SharedExpert", "TraceSink", "align_block_size",
            "build_manifest", "dispatch", "fp4_dequant", "fp8_block_dequant", "fp4_quantize", "load_library", "moe_layer",
-           "q3_dequant", "q3_quantize", "read_trace", "rmsnorm", "route", "workspace_size", "write_trace"]
+           "q3_dequant", "q3_quantize", "rmsnorm", "route", "workspace_size", "Geometry", "Trace"]

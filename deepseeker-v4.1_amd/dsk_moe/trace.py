@@ -1,183 +1,309 @@
-"""Router traces in the reference's ``deepseeker.trace/v1`` JSONL schema.
+"""Router traces in the ``deepseeker.trace/v1`` JSONL format.
 
-The reference records the authoritative top-k of every (request, token, layer)
-through ``moe_layer``'s ``trace_hook(layer, idx, weights)``
-(``src/deepseeker/mlx_forward.py:380-381, 407-408``), collected by a sink
-(``scripts/run_mlx.py:34-50``) and written as JSONL (``src/deepseeker/trace.py``):
+The reference records the top-k of every (request, token, layer) through
+``moe_layer``'s ``trace_hook(layer, idx, weights)``
+(``src/deepseeker/mlx_forward.py:380-381, 407-408``), collects it in a sink
+(``scripts/run_mlx.py:34-50``) and stores it as JSONL; the format is defined
+in ``src/deepseeker/trace.py:1-21``.  What the format fixes, and this module
+therefore keeps:
 
-* line 1, the header: ``kind = "header"``, ``schema = "deepseeker.trace/v1"``,
-  ``repo_id``, ``revision``, ``source``, ``n_layers``, ``n_routed_experts``,
-  ``top_k``, ``created_at_utc`` (and optionally ``seed``);
-* routing records: ``request_id``, ``token_pos`` (>= 0), ``layer``, ``experts``
-  (top_k distinct ids in [0, E)), ``scores`` (optional, aligned with experts;
-  the hook passes the route weights), ``timing_ms`` / ``bytes_moved``
-  (optional numbers), ``extra`` (optional object);
-* subsystem events: ``kind = "event"`` with ``extra.kind`` "engram" or "kv".
+* line 1 is a header object: ``kind "header"``, ``schema
+  "deepseeker.trace/v1"``, ``repo_id``, ``revision``, ``source``, the routing
+  geometry ``n_layers``, ``n_routed_experts``, ``top_k``, ``created_at_utc``
+  and optionally ``seed``;
+* every further line is a routing record (``kind "record"``, or no kind) with
+  ``request_id`` (non-empty string), ``token_pos`` (>= 0), ``layer`` (in
+  ``[0, n_layers)``), ``experts`` (``top_k`` distinct ids in ``[0, E)``) and
+  the optional ``scores`` (``top_k`` numbers), ``timing_ms``, ``bytes_moved``
+  (numbers) and ``extra`` (an object); or a subsystem event (``kind
+  "event"``) with ``request_id``, ``token_pos``, ``layer`` and an ``extra``
+  object whose ``kind`` is ``"engram"`` or ``"kv"``.
 
-This module reads and writes that format (traces written here validate with
-the reference's reader and the reference's traces with this one), validates
-records with the same rules, summarises traces, and provides ``TraceSink``,
-which turns the device routing of ``moe_layer``, ``MoELayer`` and ``MoEStack``
-into records.  ``routing_batches`` regroups a trace's records into the token
-batches a layer saw, for replaying the recorded routing through the dispatch
-and expert kernels.
+The validity rules live in one table (``FIELDS``: per record kind, the fields
+with their presence and value rule) read by one checker (``check``); the
+file is handled by ``Trace`` (load / save / histogram / summary / per-layer
+token batches).  ``TraceSink`` turns the device routing of ``moe_layer``,
+``MoELayer`` and ``MoEStack`` into routing records, and ``Trace.batches``
+regroups recorded routing into the token runs a layer saw, for replaying it
+through the dispatch and expert kernels.
 """
 
 from __future__ import annotations
 
 import datetime
 import json
+from dataclasses import dataclass, field
 from pathlib import Path
+from typing import Callable, Iterator
 
 import numpy as np
 
 SCHEMA = "deepseeker.trace/v1"
-HEADER_KIND = "header"
-
-
-def arch_config(manifest: dict) -> dict:
-    """Routing geometry (n_layers, n_routed_experts, top_k) from a model manifest's architecture."""
-    a = manifest.get("architecture", {})
-    return {"n_layers": a["num_hidden_layers"], "n_routed_experts": a["n_routed_experts"],
-            "top_k": a["num_experts_per_tok"]}
-
-
-def make_header(repo_id: str, revision: str, source: str, cfg: dict, seed: int | None = None) -> dict:
-    for key in ("n_layers", "n_routed_experts", "top_k"):
-        v = cfg.get(key)
-        if not isinstance(v, int) or isinstance(v, bool) or v <= 0:
-            raise ValueError(f"routing geometry {key}={v!r} must be a positive integer")
-    h = {"kind": HEADER_KIND, "schema": SCHEMA, "repo_id": repo_id, "revision": revision, "source": source,
-         "n_layers": cfg["n_layers"], "n_routed_experts": cfg["n_routed_experts"], "top_k": cfg["top_k"],
-         "created_at_utc": datetime.datetime.now(datetime.timezone.utc).isoformat()}
-    if seed is not None:
-        h["seed"] = seed
-    return h
 
 
 def _is_int(v) -> bool:
     return isinstance(v, int) and not isinstance(v, bool)
 
 
-def _common_problems(r: dict, header: dict) -> list[str]:
-    p = []
-    if not isinstance(r.get("request_id"), str) or not r["request_id"]:
-        p.append("request_id must be a nonempty string")
-    if not _is_int(r.get("token_pos")) or r["token_pos"] < 0:
-        p.append(f"token_pos out of range: {r.get('token_pos')!r}")
-    if not _is_int(r.get("layer")) or not 0 <= r["layer"] < header["n_layers"]:
-        p.append(f"layer out of range: {r.get('layer')!r}")
-    return p
+def _is_number(v) -> bool:
+    return isinstance(v, (int, float)) and not isinstance(v, bool)
 
 
-def validate_record(r: dict, header: dict) -> list[str]:
-    """Problems of one record (an empty list when it is valid)."""
-    kind = r.get("kind", "record")
-    if kind == "event":
-        p = _common_problems(r, header)
-        extra = r.get("extra")
-        if not isinstance(extra, dict) or extra.get("kind") not in ("engram", "kv"):
-            p.append(f"event extra.kind must be engram or kv: {extra!r}")
-        return p
-    if kind != "record":
-        return [f"bad kind: {kind!r}"]
-    p = _common_problems(r, header)
-    k, E = header["top_k"], header["n_routed_experts"]
-    ex = r.get("experts")
-    if not isinstance(ex, list) or len(ex) != k or any(not _is_int(e) or not 0 <= e < E for e in ex):
-        p.append(f"experts must be {k} ids in [0, {E}): {ex!r}")
-    elif len(set(ex)) != len(ex):
-        p.append(f"duplicate expert ids: {ex!r}")
-    sc = r.get("scores")
-    if sc is not None and (not isinstance(sc, list) or len(sc) != k
-                           or any(not isinstance(s, (int, float)) or isinstance(s, bool) for s in sc)):
-        p.append(f"scores must align with experts: {sc!r}")
-    for key in ("timing_ms", "bytes_moved"):
-        v = r.get(key)
-        if v is not None and (not isinstance(v, (int, float)) or isinstance(v, bool)):
-            p.append(f"{key} must be numeric: {v!r}")
-    if r.get("extra") is not None and not isinstance(r["extra"], dict):
-        p.append(f"extra must be an object: {r['extra']!r}")
-    return p
+@dataclass(frozen=True)
+class Geometry:
+    """The routing geometry a trace is recorded against."""
+
+    n_layers: int
+    n_routed_experts: int
+    top_k: int
+
+    def __post_init__(self):
+        for name in ("n_layers", "n_routed_experts", "top_k"):
+            v = getattr(self, name)
+            if not _is_int(v) or v < 1:
+                raise ValueError(f"trace geometry: {name} = {v!r} is not a positive integer")
+
+    @classmethod
+    def of_header(cls, header: dict) -> "Geometry":
+        return cls(header.get("n_layers"), header.get("n_routed_experts"), header.get("top_k"))
+
+    @classmethod
+    def of_manifest(cls, manifest: dict) -> "Geometry":
+        """From a ``deepseeker.model-manifest/v1`` architecture block."""
+        arch = manifest.get("architecture") or {}
+        return cls(arch.get("num_hidden_layers"), arch.get("n_routed_experts"),
+                   arch.get("num_experts_per_tok"))
+
+    def header(self, *, repo_id: str, revision: str, source: str, seed: int | None = None) -> dict:
+        h = {"kind": "header", "schema": SCHEMA, "repo_id": repo_id, "revision": revision,
+             "source": source, "n_layers": self.n_layers, "n_routed_experts": self.n_routed_experts,
+             "top_k": self.top_k,
+             "created_at_utc": datetime.datetime.now(datetime.timezone.utc).isoformat()}
+        if seed is not None:
+            h["seed"] = seed
+        return h
 
 
-def write_trace(path: str | Path, header: dict, records: list[dict]) -> int:
-    """Header line + one line per record (routing records get ``kind: "record"``)."""
-    with open(path, "w", encoding="utf-8") as f:
-        f.write(json.dumps(header) + "\n")
-        for r in records:
-            f.write(json.dumps(r if "kind" in r else {"kind": "record", **r}) + "\n")
-    return len(records)
+# ------------------------------------------------------------------ field rules
+# A rule returns None for an acceptable value, else the reason it is not.
+Rule = Callable[[object, Geometry], "str | None"]
 
 
-def read_trace(path: str | Path) -> tuple[dict, list[dict]]:
-    """(header, records); raises ValueError at the first malformed line.  Routing
-    records come back without their ``kind`` key, events keep it."""
-    with open(path, encoding="utf-8") as f:
-        lines = [ln for ln in f if ln.strip()]
-    if not lines:
-        raise ValueError("empty trace file")
-    try:
-        header = json.loads(lines[0])
-    except ValueError as exc:
-        raise ValueError(f"line 1: invalid JSON: {exc}") from exc
-    if not isinstance(header, dict) or header.get("kind") != HEADER_KIND or header.get("schema") != SCHEMA:
-        raise ValueError(f"line 1: not a {SCHEMA} header: {lines[0][:120]!r}")
-    records = []
-    for n, ln in enumerate(lines[1:], 2):
+def _nonempty_text(v, g: Geometry):
+    return None if isinstance(v, str) and v else f"want a non-empty string, got {v!r}"
+
+
+def _index_below(limit: Callable[[Geometry], "int | None"]) -> Rule:
+    def rule(v, g: Geometry):
+        hi = limit(g)
+        if _is_int(v) and v >= 0 and (hi is None or v < hi):
+            return None
+        span = "[0, inf)" if hi is None else f"[0, {hi})"
+        return f"want an integer in {span}, got {v!r}"
+    return rule
+
+
+def _expert_ids(v, g: Geometry):
+    if not isinstance(v, list) or len(v) != g.top_k:
+        return f"want a list of {g.top_k} expert ids, got {v!r}"
+    if not all(_is_int(e) and 0 <= e < g.n_routed_experts for e in v):
+        return f"every id must be an integer in [0, {g.n_routed_experts}), got {v!r}"
+    if len(set(v)) != len(v):
+        return f"ids must be distinct, got {v!r}"
+    return None
+
+
+def _per_slot_numbers(v, g: Geometry):
+    if isinstance(v, list) and len(v) == g.top_k and all(_is_number(s) for s in v):
+        return None
+    return f"want {g.top_k} numbers (one per expert), got {v!r}"
+
+
+def _number(v, g: Geometry):
+    return None if _is_number(v) else f"want a number, got {v!r}"
+
+
+def _mapping(v, g: Geometry):
+    return None if isinstance(v, dict) else f"want an object, got {v!r}"
+
+
+def _event_payload(v, g: Geometry):
+    if isinstance(v, dict) and v.get("kind") in EVENT_KINDS:
+        return None
+    return f"want an object whose kind is one of {sorted(EVENT_KINDS)}, got {v!r}"
+
+
+EVENT_KINDS = frozenset({"engram", "kv"})
+
+
+@dataclass(frozen=True)
+class Field:
+    key: str
+    required: bool
+    rule: Rule
+
+
+_WHO = (Field("request_id", True, _nonempty_text),
+        Field("token_pos", True, _index_below(lambda g: None)),
+        Field("layer", True, _index_below(lambda g: g.n_layers)))
+
+# record kind -> the fields it may carry (absent or null optional fields are skipped)
+FIELDS: dict[str, tuple[Field, ...]] = {
+    "record": _WHO + (Field("experts", True, _expert_ids),
+                      Field("scores", False, _per_slot_numbers),
+                      Field("timing_ms", False, _number),
+                      Field("bytes_moved", False, _number),
+                      Field("extra", False, _mapping)),
+    "event": _WHO + (Field("extra", True, _event_payload),),
+}
+
+
+def check(record: dict, geometry: Geometry) -> list[str]:
+    """Every way ``record`` breaks the format (empty when it is valid)."""
+    if not isinstance(record, dict):
+        return [f"a line must hold a JSON object, got {type(record).__name__}"]
+    kind = record.get("kind", "record")
+    fields = FIELDS.get(kind)
+    if fields is None:
+        return [f"kind {kind!r}: want one of {sorted(FIELDS)}"]
+    found = []
+    for f in fields:
+        v = record.get(f.key)
+        if v is None:
+            if f.required:
+                found.append(f"{f.key}: required")
+            continue
+        why = f.rule(v, geometry)
+        if why:
+            found.append(f"{f.key}: {why}")
+    return found
+
+
+# ------------------------------------------------------------------ files
+def _is_routing(r: dict) -> bool:
+    return r.get("kind", "record") == "record"
+
+
+@dataclass
+class Trace:
+    """A header and its records.  Routing records are kept without a ``kind``
+    key (as ``TraceSink`` makes them); events keep ``kind: "event"``."""
+
+    header: dict
+    records: list = field(default_factory=list)
+
+    @property
+    def geometry(self) -> Geometry:
+        return Geometry.of_header(self.header)
+
+    @staticmethod
+    def _lines(path) -> Iterator[tuple[int, object]]:
+        with open(path, encoding="utf-8") as f:
+            for n, text in enumerate(f, 1):
+                if not text.strip():
+                    continue
+                try:
+                    yield n, json.loads(text)
+                except json.JSONDecodeError as exc:
+                    raise ValueError(f"{path}:{n}: not JSON ({exc.msg})") from exc
+
+    @classmethod
+    def load(cls, path: str | Path) -> "Trace":
+        """Read and check a trace; the first broken line raises ValueError."""
+        lines = cls._lines(path)
+        first = next(lines, None)
+        if first is None:
+            raise ValueError(f"{path}: no header (the file has no lines)")
+        n, head = first
+        if not isinstance(head, dict) or head.get("kind") != "header" or head.get("schema") != SCHEMA:
+            raise ValueError(f"{path}:{n}: want a {SCHEMA} header object first")
         try:
-            r = json.loads(ln)
+            geo = Geometry.of_header(head)
         except ValueError as exc:
-            raise ValueError(f"line {n}: invalid JSON: {exc}") from exc
-        if not isinstance(r, dict):
-            raise ValueError(f"line {n}: a record must be an object")
-        problems = validate_record(r, header)
-        if problems:
-            raise ValueError(f"line {n}: {problems[0]}")
-        if r.get("kind", "record") == "record":
-            r.pop("kind", None)
-        records.append(r)
-    return header, records
+            raise ValueError(f"{path}:{n}: {exc}") from exc
+        out = cls(head)
+        for n, rec in lines:
+            broken = check(rec, geo)
+            if broken:
+                raise ValueError(f"{path}:{n}: {broken[0]}")
+            if _is_routing(rec):
+                rec = {k: v for k, v in rec.items() if k != "kind"}
+            out.records.append(rec)
+        return out
 
+    def save(self, path: str | Path) -> int:
+        """Header, then one line per record (routing records tagged ``kind: "record"``);
+        returns the number of records written."""
+        with open(path, "w", encoding="utf-8") as f:
+            f.write(json.dumps(self.header) + "\n")
+            for r in self.records:
+                tagged = r if "kind" in r else dict(kind="record", **r)
+                f.write(json.dumps(tagged) + "\n")
+        return len(self.records)
 
-def expert_records(records: list[dict]) -> list[dict]:
-    """Routing records only (subsystem events dropped)."""
-    return [r for r in records if r.get("kind", "record") == "record"]
+    def routing(self) -> list[dict]:
+        """Routing records only (subsystem events left out)."""
+        return [r for r in self.records if _is_routing(r)]
 
+    def histogram(self) -> np.ndarray:
+        """``[n_layers, n_routed_experts]`` int64: times each expert was selected per layer."""
+        geo = self.geometry
+        counts = np.zeros((geo.n_layers, geo.n_routed_experts), dtype=np.int64)
+        rows = self.routing()
+        if rows:
+            layers = np.repeat([r["layer"] for r in rows], geo.top_k)
+            experts = np.concatenate([r["experts"] for r in rows])
+            np.add.at(counts, (layers, experts), 1)
+        return counts
 
-def layer_histogram(records: list[dict], n_layers: int) -> dict[int, dict[int, int]]:
-    """Per layer, {expert id: times selected}."""
-    hist: dict[int, dict[int, int]] = {layer: {} for layer in range(n_layers)}
-    for r in expert_records(records):
-        b = hist[r["layer"]]
-        for e in r["experts"]:
-            b[e] = b.get(e, 0) + 1
-    return hist
+    def summary(self) -> dict:
+        """Record and request counts, distinct experts per layer, and the share of
+        consecutive token pairs (same request and layer) that kept the same set."""
+        rows = self.routing()
+        distinct = (self.histogram() > 0).sum(axis=1)
+        kept = pairs = 0
+        if rows:
+            # order by (request, layer, position); a pair is two neighbours one position apart
+            req_id = {q: i for i, q in enumerate(sorted({r["request_id"] for r in rows}))}
+            key = np.array([(req_id[r["request_id"]], r["layer"], r["token_pos"]) for r in rows])
+            sets = np.sort(np.array([r["experts"] for r in rows]), axis=1)
+            order = np.lexsort((key[:, 2], key[:, 1], key[:, 0]))
+            key, sets = key[order], sets[order]
+            adj = (key[1:, 0] == key[:-1, 0]) & (key[1:, 1] == key[:-1, 1]) & (key[1:, 2] == key[:-1, 2] + 1)
+            pairs = int(adj.sum())
+            kept = int((adj & (sets[1:] == sets[:-1]).all(axis=1)).sum())
+        return {"records": len(rows), "requests": len({r["request_id"] for r in rows}),
+                "distinct_experts_per_layer": distinct.tolist(),
+                "mean_distinct": float(distinct.mean()) if distinct.size else 0.0,
+                "adjacent_same_set_ratio": kept / pairs if pairs else None}
 
-
-def trace_stats(header: dict, records: list[dict]) -> dict:
-    """Record and request counts, distinct experts per layer, and the share of
-    adjacent tokens (same request and layer) that kept the same expert set."""
-    recs = expert_records(records)
-    hist = layer_histogram(recs, header["n_layers"])
-    unique = {layer: len(b) for layer, b in hist.items()}
-    sets = {(r["request_id"], r["layer"], r["token_pos"]): set(r["experts"]) for r in recs}
-    same = pairs = 0
-    for (req, layer, pos), s in sets.items():
-        nxt = sets.get((req, layer, pos + 1))
-        if nxt is not None:
-            pairs += 1
-            same += s == nxt
-    return {"records": len(recs), "requests": len({r["request_id"] for r in recs}),
-            "unique_experts_per_layer": unique,
-            "mean_unique": sum(unique.values()) / len(unique) if unique else 0.0,
-            "adjacent_same_set_ratio": same / pairs if pairs else None}
+    def batches(self, layer: int) -> list[tuple[str, int, np.ndarray, np.ndarray | None]]:
+        """The token batches one layer saw: per request, runs of consecutive
+        positions, as (request_id, first position, experts [T, k] int32, scores
+        [T, k] float32, or None when a record of the run has no scores)."""
+        by_req: dict[str, dict[int, dict]] = {}
+        for r in self.routing():
+            if r["layer"] == layer:
+                by_req.setdefault(r["request_id"], {})[r["token_pos"]] = r
+        out = []
+        for req, at in by_req.items():
+            pos = np.array(sorted(at))
+            cuts = np.flatnonzero(np.diff(pos) != 1) + 1
+            for run in np.split(pos, cuts):
+                recs = [at[int(p)] for p in run]
+                ex = np.array([r["experts"] for r in recs], dtype=np.int32)
+                sc = None
+                if all(r.get("scores") is not None for r in recs):
+                    sc = np.array([r["scores"] for r in recs], dtype=np.float32)
+                out.append((req, int(run[0]), ex, sc))
+        return out
 
 
 class TraceSink:
-    """Collects routing as trace records: pass ``sink.router`` as ``trace_hook``
-    (``moe_layer``) or ``trace=sink`` (``MoELayer``, ``MoEStack``).  ``idx`` and
-    ``weights`` are per token, in ascending key order, like the reference's hook."""
+    """Collects device routing as routing records: pass ``sink.router`` as
+    ``trace_hook`` (``moe_layer``) or ``trace=sink`` (``MoELayer``, ``MoEStack``).
+    ``idx`` and ``weights`` arrive per token in ascending key order, the order of
+    the reference's hook; the weights are stored as ``scores``."""
 
     def __init__(self, request_id: str, token_start: int = 0):
         self.request_id = request_id
@@ -196,25 +322,7 @@ class TraceSink:
         """Move the token position on by a batch (after a stack step)."""
         self.token_start += tokens
 
-
-def routing_batches(records: list[dict], layer: int) -> list[tuple[str, int, np.ndarray, np.ndarray | None]]:
-    """The token batches one layer saw: per request, runs of consecutive token
-    positions, as (request_id, first position, experts [T, k] int32, scores [T, k]
-    float32 or None)."""
-    rows: dict[str, dict[int, dict]] = {}
-    for r in expert_records(records):
-        if r["layer"] == layer:
-            rows.setdefault(r["request_id"], {})[r["token_pos"]] = r
-    out = []
-    for req, by_pos in rows.items():
-        pos = sorted(by_pos)
-        start = 0
-        for i in range(1, len(pos) + 1):
-            if i == len(pos) or pos[i] != pos[i - 1] + 1:
-                run = [by_pos[p] for p in pos[start:i]]
-                ex = np.asarray([r["experts"] for r in run], dtype=np.int32)
-                sc = (np.asarray([r["scores"] for r in run], dtype=np.float32)
-                      if all(r.get("scores") is not None for r in run) else None)
-                out.append((req, pos[start], ex, sc))
-                start = i
-    return out
+    def to_trace(self, geometry: Geometry, *, repo_id: str, revision: str, source: str,
+                 seed: int | None = None) -> Trace:
+        return Trace(geometry.header(repo_id=repo_id, revision=revision, source=source, seed=seed),
+                     list(self.records))

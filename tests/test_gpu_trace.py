@@ -21,7 +21,7 @@ import dsk_moe
 from dsk_moe import synth as gsynth
 from dsk_moe.layer import experts_forward
 from dsk_moe.stack import MoEStack
-from dsk_moe.trace import TraceSink, make_header, read_trace, routing_batches, validate_record
+from dsk_moe.trace import Geometry, Trace, TraceSink, check
 from oracle import layer as L
 from conftest import assert_layer_close
 from test_gpu_layer import _LazyBank
@@ -40,10 +40,10 @@ def test_stack_trace_sink():
     sink = TraceSink("req", token_start=10)
     rec = []
     stack(x, record=rec, trace=sink)
-    header = make_header("synthetic", "none", "dsk", {"n_layers": 2, "n_routed_experts": 64, "top_k": 6})
+    geo = Geometry(n_layers=2, n_routed_experts=64, top_k=6)
     assert len(sink.records) == 2 * 3
     for r in sink.records:
-        assert validate_record(r, header) == []
+        assert check(r, geo) == []
     for layer in range(2):
         got = [r for r in sink.records if r["layer"] == layer]
         assert [r["token_pos"] for r in got] == [10, 11, 12]
@@ -56,8 +56,9 @@ def test_stack_trace_sink():
 @pytest.mark.parametrize("layer_id", [0, 7, 29])
 def test_replay_recorded_routing(layer_id):
     print(f"replay recorded routing, layer {layer_id}", flush=True)
-    h, recs = read_trace(GOLDEN / "trace_mlx_en_head.jsonl")
-    _, _, experts, scores = routing_batches(recs, layer_id)[0]
+    tr = Trace.load(GOLDEN / "trace_mlx_en_head.jsonl")
+    h = tr.header
+    _, _, experts, scores = tr.batches(layer_id)[0]
     T = experts.shape[0]
     spec = L.LayerSpec(H=1024, E=h["n_routed_experts"], k=h["top_k"], I=512, I_shared=512)
     layer = gsynth.make_layer(hidden=spec.H, n_experts=spec.E, top_k=spec.k, inter=spec.I,
