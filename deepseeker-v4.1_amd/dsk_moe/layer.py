@@ -41,7 +41,7 @@ import torch
 
 from . import _lib
 from .bank import ResidentBank, SharedExpert
-from .ops import make_desc, ptr, require_device, stream_of, workspace
+from .ops import make_desc, ptr, require_device, stream_of, workspace, workspace_size
 
 
 def _roles_of(weights) -> tuple:
@@ -225,9 +225,11 @@ class MoELayer:
 
     def __call__(self, x: torch.Tensor, out: torch.Tensor | None = None,
                  idx: torch.Tensor | None = None, w: torch.Tensor | None = None,
-                 trace=None, layer_id: int = 0) -> torch.Tensor:
+                 trace=None, layer_id: int = 0, ws: torch.Tensor | None = None) -> torch.Tensor:
         """``trace(layer_id, idx, weights)`` (optional, e.g. a ``TraceSink``) receives the
-        routing on the host, in ascending key order like the reference's trace_hook."""
+        routing on the host, in ascending key order like the reference's trace_hook.
+        ``ws`` (optional): a caller-owned workspace (``ops.new_workspace``) of at least
+        ``workspace_bytes(tokens)`` bytes, used instead of the per-stream cached one."""
         dev = require_device(x, self.gate_w)
         t, h = x.shape
         if trace is not None:
@@ -240,7 +242,10 @@ class MoELayer:
                          limit=self.limit)
         if out is None:
             out = torch.empty_like(x)
-        ws = workspace(desc, dev)
+        if ws is None:
+            ws = workspace(desc, dev)
+        elif ws.numel() < workspace_size(desc) or ws.device != dev:
+            raise ValueError(f"workspace of {ws.numel()} bytes on {ws.device} is too small for this call")
         s = self.shared
         _lib.call("dsk_moe_forward", ctypes.byref(desc), ptr(x), ptr(self.gate_w), ptr(self.gate_b),
                   ptr(self.bank.table), ptr(s.w1 if s else None), ptr(s.w3 if s else None),
@@ -249,3 +254,11 @@ class MoELayer:
         if trace is not None:
             trace(layer_id, idx.flip(1).tolist(), w.flip(1).tolist())
         return out
+
+    def workspace_bytes(self, tokens: int, x_dtype: torch.dtype = torch.bfloat16) -> int:
+        """Workspace bytes a call on ``tokens`` rows of ``x_dtype`` needs."""
+        return workspace_size(make_desc(
+            tokens=tokens, hidden=self.gate_w.shape[1], n_experts=self.bank.n_experts, top_k=self.top_k,
+            inter=self.bank.inter, inter_shared=self.shared.inter if self.shared else 0,
+            score_func=self.score_func, quant=self.bank.quant, x_dtype=x_dtype,
+            gate_dtype=self.gate_w.dtype, route_scale=self.route_scale, limit=self.limit))

@@ -76,20 +76,36 @@ def workspace_size(desc: _lib.Desc) -> int:
 
 
 _WS_CACHE: dict[tuple, torch.Tensor] = {}
+# Workspaces a HIP graph captured: a graph replays raw pointers, so a captured
+# workspace is never handed back to the allocator, even after a larger one
+# replaced it in the cache.
+_WS_CAPTURED: dict[int, torch.Tensor] = {}
+
+
+def new_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """A zero-initialised device workspace of ``nbytes`` (at least 256) bytes."""
+    ws = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+    _lib.call("dsk_workspace_init", ptr(ws), ws.numel(), stream_of(device))
+    return ws
 
 
 def workspace(desc: _lib.Desc, device: torch.device) -> torch.Tensor:
     """A cached, zero-initialised device workspace of at least ``workspace_size(desc)`` bytes.
 
-    Calls that share a cached workspace must be ordered on one stream.
+    One workspace per (device, stream): calls on one stream are ordered, so they
+    may share it; calls on different streams get different workspaces.  A
+    workspace used while the stream is being captured into a HIP graph stays
+    allocated for the life of the process.
     """
     need = workspace_size(desc)
-    key = (device.type, device.index)
+    stream = torch.cuda.current_stream(device)
+    key = (device.type, device.index, stream.cuda_stream)
     ws = _WS_CACHE.get(key)
     if ws is None or ws.numel() < need:
-        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=device)
-        _lib.call("dsk_workspace_init", ptr(ws), ws.numel(), stream_of(device))
+        ws = new_workspace(need, device)
         _WS_CACHE[key] = ws
+    if torch.cuda.is_current_stream_capturing():
+        _WS_CAPTURED[ws.data_ptr()] = ws
     return ws
 
 

@@ -20,7 +20,7 @@ import torch
 
 from . import _lib
 from .layer import MoELayer
-from .ops import ptr, require_device, stream_of
+from .ops import new_workspace, ptr, require_device, stream_of
 
 _DTYPES = {torch.bfloat16: 0, torch.float32: 1}
 
@@ -61,7 +61,7 @@ class MoEStack:
         return torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)   # h, y, d
 
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None, bufs=None,
-                record: list | None = None, trace=None) -> torch.Tensor:
+                record: list | None = None, trace=None, ws: torch.Tensor | None = None) -> torch.Tensor:
         """h_L for input rows x [T, H].  ``record`` (optional list) receives, per
         layer, copies of (h_l, rmsnorm(h_l), idx_l, layer output); ``trace``
         (optional, e.g. a ``TraceSink``) receives every layer's routing as
@@ -79,7 +79,7 @@ class MoEStack:
                 prev = h
             if record is not None:
                 idx = torch.empty((x.shape[0], layer.top_k), dtype=torch.int32, device=x.device)
-            layer(y, out=d, idx=idx, trace=trace, layer_id=l)
+            layer(y, out=d, idx=idx, trace=trace, layer_id=l, ws=ws)
             if record is not None:
                 record.append((prev.clone(), y.clone(), idx, d.clone()))
         rmsnorm(prev, self.eps, residual=d, h_out=out, out=False)
@@ -88,22 +88,25 @@ class MoEStack:
     __call__ = forward
 
     def capture(self, tokens: int, dtype: torch.dtype = torch.bfloat16, warmup: int = 2) -> None:
-        """Record the stack for ``tokens`` rows as one HIP graph (static input / output buffers)."""
+        """Record the stack for ``tokens`` rows as one HIP graph (static input / output
+        buffers).  The graph owns its workspace (sized for the largest layer), so
+        later eager calls of any size, or other captures, cannot move it."""
         dev = self.layers[0].gate_w.device
         hidden = self.layers[0].gate_w.shape[1]
         self._x = torch.zeros((tokens, hidden), dtype=dtype, device=dev)
         self._out = torch.empty_like(self._x)
         self._bufs = self._buffers(self._x)
+        self._ws = new_workspace(max(l.workspace_bytes(tokens, dtype) for l in self.layers), dev)
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
             for _ in range(warmup):
-                self.forward(self._x, out=self._out, bufs=self._bufs)
+                self.forward(self._x, out=self._out, bufs=self._bufs, ws=self._ws)
         torch.cuda.current_stream(dev).wait_stream(side)
         torch.cuda.synchronize(dev)
         self._graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self._graph):
-            self.forward(self._x, out=self._out, bufs=self._bufs)
+            self.forward(self._x, out=self._out, bufs=self._bufs, ws=self._ws)
         torch.cuda.synchronize(dev)
 
     def replay(self, x: torch.Tensor | None = None) -> torch.Tensor:

@@ -114,3 +114,26 @@ def test_full_stack_verify_and_graph(stack40):
         assert torch.equal(got.view(torch.int16), eager.view(torch.int16)), f"replay {rep}"
     # the stream moved: output differs from input and stays finite
     assert not torch.equal(got, xr) and torch.isfinite(got.float()).all()
+
+
+def test_captured_stack_keeps_its_workspace():
+    """A captured stack owns its workspace: an eager call that needs a larger
+    one (T=300, prefill sizes) cannot free memory the graph still writes."""
+    print("stack capture(1), eager T=300 layer call, replay", flush=True)
+    specs = _mixed_specs()[:2]
+    data = [synth.make_layer(sp, 60 + l, 1) for l, sp in enumerate(specs)]
+    layers = [dsk_moe.MoELayer(d["gate_w"].to(DEV), d["gate_b"].to(DEV), to_bank(d["bank"]),
+                               to_shared(d["shared"]), sp.k) for d, sp in zip(data, specs)]
+    stack = MoEStack(layers, eps=1e-6)
+    stack.capture(1)
+    g = torch.Generator(device=DEV).manual_seed(61)
+    big = torch.randn((300, 1024), generator=g, device=DEV).to(torch.bfloat16)
+    for rep in range(3):
+        x = torch.randn((1, 1024), generator=g, device=DEV).to(torch.bfloat16)
+        layers[0](big)                  # grows (replaces) the cached per-stream workspace
+        torch.cuda.synchronize()
+        got = stack.replay(x).clone()
+        torch.cuda.synchronize()
+        want = stack(x).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {rep}"
