@@ -85,21 +85,25 @@ def fp4_codes(packed: np.ndarray) -> np.ndarray:
     return out
 
 
+# value pair of every packed byte: (low nibble, high nibble)
+_FP4_PAIRS = np.stack([FP4_TABLE[np.arange(256) & 15], FP4_TABLE[np.arange(256) >> 4]], axis=-1)
+
+
 def fp4_dequant(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
     """FP4 role [..., K/2] u8 + [..., K/32] u8 -> float32 [..., K].
 
     Same arithmetic as the reference's ``reference_dequant``
     (``src/deepseeker/metal_fp4.py:122-131``): table value times the decoded
     scale, one float32 multiply per element (exact: both factors are short).
+    The table is looked up per byte (both nibbles at once, low first).
     """
-    codes = fp4_codes(packed)
-    k = codes.shape[-1]
+    p = np.asarray(packed, dtype=np.uint8)
+    k = p.shape[-1] * 2
     s = np.asarray(scales, dtype=np.uint8)
     if s.shape[-1] * FP4_GROUP != k:
         raise ValueError(f"scales {s.shape} do not cover K={k} in groups of 32")
-    vals = FP4_TABLE[codes]
-    gain = np.repeat(e8m0_to_f32(s), FP4_GROUP, axis=-1)
-    return (vals * gain).astype(np.float32)
+    vals = np.take(_FP4_PAIRS, p, axis=0).reshape(p.shape[:-1] + (k // FP4_GROUP, FP4_GROUP))
+    return (vals * e8m0_to_f32(s)[..., None]).reshape(p.shape[:-1] + (k,))
 
 
 def fp4_scale_exponent(amax: np.ndarray) -> np.ndarray:

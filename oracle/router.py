@@ -40,7 +40,9 @@ and by comparing ``exp``/``log1p``/``sqrt`` with ``math`` on many points.
 
 from __future__ import annotations
 
+import concurrent.futures as cf
 import math
+import os
 from fractions import Fraction
 
 import numpy as np
@@ -121,10 +123,14 @@ def sqrt_round_f32(v: np.ndarray) -> np.ndarray:
 GATE_SEGMENTS = 4
 
 
-def gate_logits(x: np.ndarray, gate_w: np.ndarray, chunk_elems: int = 1 << 24) -> np.ndarray:
+def gate_logits(x: np.ndarray, gate_w: np.ndarray, chunk_elems: int = 1 << 19,
+                workers: int | None = None) -> np.ndarray:
     """z = f32(x) @ f32(W).T in the fixed segment/lane order described in the module docstring.
 
     x: [T, H] (any float dtype, converted exactly to float32), gate_w: [E, H].
+    Token chunks are independent, so they are spread over ``workers`` threads
+    (numpy releases the GIL in its elementwise loops); the arithmetic of every
+    logit is the same whatever the chunking.
     """
     x = np.asarray(x, dtype=np.float32)
     w = np.asarray(gate_w, dtype=np.float32)
@@ -141,7 +147,8 @@ def gate_logits(x: np.ndarray, gate_w: np.ndarray, chunk_elems: int = 1 << 24) -
     out = np.empty((t, e), dtype=np.float32)
     tc = max(1, chunk_elems // max(1, e * GATE_LANES))
     lanes = np.arange(GATE_LANES)
-    for t0 in range(0, t, tc):
+
+    def chunk(t0: int) -> None:
         xs = xr[t0:t0 + tc]
         z = None
         for sw in range(GATE_SEGMENTS):
@@ -153,6 +160,15 @@ def gate_logits(x: np.ndarray, gate_w: np.ndarray, chunk_elems: int = 1 << 24) -
                 p = p + p[:, :, lanes ^ s]
             z = p[:, :, 0] if z is None else (z + p[:, :, 0]).astype(np.float32)
         out[t0:t0 + tc] = z
+
+    starts = list(range(0, t, tc))
+    n = min(len(starts), workers or min(16, os.cpu_count() or 1))
+    if n <= 1:
+        for t0 in starts:
+            chunk(t0)
+    else:
+        with cf.ThreadPoolExecutor(max_workers=n) as ex:
+            list(ex.map(chunk, starts))
     return out
 
 

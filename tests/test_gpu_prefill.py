@@ -73,28 +73,40 @@ def test_prefill_matches_general_path_routing_and_is_deterministic():
     assert_layer_close(a[:255].float(), g.float())
 
 
-@pytest.mark.parametrize("T,zipf", [(4096, 1.1), (512, None)])
-def test_full_size_prefill(T, zipf):
+@pytest.mark.parametrize("T,zipf,step", [(4096, 1.1, 1), (512, None, 8)])
+def test_full_size_prefill(T, zipf, step):
     """hidden 4096, 256 FP4 experts, top-8, inter 2048, bf16 shared 2048 (GPU-generated).
 
-    The whole batch runs on the GPU; a token's routing and output depend on its
-    own row only, so a strided sample of 256 rows (one in every token tile of
-    every expert of size > 16) is checked against the oracle run on those rows.
+    Routing (indices and weights) of the fused forward on every row against the
+    oracle router; outputs of every ``step``-th row against the oracle layer
+    (T=4096 with a Zipf(1.1) gate bias: every row; a token's output depends on
+    its own row only, so the uniform T=512 case checks a strided sample).
     """
-    print(f"prefill full-size fp4 T={T} zipf={zipf}", flush=True)
+    from conftest import DeviceBankView
+    from oracle import router as R
+    print(f"prefill full-size fp4 T={T} zipf={zipf} rows every {step}", flush=True)
     layer = gsynth.make_layer(hidden=4096, n_experts=256, top_k=8, inter=2048,
                               inter_shared=2048, seed=5, device=DEV, zipf_s=zipf)
     g = torch.Generator(device=DEV).manual_seed(300 + T)
     x = torch.randn((T, 4096), generator=g, device=DEV).to(torch.bfloat16)
     idx = torch.empty((T, 8), dtype=torch.int32, device=DEV)
-    out = layer(x, idx=idx).cpu()
-    sub = torch.arange(0, T, T // 256)
+    w = torch.empty((T, 8), dtype=torch.float32, device=DEV)
+    out = layer(x, idx=idx, w=w).cpu()
+    idx_h = idx.cpu().numpy()
+    r_idx, r_w, _, _ = R.route(x.cpu().float().numpy(), layer.gate_w.cpu().numpy(), layer.gate_b.cpu().numpy(),
+                               8, R.SCORE_SIGMOID, 2.5)
+    np.testing.assert_array_equal(idx_h, r_idx)
+    np.testing.assert_array_equal(w.cpu().numpy(), r_w)
+    sub = torch.arange(0, T, step)
     spec = L.LayerSpec(H=4096, E=256, k=8, I=2048, I_shared=2048)
     shared = tuple(t.cpu() for t in (layer.shared.w1, layer.shared.w3, layer.shared.w2))
-    r = L.moe_forward(x.cpu()[sub], layer.gate_w.cpu(), layer.gate_b.cpu(), _LazyBank(layer.bank),
-                      shared, spec)
-    np.testing.assert_array_equal(idx.cpu().numpy()[sub.numpy()], r["idx"])
+    view = DeviceBankView(layer.bank).prefetch(idx_h[sub.numpy()].ravel())
+    try:
+        r = L.moe_forward(x.cpu()[sub], layer.gate_w.cpu(), layer.gate_b.cpu(), view, shared, spec)
+    finally:
+        view.close()
+    np.testing.assert_array_equal(idx_h[sub.numpy()], r["idx"])
     c, rel = assert_layer_close(out[sub].float(), r["y_ref"])
-    counts = torch.bincount(idx.cpu().flatten().long(), minlength=256)
+    counts = np.bincount(idx_h.ravel(), minlength=256)
     print(f"cos={c:.9f} rel={rel:.2e} max_rows={int(counts.max())} active={int((counts > 0).sum())}",
           flush=True)
