@@ -25,6 +25,29 @@ int hip_check(hipError_t e, const char* what) {
   return fail(DSK_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+thread_local StageClock g_stage_clock;
+
+void stage_close() { g_stage_clock.open = -1; }
+
+hipError_t stage_open(int stage) {
+  StageClock& c = g_stage_clock;
+  if (!c.ev) return hipSuccess;
+  c.open = stage;
+  c.launched = false;
+  return hipSuccess;
+}
+
+namespace {
+// Arms the stage clock for one timed forward (this thread) and disarms it on exit.
+struct StageTiming {
+  explicit StageTiming(const hipEvent_t* ev) {
+    g_stage_clock = StageClock{};
+    g_stage_clock.ev = ev;
+  }
+  ~StageTiming() { g_stage_clock = StageClock{}; }
+};
+}  // namespace
+
 static size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 Workspace workspace_layout(const dsk_moe_desc& d) {
@@ -178,7 +201,7 @@ int dsk_experts(const dsk_moe_desc* d, const dsk_expert_ptrs* table, const void*
   a.table = table; a.ws1 = ws1; a.ws3 = ws3; a.ws2 = ws2; a.shared_out = shared_out; a.x = x; a.weights = weights;
   a.counts = counts; a.offsets = offsets; a.perm = perm; a.rank = rank; a.active = active;
   a.out = out; a.ws = static_cast<char*>(workspace);
-  return hip_check(launch_experts(*d, L, a, static_cast<hipStream_t>(stream), nullptr, 1),
+  return hip_check(launch_experts(*d, L, a, static_cast<hipStream_t>(stream), 1),
                    "dsk_experts launch");
 }
 
@@ -235,25 +258,25 @@ static int forward_impl(const dsk_moe_desc* d, const void* x, const void* gate_w
   a.scores = scores; a.bias = gate_b;
   a.route = DecodeRoute{idx_buf, w_buf, ra.out.desc, active, ra.rowmap, ra.out.xrow, ra.out.wrow, rank};
   const bool decode = decode_pipeline(*d);
-  if (ev && (rc = hip_check(hipEventRecord(ev[0], s), "event record"))) return rc;
+  StageTiming timing(ev);
+  stage_open(kStageGate);
   if (decode) {
     // gate scores; then the top-k and the slot map beside the shared expert's gate/up
     for (int r = 0; r < repeat && !rc; ++r) rc = hip_check(launch_gate_scores(*d, ra, s), "gate launch");
     if (rc) return rc;
-    if (ev && (rc = hip_check(hipEventRecord(ev[1], s), "event record"))) return rc;
+    stage_open(kStageRoute);
     rc = hip_check(launch_route_shared(*d, L, a, s, repeat), "route / shared gate-up launch");
     if (rc) return rc;
-    if (ev && (rc = hip_check(hipEventRecord(ev[2], s), "event record"))) return rc;
-    return hip_check(launch_experts_decode(*d, L, a, s, ev ? ev + 3 : nullptr, repeat),
-                     "decode experts launch");
+    rc = hip_check(launch_experts_decode(*d, L, a, s, repeat), "decode experts launch");
+  } else {
+    // gate (the fused router of a few tokens also selects and dispatches), then top-k + dispatch
+    for (int r = 0; r < repeat && !rc; ++r)
+      rc = hip_check(launch_route_dispatch(*d, ra, s), "route launch");
+    if (rc) return rc;
+    rc = hip_check(launch_experts(*d, L, a, s, repeat), "experts launch");
   }
-  for (int r = 0; r < repeat && !rc; ++r)
-    rc = hip_check(launch_route_dispatch(*d, ra, s), "route launch");
-  if (rc) return rc;
-  // the fused router also dispatches: both stage events mark its end
-  if (ev && (rc = hip_check(hipEventRecord(ev[1], s), "event record"))) return rc;
-  if (ev && (rc = hip_check(hipEventRecord(ev[2], s), "event record"))) return rc;
-  return hip_check(launch_experts(*d, L, a, s, ev ? ev + 3 : nullptr, repeat), "experts launch");
+  stage_close();
+  return rc;
 }
 
 int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, const float* gate_b,

@@ -1271,8 +1271,8 @@ hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const 
   const unsigned blocks = static_cast<unsigned>(1 + p.Is / (p.T <= 8 ? 8 : 16));
   const size_t lds = rs_lds_bytes(p);
   for (int r = 0; r < repeat; ++r) {
-    if (p.x_f32) k_route_shared<true><<<blocks, kRsW * 64, lds, s>>>(p);
-    else k_route_shared<false><<<blocks, kRsW * 64, lds, s>>>(p);
+    if (p.x_f32) launch_kernel(k_route_shared<true>, blocks, kRsW * 64, lds, s, p);
+    else launch_kernel(k_route_shared<false>, blocks, kRsW * 64, lds, s, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1280,7 +1280,7 @@ hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const 
 }
 
 hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
-                                 hipStream_t s, const hipEvent_t* ev, int repeat) {
+                                 hipStream_t s, int repeat) {
   const DecodeArgs p = decode_args(d, L, a);
   const int groups = (p.up_tiles + kUpItems - 1) / kUpItems;
   const int max_slots = d.n_experts < d.tokens * d.top_k ? d.n_experts : d.tokens * d.top_k;
@@ -1296,6 +1296,7 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   const bool q3fwin = d.hidden % (kQ3fKS * kUpBatch * 128) == 0;
   const bool q3f2 = (d.hidden / 128 + kQ3fKS - 1) / kQ3fKS > kUpBatch;   // a wave's range is two or more batches
   const unsigned q3f_blocks = static_cast<unsigned>(max_slots * ((p.up_tiles + kQ3fItems - 1) / kQ3fItems));
+  if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   if (d.tokens >= kDecodeGroupedUpMin && grouped_path(d)) {
     e = launch_grouped_up_routed(d, L, a, a.route.desc, a.route.xrow, a.route.wrow, s, repeat);
     if (e != hipSuccess) return e;
@@ -1305,33 +1306,32 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
     const bool q3f = q3 && d.tokens <= kQ3fMaxTokens && q3f_lds <= kMaxLds;
     for (int r = 0; r < repeat; ++r) {
       if (q3f && !q3f2) {
-        if (q3fwin && !p.x_f32) k_up_q3<true, false, false><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
-        else if (q3fwin) k_up_q3<true, true, false><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
-        else if (!p.x_f32) k_up_q3<false, false, false><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
-        else k_up_q3<false, true, false><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
+        if (q3fwin && !p.x_f32) launch_kernel(k_up_q3<true, false, false>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
+        else if (q3fwin) launch_kernel(k_up_q3<true, true, false>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
+        else if (!p.x_f32) launch_kernel(k_up_q3<false, false, false>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
+        else launch_kernel(k_up_q3<false, true, false>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
       } else if (q3f) {
-        if (q3fwin && !p.x_f32) k_up_q3<true, false, true><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
-        else if (q3fwin) k_up_q3<true, true, true><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
-        else if (!p.x_f32) k_up_q3<false, false, true><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
-        else k_up_q3<false, true, true><<<q3f_blocks, kQ3fW * 64, q3f_lds, s>>>(p);
+        if (q3fwin && !p.x_f32) launch_kernel(k_up_q3<true, false, true>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
+        else if (q3fwin) launch_kernel(k_up_q3<true, true, true>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
+        else if (!p.x_f32) launch_kernel(k_up_q3<false, false, true>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
+        else launch_kernel(k_up_q3<false, true, true>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
       }
-      else if (q3 && q3win && !p.x_f32) k_up_stream<kUpBatch, true, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-      else if (q3 && q3win) k_up_stream<kUpBatch, true, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-      else if (q3 && !p.x_f32) k_up_stream<kUpBatch, false, false, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-      else if (q3) k_up_stream<kUpBatch, false, true, true><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-      else if (win && !p.x_f32) k_up_stream<kUpBatch, true, false, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-      else if (win) k_up_stream<kUpBatch, true, true, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-      else if (!p.x_f32) k_up_stream<kUpBatch, false, false, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
-      else k_up_stream<kUpBatch, false, true, false><<<up_blocks, kUpW * 64, up_lds, s>>>(p);
+      else if (q3 && q3win && !p.x_f32) launch_kernel(k_up_stream<kUpBatch, true, false, true>, up_blocks, kUpW * 64, up_lds, s, p);
+      else if (q3 && q3win) launch_kernel(k_up_stream<kUpBatch, true, true, true>, up_blocks, kUpW * 64, up_lds, s, p);
+      else if (q3 && !p.x_f32) launch_kernel(k_up_stream<kUpBatch, false, false, true>, up_blocks, kUpW * 64, up_lds, s, p);
+      else if (q3) launch_kernel(k_up_stream<kUpBatch, false, true, true>, up_blocks, kUpW * 64, up_lds, s, p);
+      else if (win && !p.x_f32) launch_kernel(k_up_stream<kUpBatch, true, false, false>, up_blocks, kUpW * 64, up_lds, s, p);
+      else if (win) launch_kernel(k_up_stream<kUpBatch, true, true, false>, up_blocks, kUpW * 64, up_lds, s, p);
+      else if (!p.x_f32) launch_kernel(k_up_stream<kUpBatch, false, false, false>, up_blocks, kUpW * 64, up_lds, s, p);
+      else launch_kernel(k_up_stream<kUpBatch, false, true, false>, up_blocks, kUpW * 64, up_lds, s, p);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
   }
-  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
+  if ((e = stage_open(kStageDown)) != hipSuccess) return e;
   if (d.tokens >= kDecodeGroupedDownMin && grouped_path(d)) {
     // routed and shared down per slot (one output row per dispatch row), then the combine
     if ((e = launch_grouped_down(d, L, a, a.route.desc, s, repeat)) != hipSuccess) return e;
-    if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
-    return launch_combine(d, L, a, s, ev ? ev + 2 : nullptr, repeat);
+    return launch_combine(d, L, a, s, repeat);
   }
   const int n_rows = d.tokens * d.top_k;
   const int max_u = d.n_experts < n_rows ? d.n_experts : n_rows;
@@ -1344,11 +1344,9 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
                           64 + static_cast<size_t>(max_u) * d.tokens * 4;
     if (dq_lds <= kMaxLds) {
       for (int r = 0; r < repeat; ++r) {
-        k_down_q3<<<static_cast<unsigned>(d.hidden / 16), kDqW * 64, dq_lds, s>>>(p);
+        launch_kernel(k_down_q3, static_cast<unsigned>(d.hidden / 16), kDqW * 64, dq_lds, s, p);
         if ((e = hipGetLastError()) != hipSuccess) return e;
       }
-      if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
-      if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return e;
       return hipSuccess;
     }
   }
@@ -1361,15 +1359,13 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
                       d.inter == kStW * kStKB * 128 && d.inter_shared <= kStW * kStKB * 128;
   for (int r = 0; r < repeat; ++r) {
     const unsigned blocks = static_cast<unsigned>(d.hidden / 16);
-    if (staged && q3) k_down_decode_staged<RawQ3><<<blocks, kStW * 64, dn_lds, s>>>(p);
-    else if (staged) k_down_decode_staged<RawFP4><<<blocks, kStW * 64, dn_lds, s>>>(p);
-    else if (q3) k_down_decode<RawQ3><<<blocks, kDownW * 64, 0, s>>>(p);
-    else k_down_decode<RawFP4><<<blocks, kDownW * 64, 0, s>>>(p);
+    if (staged && q3) launch_kernel(k_down_decode_staged<RawQ3>, blocks, kStW * 64, dn_lds, s, p);
+    else if (staged) launch_kernel(k_down_decode_staged<RawFP4>, blocks, kStW * 64, dn_lds, s, p);
+    else if (q3) launch_kernel(k_down_decode<RawQ3>, blocks, kDownW * 64, 0, s, p);
+    else launch_kernel(k_down_decode<RawFP4>, blocks, kDownW * 64, 0, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  // down and combine are one kernel here: both stage events mark its end
-  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
-  if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return e;
+  // down and combine are one kernel here (the combine stage launches nothing)
   return hipSuccess;
 }
 

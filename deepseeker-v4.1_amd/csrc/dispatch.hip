@@ -22,7 +22,7 @@ hipError_t launch_dispatch(const dsk_moe_desc& d, const int32_t* idx, const floa
   const int N = d.tokens * d.top_k;
   const int S = (E <= 512) ? 16 : 8;
   const size_t lds = static_cast<size_t>(S * E + E + 32) * sizeof(int32_t);
-  k_dispatch<<<1, S * 64, lds, s>>>(idx, N, E, d.top_k, bits_for(E), wflat, table, o);
+  launch_kernel(k_dispatch, 1, S * 64, lds, s, idx, N, E, d.top_k, bits_for(E), wflat, table, o);
   return hipGetLastError();
 }
 

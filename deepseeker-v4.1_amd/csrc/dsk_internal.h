@@ -1,6 +1,7 @@
 // Internal declarations shared by the HIP translation units of libdsk_moe.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stddef.h>
@@ -13,6 +14,43 @@ namespace dsk {
 // ---------------------------------------------------------------- errors
 int fail(int code, const char* fmt, ...);   // records the message, returns code
 int hip_check(hipError_t e, const char* what);
+
+// ---------------------------------------------------------------- stage timing
+// The timed forward (dsk_moe_forward_timed) arms a thread-local table of two
+// events per stage.  Every kernel launched through launch_kernel() while a
+// stage is open carries the stage's start event (on its first launch) and
+// its stop event (on every launch, so the last launch's end counts): the
+// events then hold the kernels' own begin / end timestamps, the ones a
+// profiler reports, with no marker packets between the kernels.
+enum StageId { kStageGate = 0, kStageRoute, kStageUp, kStageDown, kStageCombine, kStageCount };
+static_assert(2 * kStageCount == DSK_STAGE_EVENTS, "two events per stage");
+struct StageClock {
+  const hipEvent_t* ev = nullptr;  // 2 * kStageCount events, or null (not timing)
+  int open = -1;                   // stage whose kernels are being launched
+  bool launched = false;           // the open stage has launched a kernel
+};
+extern thread_local StageClock g_stage_clock;
+// Opens `stage` (the next launches belong to it); no-op unless timing.  A
+// stage that launches nothing leaves its events unrecorded.
+hipError_t stage_open(int stage);
+void stage_close();
+
+template <class T> struct same_type { using type = T; };
+
+// Kernel launch (all launches of the library go through here).
+template <typename... P>
+inline hipError_t launch_kernel(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                                typename same_type<P>::type... args) {
+  void* argv[] = {const_cast<void*>(static_cast<const void*>(&args))..., nullptr};
+  hipEvent_t start = nullptr, stop = nullptr;
+  StageClock& c = g_stage_clock;
+  if (c.ev && c.open >= 0) {
+    if (!c.launched) start = c.ev[2 * c.open];
+    stop = c.ev[2 * c.open + 1];
+    c.launched = true;
+  }
+  return hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, argv, lds, s, start, stop, 0);
+}
 
 // ---------------------------------------------------------------- types
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -183,35 +221,34 @@ struct ExpertsArgs {
   DecodeRoute route;
 };
 
-// ev (nullable): 3 events recorded after the gate/up kernel, the down kernel
-// and the combine kernel.
+// Opens the gate/up, down and combine stages as it launches them.
 // repeat: each kernel is launched that many times in a row (timing only).
 hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L,
-                          const ExpertsArgs& a, hipStream_t s, const hipEvent_t* ev, int repeat);
+                          const ExpertsArgs& a, hipStream_t s, int repeat);
 
 hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t s);
 hipError_t launch_rmsnorm(const void* x, const void* res, const float* gamma, int64_t rows, int H, float eps,
                           int dtype, void* h_out, void* y, hipStream_t s);
 
 // Prefill GEMM path (prefill_gemm(d)): tile list, gate/up, down; the caller
-// runs the combine.  ev (nullable): 2 events, after gate/up and after down.
+// runs the combine.  Opens the gate/up and down stages.
 struct PrefillArgs {
   const SlotDesc* desc; const int32_t* active; const int32_t* xrow; const float* wrow;
   const void* x; const void* ws1; const void* ws3; const void* ws2;
   char* ws;
 };
 hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, const PrefillArgs& a,
-                                  hipStream_t s, const hipEvent_t* ev, int repeat);
+                                  hipStream_t s, int repeat);
 
 // Grouped path for batches below the prefill size (bf16 x, shapes that
 // tile): per slot, column tiles of its dispatch rows with only their
 // activation rows staged; the shared expert as a pseudo-slot.  Writes the
-// routed rows y and the shared output ys for launch_combine.  ev (nullable):
-// 2 events, after gate/up and after down.
+// routed rows y and the shared output ys for launch_combine.  Opens the
+// gate/up and down stages.
 bool grouped_path(const dsk_moe_desc& d);
 hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                   const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
-                                  const hipEvent_t* ev, int repeat);
+                                  int repeat);
 // Its kernels one at a time, for the decode pipeline: the routed gate/up
 // alone (from kDecodeGroupedUpMin tokens) and the down (routed rows from h,
 // shared from hs; from kDecodeGroupedDownMin tokens).
@@ -221,23 +258,21 @@ hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, c
 hipError_t launch_grouped_down(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                const SlotDesc* desc, hipStream_t s, int repeat);
 // out[t] = cast(sum of the token's routed rows y in ascending expert id +
-// shared); ev (nullable): 1 event after it.
+// shared); the combine stage.
 hipError_t launch_combine(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
-                          const hipEvent_t* ev, int repeat);
+                          int repeat);
 
 // Decode pipeline (decode_pipeline(d)), four kernels:
 //   launch_gate_scores    gate scores (a.scores);
 //   launch_route_shared   top-k and slot map (a.route) in one block beside the shared
 //                         expert's gate/up (hs);
 //   launch_experts_decode the routed gate/up, then the routed and shared down and the
-//                         combine in one kernel.  ev (nullable): 3 events as for
-//                         launch_experts.
+//                         combine in one kernel (stages as for launch_experts).
 hipError_t launch_gate_scores(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
 hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                hipStream_t s, int repeat);
 hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L,
-                                 const ExpertsArgs& a, hipStream_t s, const hipEvent_t* ev,
-                                 int repeat);
+                                 const ExpertsArgs& a, hipStream_t s, int repeat);
 
 hipError_t launch_fp8_block_dequant(const uint8_t* codes, const uint8_t* scales, int64_t rows, int64_t cols,
                                     void* out, int out_dtype, hipStream_t s);

@@ -494,15 +494,15 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, co
 
 template <int NT, bool XLO>
 hipError_t launch_up(const UpArgs& a, unsigned blocks, bool q3, hipStream_t s) {
-  if (q3) k_up_fp4<NT, XLO, true><<<blocks, kUpWaves * 64, 0, s>>>(a);
-  else k_up_fp4<NT, XLO, false><<<blocks, kUpWaves * 64, 0, s>>>(a);
+  if (q3) launch_kernel(k_up_fp4<NT, XLO, true>, blocks, kUpWaves * 64, 0, s, a);
+  else launch_kernel(k_up_fp4<NT, XLO, false>, blocks, kUpWaves * 64, 0, s, a);
   return hipGetLastError();
 }
 
 template <int NT>
 hipError_t launch_down(const DownArgs& a, unsigned blocks, bool q3, hipStream_t s) {
-  if (q3) k_down_fp4<NT, true><<<blocks, kDownWaves * 64, 0, s>>>(a);
-  else k_down_fp4<NT, false><<<blocks, kDownWaves * 64, 0, s>>>(a);
+  if (q3) launch_kernel(k_down_fp4<NT, true>, blocks, kDownWaves * 64, 0, s, a);
+  else launch_kernel(k_down_fp4<NT, false>, blocks, kDownWaves * 64, 0, s, a);
   return hipGetLastError();
 }
 
@@ -518,34 +518,34 @@ hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t s) {
   const int64_t n16 = static_cast<int64_t>(bytes / 16);
   if (n16 > 0) {
     const int64_t blocks = (n16 + 255) / 256;
-    k_zero_fill<<<static_cast<unsigned>(blocks < 4096 ? blocks : 4096), 256, 0, s>>>(
+    launch_kernel(k_zero_fill, static_cast<unsigned>(blocks < 4096 ? blocks : 4096), 256, 0, s,
         static_cast<u32x4*>(p), n16);
   }
   return hipGetLastError();
 }
 
-// out[t] from the routed rows y and the shared output; ev (nullable): 1 event after it.
+// out[t] from the routed rows y and the shared output (the combine stage).
 hipError_t launch_combine(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
-                          const hipEvent_t* ev, int repeat) {
+                          int repeat) {
   const int T = d.tokens, H = d.hidden, Is = d.inter_shared, k = d.top_k;
   const float* y = reinterpret_cast<const float*>(a.ws + L.y);
   const float* ys = reinterpret_cast<const float*>(a.ws + L.ys);
   dim3 cg(static_cast<unsigned>(T), static_cast<unsigned>((H + 1023) / 1024));
   const int mode = Is > 0 ? kSharedF32 : (a.shared_out ? kSharedExt : kNoShared);
-  hipError_t e = hipSuccess;
+  hipError_t e = stage_open(kStageCombine);
+  if (e != hipSuccess) return e;
   for (int r = 0; r < repeat; ++r) {
     if (d.x_dtype == DSK_DTYPE_F32)
-      k_combine<false><<<cg, 256, 0, s>>>(y, ys, a.shared_out, a.rank, H, k, mode, a.out);
+      launch_kernel(k_combine<false>, cg, 256, 0, s, y, ys, a.shared_out, a.rank, H, k, mode, a.out);
     else
-      k_combine<true><<<cg, 256, 0, s>>>(y, ys, a.shared_out, a.rank, H, k, mode, a.out);
+      launch_kernel(k_combine<true>, cg, 256, 0, s, y, ys, a.shared_out, a.rank, H, k, mode, a.out);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  if (ev) e = hipEventRecord(ev[0], s);
   return e;
 }
 
 hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
-                          hipStream_t s, const hipEvent_t* ev, int repeat) {
+                          hipStream_t s, int repeat) {
   const int T = d.tokens, H = d.hidden, I = d.inter, Is = d.inter_shared, k = d.top_k;
   const int max_slots = (d.n_experts < T * k) ? d.n_experts : T * k;
   const bool x_f32 = d.x_dtype == DSK_DTYPE_F32;
@@ -559,7 +559,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
     int32_t* xr = reinterpret_cast<int32_t*>(a.ws + L.xrow);
     float* wr = reinterpret_cast<float*>(a.ws + L.wrow);
     const int n = T * k > d.n_experts ? T * k : d.n_experts;
-    k_prepare<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(
+    launch_kernel(k_prepare, static_cast<unsigned>((n + 255) / 256), 256, 0, s,
         a.counts, a.offsets, a.perm, a.active, a.weights, a.table, T * k, d.n_experts, k, dd, xr, wr);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     desc = dd; xrow = xr; wrow = wr;
@@ -568,18 +568,19 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
   const uint16_t* xb_lo = nullptr;
   if (prefill_gemm(d)) {
     PrefillArgs pa{desc, a.active, xrow, wrow, a.x, a.ws1, a.ws3, a.ws2, a.ws};
-    if ((e = launch_experts_prefill(d, L, pa, s, ev, repeat)) != hipSuccess) return e;
-    return launch_combine(d, L, a, s, ev ? ev + 2 : nullptr, repeat);
+    if ((e = launch_experts_prefill(d, L, pa, s, repeat)) != hipSuccess) return e;
+    return launch_combine(d, L, a, s, repeat);
   }
   if (grouped_path(d)) {
-    if ((e = launch_experts_grouped(d, L, a, desc, xrow, wrow, s, ev, repeat)) != hipSuccess) return e;
-    return launch_combine(d, L, a, s, ev ? ev + 2 : nullptr, repeat);
+    if ((e = launch_experts_grouped(d, L, a, desc, xrow, wrow, s, repeat)) != hipSuccess) return e;
+    return launch_combine(d, L, a, s, repeat);
   }
+  if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   if (x_f32) {
     uint16_t* hi = reinterpret_cast<uint16_t*>(a.ws + L.xb_hi);
     uint16_t* lo = reinterpret_cast<uint16_t*>(a.ws + L.xb_lo);
     const int64_t n = static_cast<int64_t>(T) * H;
-    k_split_x<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(static_cast<const float*>(a.x), n, hi, lo);
+    launch_kernel(k_split_x, static_cast<unsigned>((n + 255) / 256), 256, 0, s, static_cast<const float*>(a.x), n, hi, lo);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     xb_hi = hi;
     xb_lo = lo;
@@ -603,7 +604,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
     else e = nt == 1 ? launch_up<1, false>(u, up_blocks, q3, s) : nt == 2 ? launch_up<2, false>(u, up_blocks, q3, s) : launch_up<4, false>(u, up_blocks, q3, s);
     if (e != hipSuccess) return e;
   }
-  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
+  if ((e = stage_open(kStageDown)) != hipSuccess) return e;
 
   DownArgs dn{};
   dn.T = T; dn.H = H; dn.I = I; dn.Is = Is;
@@ -619,8 +620,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
     e = nt == 1 ? launch_down<1>(dn, down_blocks, q3, s) : nt == 2 ? launch_down<2>(dn, down_blocks, q3, s) : launch_down<4>(dn, down_blocks, q3, s);
     if (e != hipSuccess) return e;
   }
-  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
-  return launch_combine(d, L, a, s, ev ? ev + 2 : nullptr, repeat);
+  return launch_combine(d, L, a, s, repeat);
 }
 
 }  // namespace dsk

@@ -282,8 +282,8 @@ hipError_t launch_fp8_block_dequant(const uint8_t* codes, const uint8_t* scales,
                                     void* out, int out_dtype, hipStream_t s) {
   const int64_t chunks = rows * (cols / 16);
   if (chunks == 0) return hipSuccess;
-  if (out_dtype == DSK_DTYPE_F32) k_fp8_block_dequant<false><<<grid_for(chunks), kThreads, 0, s>>>(codes, scales, rows, cols, out);
-  else k_fp8_block_dequant<true><<<grid_for(chunks), kThreads, 0, s>>>(codes, scales, rows, cols, out);
+  if (out_dtype == DSK_DTYPE_F32) launch_kernel(k_fp8_block_dequant<false>, grid_for(chunks), kThreads, 0, s, codes, scales, rows, cols, out);
+  else launch_kernel(k_fp8_block_dequant<true>, grid_for(chunks), kThreads, 0, s, codes, scales, rows, cols, out);
   return hipGetLastError();
 }
 
@@ -292,10 +292,10 @@ hipError_t launch_fp4_dequant(const uint8_t* packed, const uint8_t* scales, int6
   int64_t groups = rows * (cols / 32);
   if (groups == 0) return hipSuccess;
   if (out_dtype == DSK_DTYPE_F32)
-    k_fp4_dequant_f32<<<grid_for(groups), kThreads, 0, s>>>(packed, scales, groups,
+    launch_kernel(k_fp4_dequant_f32, grid_for(groups), kThreads, 0, s, packed, scales, groups,
                                                               static_cast<float*>(out));
   else
-    k_fp4_dequant_bf16<<<grid_for(groups), kThreads, 0, s>>>(packed, scales, groups,
+    launch_kernel(k_fp4_dequant_bf16, grid_for(groups), kThreads, 0, s, packed, scales, groups,
                                                                static_cast<uint16_t*>(out));
   return hipGetLastError();
 }
@@ -304,7 +304,7 @@ hipError_t launch_fp4_quantize(const float* w, int64_t rows, int64_t cols, uint8
                                uint8_t* scales, hipStream_t s) {
   int64_t groups = rows * (cols / 32);
   if (groups == 0) return hipSuccess;
-  k_fp4_quantize<<<grid_for(groups), kThreads, 0, s>>>(w, groups, packed, scales);
+  launch_kernel(k_fp4_quantize, grid_for(groups), kThreads, 0, s, w, groups, packed, scales);
   return hipGetLastError();
 }
 
@@ -312,7 +312,7 @@ hipError_t launch_q3_quantize(const float* w, int64_t rows, int64_t cols, uint8_
                               uint16_t* scales, uint16_t* biases, hipStream_t s) {
   int64_t blocks = rows * (cols / 128);
   if (blocks == 0) return hipSuccess;
-  k_q3_quantize<<<grid_for(blocks), kThreads, 0, s>>>(w, blocks, static_cast<int>(cols), packed, scales, biases);
+  launch_kernel(k_q3_quantize, grid_for(blocks), kThreads, 0, s, w, blocks, static_cast<int>(cols), packed, scales, biases);
   return hipGetLastError();
 }
 
@@ -321,7 +321,7 @@ hipError_t launch_q3_dequant(const uint8_t* packed, const uint16_t* scales,
                              int out_dtype, hipStream_t s) {
   int64_t blocks = rows * (cols / 128);
   if (blocks == 0) return hipSuccess;
-  k_q3_dequant<<<grid_for(blocks), kThreads, 0, s>>>(packed, scales, biases, blocks, static_cast<int>(cols),
+  launch_kernel(k_q3_dequant, grid_for(blocks), kThreads, 0, s, packed, scales, biases, blocks, static_cast<int>(cols),
                                                      out_dtype == DSK_DTYPE_BF16, out);
   return hipGetLastError();
 }

@@ -638,8 +638,8 @@ hipError_t grouped_down(const dsk_moe_desc& d, const GroupedArgs& p, hipStream_t
   const unsigned blocks = static_cast<unsigned>(p.dn_shared + max_slots(d) * p.dn_groups);
   const size_t lds = down_lds(d);
   for (int r = 0; r < repeat; ++r) {
-    if (d.quant == DSK_QUANT_Q3) k_down_grouped<RawQ3><<<blocks, kDW * 64, lds, s>>>(p);
-    else k_down_grouped<RawFP4><<<blocks, kDW * 64, lds, s>>>(p);
+    if (d.quant == DSK_QUANT_Q3) launch_kernel(k_down_grouped<RawQ3>, blocks, kDW * 64, lds, s, p);
+    else launch_kernel(k_down_grouped<RawFP4>, blocks, kDW * 64, lds, s, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -650,20 +650,19 @@ hipError_t grouped_down(const dsk_moe_desc& d, const GroupedArgs& p, hipStream_t
 
 hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                   const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
-                                  const hipEvent_t* ev, int repeat) {
+                                  int repeat) {
   const GroupedArgs p = grouped_args(d, L, a, desc, xrow, wrow);
   const unsigned up_blocks = static_cast<unsigned>(p.up_shared + max_slots(d) * p.up_groups);
   const size_t ul = up_lds(d);
   hipError_t e;
+  if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   for (int r = 0; r < repeat; ++r) {
-    if (d.quant == DSK_QUANT_Q3) k_up_grouped<RawQ3><<<up_blocks, kGW * 64, ul, s>>>(p);
-    else k_up_grouped<RawFP4><<<up_blocks, kGW * 64, ul, s>>>(p);
+    if (d.quant == DSK_QUANT_Q3) launch_kernel(k_up_grouped<RawQ3>, up_blocks, kGW * 64, ul, s, p);
+    else launch_kernel(k_up_grouped<RawFP4>, up_blocks, kGW * 64, ul, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
-  if ((e = grouped_down(d, p, s, repeat)) != hipSuccess) return e;
-  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
-  return hipSuccess;
+  if ((e = stage_open(kStageDown)) != hipSuccess) return e;
+  return grouped_down(d, p, s, repeat);
 }
 
 hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
@@ -674,8 +673,8 @@ hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, c
   const unsigned blocks = static_cast<unsigned>(max_slots(d) * p.up_groups);
   const size_t lds = up_lds(d);
   for (int r = 0; r < repeat; ++r) {
-    if (d.quant == DSK_QUANT_Q3) k_up_grouped<RawQ3><<<blocks, kGW * 64, lds, s>>>(p);
-    else k_up_grouped<RawFP4><<<blocks, kGW * 64, lds, s>>>(p);
+    if (d.quant == DSK_QUANT_Q3) launch_kernel(k_up_grouped<RawQ3>, blocks, kGW * 64, lds, s, p);
+    else launch_kernel(k_up_grouped<RawFP4>, blocks, kGW * 64, lds, s, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -103,9 +103,9 @@ hipError_t launch_rmsnorm(const void* x, const void* res, const float* gamma, in
                           int dtype, void* h_out, void* y, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   if (dtype == DSK_DTYPE_BF16)
-    k_rmsnorm<true><<<static_cast<unsigned>(rows), kNormThreads, 0, s>>>(x, res, gamma, H, eps, h_out, y);
+    launch_kernel(k_rmsnorm<true>, static_cast<unsigned>(rows), kNormThreads, 0, s, x, res, gamma, H, eps, h_out, y);
   else
-    k_rmsnorm<false><<<static_cast<unsigned>(rows), kNormThreads, 0, s>>>(x, res, gamma, H, eps, h_out, y);
+    launch_kernel(k_rmsnorm<false>, static_cast<unsigned>(rows), kNormThreads, 0, s, x, res, gamma, H, eps, h_out, y);
   return hipGetLastError();
 }
 

@@ -471,12 +471,12 @@ int prefill_max_tiles(const dsk_moe_desc& d) {
 }
 
 hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, const PrefillArgs& a,
-                                  hipStream_t s, const hipEvent_t* ev, int repeat) {
+                                  hipStream_t s, int repeat) {
   const int T = d.tokens, H = d.hidden, I = d.inter, Is = d.inter_shared;
   const bool q3 = d.quant == DSK_QUANT_Q3;
   const int max_tiles = prefill_max_tiles(d);
   int32_t* tiles = reinterpret_cast<int32_t*>(a.ws + L.pf_tiles);
-  k_pf_tiles<<<1, 1024, 0, s>>>(a.desc, a.active, d.n_experts, T, Is > 0 ? 1 : 0, max_tiles, tiles);
+  launch_kernel(k_pf_tiles, 1, 1024, 0, s, a.desc, a.active, d.n_experts, T, Is > 0 ? 1 : 0, max_tiles, tiles);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
 
@@ -493,23 +493,22 @@ hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, con
   p.y = reinterpret_cast<float*>(a.ws + L.y);
   p.ys = reinterpret_cast<float*>(a.ws + L.ys);
 
+  if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   p.row_tiles = (I > Is ? I : Is) / 128;
   const unsigned up_blocks = static_cast<unsigned>(max_tiles * p.row_tiles);
   for (int r = 0; r < repeat; ++r) {
-    if (q3) k_pf_up<true><<<up_blocks, kPfThreads, kPfLdsBytes, s>>>(p);
-    else k_pf_up<false><<<up_blocks, kPfThreads, kPfLdsBytes, s>>>(p);
+    if (q3) launch_kernel(k_pf_up<true>, up_blocks, kPfThreads, kPfLdsBytes, s, p);
+    else launch_kernel(k_pf_up<false>, up_blocks, kPfThreads, kPfLdsBytes, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return e;
-
+  if ((e = stage_open(kStageDown)) != hipSuccess) return e;
   p.row_tiles = H / kPfRows;
   const unsigned down_blocks = static_cast<unsigned>(max_tiles * p.row_tiles);
   for (int r = 0; r < repeat; ++r) {
-    if (q3) k_pf_down<true><<<down_blocks, kPfThreads, kPfLdsBytes, s>>>(p);
-    else k_pf_down<false><<<down_blocks, kPfThreads, kPfLdsBytes, s>>>(p);
+    if (q3) launch_kernel(k_pf_down<true>, down_blocks, kPfThreads, kPfLdsBytes, s, p);
+    else launch_kernel(k_pf_down<false>, down_blocks, kPfThreads, kPfLdsBytes, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return e;
   return hipSuccess;
 }
 

@@ -233,10 +233,10 @@ hipError_t launch_gate_wide(const dsk_moe_desc& d, const GateArgs& g, hipStream_
                                                 ((d.n_experts + kGwExp - 1) / kGwExp));
   const bool xb = d.x_dtype == DSK_DTYPE_BF16, wb = d.gate_dtype == DSK_DTYPE_BF16;
   const size_t lds = 2 * static_cast<size_t>(kGwTok * 256 * (xb ? 2 : 4) + kGwExp * 256 * (wb ? 2 : 4));
-  if (xb && wb) k_gate_wide<true, true><<<blocks, kGwThreads, lds, s>>>(g);
-  else if (xb) k_gate_wide<true, false><<<blocks, kGwThreads, lds, s>>>(g);
-  else if (wb) k_gate_wide<false, true><<<blocks, kGwThreads, lds, s>>>(g);
-  else k_gate_wide<false, false><<<blocks, kGwThreads, lds, s>>>(g);
+  if (xb && wb) launch_kernel(k_gate_wide<true, true>, blocks, kGwThreads, lds, s, g);
+  else if (xb) launch_kernel(k_gate_wide<true, false>, blocks, kGwThreads, lds, s, g);
+  else if (wb) launch_kernel(k_gate_wide<false, true>, blocks, kGwThreads, lds, s, g);
+  else launch_kernel(k_gate_wide<false, false>, blocks, kGwThreads, lds, s, g);
   return hipGetLastError();
 }
 
@@ -248,10 +248,10 @@ hipError_t launch_gate(const dsk_moe_desc& d, const GateArgs& g, hipStream_t s) 
   size_t lds = (kSegments * TW * EW + 4) * sizeof(float);
   if (kFused) lds += static_cast<size_t>(4 * d.n_experts + d.n_experts + 32) * sizeof(int32_t);
   const bool xb = d.x_dtype == DSK_DTYPE_BF16, wb = d.gate_dtype == DSK_DTYPE_BF16;
-  if (xb && wb) k_gate<TW, EW, true, true, kFused><<<blocks, 256, lds, s>>>(g);
-  else if (xb) k_gate<TW, EW, true, false, kFused><<<blocks, 256, lds, s>>>(g);
-  else if (wb) k_gate<TW, EW, false, true, kFused><<<blocks, 256, lds, s>>>(g);
-  else k_gate<TW, EW, false, false, kFused><<<blocks, 256, lds, s>>>(g);
+  if (xb && wb) launch_kernel(k_gate<TW, EW, true, true, kFused>, blocks, 256, lds, s, g);
+  else if (xb) launch_kernel(k_gate<TW, EW, true, false, kFused>, blocks, 256, lds, s, g);
+  else if (wb) launch_kernel(k_gate<TW, EW, false, true, kFused>, blocks, 256, lds, s, g);
+  else launch_kernel(k_gate<TW, EW, false, false, kFused>, blocks, 256, lds, s, g);
   return hipGetLastError();
 }
 
@@ -271,8 +271,9 @@ hipError_t launch_route_unfused(const dsk_moe_desc& d, const GateArgs& g, hipStr
                  : (d.tokens >= 16)              ? launch_gate<4, 4, false>(d, g, s)
                                                  : launch_gate<1, 1, false>(d, g, s);
   if (e != hipSuccess) return e;
+  if ((e = stage_open(kStageRoute)) != hipSuccess) return e;
   const unsigned blocks = static_cast<unsigned>((d.tokens + 3) / 4);
-  k_topk<<<blocks, 256, 0, s>>>(g.scores, g.bias, d.tokens, d.n_experts, d.top_k, d.route_scale,
+  launch_kernel(k_topk, blocks, 256, 0, s, g.scores, g.bias, d.tokens, d.n_experts, d.top_k, d.route_scale,
                                 g.idx, g.weights);
   return hipGetLastError();
 }
@@ -298,7 +299,7 @@ hipError_t launch_route_dispatch(const dsk_moe_desc& d, const RouteArgs& a, hipS
   if (d.tokens <= kFusedMaxTokens) {
     return d.tokens == 1 ? launch_gate<1, 4, true>(d, g, s) : launch_gate<4, 1, true>(d, g, s);
   }
-  hipError_t e = launch_route_unfused(d, g, s);
+  hipError_t e = launch_route_unfused(d, g, s);   // opens the route stage after the gate
   if (e != hipSuccess) return e;
   return launch_dispatch(d, a.idx, a.weights, a.table, a.out, s);
 }

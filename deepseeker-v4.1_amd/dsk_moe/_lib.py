@@ -25,7 +25,7 @@ QUANT_FP4 = 0
 QUANT_Q3 = 1
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
-STAGE_EVENTS = 6
+STAGE_EVENTS = 10
 
 # Every function the header declares: name -> (restype, argtypes).
 _vp = ctypes.c_void_p

@@ -142,20 +142,24 @@ int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w,
                     int32_t* idx, float* weights, void* workspace,
                     size_t workspace_bytes, void* stream);
 
-/* dsk_moe_forward that also records DSK_STAGE_EVENTS hipEvent_t (events[i],
- * created by the caller) on the stream: before the router, after the gate
- * scores (decode pipeline; the general path's router also dispatches, so
- * there it is the same point as the next), after the top-k and dispatch,
- * after the gate/up kernel, after the down kernel and after the combine
- * (the decode pipeline combines inside the down kernel: same point).  Each
- * stage's kernels are launched `repeat` times in a row between its events
- * (every stage recomputes its outputs from its inputs, so the result is that
- * of one forward); a stage's duration is its event interval / repeat.  Each
- * event is a marker packet that itself takes GPU time (a few microseconds on
- * MI355X): time an empty pair of events to subtract it.
+/* dsk_moe_forward that times its five stages with DSK_STAGE_EVENTS hipEvent_t
+ * created by the caller: events[2i] and events[2i+1] receive the begin
+ * timestamp of stage i's first kernel and the end timestamp of its last
+ * kernel (the kernels are launched with hipExtLaunchKernel carrying the
+ * events, so no marker packet runs between kernels and the interval is the
+ * kernels' own execution time, as a profiler reports it).  Stages: 0 gate
+ * scores (the fused router of up to 8 tokens also selects and dispatches
+ * here), 1 top-k and dispatch (the decode pipeline: top-k and slot map beside
+ * the shared expert's gate/up), 2 gate/up, 3 down, 4 combine.  A stage that
+ * launches no kernel (the decode pipeline of 1-2 tokens combines inside its
+ * down kernel) leaves its two events unrecorded.  Each
+ * stage's kernels are launched `repeat` times in a row (every stage recomputes
+ * its outputs from its inputs, so the result is that of one forward).
+ * Create the events with hipEventDisableSystemFence where no system-scope
+ * release is wanted at a stop timestamp.
  * No counterpart in the reference: it is for callers that time the stages
  * (the benchmark). */
-#define DSK_STAGE_EVENTS 6
+#define DSK_STAGE_EVENTS 10
 int dsk_moe_forward_timed(const dsk_moe_desc* d, const void* x, const void* gate_w,
                           const float* gate_b, const dsk_expert_ptrs* table,
                           const void* ws1, const void* ws3, const void* ws2,

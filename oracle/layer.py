@@ -100,17 +100,21 @@ def shared_forward(x32: torch.Tensor, ws1, ws3, ws2, limit: float) -> torch.Tens
     return h @ w2.T
 
 
-def moe_forward(x, gate_w, gate_b, bank: ExpertBank, shared, spec: LayerSpec) -> dict:
+def moe_forward(x, gate_w, gate_b, bank: ExpertBank, shared, spec: LayerSpec,
+                routing: tuple | None = None) -> dict:
     """Whole layer.  ``x``: torch [T, H] bf16 or float32 (CPU); ``shared`` is
     ``(ws1, ws3, ws2)`` bf16 tensors or None.  Returns a dict with ``out``
     (x.dtype), ``y_ref`` (float32 before the final cast), ``idx``, ``w``,
     ``scores``, ``counts``, ``offsets``, ``perm``, ``rank``.
+    ``routing``: the ``(idx, w, scores, logits)`` of ``router.route`` on these
+    inputs when the caller already has it (it is not recomputed).
     """
     xt = x.detach().to("cpu")
     x32 = xt.to(torch.float32)
-    idx, w, s, _ = R.route(x32.numpy(), _as_f32_torch(gate_w).numpy(),
-                           _as_f32_torch(gate_b).numpy(), spec.k,
-                           spec.score_func, spec.route_scale)
+    if routing is None:
+        routing = R.route(x32.numpy(), _as_f32_torch(gate_w).numpy(), _as_f32_torch(gate_b).numpy(),
+                          spec.k, spec.score_func, spec.route_scale)
+    idx, w, s, _ = routing
     counts, offsets, perm, rank = D.dispatch(idx, spec.E)
     t = x32.shape[0]
     acc = torch.zeros((t, spec.H), dtype=torch.float32)
