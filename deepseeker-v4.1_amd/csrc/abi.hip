@@ -205,27 +205,39 @@ int dsk_experts(const dsk_moe_desc* d, const dsk_expert_ptrs* table, const void*
                    "dsk_experts launch");
 }
 
-static int forward_impl(const dsk_moe_desc* d, const void* x, const void* gate_w,
-                        const float* gate_b, const dsk_expert_ptrs* table, const void* ws1,
-                        const void* ws3, const void* ws2, const void* shared_out, void* out,
-                        int32_t* idx, float* weights, void* workspace, size_t workspace_bytes,
-                        void* stream, void* const* events, int repeat) {
+}  // extern "C"
+
+int dsk::check_forward(const dsk_moe_desc* d, const void* x, const void* gate_w,
+                       const float* gate_b, const dsk_expert_ptrs* table, const void* ws1,
+                       const void* ws3, const void* ws2, const void* shared_out, void* out,
+                       const void* workspace, bool own_scratch, void* const* events, int repeat) {
   int rc = check_expert_desc(d);
   if (rc) return rc;
-  if (!x || !gate_w || !gate_b || !table || !out || !workspace)
+  if (!x || !gate_w || !gate_b || !table || !out || (!workspace && !own_scratch))
     return fail(DSK_EINVAL, "dsk_moe_forward: NULL pointer argument");
   if (d->inter_shared > 0 && (!ws1 || !ws3 || !ws2))
     return fail(DSK_EINVAL, "dsk_moe_forward: shared expert weights are NULL but inter_shared=%d",
                 d->inter_shared);
   if (shared_out && !aligned(shared_out, 16))
     return fail(DSK_EALIGN, "dsk_moe_forward: shared_out must be 16-byte aligned");
-  if (!aligned(x, 16) || !aligned(gate_w, 16) || !aligned(out, 16) || !aligned(workspace, 256) ||
+  if (!aligned(x, 16) || !aligned(gate_w, 16) || !aligned(out, 16) || (!own_scratch && !aligned(workspace, 256)) ||
       (d->inter_shared > 0 && (!aligned(ws1, 16) || !aligned(ws3, 16) || !aligned(ws2, 16))))
     return fail(DSK_EALIGN, "dsk_moe_forward: x/gate_w/out/shared need 16-byte, workspace 256-byte alignment");
   if (events)
     for (int i = 0; i < DSK_STAGE_EVENTS; ++i)
       if (!events[i]) return fail(DSK_EINVAL, "dsk_moe_forward_timed: event %d is NULL", i);
   if (repeat < 1 || repeat > 1000) return fail(DSK_EINVAL, "repeat=%d must be in [1, 1000]", repeat);
+  return DSK_OK;
+}
+
+int dsk::forward_layer(const dsk_moe_desc* d, const void* x, const void* gate_w,
+                       const float* gate_b, const dsk_expert_ptrs* table, const void* ws1,
+                       const void* ws3, const void* ws2, const void* shared_out, void* out,
+                       int32_t* idx, float* weights, void* workspace, size_t workspace_bytes,
+                       void* stream, void* const* events, int repeat) {
+  int rc = check_forward(d, x, gate_w, gate_b, table, ws1, ws3, ws2, shared_out, out, workspace, false, events,
+                         repeat);
+  if (rc) return rc;
   const Workspace L = workspace_layout(*d);
   if (workspace_bytes < L.total)
     return fail(DSK_ESPACE, "workspace %zu bytes < required %zu", workspace_bytes, L.total);
@@ -279,12 +291,14 @@ static int forward_impl(const dsk_moe_desc* d, const void* x, const void* gate_w
   return rc;
 }
 
+extern "C" {
+
 int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, const float* gate_b,
                     const dsk_expert_ptrs* table, const void* ws1, const void* ws3,
                     const void* ws2, const void* shared_out, void* out, int32_t* idx,
                     float* weights, void* workspace, size_t workspace_bytes, void* stream) {
-  return forward_impl(d, x, gate_w, gate_b, table, ws1, ws3, ws2, shared_out, out, idx, weights,
-                      workspace, workspace_bytes, stream, nullptr, 1);
+  return forward_layer(d, x, gate_w, gate_b, table, ws1, ws3, ws2, shared_out, out, idx, weights,
+                       workspace, workspace_bytes, stream, nullptr, 1);
 }
 
 int dsk_moe_forward_timed(const dsk_moe_desc* d, const void* x, const void* gate_w,
@@ -294,8 +308,8 @@ int dsk_moe_forward_timed(const dsk_moe_desc* d, const void* x, const void* gate
                           size_t workspace_bytes, void* stream, void* const* events,
                           int32_t repeat) {
   if (!events) return fail(DSK_EINVAL, "dsk_moe_forward_timed: events is NULL");
-  return forward_impl(d, x, gate_w, gate_b, table, ws1, ws3, ws2, shared_out, out, idx, weights,
-                      workspace, workspace_bytes, stream, events, repeat);
+  return forward_layer(d, x, gate_w, gate_b, table, ws1, ws3, ws2, shared_out, out, idx, weights,
+                       workspace, workspace_bytes, stream, events, repeat);
 }
 
 int dsk_fp4_dequant(const uint8_t* packed, const uint8_t* scales, int64_t rows, int64_t cols,

@@ -227,6 +227,19 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L,
                           const ExpertsArgs& a, hipStream_t s, int repeat);
 
 hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t s);
+
+// The whole layer (dsk_moe_forward / _timed / _noalloc): check_forward validates
+// every argument on the host (DSK_OK or a DSK_E* code with the message set;
+// own_scratch: the library's scratch stands in for the caller's workspace);
+// forward_layer validates, then launches on `stream` into `workspace`.
+int check_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, const float* gate_b,
+                  const dsk_expert_ptrs* table, const void* ws1, const void* ws3, const void* ws2,
+                  const void* shared_out, void* out, const void* workspace, bool own_scratch,
+                  void* const* events, int repeat);
+int forward_layer(const dsk_moe_desc* d, const void* x, const void* gate_w, const float* gate_b,
+                  const dsk_expert_ptrs* table, const void* ws1, const void* ws3, const void* ws2,
+                  const void* shared_out, void* out, int32_t* idx, float* weights, void* workspace,
+                  size_t workspace_bytes, void* stream, void* const* events, int repeat);
 hipError_t launch_rmsnorm(const void* x, const void* res, const float* gamma, int64_t rows, int H, float eps,
                           int dtype, void* h_out, void* y, hipStream_t s);
 

@@ -26,6 +26,7 @@ QUANT_Q3 = 1
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
 STAGE_EVENTS = 10
+SCRATCH_BYTES = 32 << 20
 
 # Every function the header declares: name -> (restype, argtypes).
 _vp = ctypes.c_void_p
@@ -63,6 +64,8 @@ SIGNATURES = {
                                        _vp, _vp, _vp, _sz, _vp]),
     "dsk_moe_forward_timed": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                              _vp, _vp, _vp, _sz, _vp, _vp, _i32]),
+    "dsk_moe_forward_noalloc": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                               _vp, _vp, _vp]),
     "dsk_workspace_init": (ctypes.c_int, [_vp, _sz, _vp]),
     "dsk_fp4_dequant": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _i32, _vp]),
     "dsk_fp4_quantize": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),

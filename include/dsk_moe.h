@@ -167,6 +167,25 @@ int dsk_moe_forward_timed(const dsk_moe_desc* d, const void* x, const void* gate
                           void* workspace, size_t workspace_bytes, void* stream,
                           void* const* events, int32_t repeat);
 
+/* Whole layer as dsk_moe_forward, on the library's own scratch memory instead
+ * of a caller workspace: it allocates nothing (no hipMalloc, hipFree or
+ * allocating library call).  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Each GPU the
+ * library runs on holds one scratch array of DSK_SCRATCH_BYTES for the life
+ * of the process (its device address is looked up on the first call on that
+ * GPU); a call whose dsk_workspace_size exceeds it fails with DSK_ESPACE
+ * before any launch (e.g. the full-size 256-expert layer up to ~128 tokens
+ * fits).  All calls on one GPU share that array and it keeps the last call's
+ * contents: calls that overlap in time on one GPU (several streams or host
+ * threads) race, and the caller must order them. */
+#define DSK_SCRATCH_BYTES (32u << 20)
+int dsk_moe_forward_noalloc(const dsk_moe_desc* d, const void* x, const void* gate_w,
+                            const float* gate_b, const dsk_expert_ptrs* table,
+                            const void* ws1, const void* ws3, const void* ws2,
+                            const void* shared_out, void* out, int32_t* idx, float* weights,
+                            void* stream);
+
 /* FP4 dequant: replaces metal_dequant / the Metal e2m1 kernels
  * (src/deepseeker/metal_fp4.py:28-66, 139-155) and dequant_fp4_rowmajor
  * (src/deepseeker/mlx_weights.py:148-166).  [rows, cols] FP4 role -> out
