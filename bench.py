@@ -7,25 +7,37 @@ of 2048, FP4 e2m1/E8M0 routed weights quantised from N(0, 0.02), sigmoid gate
 with route scale 2.5, B = 1 token of bf16 N(0, 1).  All weights are resident
 in HBM before timing.  A step is one layer forward; steps rotate over
 ``--layers`` independently drawn layers and ``--inputs`` token batches, so
-that consecutive steps read different experts (more than the 256 MB
-Infinity Cache per cycle).
+consecutive steps read different experts (each cycle moves more than the
+256 MB Infinity Cache).
 
-Prints ONE JSON line: tokens/s of the layer (the metric), the roofline of
-the dominant kernel (the routed + shared gate/up kernel: algorithmic bytes
-per launch over its HIP-event-timed average duration), and a CPU baseline
-(the oracle, timed on a bounded sample on this host's cores).
+``value`` is tokens/s over exactly ``--steps`` timed steps (wall clock,
+synchronised on both sides).  Kernel times come from a separate run of
+``--timed-steps`` steps of the same rotation through
+``dsk_moe_forward_timed``: every stage's kernels carry HIP events as their
+own begin / end timestamps (hipExtLaunchKernel), the durations a profiler
+reports; medians, p10 and p90 over those steps are printed.
 
-    python bench.py [--steps K] [--warmup W] [--tokens T] [--no-sweep] [--no-cpu]
-    python bench.py --mode copy --bytes N      # plain copy kernel of known size
+Prints ONE JSON line: the metric, the roofline of the routed-expert stage
+(routed gate/up + down kernels: routed-expert bytes / their time, the
+primary decode fraction), each kernel's algorithmic bytes and fraction, the
+whole layer's fraction, the measured copy / GEMM peaks of this box, a sweep
+of the other batch sizes, and CPU baselines (the oracle on a bounded sample
+of each workload, on this host's cores).
+
+    python bench.py [--steps K] [--warmup W] [--tokens T] [--quant fp4|q3] [--zipf S]
+                    [--no-sweep] [--no-cpu]
+    python bench.py --mode copy  --bytes N    # device copy of known size (bandwidth, counter scale)
+    python bench.py --mode read  --bytes N    # streaming read (sum) of N bytes
+    python bench.py --mode mfma               # bf16 GEMM 8192^3, random and constant operands
 """
 
 from __future__ import annotations
 
 import argparse
+import concurrent.futures as cf
 import ctypes
 import json
 import os
-import platform
 import sys
 import time
 from pathlib import Path
@@ -44,44 +56,51 @@ from dsk_moe import synth as gsynth  # noqa: E402
 from dsk_moe.ops import make_desc, ptr, stream_of, workspace  # noqa: E402
 
 METRIC = "MoE-layer tokens/s at B=1/64/4096; % of HBM GB/s (decode) / MFMA peak (prefill)"
-PEAK_HBM = 8.0e12          # MI355X HBM3E, bytes/s
-PEAK_BF16 = 2.5e15         # MI355X dense bf16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12          # MI355X HBM3E, bytes/s (published)
+PEAK_BF16 = 2.5e15         # MI355X dense bf16 MFMA, FLOP/s (published)
 H, E, K_TOP, I, IS = 4096, 256, 8, 2048, 2048
-SPIN_CYCLES = 50_000_000   # head-start kernel before the event-timed launches (~20 ms)
+SPIN_CYCLES = 50_000_000   # head-start kernel before each chunk of timed steps (~20 ms)
+STAGES = ("gate", "route", "gate_up", "down", "combine")
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
 
 
 # ------------------------------------------------------------------ HIP events
 class HipEvents:
-    """Raw hipEvent_t objects (the library records them on the layer's stream)."""
+    """Raw hipEvent_t objects handed to dsk_moe_forward_timed."""
 
     def __init__(self, n: int):
         self.hip = ctypes.CDLL("libamdhip64.so")
-        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
         self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
                                                  ctypes.c_void_p]
-        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
         self.ev = []
         for _ in range(n):
             h = ctypes.c_void_p()
-            if self.hip.hipEventCreate(ctypes.byref(h)) != 0:
-                raise RuntimeError("hipEventCreate failed")
+            if self.hip.hipEventCreateWithFlags(ctypes.byref(h), HIP_EVENT_DISABLE_SYSTEM_FENCE) != 0:
+                raise RuntimeError("hipEventCreateWithFlags failed")
             self.ev.append(h)
 
     def array(self, start: int, n: int):
         return (ctypes.c_void_p * n)(*[e.value for e in self.ev[start:start + n]])
 
-    def record(self, i: int, stream: ctypes.c_void_p) -> None:
-        if self.hip.hipEventRecord(self.ev[i], stream) != 0:
-            raise RuntimeError("hipEventRecord failed")
-
     def ms(self, a: int, b: int) -> float:
+        """Elapsed ms from event a to event b; NaN when either was never recorded
+        (a stage that launched no kernel)."""
         out = ctypes.c_float()
-        if self.hip.hipEventElapsedTime(ctypes.byref(out), self.ev[a], self.ev[b]) != 0:
-            raise RuntimeError("hipEventElapsedTime failed")
+        rc = self.hip.hipEventElapsedTime(ctypes.byref(out), self.ev[a], self.ev[b])
+        if rc != 0:
+            self.hip.hipGetLastError()        # the failed query must not surface in a later HIP call
+            return float("nan")
         return float(out.value)
 
+    def close(self) -> None:
+        for e in self.ev:
+            self.hip.hipEventDestroy(e)
+        self.ev = []
 
-# ------------------------------------------------------------------ byte/flop models
+
+# ------------------------------------------------------------------ byte / flop models
 def fp4_role_bytes(n: int, k: int) -> int:
     return n * k // 2 + n * k // 32
 
@@ -90,99 +109,165 @@ def q3_role_bytes(n: int, k: int) -> int:
     return n * k * 3 // 8 + 2 * (n * k // 64) * 2                 # codes + fp16 scale + fp16 bias
 
 
+def role_bytes(n: int, k: int, quant: str) -> int:
+    return q3_role_bytes(n, k) if quant == "q3" else fp4_role_bytes(n, k)
+
+
 def expert_bytes(quant: str = "fp4") -> int:
-    if quant == "q3":
-        return 2 * q3_role_bytes(I, H) + q3_role_bytes(H, I)    # 11,010,048 at the full shape
-    return 2 * fp4_role_bytes(I, H) + fp4_role_bytes(H, I)      # 13,369,344 at the full shape
+    """13,369,344 (FP4) / 11,010,048 (q3) at the full shape."""
+    return 2 * role_bytes(I, H, quant) + role_bytes(H, I, quant)
 
 
-def up_kernel_bytes(u: int, t: int, quant: str = "fp4") -> int:
-    """Algorithmic HBM bytes of one routed gate/up launch (the decode path's
-    k_up_stream): routed w1+w3 of the u active experts, x, and the h planes
-    written (bf16 hi and lo)."""
-    role = q3_role_bytes(I, H) if quant == "q3" else fp4_role_bytes(I, H)
-    return u * 2 * role + t * H * 2 + t * K_TOP * I * 4
+def stage_bytes(u: int, t: int, quant: str) -> dict:
+    """Algorithmic HBM bytes of each decode-pipeline stage for u active experts, t tokens:
+    gate (fp32 gate + x + scores), route (shared w1/w3 + scores + h_s planes), gate/up
+    (routed w1/w3 + x + h planes), down (routed w2 + shared w2 + h / h_s planes + out)."""
+    return {"gate": E * H * 4 + t * H * 2 + t * E * 4,
+            "route": 2 * IS * H * 2 + t * E * 4 + t * IS * 4,
+            "gate_up": u * 2 * role_bytes(I, H, quant) + t * H * 2 + t * K_TOP * I * 4,
+            "down": u * role_bytes(H, I, quant) + H * IS * 2 + t * K_TOP * I * 4 + t * IS * 4 + t * H * 2,
+            "combine": 0}
 
 
 def layer_bytes(u: int, t: int, quant: str = "fp4") -> int:
     return u * expert_bytes(quant) + 3 * IS * H * 2 + E * H * 4 + 2 * t * H * 2
 
 
-PREFILL_MIN_TOKENS = 128     # batches from this size run the expert products as MFMA GEMM tiles
-
-
 def layer_flops(t: int) -> int:
     return 2 * t * K_TOP * 3 * H * I + 2 * t * 3 * H * IS + 2 * t * H * E
 
 
-def measured_traffic(kernel: str, workload: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
-    measurement (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), or
-    None when no measurement for this kernel on this workload exists."""
+def up_flops(t: int) -> int:
+    """gate/up GEMM of the prefill path: routed (t*k rows) and shared (t rows) w1, w3."""
+    return 2 * t * K_TOP * 2 * H * I + 2 * t * 2 * H * IS
+
+
+PREFILL_MIN_TOKENS = 128     # batches from this size run the expert products as MFMA GEMM tiles
+
+
+def measured_traffic(kernels: list[str], workload: str):
+    """HBM bytes per launch of `kernels` (summed) from the committed rocprofv3 --pmc
+    measurement (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), or None
+    when one of them has no measurement on this workload."""
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
         return None
-    entry = json.loads(path.read_text()).get(kernel)
-    if not entry or entry.get("workload") != workload:
+    table = json.loads(path.read_text())
+    total = 0
+    for k in kernels:
+        entry = table.get(k)
+        if not entry or entry.get("workload") != workload:
+            return None
+        total += int(entry["bytes_per_launch"])
+    return total
+
+
+def pct(a: np.ndarray) -> dict | None:
+    """median / p10 / p90 (None for a stage that launched no kernel)."""
+    a = np.asarray(a, dtype=np.float64)
+    if np.isnan(a).all():
         return None
-    return int(entry["bytes_per_launch"])
+    return {"median": round(float(np.nanmedian(a)), 2), "p10": round(float(np.nanpercentile(a, 10)), 2),
+            "p90": round(float(np.nanpercentile(a, 90)), 2)}
 
 
 # ------------------------------------------------------------------ timed forward
-def forward_timed(layer, x, out, idx, w, ev: HipEvents, slot: int, repeat: int):
+def forward_timed(layer, x, out, idx, w, ev: HipEvents, slot: int):
     dev = x.device
-    desc = make_desc(tokens=x.shape[0], hidden=H, n_experts=E, top_k=K_TOP, inter=I,
-                     inter_shared=IS, score_func=layer.score_func, quant=layer.bank.quant,
-                     x_dtype=x.dtype, gate_dtype=layer.gate_w.dtype,
-                     route_scale=layer.route_scale, limit=layer.limit)
+    desc = make_desc(tokens=x.shape[0], hidden=layer.gate_w.shape[1], n_experts=layer.bank.n_experts,
+                     top_k=layer.top_k, inter=layer.bank.inter, inter_shared=layer.shared.inter,
+                     score_func=layer.score_func, quant=layer.bank.quant, x_dtype=x.dtype,
+                     gate_dtype=layer.gate_w.dtype, route_scale=layer.route_scale, limit=layer.limit)
     ws = workspace(desc, dev)
     s = layer.shared
     _lib.call("dsk_moe_forward_timed", ctypes.byref(desc), ptr(x), ptr(layer.gate_w),
               ptr(layer.gate_b), ptr(layer.bank.table), ptr(s.w1), ptr(s.w3), ptr(s.w2),
               ptr(None), ptr(out), ptr(idx), ptr(w), ptr(ws), ws.numel(), stream_of(dev),
-              ev.array(slot * _lib.STAGE_EVENTS, _lib.STAGE_EVENTS), repeat)
+              ev.array(slot * _lib.STAGE_EVENTS, _lib.STAGE_EVENTS), 1)
 
 
-def run_workload(layers, t: int, steps: int, warmup: int, n_inputs: int, seed: int = 123):
-    """Time `steps` layer forwards at batch t; returns a dict of measurements."""
+def run_workload(layers, t: int, steps: int, warmup: int, n_inputs: int, timed_steps: int,
+                 seed: int = 123) -> dict:
+    """`steps` back-to-back layer forwards at batch t (wall clock), then `timed_steps`
+    forwards of the same rotation with kernel-timestamp events per stage."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(seed + t)
     xs = [torch.randn((t, H), generator=g, device=dev).to(torch.bfloat16) for _ in range(n_inputs)]
     out = torch.empty((t, H), dtype=torch.bfloat16, device=dev)
-    idxs = [torch.empty((t, K_TOP), dtype=torch.int32, device=dev) for _ in range(steps)]
-    ws_ = torch.empty((t, K_TOP), dtype=torch.float32, device=dev)
+    k = layers[0].top_k
+    idx = torch.empty((t, k), dtype=torch.int32, device=dev)
+    wts = torch.empty((t, k), dtype=torch.float32, device=dev)
     nl = len(layers)
     for s in range(warmup):
         layers[s % nl](xs[s % n_inputs], out=out)
     torch.cuda.synchronize()
-    # 1) throughput: back-to-back layers, no events inside the timed region
     t0 = time.perf_counter()
     for s in range(steps):
-        layers[s % nl](xs[s % n_inputs], out=out, idx=idxs[s])
+        layers[s % nl](xs[s % n_inputs], out=out)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # 2) stage timing: one launch per stage, events between the stages, same
-    # rotation as above (cold weights).  A spin kernel first gives the GPU a
-    # head start so that the host has queued every launch and event before the
-    # GPU reaches it: the events then time GPU work only, not submission.
-    # Each recorded event also costs GPU time (a marker packet): an empty pair
-    # of events after every step measures it, and it is subtracted from the
-    # stage times.
-    n_t = min(steps, 40)
+    # kernel timing: chunks of 40 steps, each after a spin kernel that gives the host a
+    # head start, so every launch is queued before the GPU reaches it
     ne = _lib.STAGE_EVENTS
-    ev = HipEvents(n_t * ne)
-    mk = HipEvents(2 * n_t)
-    stream = stream_of(dev)
-    torch.cuda._sleep(SPIN_CYCLES)
-    for s in range(n_t):
-        forward_timed(layers[s % nl], xs[s % n_inputs], out, idxs[s], ws_, ev, s, 1)
-        mk.record(2 * s, stream)
-        mk.record(2 * s + 1, stream)
-    torch.cuda.synchronize()
-    st = np.array([[ev.ms(s * ne + i, s * ne + i + 1) for i in range(5)] for s in range(n_t)])
-    marker = np.array([mk.ms(2 * s, 2 * s + 1) for s in range(n_t)])
-    uniq = [len(torch.unique(ix).tolist()) for ix in idxs[:n_t]]
-    return {"wall_s": wall, "stage_ms": st, "marker_ms": marker, "unique": uniq}
+    stage_ms, layer_ms, uniq = [], [], []
+    chunk = 40
+    for c0 in range(0, timed_steps, chunk):
+        n = min(chunk, timed_steps - c0)
+        ev = HipEvents(n * ne)
+        idxs = [torch.empty((t, k), dtype=torch.int32, device=dev) for _ in range(n)]
+        torch.cuda._sleep(SPIN_CYCLES)
+        for i in range(n):
+            s = c0 + i
+            forward_timed(layers[s % nl], xs[s % n_inputs], out, idxs[i], wts, ev, i)
+        torch.cuda.synchronize()
+        for i in range(n):
+            row = [ev.ms(i * ne + 2 * j, i * ne + 2 * j + 1) for j in range(len(STAGES))]
+            stage_ms.append(row)
+            # the layer's kernel time: the stages' kernels back to back (launching with
+            # timestamp events spaces the kernels out, so the span between the first
+            # begin and the last end is not the layer's time in an untimed run)
+            layer_ms.append(float(np.nansum(row)))
+            uniq.append(len(torch.unique(idxs[i]).tolist()))
+        ev.close()
+    return {"wall_s": wall, "stage_us": np.array(stage_ms) * 1e3, "layer_us": np.array(layer_ms) * 1e3,
+            "unique": np.array(uniq)}
+
+
+def decode_summary(r: dict, t: int, quant: str, steps: int) -> dict:
+    """Per-stage kernel times and fractions of the decode / grouped path."""
+    st, u = r["stage_us"], r["unique"]
+    sb = [stage_bytes(int(x), t, quant) for x in u]
+    kern = {}
+    for j, name in enumerate(STAGES):
+        b = np.array([s[name] for s in sb], dtype=np.float64)
+        us = st[:, j]
+        e = {"us": pct(us)}
+        if b.sum() > 0 and not np.isnan(us).any():
+            e["bytes_mean"] = int(b.mean())
+            e["hbm_frac"] = round(float(b.sum() / (us.sum() * 1e-6)) / PEAK_HBM, 4)
+        kern[name] = e
+    routed = u.astype(np.float64) * expert_bytes(quant)
+    routed_us = st[:, 2] + st[:, 3]
+    lb = np.array([layer_bytes(int(x), t, quant) for x in u], dtype=np.float64)
+    wall_step = r["wall_s"] / steps
+    return {"stages": kern,
+            "routed_stage": {"bytes_mean": int(routed.mean()), "us": pct(routed_us),
+                             "hbm_frac": round(float(routed.sum() / (routed_us.sum() * 1e-6)) / PEAK_HBM, 4)},
+            "layer": {"bytes_mean": int(lb.mean()), "kernels_us": pct(r["layer_us"]),
+                      "hbm_frac": round(float(lb.sum() / (r["layer_us"].sum() * 1e-6)) / PEAK_HBM, 4),
+                      "hbm_frac_wall": round(float(lb.mean() / wall_step) / PEAK_HBM, 4)},
+            "unique_experts_mean": float(u.mean())}
+
+
+def prefill_summary(r: dict, t: int, steps: int) -> dict:
+    st = r["stage_us"]
+    up = st[:, 2]
+    return {"stages": {n: {"us": pct(st[:, j])} for j, n in enumerate(STAGES)},
+            "k_pf_up_mfma_frac": round(up_flops(t) / (float(np.median(up)) * 1e-6) / PEAK_BF16, 4),
+            "layer": {"flops": layer_flops(t), "kernels_us": pct(r["layer_us"]),
+                      "mfma_frac": round(layer_flops(t) / (float(np.median(r["layer_us"])) * 1e-6) / PEAK_BF16, 4),
+                      "mfma_frac_wall": round(layer_flops(t) / (r["wall_s"] / steps) / PEAK_BF16, 4)},
+            "unique_experts_mean": float(r["unique"].mean())}
 
 
 # ------------------------------------------------------------------ layer stack
@@ -218,7 +303,6 @@ def run_stack(n_layers: int, batches, steps: int, warmup: int = 3, n_inputs: int
             stack.replay(xs[i % n_inputs])
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        # the same steps launched eagerly (per-kernel launches from the host)
         bufs = stack._buffers(xs[0])
         eo = torch.empty_like(xs[0])
         for i in range(warmup):
@@ -243,54 +327,96 @@ def run_stack(n_layers: int, batches, steps: int, warmup: int = 3, n_inputs: int
 
 
 # ------------------------------------------------------------------ CPU baseline
-def cpu_baseline(layer, n_tokens: int = 3):
-    """The oracle (torch fp32 + numpy, the reference's algorithm restated) on
-    this host, one token per layer call, experts dequantised lazily."""
-    from oracle import formats as F
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+class HostBank:
+    """Routed experts of a resident layer copied to host memory as raw bytes (before
+    timing); ``dequant`` decodes with the oracle's format code.  ``prefetch`` decodes
+    the roles the oracle layer will ask for on a thread pool, in its order."""
+
+    def __init__(self, layer, experts, pool: cf.ThreadPoolExecutor):
+        from oracle import formats as F
+        self.F, self.quant, self.pool = F, layer.bank.quant, pool
+        ex = torch.tensor(sorted(set(int(e) for e in experts)), dtype=torch.long, device="cuda:0")
+        self.pos = {int(e): i for i, e in enumerate(ex.tolist())}
+        self.raw = {r: [t.index_select(0, ex).cpu().numpy() for t in layer.bank.roles[r]]
+                    for r in ("w1", "w3", "w2")}
+        self.ready: dict = {}
+
+    def _decode(self, e: int, role: str):
+        parts = [a[self.pos[e]] for a in self.raw[role]]
+        return self.F.fp4_dequant(*parts) if self.quant == "fp4" else self.F.q3_dequant(*parts)
+
+    def prefetch(self, experts) -> None:
+        self.ready = {(int(e), r): self.pool.submit(self._decode, int(e), r)
+                      for e in sorted(set(int(v) for v in experts)) for r in ("w1", "w3", "w2")}
+
+    def dequant(self, e, role):
+        f = self.ready.pop((int(e), role), None)
+        return f.result() if f is not None else self._decode(int(e), role)
+
+
+def oracle_call(layer, x: torch.Tensor, bank: HostBank, shared, spec, gate) -> float:
+    """Seconds for one oracle layer forward (router, lazy dequant of the selected
+    experts on the thread pool, expert math, combine)."""
     from oracle import layer as L
+    from oracle import router as R
+    t0 = time.perf_counter()
+    routing = R.route(x.float().numpy(), gate[0], gate[1], spec.k, spec.score_func, spec.route_scale)
+    bank.prefetch(routing[0].ravel())
+    L.moe_forward(x, None, None, bank, shared, spec, routing=routing)
+    return time.perf_counter() - t0
+
+
+def cpu_baseline(layer, zipf_layer=None) -> dict:
+    """The oracle (torch fp32 + numpy: the reference's algorithm restated) on this
+    host's cores, on bounded samples: B=1 (median of 5 calls after 1 warm-up), B=64
+    (one call), and 1024 of the 4096 tokens of the Zipf prefill workload (one call)."""
+    from oracle import layer as L
+    from oracle import router as R
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     spec = L.LayerSpec(H=H, E=E, k=K_TOP, I=I, I_shared=IS)
-    gate_w, gate_b = layer.gate_w.cpu(), layer.gate_b.cpu()
-    shared = tuple(t.cpu() for t in (layer.shared.w1, layer.shared.w3, layer.shared.w2))
     g = torch.Generator().manual_seed(7)
-    xs = [torch.randn((1, H), generator=g).to(torch.bfloat16) for _ in range(n_tokens + 1)]
-    raw = {}
-    idx_all = set()
-    for x in xs:                                    # fetch the raw bytes the oracle will read
-        from oracle import router as R
-        idx, *_ = R.route(x.float().numpy(), gate_w.numpy(), gate_b.numpy(), K_TOP)
-        idx_all.update(int(v) for v in idx.ravel())
-    for e in idx_all:
-        raw[e] = {r: [t[e].cpu().numpy() for t in layer.bank.roles[r]] for r in ("w1", "w3", "w2")}
-
-    class HostBank:
-        quant = "fp4"
-
-        def __init__(self):
-            self.cache = {}
-
-        def dequant(self, e, role):
-            if (e, role) not in self.cache:
-                self.cache[(e, role)] = F.fp4_dequant(*raw[e][role])
-            return self.cache[(e, role)]
-
-    L.moe_forward(xs[0], gate_w, gate_b, HostBank(), shared, spec)      # warm-up
-    times = []
-    for x in xs[1:]:
-        t0 = time.perf_counter()
-        L.moe_forward(x, gate_w, gate_b, HostBank(), shared, spec)
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    return {"value": 1.0 / med, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{n_tokens} single-token layer calls (B=1) of the oracle after 1 warm-up, "
-                      f"median {med:.3f} s; experts dequantised per call; {platform.processor() or platform.machine()}, "
-                      f"torch {torch.__version__}"}
+    out = {}
+    with cf.ThreadPoolExecutor(max_workers=cores) as pool:
+        for name, lay, t, calls in (("B1", layer, 1, 6), ("B64", layer, 64, 1),
+                                    ("T4096_zipf_sample1024", zipf_layer, 1024, 1)):
+            if lay is None:
+                continue
+            gate = (lay.gate_w.cpu().float().numpy(), lay.gate_b.cpu().numpy())
+            shared = tuple(s.cpu() for s in (lay.shared.w1, lay.shared.w3, lay.shared.w2))
+            xs = [torch.randn((t, H), generator=g).to(torch.bfloat16) for _ in range(calls)]
+            needed = set()
+            for x in xs:
+                needed.update(int(v) for v in R.route(x.float().numpy(), gate[0], gate[1], K_TOP)[0].ravel())
+            bank = HostBank(lay, needed, pool)
+            times = [oracle_call(lay, x, bank, shared, spec, gate) for x in xs]
+            if calls > 1:
+                times = times[1:]                       # first call is the warm-up
+            med = float(np.median(times))
+            out[name] = {"tokens_per_s": round(t / med, 3), "s_per_call": round(med, 3),
+                         "calls_timed": len(times), "tokens_per_call": t}
+            print(f"# cpu baseline {name}: {out[name]}", file=sys.stderr, flush=True)
+    b1 = out["B1"]
+    return {"value": b1["tokens_per_s"], "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": (f"B=1: median of {b1['calls_timed']} single-token layer calls of the oracle after "
+                       f"1 warm-up (router, lazy per-expert dequant on {cores} threads, torch fp32 "
+                       f"expert math); {cpu_model()}; torch {torch.__version__}"),
+            "configs": out}
 
 
-# ------------------------------------------------------------------ copy calibration
-def copy_mode(nbytes: int, steps: int) -> None:
+# ------------------------------------------------------------------ machine peaks
+def copy_rate(nbytes: int, steps: int) -> dict:
     dev = torch.device("cuda:0")
     a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).uniform_()
     b = torch.empty_like(a)
@@ -302,8 +428,47 @@ def copy_mode(nbytes: int, steps: int) -> None:
         b.copy_(a)
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / steps
-    print(json.dumps({"mode": "copy", "bytes_read": nbytes, "bytes_written": nbytes,
-                      "ms": dt * 1e3, "GBps_rw": 2 * nbytes / dt / 1e9}), flush=True)
+    return {"mode": "copy", "bytes_read": nbytes, "bytes_written": nbytes, "ms": round(dt * 1e3, 4),
+            "GBps_read_plus_write": round(2 * nbytes / dt / 1e9, 1)}
+
+
+def read_rate(nbytes: int, steps: int) -> dict:
+    dev = torch.device("cuda:0")
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).uniform_()
+    for _ in range(3):
+        a.sum()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        a.sum()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return {"mode": "read", "bytes_read": nbytes, "ms": round(dt * 1e3, 4), "GBps": round(nbytes / dt / 1e9, 1)}
+
+
+def mfma_rate(n: int = 8192, steps: int = 20) -> dict:
+    """bf16 GEMM n x n x n through torch (hipBLASLt) with random N(0,1) operands and
+    with constant operands: the dense bf16 matrix rate this box sustains."""
+    dev = torch.device("cuda:0")
+    res = {"mode": "mfma", "gemm": f"bf16 {n}x{n}x{n}", "flop_per_call": 2 * n ** 3}
+    for kind in ("random", "constant"):
+        if kind == "random":
+            a = torch.randn((n, n), device=dev, dtype=torch.bfloat16)
+            b = torch.randn((n, n), device=dev, dtype=torch.bfloat16)
+        else:
+            a = torch.full((n, n), 0.5, device=dev, dtype=torch.bfloat16)
+            b = torch.full((n, n), 0.25, device=dev, dtype=torch.bfloat16)
+        for _ in range(3):
+            torch.matmul(a, b)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            torch.matmul(a, b)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        res[f"TFLOPs_{kind}"] = round(2 * n ** 3 / dt / 1e12, 1)
+        res[f"frac_of_peak_{kind}"] = round(2 * n ** 3 / dt / PEAK_BF16, 4)
+    return res
 
 
 # ------------------------------------------------------------------ main
@@ -312,15 +477,17 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--timed-steps", type=int, default=120, help="steps timed per kernel (median/p10/p90)")
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--inputs", type=int, default=16)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-stack", action="store_true", help="leave the 40-layer stack out of the sweep")
     ap.add_argument("--quant", choices=("fp4", "q3"), default="fp4", help="routed expert format")
     ap.add_argument("--zipf", type=float, default=None,
                     help="gate bias = log Zipf(s) popularity (skewed routing, as in the prefill sweep)")
-    ap.add_argument("--mode", choices=("layer", "copy"), default="layer")
+    ap.add_argument("--mode", choices=("layer", "copy", "read", "mfma"), default="layer")
     ap.add_argument("--bytes", type=int, default=1 << 30)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -332,7 +499,13 @@ def main() -> int:
         return 2
     dsk_moe.load_library()
     if args.mode == "copy":
-        copy_mode(args.bytes, args.steps)
+        print(json.dumps(copy_rate(args.bytes, args.steps)), flush=True)
+        return 0
+    if args.mode == "read":
+        print(json.dumps(read_rate(args.bytes, args.steps)), flush=True)
+        return 0
+    if args.mode == "mfma":
+        print(json.dumps(mfma_rate()), flush=True)
         return 0
 
     t_gen = time.perf_counter()
@@ -340,44 +513,44 @@ def main() -> int:
                                 quant=args.quant, seed=1000 + i, device="cuda:0", zipf_s=args.zipf)
               for i in range(args.layers)]
     torch.cuda.synchronize()
-    print(f"# generated {args.layers} resident layers in {time.perf_counter() - t_gen:.1f} s", file=sys.stderr, flush=True)
+    print(f"# generated {args.layers} resident layers in {time.perf_counter() - t_gen:.1f} s",
+          file=sys.stderr, flush=True)
 
     T = args.tokens
-    r = run_workload(layers, T, args.steps, args.warmup, args.inputs)
+    r = run_workload(layers, T, args.steps, args.warmup, args.inputs, args.timed_steps)
     ms_step = r["wall_s"] / args.steps * 1e3
     value = T * args.steps / r["wall_s"]
-    st = r["stage_ms"]
-    marker_ms = float(np.median(r["marker_ms"]))
-    u = np.array(r["unique"])
-    up_ms = np.maximum(st[:, 2] - marker_ms, 1e-6)
-    up_bytes = np.array([up_kernel_bytes(int(x), T, args.quant) for x in u])
-    achieved = float(up_bytes.sum() / (up_ms.sum() * 1e-3))
     prefill = T >= PREFILL_MIN_TOKENS
     workload = (f"full-size {args.quant.upper()} MoE layer {'prefill' if prefill else 'decode'}, B={T}"
                 + (f", Zipf({args.zipf}) gate bias" if args.zipf else ""))
+    timing = (f"kernel begin/end timestamps (HIP events carried by the launches), median over "
+              f"{args.timed_steps} steps of the same cold-weight rotation")
     if prefill:
-        # gate/up GEMM of the prefill path: routed (T*k rows) and shared (T rows) w1, w3
-        up_flops = 2 * T * K_TOP * 2 * H * I + 2 * T * 2 * H * IS
-        achieved_f = up_flops / (float(up_ms.mean()) * 1e-3)
-        roofline = {"bound": "mfma", "achieved": round(achieved_f / 1e12, 1), "peak": PEAK_BF16 / 1e12,
-                    "unit": "TFLOP/s", "frac": round(achieved_f / PEAK_BF16, 4),
-                    "traffic": measured_traffic("k_pf_up", workload),
+        summ = prefill_summary(r, T, args.steps)
+        up_us = summ["stages"]["gate_up"]["us"]["median"]
+        achieved = up_flops(T) / (up_us * 1e-6)
+        roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 1), "peak": PEAK_BF16 / 1e12,
+                    "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4),
+                    "traffic": measured_traffic(["k_pf_up"], workload),
                     "kernel": f"k_pf_up (routed {args.quant.upper()} + shared bf16 w1/w3 GEMM tiles, SwiGLU epilogue)",
-                    "flops_per_launch": int(up_flops),
-                    "avg_launch_us": round(float(up_ms.mean()) * 1e3, 2),
-                    "timing": "HIP events around one launch per step, minus the GPU time of an "
-                              "empty event pair"}
+                    "flops_per_launch": int(up_flops(T)), "avg_launch_us": up_us, "timing": timing}
     else:
+        summ = decode_summary(r, T, args.quant, args.steps)
+        rs = summ["routed_stage"]
+        routed_us = float(np.mean(r["stage_us"][:, 2] + r["stage_us"][:, 3]))
+        achieved = rs["bytes_mean"] / (routed_us * 1e-6)
+        up_k = "k_up_q3" if (args.quant == "q3" and T <= 8) else "k_up_stream"
+        dn_k = ("k_down_q3" if args.quant == "q3" and T <= 4 else
+                "k_down_decode_staged" if T <= 2 else "k_down_grouped + k_combine")
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
-                    "traffic": measured_traffic("k_up_stream", workload),
-                    "kernel": f"k_up_stream (routed {args.quant.upper()} w1/w3, SwiGLU and route weight epilogue)",
-                    "bytes_per_launch": int(up_bytes.mean()),
-                    "avg_launch_us": round(float(up_ms.mean()) * 1e3, 2),
-                    "timing": "HIP events around one launch per step (cold weights), minus the "
-                              "GPU time of an empty event pair"}
-    layer_b = np.array([layer_bytes(int(x), T, args.quant) for x in u])
-    stage_names = ["route", "dispatch", "gate_up", "down", "combine"]
+                    "traffic": measured_traffic(["k_up_stream", "k_down_decode_staged"], workload),
+                    "kernel": f"routed-expert stage: {up_k} (routed w1/w3, SwiGLU x route weight) + "
+                              f"{dn_k} (routed and shared w2, combine)",
+                    "bytes_per_launch": rs["bytes_mean"],
+                    "bytes_note": "routed-expert bytes only (U experts x 3 roles); the kernels also "
+                                  "move the shared w2 and activations (stages[*].bytes_mean)",
+                    "avg_launch_us": round(routed_us, 2), "timing": timing}
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
@@ -390,48 +563,47 @@ def main() -> int:
                    "gate": "sigmoid, route_scale 2.5", "tokens": T,
                    "layers_rotated": args.layers, "inputs_rotated": args.inputs},
         "roofline": roofline,
-        "stage_us": {n: round(max(float(st[:, i].mean()) - marker_ms, 0.0) * 1e3, 2)
-                     for i, n in enumerate(stage_names)},
-        "event_marker_us": round(marker_ms * 1e3, 2),
-        "layer_hbm_frac_wall": round(float(layer_b.mean() / (ms_step * 1e-3)) / PEAK_HBM, 4),
-        "unique_experts_mean": float(u.mean()),
+        "detail": summ,
     }
+    peaks = {"hbm_GBps_published": PEAK_HBM / 1e9, "bf16_TFLOPs_published": PEAK_BF16 / 1e12}
+    cp = copy_rate(1 << 30, 20)
+    rd = read_rate(1 << 31, 20)
+    peaks.update({"copy_GBps_measured": cp["GBps_read_plus_write"], "read_GBps_measured": rd["GBps"]})
+    mf = mfma_rate(8192, 10)
+    peaks.update({"bf16_gemm_TFLOPs_measured_random": mf["TFLOPs_random"],
+                  "bf16_gemm_TFLOPs_measured_constant": mf["TFLOPs_constant"]})
+    line["peaks"] = peaks
+    zl = None
     if not args.no_sweep:
         sweep = {}
         for tb in (8, 64):
-            rs = run_workload(layers, tb, 40, 5, args.inputs, seed=77)
-            us = np.array(rs["unique"])
-            lb = np.array([layer_bytes(int(x), tb) for x in us])
-            sweep[f"B{tb}"] = {"tokens_per_s": round(tb * 40 / rs["wall_s"], 1),
-                               "ms_per_step": round(rs["wall_s"] / 40 * 1e3, 4),
-                               "unique_experts_mean": float(us.mean()),
-                               "layer_hbm_frac": round(float(lb.mean() / (rs["wall_s"] / 40)) / PEAK_HBM, 4)}
+            rs_ = run_workload(layers, tb, 40, 5, args.inputs, 100, seed=77)
+            s_ = decode_summary(rs_, tb, "fp4", 40)
+            sweep[f"B{tb}"] = {"tokens_per_s": round(tb * 40 / rs_["wall_s"], 1),
+                               "ms_per_step": round(rs_["wall_s"] / 40 * 1e3, 4), **s_}
         zl = gsynth.make_layer(hidden=H, n_experts=E, top_k=K_TOP, inter=I, inter_shared=IS,
                                seed=3000, device="cuda:0", zipf_s=1.1)
-        rs = run_workload([zl], 4096, 5, 1, 2, seed=99)
-        step_s = rs["wall_s"] / 5
-        sweep["T4096_prefill_zipf"] = {"tokens_per_s": round(4096 / step_s, 1),
-                                       "ms_per_step": round(step_s * 1e3, 3),
-                                       "mfma_frac": round(layer_flops(4096) / step_s / PEAK_BF16, 4),
-                                       "stage_us": {n: round(float(rs["stage_ms"][:, i].mean()) * 1e3, 1)
-                                                    for i, n in enumerate(stage_names)}}
-        # routed experts in 3-bit affine (group 64, fp16 scale / bias), B = 1, 16, 64
+        rs_ = run_workload([zl], 4096, 10, 2, 2, 20, seed=99)
+        sweep["T4096_prefill_zipf"] = {"tokens_per_s": round(4096 * 10 / rs_["wall_s"], 1),
+                                       "ms_per_step": round(rs_["wall_s"] / 10 * 1e3, 3),
+                                       **prefill_summary(rs_, 4096, 10)}
+        # routed experts in 3-bit affine (group 64, fp16 scale / bias), B = 1, 16, 64;
+        # 4 layers rotated (each cycle moves more than the Infinity Cache)
         q3_layers = [gsynth.make_layer(hidden=H, n_experts=E, top_k=K_TOP, inter=I, inter_shared=IS,
-                                       quant="q3", seed=2000 + i, device="cuda:0") for i in range(2)]
+                                       quant="q3", seed=2000 + i, device="cuda:0") for i in range(4)]
         for tb in (1, 16, 64):
             n_steps = 100 if tb == 1 else 40
-            rs = run_workload(q3_layers, tb, n_steps, 5, args.inputs, seed=55)
-            us = np.array(rs["unique"])
-            lb = np.array([layer_bytes(int(x), tb, "q3") for x in us])
-            sweep[f"q3_B{tb}"] = {"tokens_per_s": round(tb * n_steps / rs["wall_s"], 1),
-                                  "ms_per_step": round(rs["wall_s"] / n_steps * 1e3, 4),
-                                  "unique_experts_mean": float(us.mean()),
-                                  "layer_hbm_frac": round(float(lb.mean() / (rs["wall_s"] / n_steps)) / PEAK_HBM, 4)}
+            rs_ = run_workload(q3_layers, tb, n_steps, 5, args.inputs, 100, seed=55)
+            s_ = decode_summary(rs_, tb, "q3", n_steps)
+            sweep[f"q3_B{tb}"] = {"tokens_per_s": round(tb * n_steps / rs_["wall_s"], 1),
+                                  "ms_per_step": round(rs_["wall_s"] / n_steps * 1e3, 4), **s_}
         del q3_layers
-        sweep.update(run_stack(40, (1, 2), steps=30))
+        torch.cuda.empty_cache()
+        if not args.no_stack:
+            sweep.update(run_stack(40, (1, 2), steps=30))
         line["sweep"] = sweep
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(layers[0])
+        line["cpu_baseline"] = cpu_baseline(layers[0], zl)
     print(json.dumps(line), flush=True)
     return 0
 
