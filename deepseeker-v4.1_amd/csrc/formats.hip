@@ -188,6 +188,41 @@ __device__ __forceinline__ void q3_block_codes(const uint32_t* wds /*[4][3]*/, u
   }
 }
 
+// Codes of one 128-code block -> its four lane-group chunks (words [g][3]).
+__device__ __forceinline__ void q3_block_pack(const uint8_t* q /*[128]*/, uint32_t* wds /*[12]*/) {
+#pragma unroll
+  for (int i = 0; i < 12; ++i) wds[i] = 0u;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      int m = p >> 2, i = p & 3;
+      uint32_t lo = q[32 * g + 8 * m + 2 * i], hi = q[32 * g + 8 * m + 2 * i + 1];
+      if (p < 15) {
+        int s = 3 * (p % 5);
+        wds[3 * g + p / 5] |= (lo << s) | (hi << (16 + s));
+      } else {
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+          wds[3 * g + t] |= (((lo >> t) & 1u) << 15) | (((hi >> t) & 1u) << 31);
+      }
+    }
+  }
+}
+
+// Stores the chunks of block b (row b / (cols/128), block b % (cols/128)) at their place.
+__device__ __forceinline__ void q3_block_store(uint8_t* __restrict__ packed, int cols, int64_t b,
+                                               const uint32_t* wds) {
+  const int nbk = cols / 128;
+  uint8_t* row = packed + (b / nbk) * (cols / 8 * 3);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    uint32_t* dst = reinterpret_cast<uint32_t*>(row + q3_chunk_offset(cols, static_cast<int>(b % nbk), g));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) dst[i] = wds[3 * g + i];
+  }
+}
+
 // One thread per 128-code block of one row.
 __global__ __launch_bounds__(kThreads) void k_q3_quantize(
     const float* __restrict__ w, int64_t blocks, int cols, uint8_t* __restrict__ packed,
@@ -217,32 +252,33 @@ __global__ __launch_bounds__(kThreads) void k_q3_quantize(
     biases[2 * b + grp] = __builtin_bit_cast(uint16_t, b16);
   }
   uint32_t wds[12];
+  q3_block_pack(q, wds);
+  q3_block_store(packed, cols, b, wds);
+}
+
+// Checkpoint q3 (row-major 3-byte packs: a row is a little-endian bit stream
+// with code c at bits 3c..3c+2, so a 128-code block is 48 contiguous bytes)
+// -> the canonical layout.  One thread per 128-code block of one row.
+__global__ __launch_bounds__(kThreads) void k_q3_repack(const uint8_t* __restrict__ src, int64_t blocks, int cols,
+                                                        uint8_t* __restrict__ packed) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (b >= blocks) return;
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(src + b * 48);   // rows are 48 * cols/128 bytes
+  uint32_t wv[13];
 #pragma unroll
-  for (int i = 0; i < 12; ++i) wds[i] = 0u;
+  for (int i = 0; i < 12; ++i) wv[i] = w[i];
+  wv[12] = 0u;
+  uint8_t q[128];
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-#pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      int m = p >> 2, i = p & 3;
-      uint32_t lo = q[32 * g + 8 * m + 2 * i], hi = q[32 * g + 8 * m + 2 * i + 1];
-      if (p < 15) {
-        int s = 3 * (p % 5);
-        wds[3 * g + p / 5] |= (lo << s) | (hi << (16 + s));
-      } else {
-#pragma unroll
-        for (int t = 0; t < 3; ++t)
-          wds[3 * g + t] |= (((lo >> t) & 1u) << 15) | (((hi >> t) & 1u) << 31);
-      }
-    }
+  for (int c = 0; c < 128; ++c) {
+    const int bit = 3 * c, wi = bit >> 5, sh = bit & 31;
+    uint32_t v = wv[wi] >> sh;
+    if (sh > 29) v |= wv[wi + 1] << (32 - sh);
+    q[c] = static_cast<uint8_t>(v & 7u);
   }
-  const int nbk = cols / 128;
-  uint8_t* row = packed + (b / nbk) * (cols / 8 * 3);
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    uint32_t* dst = reinterpret_cast<uint32_t*>(row + q3_chunk_offset(cols, static_cast<int>(b % nbk), g));
-#pragma unroll
-    for (int i = 0; i < 3; ++i) dst[i] = wds[3 * g + i];
-  }
+  uint32_t wds[12];
+  q3_block_pack(q, wds);
+  q3_block_store(packed, cols, b, wds);
 }
 
 __global__ __launch_bounds__(kThreads) void k_q3_dequant(
@@ -313,6 +349,13 @@ hipError_t launch_q3_quantize(const float* w, int64_t rows, int64_t cols, uint8_
   int64_t blocks = rows * (cols / 128);
   if (blocks == 0) return hipSuccess;
   launch_kernel(k_q3_quantize, grid_for(blocks), kThreads, 0, s, w, blocks, static_cast<int>(cols), packed, scales, biases);
+  return hipGetLastError();
+}
+
+hipError_t launch_q3_repack(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* packed, hipStream_t s) {
+  const int64_t blocks = rows * (cols / 128);
+  if (blocks == 0) return hipSuccess;
+  launch_kernel(k_q3_repack, grid_for(blocks), kThreads, 0, s, src, blocks, static_cast<int>(cols), packed);
   return hipGetLastError();
 }
 

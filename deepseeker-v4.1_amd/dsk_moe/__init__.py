@@ -17,8 +17,8 @@ from .layer import MoELayer, moe_layer
 from .stack import MoEStack, rmsnorm
 from .trace import Geometry, Trace, TraceSink
 from .ops import (align_block_size, dispatch, fp4_dequant, fp4_quantize, q3_dequant,
-                  q3_quantize, route, workspace_size)
+                  q3_quantize, q3_repack, route, workspace_size)
 
 __all__ = ["Checkpoint", "DskError", "MoELayer", "MoEStack", "ResidentBank", "SharedExpert", "TraceSink", "align_block_size",
            "build_manifest", "dispatch", "fp4_dequant", "fp8_block_dequant", "fp4_quantize", "load_library", "moe_layer",
-           "q3_dequant", "q3_quantize", "rmsnorm", "route", "workspace_size", "Geometry", "Trace"]
+           "q3_dequant", "q3_quantize", "q3_repack", "rmsnorm", "route", "workspace_size", "Geometry", "Trace"]

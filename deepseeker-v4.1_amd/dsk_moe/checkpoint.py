@@ -17,6 +17,12 @@ reads a layer's tensors by byte range and builds a ``MoELayer``:
 * routed experts (``I8`` packed e2m1 codes ``[N, K/2]`` + ``F8_E8M0`` scales
   ``[N, K/32]`` per role): byte-identical to the kernels' FP4 layout, copied
   into ``[E, N, K/2]`` / ``[E, N, K/32]`` device banks without arithmetic;
+* or q3 routed experts, as the reference's q3 variant stores them for layers
+  20-39 (``src/deepseeker/variant_q3.py:1-8``; ``U32_Q3_AFFINE`` words
+  ``[N, 3K/32]`` of row-major 3-byte packs + ``F16`` ``.scale`` / ``.bias``
+  ``[N, K/64]``, ``src/deepseeker/mlx_weights.py:119-141``): the codes are
+  copied to the device and put into the kernels' canonical layout by
+  ``dsk_q3_repack``, scales and biases copied unchanged;
 * shared expert (``F8_E4M3`` + block scales, or ``BF16``): dequantised on the
   device by ``dsk_fp8_block_dequant`` into bf16;
 * gate (``BF16`` or ``F32`` ``[E, H]``) and its bias (``F32`` ``[E]``).
@@ -41,13 +47,14 @@ import torch
 from . import _lib
 from .bank import ResidentBank, SharedExpert
 from .layer import MoELayer
-from .ops import ptr, require_device, stream_of
+from .ops import ptr, q3_repack, require_device, stream_of
 
 SCHEMA = "deepseeker.model-manifest/v1"
 OFFSET_CONVENTION = ("data_range is [start, end) relative to the safetensors data-section start; "
                      "file_range is absolute from file byte 0 (8-byte header length + JSON header + "
                      "relative offset).")
-_ITEM = {"BF16": 2, "F16": 2, "F32": 4, "I8": 1, "U8": 1, "F8_E4M3": 1, "F8_E8M0": 1, "I32": 4, "U32": 4}
+_ITEM = {"BF16": 2, "F16": 2, "F32": 4, "I8": 1, "U8": 1, "F8_E4M3": 1, "F8_E8M0": 1, "I32": 4, "U32": 4,
+         "U32_Q3_AFFINE": 4}
 _EXPERT = re.compile(r"^(layers|mtp)\.(\d+)\.ffn\.experts\.(\d+)\.")
 _LAYER = re.compile(r"^layers\.(\d+)\.")
 
@@ -196,10 +203,52 @@ class Checkpoint:
         return len(ids)
 
     # -------------------------------------------------------------- device objects
+    def expert_format(self, layer: int) -> str:
+        """``"fp4"`` or ``"q3"``: the routed-expert format of ``layer`` (expert 0's w1)."""
+        base = f"layers.{layer}.ffn.experts.0.w1"
+        w = self.entry(base + ".weight")
+        if w["dtype"] == "U32_Q3_AFFINE" or (base + ".bias") in self.by_name:
+            return "q3"
+        return "fp4"
+
+    def _load_q3_bank(self, layer: int, dev: torch.device, E: int) -> ResidentBank:
+        roles = {}
+        for role in ("w1", "w3", "w2"):
+            base = f"layers.{layer}.ffn.experts.0.{role}"
+            w, s, b = self.entry(base + ".weight"), self.entry(base + ".scale"), self.entry(base + ".bias")
+            if w["dtype"] not in ("U32_Q3_AFFINE", "U32", "I32") or s["dtype"] != "F16" or b["dtype"] != "F16":
+                raise ValueError(f"{base}: expected q3 words + F16 scale / bias, got "
+                                 f"{w['dtype']} / {s['dtype']} / {b['dtype']}")
+            n, words = w["shape"]
+            groups = s["shape"][1]
+            k = groups * 64
+            if tuple(s["shape"]) != (n, groups) or tuple(b["shape"]) != (n, groups) or words * 32 != 3 * k:
+                raise ValueError(f"{base}: q3 words {w['shape']} do not match scales {s['shape']} "
+                                 f"(want [N, 3K/32] with K = 64 x groups)")
+            if k % 128:
+                raise ValueError(f"{base}: K={k} is not a multiple of 128")
+            staged = torch.empty((E, n, k * 3 // 8), dtype=torch.uint8, device=dev)
+            scales = torch.empty((E, n, groups), dtype=torch.float16, device=dev)
+            biases = torch.empty((E, n, groups), dtype=torch.float16, device=dev)
+            for e in range(E):
+                name = f"layers.{layer}.ffn.experts.{e}.{role}"
+                if tuple(self.entry(name + ".weight")["shape"]) != (n, words):
+                    raise ValueError(f"{name}: shape differs from expert 0")
+                raw = np.frombuffer(self.read(name + ".weight"), dtype=np.uint8).reshape(n, -1)
+                staged[e].copy_(torch.from_numpy(raw.copy()))
+                scales[e].copy_(torch.from_numpy(self._array(name + ".scale", "<f2").copy()))
+                biases[e].copy_(torch.from_numpy(self._array(name + ".bias", "<f2").copy()))
+            roles[role] = (q3_repack(staged), scales, biases)
+            del staged
+        return ResidentBank("q3", roles)
+
     def load_bank(self, layer: int, device: torch.device | str = "cuda") -> ResidentBank:
-        """All routed experts of ``layer`` as an FP4 ``ResidentBank`` (bytes copied unchanged)."""
+        """All routed experts of ``layer`` as a ``ResidentBank``: FP4 bytes copied
+        unchanged, or q3 codes repacked into the canonical layout on the device."""
         dev = torch.device(device)
         E = self.n_experts(layer)
+        if self.expert_format(layer) == "q3":
+            return self._load_q3_bank(layer, dev, E)
         roles = {}
         for role in ("w1", "w3", "w2"):
             base = f"layers.{layer}.ffn.experts.0.{role}"

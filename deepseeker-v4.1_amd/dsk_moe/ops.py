@@ -129,6 +129,21 @@ def route(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor, top_k: in
     return w, idx, scores
 
 
+def cap_union(scores: torch.Tensor, idx: torch.Tensor, w: torch.Tensor, budget: int,
+              strict: bool = False) -> None:
+    """``dsk_cap_union`` in place on a lock-step batch's routing (the reference's
+    ``cap_union``, ``src/deepseeker/mlx_forward.py:213-254``): scores [T, E] f32
+    (un-biased), idx [T, k] int32 and w [T, k] f32 in this library's order."""
+    dev = require_device(scores, idx, w)
+    if scores.dtype != torch.float32 or idx.dtype != torch.int32 or w.dtype != torch.float32:
+        raise ValueError("scores and w must be float32, idx int32")
+    t, k = idx.shape
+    if w.shape != idx.shape or scores.dim() != 2 or scores.shape[0] != t:
+        raise ValueError("scores [T, E], idx and w [T, k] must agree")
+    _lib.call("dsk_cap_union", t, scores.shape[1], k, int(budget), 1 if strict else 0, ptr(scores), ptr(idx),
+              ptr(w), stream_of(dev))
+
+
 def dispatch(idx: torch.Tensor, n_experts: int) -> dict:
     """counts, offsets, perm, rank, active of ``dsk_dispatch`` for idx [T,k] int32."""
     dev = require_device(idx)
@@ -213,6 +228,21 @@ def q3_quantize(w: torch.Tensor):
     _lib.call("dsk_q3_quantize", ptr(w), rows, cols, ptr(packed), ptr(scales), ptr(biases),
               stream_of(dev))
     return packed, scales, biases
+
+
+def q3_repack(rowmajor: torch.Tensor) -> torch.Tensor:
+    """Checkpoint q3 codes (row-major 3-byte packs, ``[..., 3K/8]`` u8 or ``[..., 3K/32]``
+    int32 / uint32 words) -> the canonical kernel layout ``[..., 3K/8]`` u8 (``dsk_q3_repack``)."""
+    dev = require_device(rowmajor)
+    raw = rowmajor.view(torch.uint8) if rowmajor.dtype != torch.uint8 else rowmajor
+    raw = raw.reshape(rowmajor.shape[:-1] + (-1,))
+    cols = raw.shape[-1] * 8 // 3
+    if raw.shape[-1] * 8 != cols * 3 or cols % 128:
+        raise ValueError(f"q3 rows of {raw.shape[-1]} bytes do not hold a multiple of 128 codes")
+    rows = raw.numel() // raw.shape[-1]
+    out = torch.empty_like(raw)
+    _lib.call("dsk_q3_repack", ptr(raw), rows, cols, ptr(out), stream_of(dev))
+    return out
 
 
 def q3_dequant(packed: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,

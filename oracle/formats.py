@@ -277,6 +277,54 @@ def q3_unpack(packed: np.ndarray, k: int) -> np.ndarray:
     return c.reshape(n, k).astype(np.uint8)
 
 
+def q3_pack_rowmajor(q: np.ndarray) -> np.ndarray:
+    """Codes [N, K] (0..7) -> row-major 3-byte packs [N, 3K/8] u8 (the checkpoint layout).
+
+    Bytes ``3m..3m+2`` of a row hold codes ``8m..8m+7`` as one 24-bit
+    little-endian integer, code ``i`` of the pack at bits ``3i..3i+2``; equally,
+    a row is a little-endian bit stream with code ``c`` at bits ``3c..3c+2``.
+    Viewed as little-endian u32 words this is the ``[N, ceil(3K/32)]`` ``U32_Q3_AFFINE``
+    tensor of the reference's q3 checkpoints (``src/deepseeker/mlx_weights.py:119-141``;
+    written by ``scripts/requant_experts_3bit.py:69-83, 135-148``), whose word order
+    the reference calls MLX-internal: this build fixes it as stated here.
+    K must be a multiple of 8.  Pinned in the tests by the known answer
+    codes 0..7 -> 0o76543210 (bytes 88 C6 FA), by the bit-stream restatement
+    (``numpy.packbits`` in little-endian bit order) and by round trips.
+    """
+    q = np.asarray(q, dtype=np.uint32)
+    n, k = q.shape
+    if k % 8:
+        raise ValueError(f"K={k} is not a multiple of 8")
+    if q.size and q.max() > 7:
+        raise ValueError("q3 codes must be in 0..7")
+    packs = np.zeros((n, k // 8), dtype=np.uint32)
+    for i in range(8):
+        packs |= q[:, i::8] << (3 * i)
+    out = np.empty((n, k // 8, 3), dtype=np.uint8)
+    for byte in range(3):
+        out[:, :, byte] = (packs >> (8 * byte)) & 0xFF
+    return out.reshape(n, k * 3 // 8)
+
+
+def q3_unpack_rowmajor(packed: np.ndarray, k: int) -> np.ndarray:
+    """Row-major 3-byte packs [N, 3K/8] u8 -> codes [N, K] u8 (inverse of ``q3_pack_rowmajor``)."""
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    n = p.shape[0]
+    if k % 8 or p.shape[1] != k * 3 // 8:
+        raise ValueError(f"packed {p.shape} does not hold K={k} q3 codes")
+    b = p.reshape(n, k // 8, 3).astype(np.uint32)
+    packs = b[:, :, 0] | (b[:, :, 1] << 8) | (b[:, :, 2] << 16)
+    q = np.empty((n, k), dtype=np.uint8)
+    for i in range(8):
+        q[:, i::8] = (packs >> (3 * i)) & 7
+    return q
+
+
+def q3_rowmajor_to_canonical(packed: np.ndarray, k: int) -> np.ndarray:
+    """Checkpoint (row-major 3-byte packs) -> this build's canonical kernel layout."""
+    return q3_pack(q3_unpack_rowmajor(packed, k))
+
+
 def q3_quantize(w: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     """float32 [N, K] -> (packed [N, 3K/8] u8, scales f16 [N, K/64], biases f16 [N, K/64])."""
     q, s, b = q3_quantize_codes(w)

@@ -20,19 +20,31 @@ from oracle import layer as L
 
 
 def make_checkpoint(root: Path, spec: L.LayerSpec, seed: int) -> dict:
+    """``spec.quant`` "fp4": routed experts as I8 codes + F8_E8M0 scales; "q3": as the
+    reference's q3 variant stores them, U32_Q3_AFFINE words [N, 3K/32] of row-major
+    3-byte packs + F16 scale / bias [N, K/64]."""
     rng = np.random.default_rng(seed)
     H, E, I, Is = spec.H, spec.E, spec.I, spec.I_shared
     experts, dense = {}, {}
-    roles = {"w1": ([], []), "w3": ([], []), "w2": ([], [])}
+    q3 = spec.quant == L.QUANT_Q3
+    roles = {"w1": [], "w3": [], "w2": []}
     for e in range(E):
         for role, (n, k) in (("w1", (I, H)), ("w2", (H, I)), ("w3", (I, H))):
-            packed, scales = F.fp4_quantize((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+            w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
             base = f"layers.0.ffn.experts.{e}.{role}"
-            experts[base + ".weight"] = ("I8", packed.shape, packed.tobytes())
-            experts[base + ".scale"] = ("F8_E8M0", scales.shape, scales.tobytes())
-            roles[role][0].append(packed)
-            roles[role][1].append(scales)
-    bank = L.ExpertBank(L.QUANT_FP4, {r: (np.stack(p), np.stack(s)) for r, (p, s) in roles.items()})
+            if q3:
+                q, s16, b16 = F.q3_quantize_codes(w)
+                rowmajor = F.q3_pack_rowmajor(q)
+                experts[base + ".weight"] = ("U32_Q3_AFFINE", (n, 3 * k // 32), rowmajor.tobytes())
+                experts[base + ".scale"] = ("F16", s16.shape, s16.astype("<f2").tobytes())
+                experts[base + ".bias"] = ("F16", b16.shape, b16.astype("<f2").tobytes())
+                roles[role].append((F.q3_pack(q), s16, b16))
+            else:
+                packed, scales = F.fp4_quantize(w)
+                experts[base + ".weight"] = ("I8", packed.shape, packed.tobytes())
+                experts[base + ".scale"] = ("F8_E8M0", scales.shape, scales.tobytes())
+                roles[role].append((packed, scales))
+    bank = L.ExpertBank(spec.quant, {r: tuple(np.stack(c) for c in zip(*parts)) for r, parts in roles.items()})
     shared = []
     for role, (n, k) in (("w1", (Is, H)), ("w2", (H, Is)), ("w3", (Is, H))):
         codes = rng.integers(0, 256, size=(n, k), dtype=np.uint8)

@@ -64,3 +64,28 @@ def test_load_layer_from_checkpoint(tmp_path, T):
     np.testing.assert_array_equal(idx.cpu().numpy(), r["idx"])
     c, rel = assert_layer_close(out.float(), r["y_ref"])
     print(f"cos={c:.9f} rel={rel:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("T", [1, 40])
+def test_load_q3_layer_from_checkpoint(tmp_path, T):
+    """A synthetic checkpoint with q3 routed experts as the reference's q3 variant
+    stores them (U32_Q3_AFFINE words [N, 3K/32] of row-major 3-byte packs, F16
+    scale / bias): the loaded bank holds the canonical layout of the same codes
+    (repacked on the device), and the layer matches the oracle."""
+    print(f"checkpoint q3 layer T={T}", flush=True)
+    spec = L.LayerSpec(H=256, E=8, k=2, I=384, I_shared=128, quant=L.QUANT_Q3)
+    d = make_checkpoint(tmp_path, spec, 12)
+    ck = Checkpoint(tmp_path, d["manifest"])
+    assert ck.expert_format(0) == "q3"
+    layer = ck.load_layer(0, DEV, score_func="sigmoid", route_scale=spec.route_scale)
+    assert layer.bank.quant == "q3"
+    for role in ("w1", "w3", "w2"):
+        for got, want in zip(layer.bank.roles[role], d["bank"].roles[role]):
+            assert np.array_equal(got.cpu().numpy().view(np.uint8), np.ascontiguousarray(want).view(np.uint8)), role
+    x = torch.randn((T, spec.H), generator=torch.Generator().manual_seed(50 + T)).to(torch.bfloat16)
+    idx = torch.empty((T, spec.k), dtype=torch.int32, device=DEV)
+    out = layer(x.to(DEV), idx=idx).cpu()
+    r = L.moe_forward(x, d["gate_w"], d["gate_b"], d["bank"], d["shared"], spec)
+    np.testing.assert_array_equal(idx.cpu().numpy(), r["idx"])
+    c, rel = assert_layer_close(out.float(), r["y_ref"])
+    print(f"cos={c:.9f} rel={rel:.2e}", flush=True)

@@ -77,3 +77,19 @@ def test_q3_quantize_and_dequant_bit_exact(cols):
     np.testing.assert_array_equal(d_got, d_want)
     d16 = dsk_moe.q3_dequant(p_got, s_got, b_got, out_dtype=torch.bfloat16).cpu()
     assert torch.equal(d16.view(torch.int16), torch.from_numpy(d_want).to(torch.bfloat16).view(torch.int16))
+
+
+@pytest.mark.parametrize("rows,cols", [(5, 128), (64, 512), (33, 2304), (4, 5120), (7, 1408)])
+def test_q3_repack_checkpoint_layout_bit_exact(rows, cols):
+    """dsk_q3_repack: checkpoint row-major 3-byte packs -> canonical layout, against
+    the oracle's q3_pack of the same codes (superblocks and tails), from u8 bytes and
+    from the [rows, 3K/32] u32 word view the checkpoint stores."""
+    print(f"q3 repack {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(rows * cols)
+    q = rng.integers(0, 8, size=(rows, cols), dtype=np.uint8)
+    src = F.q3_pack_rowmajor(q)
+    want = F.q3_pack(q)
+    got = dsk_moe.q3_repack(torch.from_numpy(src).to(DEV)).cpu().numpy()
+    np.testing.assert_array_equal(got, want)
+    words = torch.from_numpy(src.view("<i4").copy()).to(DEV)
+    np.testing.assert_array_equal(dsk_moe.q3_repack(words).cpu().numpy(), want)

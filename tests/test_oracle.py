@@ -171,6 +171,29 @@ def test_q3_quantize_error_bound():
     assert np.all(np.abs(rt - vals) <= 0.5 * step + 2e-3)
 
 
+def test_q3_rowmajor_known_answer_and_bitstream():
+    """Checkpoint q3 layout: codes 0..7 of a pack make the 24-bit integer
+    0o76543210 (bytes 88 C6 FA, little-endian); a whole row is a little-endian
+    bit stream with code c at bits 3c..3c+2, restated here with numpy.packbits."""
+    q = np.arange(8, dtype=np.uint8)[None]
+    np.testing.assert_array_equal(F.q3_pack_rowmajor(q), [[0x88, 0xC6, 0xFA]])
+    assert 0o76543210 == 0xFAC688
+    q = np.array([[7, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 5, 0, 0, 0, 0]], dtype=np.uint8)
+    # code 0 = 7 -> bits 0..2 of byte 0; code 11 = 5 (101b) -> bits 33..35 -> byte 4 bits 1 and 3
+    np.testing.assert_array_equal(F.q3_pack_rowmajor(q), [[0x07, 0, 0, 0, 0x0A, 0]])
+    rng = np.random.default_rng(17)
+    for n, k in ((3, 128), (8, 256), (2, 2304), (1, 5120)):
+        q = rng.integers(0, 8, size=(n, k), dtype=np.uint8)
+        bits = ((q[..., None] >> np.arange(3)) & 1).astype(np.uint8).reshape(n, 3 * k)
+        stream = np.packbits(bits, axis=1, bitorder="little")
+        got = F.q3_pack_rowmajor(q)
+        np.testing.assert_array_equal(got, stream)
+        np.testing.assert_array_equal(F.q3_unpack_rowmajor(got, k), q)
+        # reference geometry (tests/test_q3.py:89-105): 3K/32 u32 words per row
+        assert got.view("<u4").shape == (n, 3 * k // 32)
+        np.testing.assert_array_equal(F.q3_unpack(F.q3_rowmajor_to_canonical(got, k), k), q)
+
+
 # ------------------------------------------------------------------ router
 def test_exp_log1p_sqrt_against_math():
     xs = np.linspace(-700, 700, 20001)
