@@ -164,6 +164,21 @@ int dsk_route(const dsk_moe_desc* d, const void* x, const void* gate_w, const fl
                    "dsk_route launch");
 }
 
+int dsk_cap_union(int32_t tokens, int32_t n_experts, int32_t top_k, int32_t budget, int32_t strict,
+                  const float* scores, int32_t* idx, float* weights, void* stream) {
+  if (tokens < 1 || n_experts < 1 || n_experts > 1024 || top_k < 1 || top_k > 16 || top_k > n_experts)
+    return fail(DSK_EINVAL, "dsk_cap_union: tokens=%d, n_experts=%d, top_k=%d out of range", tokens, n_experts,
+                top_k);
+  if (budget < 1) return fail(DSK_EINVAL, "dsk_cap_union: budget=%d must be >= 1", budget);
+  if (!scores || !idx || !weights) return fail(DSK_EINVAL, "dsk_cap_union: NULL pointer argument");
+  if (cap_union_lds(tokens, n_experts, top_k) > kMaxLds)
+    return fail(DSK_EUNSUPPORTED, "dsk_cap_union: tokens*top_k=%lld is beyond the one-block cap (%zu bytes of LDS)",
+                static_cast<long long>(tokens) * top_k, cap_union_lds(tokens, n_experts, top_k));
+  return hip_check(launch_cap_union(scores, idx, weights, tokens, n_experts, top_k, budget, strict ? 1 : 0,
+                                    static_cast<hipStream_t>(stream)),
+                   "dsk_cap_union launch");
+}
+
 int dsk_dispatch(const dsk_moe_desc* d, const int32_t* idx, int32_t* counts, int32_t* offsets,
                  int32_t* perm, int32_t* rank, int32_t* active, void* stream) {
   int rc = check_desc(d);
@@ -359,6 +374,19 @@ int dsk_q3_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* packed,
   return hip_check(launch_q3_quantize(w, rows, cols, packed, scales, biases,
                                       static_cast<hipStream_t>(stream)),
                    "dsk_q3_quantize launch");
+}
+
+int dsk_q3_repack(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* packed, void* stream) {
+  if (!src || !packed) return fail(DSK_EINVAL, "dsk_q3_repack: NULL pointer argument");
+  if (rows < 0 || cols < 0 || cols % 128 || cols > INT32_MAX)
+    return fail(DSK_EINVAL, "cols=%lld must be a multiple of 128 below 2^31", (long long)cols);
+  if (!aligned(src, 4) || !aligned(packed, 4))
+    return fail(DSK_EALIGN, "dsk_q3_repack: src and packed must be 4-byte aligned");
+  const uintptr_t a = reinterpret_cast<uintptr_t>(src), b = reinterpret_cast<uintptr_t>(packed);
+  const uintptr_t n = static_cast<uintptr_t>(rows) * static_cast<uintptr_t>(cols / 8 * 3);
+  if (n && a < b + n && b < a + n) return fail(DSK_EINVAL, "dsk_q3_repack: src and packed overlap");
+  return hip_check(launch_q3_repack(src, rows, cols, packed, static_cast<hipStream_t>(stream)),
+                   "dsk_q3_repack launch");
 }
 
 int dsk_q3_dequant(const uint8_t* packed, const uint16_t* scales, const uint16_t* biases,

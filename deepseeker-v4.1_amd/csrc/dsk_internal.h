@@ -228,6 +228,11 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L,
 
 hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t s);
 
+// cap_union of a lock-step batch's routing, in place (one block): LDS bytes and launch.
+size_t cap_union_lds(int T, int E, int k);
+hipError_t launch_cap_union(const float* scores, int32_t* idx, float* w, int T, int E, int k, int budget,
+                            int strict, hipStream_t s);
+
 // The whole layer (dsk_moe_forward / _timed / _noalloc): check_forward validates
 // every argument on the host (DSK_OK or a DSK_E* code with the message set;
 // own_scratch: the library's scratch stands in for the caller's workspace);
@@ -297,6 +302,7 @@ hipError_t launch_fp4_quantize(const float* w, int64_t rows, int64_t cols,
 hipError_t launch_q3_quantize(const float* w, int64_t rows, int64_t cols,
                               uint8_t* packed, uint16_t* scales, uint16_t* biases,
                               hipStream_t s);
+hipError_t launch_q3_repack(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* packed, hipStream_t s);
 hipError_t launch_q3_dequant(const uint8_t* packed, const uint16_t* scales,
                              const uint16_t* biases, int64_t rows, int64_t cols,
                              void* out, int out_dtype, hipStream_t s);

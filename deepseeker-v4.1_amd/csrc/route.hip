@@ -278,6 +278,113 @@ hipError_t launch_route_unfused(const dsk_moe_desc& d, const GateArgs& g, hipStr
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- union cap
+// cap_union of the reference (src/deepseeker/mlx_forward.py:213-254) on the
+// device routing of a lock-step batch, in place, one block.  idx / w arrive in
+// the build's order (descending key per row); the reference works on its
+// ascending-key order, so every order-dependent step walks a row's slots from
+// j = k-1 down to 0.  Steps (float32, no contraction):
+//   score[e]  sum of scores[t][e] over the rows t routed to e, rows ascending;
+//   keep      the `budget` largest scores, ties to the lower expert id (the
+//             reference's argpartition leaves exact ties unspecified);
+//   rescue    a row with nothing kept keeps its largest weight (the first
+//             maximum in the reference's order) unless strict;
+//   weights   scale = rowsum(w) / (rowsum(kept w) + 1e-20), w' = kept w * scale,
+//             with numpy's float32 pairwise row sum (< 8 terms one by one from
+//             0; else 8 running sums of terms i, i+8, ... combined as
+//             ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), then the tail one by one);
+//   dropped slots get index -1.
+// Nothing changes when the batch's union already fits the budget.
+constexpr int kCapThreads = 1024;
+
+__device__ __forceinline__ float numpy_row_sum(const float* v, int n) {
+  // v in the reference's order
+  if (n < 8) {
+    float r = 0.0f;
+    for (int i = 0; i < n; ++i) r = r + v[i];
+    return r;
+  }
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = v[j];
+  int i = 8;
+  for (; i < n - (n % 8); i += 8)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = r[j] + v[i + j];
+  float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  for (; i < n; ++i) res = res + v[i];
+  return res;
+}
+
+__global__ __launch_bounds__(kCapThreads) void k_cap_union(const float* __restrict__ scores, int32_t* __restrict__ idx,
+                                                           float* __restrict__ w, int T, int E, int k, int budget,
+                                                           int strict) {
+  extern __shared__ __align__(16) unsigned char lds_cap[];
+  int32_t* li = reinterpret_cast<int32_t*>(lds_cap);                 // [T*k]
+  float* sum = reinterpret_cast<float*>(li + T * k);                // [E]
+  int32_t* cnt = reinterpret_cast<int32_t*>(sum + E);               // [E]
+  uint8_t* keep = reinterpret_cast<uint8_t*>(cnt + E);              // [E]
+  __shared__ int union_size;
+  const int tid = threadIdx.x, N = T * k;
+  for (int i = tid; i < N; i += kCapThreads) li[i] = idx[i];
+  if (tid == 0) union_size = 0;
+  __syncthreads();
+  // per-expert score sums, rows ascending (an expert appears at most once per row)
+  for (int e = tid; e < E; e += kCapThreads) {
+    float s = 0.0f;
+    int c = 0;
+    for (int t = 0; t < T; ++t)
+      for (int j = 0; j < k; ++j)
+        if (li[t * k + j] == e) {
+          s = s + scores[static_cast<int64_t>(t) * E + e];
+          ++c;
+        }
+    sum[e] = s;
+    cnt[e] = c;
+    if (c > 0) atomicAdd(&union_size, 1);
+  }
+  __syncthreads();
+  if (union_size <= budget) return;                 // the union fits: unchanged
+  // rank by score (descending), ties to the lower id; keep the first `budget`
+  for (int e = tid; e < E; e += kCapThreads) {
+    const float se = sum[e];
+    int rank = 0;
+    for (int f = 0; f < E; ++f) {
+      const float sf = sum[f];
+      rank += (sf > se || (sf == se && f < e)) ? 1 : 0;
+    }
+    keep[e] = rank < budget ? 1 : 0;
+  }
+  __syncthreads();
+  // rows: kept mask, rescue, renormalised weights (slots in the reference's order)
+  for (int t = tid; t < T; t += kCapThreads) {
+    float wr[16], kw[16];
+    bool kept[16];
+    bool any = false;
+    for (int r = 0; r < k; ++r) {                   // r: reference slot = build slot k-1-r
+      const int j = k - 1 - r;
+      const int e = li[t * k + j];
+      wr[r] = w[static_cast<int64_t>(t) * k + j];
+      kept[r] = e >= 0 && e < E && keep[e];
+      any = any || kept[r];
+    }
+    if (!any && !strict) {
+      int best = 0;
+      for (int r = 1; r < k; ++r)
+        if (wr[r] > wr[best]) best = r;             // first maximum in the reference's order
+      kept[best] = true;
+    }
+    for (int r = 0; r < k; ++r) kw[r] = kept[r] ? wr[r] : 0.0f;
+    const float scale = numpy_row_sum(wr, k) / (numpy_row_sum(kw, k) + 1e-20f);
+    for (int r = 0; r < k; ++r) {
+      const int j = k - 1 - r;
+      const int64_t o = static_cast<int64_t>(t) * k + j;
+      w[o] = kw[r] * scale;
+      if (!kept[r]) idx[o] = -1;
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_route(const dsk_moe_desc& d, const void* x, const void* gate_w,
@@ -307,6 +414,16 @@ hipError_t launch_route_dispatch(const dsk_moe_desc& d, const RouteArgs& a, hipS
 hipError_t launch_gate_scores(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s) {
   const GateArgs g = route_gate_args(d, a);
   return d.tokens >= 16 ? launch_gate<4, 4, false>(d, g, s) : launch_gate<1, 1, false>(d, g, s);
+}
+
+size_t cap_union_lds(int T, int E, int k) {
+  return static_cast<size_t>(T) * k * 4 + static_cast<size_t>(E) * 9;
+}
+
+hipError_t launch_cap_union(const float* scores, int32_t* idx, float* w, int T, int E, int k, int budget,
+                            int strict, hipStream_t s) {
+  launch_kernel(k_cap_union, 1, kCapThreads, cap_union_lds(T, E, k), s, scores, idx, w, T, E, k, budget, strict);
+  return hipGetLastError();
 }
 
 }  // namespace dsk

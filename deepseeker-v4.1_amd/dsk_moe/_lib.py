@@ -58,6 +58,7 @@ SIGNATURES = {
     "dsk_workspace_size": (ctypes.c_int, [PDesc, ctypes.POINTER(_sz)]),
     "dsk_route": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "dsk_dispatch": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "dsk_cap_union": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "dsk_experts": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "dsk_moe_forward": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -71,6 +72,7 @@ SIGNATURES = {
     "dsk_fp4_quantize": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "dsk_q3_quantize": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "dsk_q3_dequant": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp]),
+    "dsk_q3_repack": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp]),
     "dsk_fp8_block_dequant": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _i32, _vp]),
     "dsk_rmsnorm": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, ctypes.c_float, _i32, _vp, _vp, _vp]),
 }

@@ -22,12 +22,19 @@ Arguments as in the reference:
   reference's ``argsort`` tail), ``layer_id``, ``prefetch_fn(layer, experts)``
   (called with the unique experts, for callers that track residency).
 
+``union_budget > 0`` on a batch of more than one row caps the batch's
+expert union as the reference's ``cap_union`` does (``:213-254, 294-305``),
+on the device (``dsk_cap_union``): the ``union_budget`` experts with the
+largest summed gate score are kept, dropped slots become -1 (the dispatch
+skips them) and each row keeps its weight sum; ``union_strict`` drops the
+one-expert rescue of rows that would lose everything; ``route_stats``
+(``{"coverage", "calls"}``) accumulates the retained weight share per row.
+
 Options of the reference that only concern SSD paging or MLX scheduling are
 accepted and have no effect on the result, which the reference documents as
 identical with or without them: ``pipeline``, ``async_submit_fn``,
 ``async_finalize_fn`` (``:273-285``), ``pinned_gather_fn`` (``:313-321``) and
-``stack_gateup`` (``:140-156``).  ``union_budget > 0`` (``cap_union``, which
-changes routing) is not implemented and raises.
+``stack_gateup`` (``:140-156``).
 
 Extensions (keyword-only): ``score_func`` ("sqrtsoftplus", the reference's
 default, or "sigmoid"), ``route_scale`` (reference default 1.5), ``out``.
@@ -41,7 +48,18 @@ import torch
 
 from . import _lib
 from .bank import ResidentBank, SharedExpert
+from .ops import cap_union as _cap_union
 from .ops import make_desc, ptr, require_device, stream_of, workspace, workspace_size
+
+
+def _coverage(w_before: torch.Tensor, idx_capped: torch.Tensor) -> float:
+    """Share of the batch's gate weight the cap retained (before rescaling), summed as
+    the reference does (numpy float32, its slot order: ascending key)."""
+    import numpy as np
+    wb = w_before.cpu().numpy()[:, ::-1]
+    kept = idx_capped.cpu().numpy()[:, ::-1] >= 0
+    total = float(wb.sum())
+    return float(np.where(kept, wb, np.float32(0.0)).sum()) / total if total > 0 else 1.0
 
 
 def _roles_of(weights) -> tuple:
@@ -88,10 +106,7 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
               score_func: str = "sqrtsoftplus", route_scale: float = 1.5,
               out: torch.Tensor | None = None) -> torch.Tensor:
     """MoE layer forward on the GPU; returns ``[T, H]`` in x's dtype."""
-    if union_budget > 0:
-        raise NotImplementedError("union_budget > 0 (cap_union) is not implemented")
-    del route_stats, union_strict, pipeline, async_submit_fn, async_finalize_fn
-    del pinned_gather_fn, stack_gateup
+    del pipeline, async_submit_fn, async_finalize_fn, pinned_gather_fn, stack_gateup
     dev = require_device(x, gate_w, gate_b)
     if x.dim() != 2:
         raise ValueError(f"x must be [T, H], got {tuple(x.shape)}")
@@ -117,7 +132,9 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
         if out.shape != x.shape or out.dtype != x.dtype:
             raise ValueError("out must match x in shape and dtype")
     stream = stream_of(dev)
+    union = union_budget > 0 and t > 1
     need_host = bank is None or trace_hook is not None or prefetch_fn is not None
+    split = need_host or union      # route first, then dispatch + experts
 
     # Route (+ dispatch) first when the host must see the routing.
     idx = torch.empty((t, top_k), dtype=torch.int32, device=dev)
@@ -131,10 +148,17 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
                      inter=probe_inter, inter_shared=shared.inter if shared else 0,
                      score_func=score_func, quant=quant or "fp4", x_dtype=x.dtype,
                      gate_dtype=gate_w.dtype, route_scale=route_scale, limit=limit)
-    if need_host:
+    if split:
         scores = torch.empty((t, e), dtype=torch.float32, device=dev)
         _lib.call("dsk_route", ctypes.byref(desc), ptr(x), ptr(gate_w), ptr(gate_b), ptr(scores),
                   ptr(idx), ptr(w), stream)
+    if union:
+        w_before = w.clone() if route_stats is not None else None
+        _cap_union(scores, idx, w, union_budget, union_strict)
+        if route_stats is not None:
+            route_stats["coverage"] += _coverage(w_before, idx) * t
+            route_stats["calls"] += float(t)
+    if need_host:
         idx_h = idx.cpu()
         uniq = sorted(set(int(v) for v in idx_h.flatten().tolist() if 0 <= v < e))
         if bank is None:
@@ -164,7 +188,7 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
     ws1 = shared.w1 if shared else None
     ws3 = shared.w3 if shared else None
     ws2 = shared.w2 if shared else None
-    if need_host:
+    if split:
         from .ops import dispatch as _dispatch  # local: same device, same stream
         d = _dispatch(idx, e)
         _lib.call("dsk_experts", ctypes.byref(desc), ptr(table), ptr(ws1), ptr(ws3), ptr(ws2),

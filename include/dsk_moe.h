@@ -115,6 +115,23 @@ int dsk_dispatch(const dsk_moe_desc* d, const int32_t* idx, int32_t* counts,
                  int32_t* offsets, int32_t* perm, int32_t* rank, int32_t* active,
                  void* stream);
 
+/* Union cap of a lock-step batch: replaces cap_union
+ * (src/deepseeker/mlx_forward.py:213-254), which moe_layer applies when
+ * union_budget > 0 and the batch has more than one row (:294-305).  In place on
+ * the router's output: idx [T,k] i32 and weights [T,k] f32 in this library's
+ * order (descending key per row), scores [T,E] f32 the un-biased gate scores
+ * that rank the experts.  If the batch's expert union exceeds `budget`, the
+ * `budget` experts with the largest summed score (rows ascending; exact ties
+ * to the lower expert id) are kept, other slots get index -1 and weight 0, a
+ * row left with nothing keeps its largest weight (first maximum in ascending
+ * key order) unless `strict`, and each row is rescaled to its original weight
+ * sum: scale = rowsum(w) / (rowsum(kept) + 1e-20) with numpy's float32 pairwise
+ * row sum in ascending key order.  One block: T*top_k*4 + E*9 bytes must fit
+ * the 160 KB of LDS (DSK_EUNSUPPORTED otherwise).  dsk_dispatch drops the -1
+ * slots. */
+int dsk_cap_union(int32_t tokens, int32_t n_experts, int32_t top_k, int32_t budget, int32_t strict,
+                  const float* scores, int32_t* idx, float* weights, void* stream);
+
 /* Experts + shared expert + combine, given routing and dispatch:
  * replaces the per-expert loop, the shared add and the final cast of
  * moe_layer (src/deepseeker/mlx_forward.py:388-419) and the shared expert
@@ -213,6 +230,17 @@ int dsk_fp4_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* packed
  * cols % 128 == 0. */
 int dsk_q3_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* packed,
                     uint16_t* scales, uint16_t* biases, void* stream);
+
+/* Q3 repack of checkpoint codes into the canonical layout: replaces the read
+ * side of the reference's q3 checkpoints, unpack_int3_affine
+ * (src/deepseeker/mlx_weights.py:119-141) over the U32_Q3_AFFINE tensors that
+ * scripts/requant_experts_3bit.py:69-83, 135-148 writes.  src [rows, 3*cols/8]
+ * bytes (= [rows, 3*cols/32] little-endian u32 words): row-major 3-byte packs,
+ * bytes 3m..3m+2 of a row holding codes 8m..8m+7 as a 24-bit little-endian
+ * integer with code i at bits 3i..3i+2 -> packed [rows, 3*cols/8] in the
+ * canonical layout above (scales and biases are unchanged).  cols % 128 == 0;
+ * src and packed must not overlap. */
+int dsk_q3_repack(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* packed, void* stream);
 
 /* Q3 dequant: replaces mx.dequantize(bits=3, group_size=64)
  * (scripts/requant_experts_3bit.py:74-75); out = f32(s)*q + f32(b). */
