@@ -33,7 +33,6 @@ constexpr int kStSlots = 2;            // experts per routed batch
 constexpr int kStMaxSlots = 16;        // active experts the staged kernel handles
 constexpr int kStRing = 4;             // routed batches in flight per wave
 constexpr int kStRedBytes = 2 * kStW * 64 * 4 * 4;   // wave partial sums, routed and shared
-constexpr int kStStage = 5;            // activation chunks per thread in flight while staging
 
 struct DecodeArgs {
   int T, H, I, Is, k;
@@ -727,10 +726,11 @@ __device__ __forceinline__ void down_epilogue(const DecodeArgs& p, f32x4 a, f32x
 // Down + combine with every routed h row (N = T*k of them) and hs staged in
 // LDS once per block.  Block = 16 output rows, kStW waves; wave w owns the K
 // blocks [kStKB*w, kStKB*w + kStKB) of every expert's w2 rows and of the
-// shared w2 rows.  The activations are staged first, while nothing else is
-// in flight (their latency would otherwise queue behind the weights); then
-// the shared batch and kStRing routed batches of kStSlots experts are all
-// issued, and computed in order as they land.  The MFMA's B columns carry the hi and lo
+// shared w2 rows.  The first NST activation chunks of every thread are loaded
+// first (all of them up to two tokens), then the shared batch and kStRing
+// routed batches of kStSlots experts are all issued, then the activations are
+// written to LDS (each store waits only for its own load, which was issued
+// ahead of the weights), and the batches are computed in order as they land.  The MFMA's B columns carry the hi and lo
 // planes of each token (T <= 8), so one MFMA per K step covers both; four
 // accumulator chains per wave for routed and for shared work, added in
 // order, then the waves in order, then hi + lo.
@@ -803,7 +803,7 @@ __device__ __forceinline__ void mma_down_batch(const DownBatch<Raw>& b, int u0, 
   }
 }
 
-template <typename Raw>
+template <typename Raw, int NST>
 __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) {
   extern __shared__ __align__(16) uint16_t lds_dn[];
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -824,56 +824,73 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
   int* ldrow = reinterpret_cast<int*>(reinterpret_cast<char*>(lds_dn) +   // [U][T] dispatch rows (rowmap copy)
                                       (act_bytes > kStRedBytes ? act_bytes : kStRedBytes));
   const int kb0 = wave * kStKB;
-  // 1. activations and dispatch rows, alone in flight (a short wait), into LDS;
-  // one dispatch-row entry per thread (U * T <= kStMaxSlots * 8 <= kStW * 64)
-  const int rm = p.rowmap[min(tid, U * p.T - 1)];
+  // 16 bytes past the dispatch rows take the stores of chunks past the end
+  uint16_t* dump = reinterpret_cast<uint16_t*>(ldrow + kStMaxSlots * 8);
+  // chunk c < hch: h row c / (I/8); c >= hch: hs row
   const int hch = N * (I / 8), sch = p.T * (Is / 8);
-  // chunk c < hch: h row c / (I/8); c >= hch: hs row; kStStage chunks per thread in flight at once
-  for (int c0 = tid; c0 < hch + sch; c0 += kStStage * kStW * 64) {
-    u32x4 vh[kStStage], vl[kStStage];
+  // global element offset and LDS destinations of chunk c (no branches: selects)
+  auto chunk_src = [&](int c, const uint16_t*& ph, const uint16_t*& pl) {
+    c = min(c, hch + sch - 1);            // chunks past the end re-read the last one
+    const bool shr = c >= hch;
+    const int cs = shr ? c - hch : c, w = shr ? Is / 8 : I / 8, k = shr ? Is : I;
+    ph = shr ? p.hs_hi : p.h_hi;
+    pl = shr ? p.hs_lo : p.h_lo;
+    return static_cast<int64_t>(cs / w) * k + (cs % w) * 8;
+  };
+  auto chunk_dst = [&](int c, uint16_t*& dh, uint16_t*& dl) {
+    const bool shr = c >= hch, past = c >= hch + sch;
+    const int cs = shr ? c - hch : c, w = shr ? Is / 8 : I / 8, stride = shr ? iss : is;
+    const int off = (cs / w) * stride + (cs % w) * 8;
+    dh = past ? dump : (shr ? sh_h : hh) + off;
+    dl = past ? dump : (shr ? sh_l : hl) + off;
+  };
+  // 1. dispatch rows (one entry per thread: U * T <= kStMaxSlots * 8 <= kStW * 64) and the
+  // first NST activation chunks of this thread, loaded ahead of the weights
+  const int rm = p.rowmap[min(tid, U * p.T - 1)];
+  u32x4 vh[NST], vl[NST];
 #pragma unroll
-    for (int j = 0; j < kStStage; ++j) {
-      // no condition on the loads (see load_raw_nc): chunks past the end re-read the last one
-      const int c = min(c0 + j * kStW * 64, hch + sch - 1);
-      const uint16_t* ph = p.h_hi;
-      const uint16_t* pl = p.h_lo;
-      int64_t e = static_cast<int64_t>(c / (I / 8)) * I + (c % (I / 8)) * 8;
-      if (c >= hch) {
-        const int cs = c - hch;
-        ph = p.hs_hi;
-        pl = p.hs_lo;
-        e = static_cast<int64_t>(cs / (Is / 8)) * Is + (cs % (Is / 8)) * 8;
-      }
-      vh[j] = ldg16(ph + e);
-      vl[j] = ldg16(pl + e);
-    }
-#pragma unroll
-    for (int j = 0; j < kStStage; ++j) {
-      const int c = c0 + j * kStW * 64;
-      if (c < hch) {
-        const int off = (c / (I / 8)) * is + (c % (I / 8)) * 8;
-        *reinterpret_cast<u32x4*>(hh + off) = vh[j];
-        *reinterpret_cast<u32x4*>(hl + off) = vl[j];
-      } else if (c < hch + sch) {
-        const int cs = c - hch;
-        const int off = (cs / (Is / 8)) * iss + (cs % (Is / 8)) * 8;
-        *reinterpret_cast<u32x4*>(sh_h + off) = vh[j];
-        *reinterpret_cast<u32x4*>(sh_l + off) = vl[j];
-      }
-    }
+  for (int j = 0; j < NST; ++j) {
+    const uint16_t *ph, *pl;
+    const int64_t e = chunk_src(tid + j * kStW * 64, ph, pl);
+    vh[j] = ldg16(ph + e);
+    vl[j] = ldg16(pl + e);
   }
-  wait_vm_all();   // only staging loads outstanding (see wait_vm_all)
-  if (tid < U * p.T) ldrow[tid] = rm;
-  // 2. every weight of the block in flight: the shared batch and kStRing routed batches
+  __builtin_amdgcn_sched_barrier(0);   // these loads go out before the weights
+  // 2. every weight of the block in flight: the shared batch and kStRing routed batches,
+  // all without conditions, so the compiler knows exactly how many loads follow the
+  // activation loads and each activation store waits for its own load only (batches
+  // past U re-read slot 0 and are not computed; without a shared expert its batch
+  // re-reads the start of h)
   RawBF16 rs[kStKB];
-  if (Is > 0) {
+  {
+    const bool sh = Is > 0;
+    const uint16_t* W = sh ? p.ws2 : p.h_hi;
 #pragma unroll
-    for (int j = 0; j < kStKB; ++j) load_raw_nc(rs[j], p.ws2, row, Is, min((kb0 + j) * 128 + g4 * 32, Is - 32));
+    for (int j = 0; j < kStKB; ++j)
+      load_raw_nc(rs[j], W, sh ? row : 0u, sh ? Is : 0, sh ? min((kb0 + j) * 128 + g4 * 32, Is - 32) : 0);
   }
   DownBatch<Raw> ring[kStRing];
 #pragma unroll
-  for (int q = 0; q < kStRing; ++q)
-    if (q * kStSlots < U) load_down_batch(ring[q], p, q * kStSlots, U, row, kb0, g4);
+  for (int q = 0; q < kStRing; ++q) load_down_batch(ring[q], p, q * kStSlots, U, row, kb0, g4);
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. the activations into LDS: the first NST chunks from registers (each store
+  // waits for its own load only), any further chunks (more than two tokens) after
+#pragma unroll
+  for (int j = 0; j < NST; ++j) {
+    uint16_t *dh, *dl;
+    chunk_dst(tid + j * kStW * 64, dh, dl);
+    *reinterpret_cast<u32x4*>(dh) = vh[j];
+    *reinterpret_cast<u32x4*>(dl) = vl[j];
+  }
+  if (tid < U * p.T) ldrow[tid] = rm;
+  for (int c = tid + NST * kStW * 64; c < hch + sch; c += kStW * 64) {
+    const uint16_t *ph, *pl;
+    const int64_t e = chunk_src(c, ph, pl);
+    uint16_t *dh, *dl;
+    chunk_dst(c, dh, dl);
+    *reinterpret_cast<u32x4*>(dh) = ldg16(ph + e);
+    *reinterpret_cast<u32x4*>(dl) = ldg16(pl + e);
+  }
   __syncthreads();
   // B column r16: plane r16 & 1 (hi, lo) of token r16 >> 1
   const int t = r16 >> 1;
@@ -1352,15 +1369,20 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   }
   const size_t act = static_cast<size_t>(n_rows) * (d.inter + 8) * 4 +
                      static_cast<size_t>(d.tokens) * (d.inter_shared + 8) * 4;
-  const size_t dn_lds = (act > kStRedBytes ? act : kStRedBytes) + static_cast<size_t>(max_u) * d.tokens * 4;
+  // activations (or the wave sums), dispatch rows [kStMaxSlots * 8], 16 bytes for chunks past the end
+  const size_t dn_lds = (act > kStRedBytes ? act : kStRedBytes) + kStMaxSlots * 8 * 4 + 16;
   // staged: all activations fit in LDS, each wave's K blocks cover I (and
   // Is), few enough experts, and at most 8 tokens (two B columns each)
   const bool staged = dn_lds <= kMaxLds && max_u <= kStMaxSlots && d.tokens <= 8 &&
                       d.inter == kStW * kStKB * 128 && d.inter_shared <= kStW * kStKB * 128;
   for (int r = 0; r < repeat; ++r) {
     const unsigned blocks = static_cast<unsigned>(d.hidden / 16);
-    if (staged && q3) launch_kernel(k_down_decode_staged<RawQ3>, blocks, kStW * 64, dn_lds, s, p);
-    else if (staged) launch_kernel(k_down_decode_staged<RawFP4>, blocks, kStW * 64, dn_lds, s, p);
+    // activation chunks per thread: all of them in the first round up to two tokens
+    const int chunks = (n_rows * (d.inter / 8) + d.tokens * (d.inter_shared / 8) + kStW * 64 - 1) / (kStW * 64);
+    if (staged && q3 && chunks <= 5) launch_kernel(k_down_decode_staged<RawQ3, 5>, blocks, kStW * 64, dn_lds, s, p);
+    else if (staged && q3) launch_kernel(k_down_decode_staged<RawQ3, 9>, blocks, kStW * 64, dn_lds, s, p);
+    else if (staged && chunks <= 5) launch_kernel(k_down_decode_staged<RawFP4, 5>, blocks, kStW * 64, dn_lds, s, p);
+    else if (staged) launch_kernel(k_down_decode_staged<RawFP4, 9>, blocks, kStW * 64, dn_lds, s, p);
     else if (q3) launch_kernel(k_down_decode<RawQ3>, blocks, kDownW * 64, 0, s, p);
     else launch_kernel(k_down_decode<RawFP4>, blocks, kDownW * 64, 0, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
