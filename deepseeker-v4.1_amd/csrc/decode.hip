@@ -31,7 +31,11 @@ constexpr int kStW = 8;                // waves
 constexpr int kStKB = 2;               // K blocks of each expert per wave (I = kStW * kStKB * 128)
 constexpr int kStSlots = 2;            // experts per routed batch
 constexpr int kStMaxSlots = 16;        // active experts the staged kernel handles
-constexpr int kStRing = 4;             // routed batches in flight per wave
+// routed batches in flight per wave: one (the next is loaded once the current one
+// has landed).  Every CU asking for all of its weights at once was slower at one
+// token (down 17.2 us) than one batch at a time (15.3 us): the products of a batch
+// then overlap the later batches' loads instead of waiting for the last byte.
+constexpr int kStRing = 1;
 constexpr int kStRedBytes = 2 * kStW * 64 * 4 * 4;   // wave partial sums, routed and shared
 
 struct DecodeArgs {
@@ -319,10 +323,10 @@ __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
 // Routed gate/up of the decode pipeline.  Each block takes kUpItems row
 // tiles of one active expert, kUpKS waves per tile, each streaming one K
 // range of its FP4 (or q3) w1/w3 rows in batches of G K blocks;
-// h[drow] = SwiGLU(gate, up) * route weight.  Two batches are in flight per
-// wave; the tokens' activations are loaded before the weights and written to
-// LDS after the weight loads have been issued; K ranges are added in wave
-// order.
+// h[drow] = SwiGLU(gate, up) * route weight.  The first batch is issued with
+// the tokens' activations, which are written to LDS once the batch is in
+// flight; the next batch goes out when the first is about to be used, so two
+// are in flight from then on (FP4); K ranges are added in wave order.
 template <int G, bool kWin, bool kF32, bool kQ3>
 __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 ? 3 : 4))) void k_up_stream(DecodeArgs p) {
   extern __shared__ __align__(16) uint16_t lds_up[];
@@ -431,14 +435,15 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
       if (kb + 3 * G < k1) ld(b1, b3, bw, kb + 3 * G);
     }
   } else {
-    // weights: two batches in flight
+    // weights: up to two batches in flight
     const uint8_t* W1 = static_cast<const uint8_t*>(d->p[0]);
     const uint8_t* S1 = static_cast<const uint8_t*>(d->p[1]);
     const uint8_t* W3 = static_cast<const uint8_t*>(d->p[3]);
     const uint8_t* S3 = static_cast<const uint8_t*>(d->p[4]);
+    // the second batch is issued after the barrier, when the first is about to be
+    // used (both issued up front: 17.9 us at one token; this way 17.3 us)
     UpBatch<G> A, B;
     load_batch<G, kWin>(A, W1, S1, W3, S3, row, K, k0, k1, g4, rok);
-    load_batch<G, kWin>(B, W1, S1, W3, S3, row, K, k0 + G, k1, g4, rok);
     if (xreg) put_staged_x<kF32, kUpW * 64>(p, xh, xl, xs, tid, xv);
     wr = tv ? p.wrow[drow] : 0.0f;
     uint8_t* xch = reinterpret_cast<uint8_t*>(red + kUpItems) + wave * 640;
@@ -446,6 +451,7 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
     const uint16_t* bh = xh + (tv ? r16 : 0) * xs;
     const uint16_t* bl = xl + (tv ? r16 : 0) * xs;
     for (int kb = k0; kb < k1; kb += 2 * G) {
+      if (kb == k0) load_batch<G, kWin>(B, W1, S1, W3, S3, row, K, k0 + G, k1, g4, rok);
       batch_scales<G, kWin>(A, xch, r16, g4);
       mma_batch<G>(A, bh, bl, K, kb, k1, g4, tv, f32, ag, au);
       if (kb + 2 * G < k1) load_batch<G, kWin>(A, W1, S1, W3, S3, row, K, kb + 2 * G, k1, g4, rok);
