@@ -78,6 +78,9 @@ Workspace workspace_layout(const dsk_moe_desc& d) {
   L.h_lo = take(N * I * 2);
   L.hs_hi = take(T * Is * 2);
   L.hs_lo = take(T * Is * 2);
+  const bool mx = mx_decode(d);
+  L.hq = take(mx ? N * 3 * T * I : 0);
+  L.hqs = take(mx ? N * 3 * T * (I / 32) : 0);
   L.y = take(N * H * 4);
   L.ys = take(T * H * 4);
   L.pf_tiles = take(prefill_gemm(d) ? (2 + 2 * static_cast<size_t>(prefill_max_tiles(d))) * 4 : 0);

@@ -13,6 +13,7 @@
 // combine of the reference's moe_layer (src/deepseeker/mlx_forward.py:388-419,
 // src/deepseeker/mlx_runner.py:765-783).
 #include "block_route.h"
+#include "mx.h"
 #include "tile.h"
 
 namespace dsk {
@@ -50,6 +51,7 @@ struct DecodeArgs {
   const uint16_t* ws1; const uint16_t* ws3;   // shared w1, w3 [Is][H] bf16
   uint16_t* hs_hi; uint16_t* hs_lo;    // [T][Is]
   uint16_t* h_hi; uint16_t* h_lo;      // [T*k][I] by dispatch row
+  uint8_t* hq; uint8_t* hqs;           // MX: [slot][3T][I] FP8 planes, [slot][3T][I/32] E8M0
   const uint16_t* ws2;                 // shared w2 [H][Is] bf16
   const void* shared_out;              // precomputed shared output [T][H] (x dtype) or null
   void* out;                           // [T][H] x dtype
@@ -481,7 +483,188 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(kF32 
   }
 }
 
-// ---------------------------------------------------------------- q3 gate/up, factored
+// ---------------------------------------------------------------- MX gate/up (FP4, bf16 x, T <= 2)
+// LDS of k_up_mx: K-range partial sums [kUpItems][kUpKS][2][64][4] f32, the
+// waves' scale-exchange tiles [kUpW][640] bytes, the 32-row maxima
+// [kUpItems][kMxMaxTokens] f32, then the activation planes xq [H/128][2T][128]
+// and their E8M0 bytes xe [H/128][2T][4].
+static_assert(kUpItems * 16 == 32, "a gate/up block's row tiles are one 32-row exponent group of h");
+static_assert(kStW * kStKB * 128 == kMxInter, "the MX down kernel's waves cover the intermediate");
+constexpr size_t kMxUpRedBytes = kUpItems * kUpKS * 2 * 64 * 4 * 4;
+constexpr size_t kMxUpXchOffset = kMxUpRedBytes;
+constexpr size_t kMxUpMaxOffset = kMxUpXchOffset + kUpW * 640;
+constexpr size_t kMxUpXqOffset = kMxUpMaxOffset + kUpItems * kMxMaxTokens * 4;
+
+// One activation chunk (8 bf16 values at K offset k8 of token t) into the
+// B-operand planes of the MX gate/up: column 2t + p holds plane p, and each
+// 32-value group's first plane has exponent ilogb(max) - 7.  The group's four
+// chunks are in consecutive lanes, and every lane of the wave takes part in
+// the max exchange (ok: this lane's chunk exists and is stored).
+__device__ __forceinline__ void put_x_mx(uint8_t* xq, uint8_t* xe, int T, int t, int k8, const u32x4& v,
+                                         bool ok) {
+  const float f0[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
+  const float f1[4] = {__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
+                       __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u)};
+  float m = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) m = fmaxf(m, fmaxf(fabsf(f0[q]), fabsf(f1[q])));
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  const int e = fp8_plane_exp(m);
+  uint32_t w0[2], w1[2];
+  fp8_planes4<2>(f0, e, w0);
+  fp8_planes4<2>(f1, e, w1);
+  if (ok) {
+    const int kb = k8 >> 7, kk = k8 & 127;
+#pragma unroll
+    for (int pl = 0; pl < 2; ++pl) {
+      const int col = kb * 2 * T + 2 * t + pl;
+      *reinterpret_cast<uint2*>(xq + col * 128 + b_perm(kk)) = uint2{w0[pl], w1[pl]};
+      if ((kk & 31) == 0) xe[col * 4 + (kk >> 5)] = static_cast<uint8_t>(e8m0_byte(e - 4 * pl));
+    }
+  }
+}
+
+// Routed gate/up of the decode pipeline for FP4 experts and one or two bf16
+// tokens, on scaled FP4 x FP8 MFMAs (mx.h).  Blocks, waves, K ranges and the
+// weight stream are those of k_up_stream (two batches of G K blocks, scale
+// windows); the activations are staged in LDS as two FP8 planes per token
+// (B column 2t + p), so one v_mfma_scale_f32_16x16x128_f8f6f4 per K block
+// and role takes the FP4 codes and their E8M0 bytes as loaded.  The K ranges
+// are added in wave order, then a token's two plane columns; h = SwiGLU(gate,
+// up) * route weight (0 for a token not routed to the slot) leaves as three
+// FP8 planes per (slot, token) with one exponent per 32-row group -- the two
+// row tiles of a block -- in the B-operand layout of k_down_mx.
+template <int G>
+__global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_up_mx(DecodeArgs p) {
+  extern __shared__ __align__(16) uint16_t lds_up[];
+  const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int groups = (p.up_tiles + kUpItems - 1) / kUpItems;
+  const int rb = static_cast<int>(blockIdx.x);
+  const int slot = rb / groups;
+  if (slot >= p.active[0]) return;
+  const int T = p.T, K = p.H;
+  const int item = wave / kUpKS, ks = wave % kUpKS;
+  const int rt = (rb % groups) * kUpItems + item;
+  const bool rok = rt < p.up_tiles;
+  char* base = reinterpret_cast<char*>(lds_up);
+  float (*red)[kUpKS][2][64][4] = reinterpret_cast<float (*)[kUpKS][2][64][4]>(base);
+  uint8_t* xch = reinterpret_cast<uint8_t*>(base + kMxUpXchOffset) + wave * 640;
+  float* gmax = reinterpret_cast<float*>(base + kMxUpMaxOffset);
+  uint8_t* xq = reinterpret_cast<uint8_t*>(base + kMxUpXqOffset);
+  const int nblk = K / 128;
+  uint8_t* xe = xq + nblk * 2 * T * 128;
+  // 1. the first two activation chunks of this thread, ahead of the weights
+  const int cpr = K / 8, xchunks = T * cpr;
+  constexpr int NT = kUpW * 64;
+  u32x4 xv[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = min(tid + j * NT, xchunks - 1);   // no condition on the load (see load_raw_nc)
+    xv[j] = ldg16(static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8);
+  }
+  // 2. the first weight batch
+  const SlotDesc* d = p.desc + slot;
+  const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
+  const int per = (nblk + kUpKS - 1) / kUpKS;
+  const int k0 = min(ks * per, nblk), k1 = min(k0 + per, nblk);
+  const uint8_t* W1 = static_cast<const uint8_t*>(d->p[0]);
+  const uint8_t* S1 = static_cast<const uint8_t*>(d->p[1]);
+  const uint8_t* W3 = static_cast<const uint8_t*>(d->p[3]);
+  const uint8_t* S3 = static_cast<const uint8_t*>(d->p[4]);
+  UpBatch<G> A, B;
+  load_batch<G, true>(A, W1, S1, W3, S3, row, K, k0, k1, g4, rok);
+  // 3. the activations as FP8 planes (chunk rounds of the whole block, so that
+  // the lanes of a 32-group are all present in each round)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = tid + j * NT;
+    put_x_mx(xq, xe, T, min(c, xchunks - 1) / cpr, (min(c, xchunks - 1) % cpr) * 8, xv[j], c < xchunks);
+  }
+  for (int c0 = 2 * NT; c0 < xchunks; c0 += NT) {
+    const int c = min(c0 + tid, xchunks - 1);
+    const u32x4 v = ldg16(static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8);
+    put_x_mx(xq, xe, T, c / cpr, (c % cpr) * 8, v, c0 + tid < xchunks);
+  }
+  __syncthreads();
+  // B column of this lane: plane r16 & 1 of token r16 >> 1 (columns past 2T
+  // repeat the last one; their results are not used)
+  const int bc = min(r16, 2 * T - 1);
+  f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
+  auto mm = [&](UpBatch<G>& b, int kb) {
+    batch_scales<G, true>(b, xch, r16, g4);
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      if (kb + i < k1) {
+        const int col = (kb + i) * 2 * T + bc;
+        const u32x4* src = reinterpret_cast<const u32x4*>(xq + col * 128 + g4 * 32);
+        const u32x4 blo = src[0], bhi = src[1];
+        const uint32_t bs = xe[col * 4 + g4];
+        ag = mx_mfma(b.c1[i], b.s1[i], blo, bhi, bs, ag);
+        au = mx_mfma(b.c3[i], b.s3[i], blo, bhi, bs, au);
+      }
+    }
+  };
+  for (int kb = k0; kb < k1; kb += 2 * G) {
+    if (kb == k0) load_batch<G, true>(B, W1, S1, W3, S3, row, K, k0 + G, k1, g4, rok);
+    mm(A, kb);
+    if (kb + 2 * G < k1) load_batch<G, true>(A, W1, S1, W3, S3, row, K, kb + 2 * G, k1, g4, rok);
+    if (kb + G < k1) mm(B, kb + G);
+    if (kb + 3 * G < k1) load_batch<G, true>(B, W1, S1, W3, S3, row, K, kb + 3 * G, k1, g4, rok);
+  }
+  // 4. K ranges added in order ((r0 + r1) + r2) + r3, then the two plane columns
+  *reinterpret_cast<f32x4*>(&red[item][ks][0][lane][0]) = ag;
+  *reinterpret_cast<f32x4*>(&red[item][ks][1][lane][0]) = au;
+  __syncthreads();
+  const int t = r16 >> 1;
+  float hv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (ks == 0) {
+#pragma unroll
+    for (int w = 1; w < kUpKS; ++w) {
+      ag += *reinterpret_cast<const f32x4*>(&red[item][w][0][lane][0]);
+      au += *reinterpret_cast<const f32x4*>(&red[item][w][1][lane][0]);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ag[q] += __shfl_xor(ag[q], 1, 64);
+      au[q] += __shfl_xor(au[q], 1, 64);
+    }
+    const int drow = t < T ? p.rowmap[slot * T + t] : -1;
+    const bool tv = drow >= 0 && rok;
+    const float wr = tv ? p.wrow[drow] : 0.0f;
+    float m = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      hv[q] = tv ? silu_clamped(ag[q], au[q], p.limit) * wr : 0.0f;
+      m = fmaxf(m, fabsf(hv[q]));
+    }
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (lane < 2 * T && (lane & 1) == 0) gmax[item * kMxMaxTokens + t] = m;
+  }
+  __syncthreads();
+  if (ks == 0 && rok && (r16 & 1) == 0 && t < T) {
+    // one exponent per 32-row group: the block's two row tiles
+    float mg = gmax[t];
+#pragma unroll
+    for (int it = 1; it < kUpItems; ++it) mg = fmaxf(mg, gmax[it * kMxMaxTokens + t]);
+    const int e = fp8_plane_exp(mg);
+    uint32_t w[3];
+    fp8_planes4<3>(hv, e, w);
+    const int I = p.I, r = rt * 16 + 4 * g4;
+    const int64_t col = static_cast<int64_t>(slot) * 3 * T + 3 * t;
+    uint8_t* dst = p.hq + (r >> 7) * 128 + b_perm(r & 127);
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) *reinterpret_cast<uint32_t*>(dst + (col + pl) * I) = w[pl];
+    if (item == 0 && g4 == 0) {
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl) p.hqs[(col + pl) * (I / 32) + rt / kUpItems] = static_cast<uint8_t>(e8m0_byte(e - 4 * pl));
+    }
+  }
+}
+
 // ---------------------------------------------------------------- q3 gate/up, factored
 constexpr int kQ3fItems = 1;                      // row tiles of a block
 constexpr int kQ3fKS = 8;                         // K ranges of a row tile (one wave each)
@@ -945,6 +1128,163 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
   }
 }
 
+// ---------------------------------------------------------------- MX down (FP4, T <= 2)
+constexpr int kMxSlots = 8;   // routed experts per round of k_down_mx (all of them at one token)
+
+// Wave-private LDS of k_down_mx, after the wave partial sums: the round's h
+// planes of the wave's two K blocks [kMxSlots][3T][256 B] (B-operand order),
+// their E8M0 windows [kMxSlots][3T][8 B] (rounded up to 256 B) and the hs
+// hi / lo planes of the wave's K range [2T][256] bf16.
+constexpr int mx_dn_h_bytes(int T) { return kMxSlots * 3 * T * 256; }
+constexpr int mx_dn_s_bytes(int T) { return (kMxSlots * 3 * T * 8 + 255) / 256 * 256; }
+constexpr int mx_dn_wave_bytes(int T) { return mx_dn_h_bytes(T) + mx_dn_s_bytes(T) + 2 * T * 512; }
+static_assert((kMxSlots * 3) % 4 == 0, "h DMA instructions cover whole (slot, column) pairs");
+
+// Down + combine of the decode pipeline for FP4 experts and T (one or two)
+// tokens on scaled FP4 x FP8 MFMAs.  Block = 16 output rows, kStW waves;
+// wave w owns the K blocks [kStKB*w, kStKB*w + kStKB) of every active
+// expert's w2 rows and of the shared w2 rows.  Everything of a round of
+// kMxSlots experts is in flight at once: first the wave's slices of the FP8 h
+// planes k_up_mx wrote (B column 3t + p: plane p of token t; zero planes for a
+// token not routed to the slot), of their E8M0 windows and of the hs planes,
+// 16 contiguous bytes per lane, then the shared w2 rows and every expert's w2
+// codes and scale windows.  The slices go to wave-private LDS as they land
+// (each store waits for its own load), and each expert is computed as its
+// weights land, one v_mfma_scale_f32_16x16x128_f8f6f4 per K block with the B
+// operand read back from LDS.  Slots past the active count re-read slot 0
+// and are computed with zero codes (straight-line code, so that every wait is
+// for the loads it needs only).  Shared: bf16 MFMAs on the hs hi / lo columns
+// (2t + plane).  Four routed accumulator chains added in order, the waves in
+// order, then a token's plane columns ((p0 + p1) + p2; hi + lo) and the final
+// add and cast.
+template <int T>
+__global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
+  extern __shared__ __align__(16) uint8_t lds_mx[];
+  constexpr int C = 3 * T;
+  float (*red)[kStW][64][4] = reinterpret_cast<float (*)[kStW][64][4]>(lds_mx);
+  const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int row0 = blockIdx.x * 16;
+  const uint32_t row = static_cast<uint32_t>(row0 + r16);
+  const int U = p.active[0];
+  const int I = p.I, Is = p.Is;
+  const int kb0 = wave * kStKB;
+  uint8_t* hl = lds_mx + kStRedBytes + wave * mx_dn_wave_bytes(T);   // [kMxSlots][C][256]
+  uint8_t* sl = hl + mx_dn_h_bytes(T);                                // [kMxSlots][C][8]
+  uint16_t* hsl = reinterpret_cast<uint16_t*>(sl + mx_dn_s_bytes(T));  // [2T][256]
+  // B columns of this lane (past the last one, repeats of it; their results are not used)
+  const int bc = min(r16, C - 1), sc = min(r16, 2 * T - 1);
+  // 1. the wave's hs slice (column 2t + plane, 256 values from K = 128 kb0, clamped
+  // into the row) and the shared w2 rows; without a shared expert both read the
+  // start of the h planes and are not computed
+  const bool sh = Is > 0;
+  const uint16_t* dummy = reinterpret_cast<const uint16_t*>(p.hq);
+  u32x4 hsv[T];
+#pragma unroll
+  for (int q = 0; q < T; ++q) {
+    const int col = 2 * q + (lane >> 5);
+    const uint16_t* src = ((col & 1) ? p.hs_lo : p.hs_hi) + (col >> 1) * Is + min(kb0 * 128 + (lane & 31) * 8, Is - 8);
+    hsv[q] = ldg16(sh ? src : dummy);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  RawBF16 rs[kStKB];
+#pragma unroll
+  for (int j = 0; j < kStKB; ++j)
+    load_raw_nc(rs[j], sh ? p.ws2 : dummy, sh ? row : 0u, sh ? Is : 0, sh ? min((kb0 + j) * 128 + g4 * 32, Is - 32) : 0);
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[4] = {z, z, z, z}, accs[4] = {z, z, z, z};
+  auto round = [&](int u0, auto first) {
+    // 2. the round's h planes and E8M0 windows (slots past U re-read slot 0):
+    // lane l takes 16 bytes of (slot, column) pair 4q + l / 16, 4 bytes of pair 32q + l / 2
+    constexpr int NH = kMxSlots * C / 4, NS = mx_dn_s_bytes(T) / 256;
+    u32x4 hv[NH];
+    uint32_t sv[NS];
+#pragma unroll
+    for (int q = 0; q < NH; ++q) {
+      const int pair = 4 * q + (lane >> 4), i = pair / C, c = pair - i * C;
+      const int su = u0 + i < U ? u0 + i : 0;
+      hv[q] = ldg16(p.hq + static_cast<uint32_t>(su * C + c) * static_cast<uint32_t>(I) + kb0 * 128 + (lane & 15) * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      const int pair = min(32 * q + (lane >> 1), kMxSlots * C - 1), i = pair / C, c = pair - i * C;
+      const int su = u0 + i < U ? u0 + i : 0;
+      sv[q] = ldg<uint32_t>(p.hqs + static_cast<uint32_t>(su * C + c) * static_cast<uint32_t>(I / 32) + kb0 * 4 + 4 * (lane & 1));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. every expert's w2 codes and scale windows
+    u32x4 wc[kMxSlots][kStKB];
+    u32x2 ws[kMxSlots];
+#pragma unroll
+    for (int i = 0; i < kMxSlots; ++i) {
+      const int su = u0 + i < U ? u0 + i : 0;
+      const uint8_t* W = static_cast<const uint8_t*>(desc_ptr(p.desc, su, 6));
+      const uint8_t* S = static_cast<const uint8_t*>(desc_ptr(p.desc, su, 7));
+#pragma unroll
+      for (int j = 0; j < kStKB; ++j) wc[i][j] = ldg16(W + row * static_cast<uint32_t>(I / 2) + (kb0 + j) * 64 + g4 * 16);
+      ws[i] = ldg<u32x2>(S + row * static_cast<uint32_t>(I / 32) + kb0 * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 4. the slices into the wave's LDS (in the lane order they were loaded)
+    if constexpr (decltype(first)::value) {
+#pragma unroll
+      for (int q = 0; q < T; ++q) *reinterpret_cast<u32x4*>(hsl + q * 512 + lane * 8) = hsv[q];
+    }
+#pragma unroll
+    for (int q = 0; q < NH; ++q) *reinterpret_cast<u32x4*>(hl + q * 1024 + lane * 16) = hv[q];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) *reinterpret_cast<uint32_t*>(sl + q * 256 + lane * 4) = sv[q];
+    // 5. the shared product (first round), then the experts in slot order as they land
+    if constexpr (decltype(first)::value) {
+#pragma unroll
+      for (int j = 0; j < kStKB; ++j) {
+        // K blocks past the shared intermediate (and all of them without one) add zero
+        const bool ok = (kb0 + j) * 128 < Is;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const u32x4 b = *reinterpret_cast<const u32x4*>(hsl + sc * 256 + j * 128 + g4 * 32 + 8 * jj);
+          accs[jj] = mfma16(a_operand(rs[j], jj), ok ? as_bf16x8(b) : bf16x8{}, accs[jj]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kMxSlots; ++i) {
+      const bool live = u0 + i < U;
+#pragma unroll
+      for (int j = 0; j < kStKB; ++j) {
+        const uint8_t* src = hl + (i * C + bc) * 256 + j * 128 + g4 * 32;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(src);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(src + 16);
+        const uint32_t hs = sl[(i * C + bc) * 8 + 4 * j + g4];
+        const uint32_t wsb = ((j == 0 ? ws[i].x : ws[i].y) >> (8 * g4)) & 0xffu;
+        const u32x4 codes = live ? wc[i][j] : u32x4{0u, 0u, 0u, 0u};
+        acc[(2 * i + j) & 3] = mx_mfma(codes, wsb, lo, hi, hs, acc[(2 * i + j) & 3]);
+      }
+    }
+  };
+  round(0, std::true_type{});
+  for (int u0 = kMxSlots; u0 < U; u0 += kMxSlots) round(u0, std::false_type{});
+  *reinterpret_cast<f32x4*>(&red[0][wave][lane][0]) = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+  *reinterpret_cast<f32x4*>(&red[1][wave][lane][0]) = ((accs[0] + accs[1]) + accs[2]) + accs[3];
+  __syncthreads();
+  if (wave == 0) {
+    f32x4 a = z, shv = z;
+    for (int w = 0; w < kStW; ++w) {
+      a += *reinterpret_cast<const f32x4*>(&red[0][w][lane][0]);
+      shv += *reinterpret_cast<const f32x4*>(&red[1][w][lane][0]);
+    }
+    // token t = r16 of this lane group: routed columns 3t .. 3t + 2, shared 2t, 2t + 1
+    const int t = min(r16, T - 1), gb = lane & 48;
+    f32x4 ra, rsh;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ra[q] = (__shfl(a[q], gb + 3 * t, 64) + __shfl(a[q], gb + 3 * t + 1, 64)) + __shfl(a[q], gb + 3 * t + 2, 64);
+      rsh[q] = __shfl(shv[q], gb + 2 * t, 64) + __shfl(shv[q], gb + 2 * t + 1, 64);
+    }
+    if (r16 < T) down_epilogue(p, ra, rsh, row0, r16, g4);
+  }
+}
+
 // ---------------------------------------------------------------- q3 down, factored
 constexpr int kDqW = 8;             // waves: 0..3 routed, 4..7 shared
 constexpr int kDqRouted = 4;        // routed waves: one 512-code superblock of I each (I = 2048)
@@ -1260,6 +1600,8 @@ DecodeArgs decode_args(const dsk_moe_desc& d, const Workspace& L, const ExpertsA
   p.hs_lo = reinterpret_cast<uint16_t*>(a.ws + L.hs_lo);
   p.h_hi = reinterpret_cast<uint16_t*>(a.ws + L.h_hi);
   p.h_lo = reinterpret_cast<uint16_t*>(a.ws + L.h_lo);
+  p.hq = reinterpret_cast<uint8_t*>(a.ws + L.hq);
+  p.hqs = reinterpret_cast<uint8_t*>(a.ws + L.hqs);
   p.ws2 = static_cast<const uint16_t*>(a.ws2);
   p.shared_out = a.shared_out;
   p.out = a.out;
@@ -1279,6 +1621,10 @@ size_t up_lds_bytes(const DecodeArgs& p) {
 size_t up_q3_lds_bytes(const DecodeArgs& p) {
   return static_cast<size_t>(p.x_f32 ? 2 : 1) * p.T * (p.H + 8) * 2 +
          static_cast<size_t>(p.H / 128) * kQ3fMaxTokens * 16 + kQ3fItems * kQ3fKS * 2 * 64 * 2 * 4 + 64;
+}
+
+size_t up_mx_lds_bytes(const DecodeArgs& p) {
+  return kMxUpXqOffset + static_cast<size_t>(p.H / 128) * 2 * p.T * (128 + 4);
 }
 
 size_t rs_lds_bytes(const DecodeArgs& p) {
@@ -1313,6 +1659,7 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   // scale windows need 4-byte aligned scale rows (H a multiple of 128)
   const bool win = d.hidden % 128 == 0;
   const bool q3 = d.quant == DSK_QUANT_Q3;
+  const bool mx = mx_decode(d);
   // q3 (scale, bias) windows: every wave's K range a whole number of G-block
   // batches inside the row (so also 16-byte aligned windows)
   const bool q3win = d.hidden % (kUpKS * kUpBatch * 128) == 0;
@@ -1339,6 +1686,7 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
         else if (!p.x_f32) launch_kernel(k_up_q3<false, false, true>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
         else launch_kernel(k_up_q3<false, true, true>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
       }
+      else if (mx) launch_kernel(k_up_mx<kUpBatch>, up_blocks, kUpW * 64, up_mx_lds_bytes(p), s, p);
       else if (q3 && q3win && !p.x_f32) launch_kernel(k_up_stream<kUpBatch, true, false, true>, up_blocks, kUpW * 64, up_lds, s, p);
       else if (q3 && q3win) launch_kernel(k_up_stream<kUpBatch, true, true, true>, up_blocks, kUpW * 64, up_lds, s, p);
       else if (q3 && !p.x_f32) launch_kernel(k_up_stream<kUpBatch, false, false, true>, up_blocks, kUpW * 64, up_lds, s, p);
@@ -1355,6 +1703,15 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
     // routed and shared down per slot (one output row per dispatch row), then the combine
     if ((e = launch_grouped_down(d, L, a, a.route.desc, s, repeat)) != hipSuccess) return e;
     return launch_combine(d, L, a, s, repeat);
+  }
+  if (mx) {
+    for (int r = 0; r < repeat; ++r) {
+      const size_t lds = kStRedBytes + kStW * mx_dn_wave_bytes(d.tokens);
+      if (d.tokens == 1) launch_kernel(k_down_mx<1>, static_cast<unsigned>(d.hidden / 16), kStW * 64, lds, s, p);
+      else launch_kernel(k_down_mx<2>, static_cast<unsigned>(d.hidden / 16), kStW * 64, lds, s, p);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    return hipSuccess;
   }
   const int n_rows = d.tokens * d.top_k;
   const int max_u = d.n_experts < n_rows ? d.n_experts : n_rows;

@@ -37,10 +37,12 @@ void stage_close();
 
 template <class T> struct same_type { using type = T; };
 
-// Kernel launch (all launches of the library go through here).
+// Kernel launch (all launches of the library go through here).  A failed
+// launch is also the thread's last HIP error, which every launcher reads with
+// hipGetLastError() after its launches.
 template <typename... P>
-inline hipError_t launch_kernel(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t s,
-                                typename same_type<P>::type... args) {
+inline void launch_kernel(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                          typename same_type<P>::type... args) {
   void* argv[] = {const_cast<void*>(static_cast<const void*>(&args))..., nullptr};
   hipEvent_t start = nullptr, stop = nullptr;
   StageClock& c = g_stage_clock;
@@ -49,7 +51,7 @@ inline hipError_t launch_kernel(void (*kernel)(P...), dim3 grid, dim3 block, siz
     stop = c.ev[2 * c.open + 1];
     c.launched = true;
   }
-  return hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, argv, lds, s, start, stop, 0);
+  static_cast<void>(hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, argv, lds, s, start, stop, 0));
 }
 
 // ---------------------------------------------------------------- types
@@ -127,6 +129,8 @@ struct Workspace {
   size_t xb_hi, xb_lo;      // B-operand planes of x   [T][H]  (16-bit)
   size_t h_hi, h_lo;        // routed intermediate      [T*k][I] (16-bit)
   size_t hs_hi, hs_lo;      // shared intermediate      [T][Is]  (16-bit)
+  size_t hq, hqs;           // MX decode: routed intermediate as FP8 planes [T*k][3T][I]
+                            // and their E8M0 bytes [T*k][3T][I/32] (mx_decode only)
   size_t y;                 // routed outputs          [T*k][H] f32
   size_t ys;                // shared output           [T][H]   f32
   size_t pf_tiles;          // prefill GEMM tile list  [2 + 2 * prefill_max_tiles]
@@ -170,6 +174,21 @@ inline bool decode_pipeline(const dsk_moe_desc& d) {
                            (d.hidden + 8) * 2 + kUpLdsFixed;
   return d.tokens <= kDecodeMaxTokens && d.tokens * d.top_k <= kDecodeMaxPositions &&
          x_lds <= kMaxLds;
+}
+
+// FP4 experts, bf16 activations and one or two tokens: the decode gate/up and
+// down kernels run the routed products as scaled FP4 x FP8 MFMAs, with the
+// activations split into FP8 planes (two for x, three for h) on the B side.
+// The down kernel's eight waves take two K blocks each of an intermediate of
+// kMxInter (and of a shared intermediate up to that size).
+constexpr int kMxMaxTokens = 2;
+constexpr int kMxInter = 2048;
+inline bool mx_decode(const dsk_moe_desc& d) {
+  // gate/up LDS: 21.5 KB of partial sums and exchange tiles, 2.07 T H bytes of activation planes
+  const size_t up_lds = 32768 + static_cast<size_t>(d.tokens) * d.hidden * 3;
+  return d.quant == DSK_QUANT_FP4 && d.x_dtype == DSK_DTYPE_BF16 && d.tokens <= kMxMaxTokens &&
+         decode_pipeline(d) && d.hidden % 128 == 0 && d.inter == kMxInter &&
+         d.inter_shared <= kMxInter && d.inter_shared % 128 == 0 && up_lds <= kMaxLds;
 }
 
 // ---------------------------------------------------------------- launchers

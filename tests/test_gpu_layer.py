@@ -162,7 +162,7 @@ class _LazyBank:
         return self._cache[key]
 
 
-@pytest.mark.parametrize("T", [1, 8])
+@pytest.mark.parametrize("T", [1, 2, 8])
 def test_full_size_fp4_decode(T):
     """hidden 4096, 256 experts, top-8, inter 2048, bf16 shared 2048 (GPU-generated)."""
     print(f"layer full-size fp4 T={T}", flush=True)

@@ -1,0 +1,123 @@
+"""Decode pipeline on scaled FP4 x FP8 MFMAs: FP4 experts, bf16 tokens, one or
+two tokens, expert intermediate 2048.  The gate/up kernel takes the tokens'
+activations as two FP8 planes per 32-value group (an E8M0 exponent each) and
+writes h as three FP8 planes per 32-row group; the down kernel multiplies the
+FP4 w2 codes with those planes directly.
+
+Routing indices bit-exact; outputs within the layer tolerance (cosine >=
+0.99999 and max|y - y_ref| / max|y_ref| <= 1e-2) against the oracle.  Cases:
+hidden 512 (one weight batch per K range) and 1536 (K ranges of three blocks,
+a partial batch), a shared intermediate below 2048, no shared expert (with and
+without a callable shared output), two tokens routed to the same experts (every
+slot has both tokens) and to different ones (slots with one token carry zero
+planes for the other), few experts (every slot shared), and activations
+spanning 2^-12 .. 2^12 inside each 32-value group (the small values lose their
+low bits relative to the group's largest, which bounds their share of the dot
+product).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import dsk_moe
+from dsk_moe import synth as gsynth
+from oracle import layer as L
+from conftest import assert_layer_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+class _LazyBank:
+    """Oracle view of a GPU ResidentBank: copies one expert role at a time."""
+
+    def __init__(self, bank: dsk_moe.ResidentBank):
+        self.bank, self.quant, self._cache = bank, bank.quant, {}
+
+    def dequant(self, e, role):
+        key = (e, role)
+        if key not in self._cache:
+            from oracle import formats as F
+            parts = [t[e].cpu().numpy() for t in self.bank.roles[role]]
+            self._cache[key] = F.fp4_dequant(*parts)
+        return self._cache[key]
+
+
+def _check(layer, x, spec, shared_fn=None, shared_ref=None):
+    T, k = x.shape[0], spec.k
+    idx = torch.empty((T, k), dtype=torch.int32, device=DEV)
+    if shared_fn is None:
+        out = layer(x, idx=idx).cpu()
+        shared = None if layer.shared is None else tuple(
+            t.cpu() for t in (layer.shared.w1, layer.shared.w3, layer.shared.w2))
+    else:
+        # the reference's call signature (no routing out; its defaults replaced)
+        out = dsk_moe.moe_layer(x, layer.gate_w, layer.gate_b, layer.bank, shared_fn, k, layer.limit,
+                                score_func="sigmoid", route_scale=layer.route_scale).cpu()
+        shared, idx = None, None
+    r = L.moe_forward(x.cpu(), layer.gate_w.cpu(), layer.gate_b.cpu(), _LazyBank(layer.bank), shared, spec)
+    if idx is not None:
+        np.testing.assert_array_equal(idx.cpu().numpy(), r["idx"])
+    want = r["y_ref"] if shared_ref is None else r["y_ref"] + shared_ref
+    c, rel = assert_layer_close(out.float(), want)
+    print(f"cos={c:.9f} rel={rel:.2e} experts={np.unique(r['idx']).size}", flush=True)
+    return r
+
+
+@pytest.mark.parametrize("H,Is,T", [(512, 2048, 1), (512, 2048, 2), (1536, 1024, 2), (1536, 1024, 1)])
+def test_mx_decode_shapes(H, Is, T):
+    print(f"mx decode H={H} Is={Is} T={T}", flush=True)
+    layer = gsynth.make_layer(hidden=H, n_experts=32, top_k=4, inter=2048, inter_shared=Is,
+                              seed=700 + H + T, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(710 + H + T)
+    x = torch.randn((T, H), generator=g, device=DEV).to(torch.bfloat16)
+    _check(layer, x, L.LayerSpec(H=H, E=32, k=4, I=2048, I_shared=Is))
+
+
+def test_mx_decode_no_shared():
+    print("mx decode no shared expert, then a callable shared output", flush=True)
+    layer = gsynth.make_layer(hidden=512, n_experts=32, top_k=4, inter=2048, inter_shared=0,
+                              seed=720, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(721)
+    x = torch.randn((2, 512), generator=g, device=DEV).to(torch.bfloat16)
+    spec = L.LayerSpec(H=512, E=32, k=4, I=2048, I_shared=0)
+    _check(layer, x, spec)
+    _check(layer, x, spec, shared_fn=lambda t: torch.full_like(t, 0.125), shared_ref=0.125)
+
+
+def test_mx_decode_same_and_disjoint_experts():
+    """Two identical tokens (every slot has both), then two tokens of opposite
+    sign (mostly different experts: slots with one token)."""
+    layer = gsynth.make_layer(hidden=512, n_experts=64, top_k=6, inter=2048, inter_shared=2048,
+                              seed=730, device=DEV)
+    spec = L.LayerSpec(H=512, E=64, k=6, I=2048, I_shared=2048)
+    g = torch.Generator(device=DEV).manual_seed(731)
+    x1 = torch.randn((1, 512), generator=g, device=DEV).to(torch.bfloat16)
+    print("mx decode identical tokens", flush=True)
+    r = _check(layer, torch.cat([x1, x1]), spec)
+    assert np.unique(r["idx"]).size == 6
+    print("mx decode opposite tokens", flush=True)
+    r = _check(layer, torch.cat([x1, -x1]), spec)
+    assert np.unique(r["idx"]).size > 6
+
+
+def test_mx_decode_few_experts():
+    print("mx decode 8 experts, top-4, two tokens", flush=True)
+    layer = gsynth.make_layer(hidden=1024, n_experts=8, top_k=4, inter=2048, inter_shared=2048,
+                              seed=740, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(741)
+    x = torch.randn((2, 1024), generator=g, device=DEV).to(torch.bfloat16)
+    _check(layer, x, L.LayerSpec(H=1024, E=8, k=4, I=2048, I_shared=2048))
+
+
+def test_mx_decode_wide_range_activations():
+    print("mx decode activations spanning 2^-12 .. 2^12", flush=True)
+    layer = gsynth.make_layer(hidden=512, n_experts=32, top_k=4, inter=2048, inter_shared=2048,
+                              seed=750, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(751)
+    mag = torch.exp2(torch.randint(-12, 13, (2, 512), generator=g, device=DEV).float())
+    x = (torch.randn((2, 512), generator=g, device=DEV) * mag).to(torch.bfloat16)
+    _check(layer, x, L.LayerSpec(H=512, E=32, k=4, I=2048, I_shared=2048))
