@@ -556,7 +556,10 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
   uint8_t* xq = reinterpret_cast<uint8_t*>(base + kMxUpXqOffset);
   const int nblk = K / 128;
   uint8_t* xe = xq + nblk * 2 * T * 128;
-  // 1. the first two activation chunks of this thread, ahead of the weights
+  // 1. this lane's dispatch row (output column 2t + p: token t) and the first two
+  // activation chunks of this thread, ahead of the weights
+  const int t = r16 >> 1;
+  const int drow = t < T ? p.rowmap[slot * T + t] : -1;
   const int cpr = K / 8, xchunks = T * cpr;
   constexpr int NT = kUpW * 64;
   u32x4 xv[2];
@@ -576,6 +579,8 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
   const uint8_t* S3 = static_cast<const uint8_t*>(d->p[4]);
   UpBatch<G> A, B;
   load_batch<G, true>(A, W1, S1, W3, S3, row, K, k0, k1, g4, rok);
+  const bool tv = drow >= 0 && rok;
+  const float wr = tv ? p.wrow[drow] : 0.0f;
   // 3. the activations as FP8 planes (chunk rounds of the whole block, so that
   // the lanes of a 32-group are all present in each round)
 #pragma unroll
@@ -618,7 +623,6 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
   *reinterpret_cast<f32x4*>(&red[item][ks][0][lane][0]) = ag;
   *reinterpret_cast<f32x4*>(&red[item][ks][1][lane][0]) = au;
   __syncthreads();
-  const int t = r16 >> 1;
   float hv[4] = {0.f, 0.f, 0.f, 0.f};
   if (ks == 0) {
 #pragma unroll
@@ -626,27 +630,20 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
       ag += *reinterpret_cast<const f32x4*>(&red[item][w][0][lane][0]);
       au += *reinterpret_cast<const f32x4*>(&red[item][w][1][lane][0]);
     }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      ag[q] += __shfl_xor(ag[q], 1, 64);
-      au[q] += __shfl_xor(au[q], 1, 64);
-    }
-    const int drow = t < T ? p.rowmap[slot * T + t] : -1;
-    const bool tv = drow >= 0 && rok;
-    const float wr = tv ? p.wrow[drow] : 0.0f;
     float m = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      hv[q] = tv ? silu_clamped(ag[q], au[q], p.limit) * wr : 0.0f;
+      const float h = silu_clamped_fast(ag[q] + lane_xor1(ag[q]), au[q] + lane_xor1(au[q]), p.limit) * wr;
+      hv[q] = tv ? h : 0.0f;
       m = fmaxf(m, fabsf(hv[q]));
     }
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    // one exponent per (token, 32-row group): the largest |h| of the lane's
+    // column over this tile, then over the block's two tiles
+    m = max_over_rows(m);
     if (lane < 2 * T && (lane & 1) == 0) gmax[item * kMxMaxTokens + t] = m;
   }
   __syncthreads();
   if (ks == 0 && rok && (r16 & 1) == 0 && t < T) {
-    // one exponent per 32-row group: the block's two row tiles
     float mg = gmax[t];
 #pragma unroll
     for (int it = 1; it < kUpItems; ++it) mg = fmaxf(mg, gmax[it * kMxMaxTokens + t]);

@@ -70,6 +70,30 @@ __device__ __forceinline__ float pow2f(int e) {
   return __uint_as_float(static_cast<uint32_t>(b < 1 ? 1 : (b > 254 ? 254 : b)) << 23);
 }
 
+// Value of lane l ^ 1 (DPP quad permutation [1, 0, 3, 2]).
+__device__ __forceinline__ float lane_xor1(float v) {
+  return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0xB1, 0xF, 0xF, false));
+}
+
+// Maximum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows; the
+// swaps exchange a lane's value with its partner row's, so the larger of the
+// two results is the pair's maximum whichever way round they come back).
+__device__ __forceinline__ float max_over_rows(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(v, fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1])));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(v, fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1])));
+}
+
+// SiLU(min(g, limit)) * clamp(u, -limit, limit) with e^-x = 2^(-x log2 e) on
+// the exponential unit and the hardware reciprocal (a few ulp; the FP8 planes
+// the result goes into keep 2^-14 of their group's largest value).
+__device__ __forceinline__ float silu_clamped_fast(float g, float u, float limit) {
+  const float gg = fminf(g, limit);
+  const float uu = fminf(fmaxf(u, -limit), limit);
+  return gg * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * gg)) * uu;
+}
+
 // NP planes of 4 values (one 4-byte word per plane, value q in byte q).
 template <int NP>
 __device__ __forceinline__ void fp8_planes4(const float (&v)[4], int e, uint32_t (&w)[NP]) {
