@@ -120,12 +120,13 @@ def expert_bytes(quant: str = "fp4") -> int:
 
 def stage_bytes(u: int, t: int, quant: str) -> dict:
     """Algorithmic HBM bytes of each decode-pipeline stage for u active experts, t tokens:
-    gate (fp32 gate + x + scores), route (shared w1/w3 + scores + h_s planes), gate/up
-    (routed w1/w3 + x + h planes), down (routed w2 + shared w2 + h / h_s planes + out)."""
-    return {"gate": E * H * 4 + t * H * 2 + t * E * 4,
-            "route": 2 * IS * H * 2 + t * E * 4 + t * IS * 4,
+    gate (fp32 gate + shared w1/w3 + x + scores + h_s planes), route (shared w2 + scores +
+    h_s planes + shared output), gate/up (routed w1/w3 + x + h planes), down (routed w2 +
+    h planes + shared output + out)."""
+    return {"gate": E * H * 4 + 2 * IS * H * 2 + t * H * 2 + t * E * 4 + t * IS * 4,
+            "route": H * IS * 2 + t * E * 4 + t * IS * 4 + t * H * 2,
             "gate_up": u * 2 * role_bytes(I, H, quant) + t * H * 2 + t * K_TOP * I * 4,
-            "down": u * role_bytes(H, I, quant) + H * IS * 2 + t * K_TOP * I * 4 + t * IS * 4 + t * H * 2,
+            "down": u * role_bytes(H, I, quant) + t * K_TOP * I * 4 + 2 * t * H * 2,
             "combine": 0}
 
 
@@ -539,17 +540,18 @@ def main() -> int:
         rs = summ["routed_stage"]
         routed_us = float(np.mean(r["stage_us"][:, 2] + r["stage_us"][:, 3]))
         achieved = rs["bytes_mean"] / (routed_us * 1e-6)
-        up_k = "k_up_q3" if (args.quant == "q3" and T <= 8) else "k_up_stream"
-        dn_k = ("k_down_q3" if args.quant == "q3" and T <= 4 else
+        mx = args.quant == "fp4" and T <= 2
+        up_k = "k_up_q3" if (args.quant == "q3" and T <= 8) else ("k_up_mx" if mx else "k_up_stream")
+        dn_k = ("k_down_q3" if args.quant == "q3" and T <= 4 else "k_down_mx" if mx else
                 "k_down_decode_staged" if T <= 2 else "k_down_grouped + k_combine")
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
-                    "traffic": measured_traffic(["k_up_stream", "k_down_decode_staged"], workload),
+                    "traffic": measured_traffic([up_k, dn_k], workload),
                     "kernel": f"routed-expert stage: {up_k} (routed w1/w3, SwiGLU x route weight) + "
-                              f"{dn_k} (routed and shared w2, combine)",
+                              f"{dn_k} (routed w2, add of the shared output)",
                     "bytes_per_launch": rs["bytes_mean"],
                     "bytes_note": "routed-expert bytes only (U experts x 3 roles); the kernels also "
-                                  "move the shared w2 and activations (stages[*].bytes_mean)",
+                                  "move activations (stages[*].bytes_mean)",
                     "avg_launch_us": round(routed_us, 2), "timing": timing}
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1,

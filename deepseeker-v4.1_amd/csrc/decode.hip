@@ -47,6 +47,10 @@ struct DecodeArgs {
   float* scores; const float* bias; const dsk_expert_ptrs* table;
   int E; float route_scale;
   DecodeRoute route;
+  // gate scores of k_gate_shared
+  const void* gate_w; int score_func;
+  // shared output of k_route_sdown [T][H] (x dtype)
+  void* shared_x;
   const void* x; int x_f32;
   const uint16_t* ws1; const uint16_t* ws3;   // shared w1, w3 [Is][H] bf16
   uint16_t* hs_hi; uint16_t* hs_lo;    // [T][Is]
@@ -276,50 +280,143 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint
   }
 }
 
-// Routing and the shared expert's gate/up, one kernel: block 0 runs the
-// top-k of every token and the slot map of the routed kernels
-// (block_route); blocks 1 .. Is/16 each take one 16-row tile of the shared
-// expert (bf16 w1/w3, K split over the block's waves); hs = SwiGLU(gate, up)
-// as bf16 hi/lo planes.  The routing block's dependent loads and wave
-// reductions overlap the shared expert's weight stream.
-// Shared tiles of 8 rows up to 8 tokens (a 2048-row shared expert: 256
-// tiles, one per CU; K-block pairs per MFMA, see shared_up_tile), else 16.
+// The decode pipeline's first two kernels carry the shared expert beside the
+// routing: k_gate_shared computes the gate scores and the shared expert's
+// gate/up (both need only x), k_route_sdown runs the top-k and slot map in
+// one block beside the shared expert's down product, which it writes to
+// shared_x in x's dtype (the routed down kernels then add it as a
+// precomputed shared output).
+// Shared gate/up tiles of 8 rows up to 8 tokens (a 2048-row shared expert:
+// 256 tiles; K-block pairs per MFMA, see shared_up_tile), else 16.
 constexpr int kRsW = 8;
-// LDS of k_route_shared: the routing block's state and after it the expert
-// pointer table, or a shared tile's activation planes and then (over them)
-// its wave partial sums [kRsW][2][64][4] f32.
+// LDS of both kernels: the routing block's state and after it the expert
+// pointer table, a shared gate/up tile's activation planes and then (over
+// them) its wave partial sums [kRsW][2][64][4] f32, a shared down tile's
+// wave partial sums [kRsW][64][4] f32, or two gate tiles' segment sums.
 constexpr size_t kRsRedBytes = kRsW * 2 * 64 * 4 * 4;
 constexpr size_t kRsTabOffset = (sizeof(BlockRoute) + 15) / 16 * 16;
 static_assert(kRsTabOffset < kRsRedBytes, "routing block state must fit the route/shared LDS");
+// k_route_sdown: the routing state and the whole expert pointer table (read
+// once with the scores, so the slot descriptors need no dependent load).
+__host__ __device__ inline size_t route_lds_bytes(int E) {
+  const size_t need = kRsTabOffset + static_cast<size_t>(E) * sizeof(dsk_expert_ptrs);
+  return need > kRsRedBytes ? need : kRsRedBytes;
+}
+constexpr int kRsTileDelay = 60;   // x 64 clocks (~1.6 us)
 
+__host__ __device__ inline int shared_up_tiles(int T, int Is) { return Is / (T <= 8 ? 8 : 16); }
+
+// Blocks [0, shared_up_tiles): one shared gate/up tile each; the rest: two
+// gate tiles each (waves 0-3 and 4-7: one token x one expert of the score
+// grid, tile = token * E + expert, as the router's own gate kernel).
+template <bool kF32, bool kWBF16>
+__global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gate_shared(
+    DecodeArgs p) {
+  extern __shared__ __align__(16) uint16_t lds_up[];
+  const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_sh = shared_up_tiles(p.T, p.Is);
+  const int b = static_cast<int>(blockIdx.x);
+  if (b < n_sh) {
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const int xs = p.H + 8;
+    uint16_t* xh = lds_up;
+    uint16_t* xl = lds_up + p.T * xs;
+    u32x4 xv[kUpXRegChunks][2];
+    const bool xreg = load_x<kF32, kRsW * 64>(p, xh, xl, xs, tid, xv);
+    if (p.T <= 8) shared_up_tile<kF32, kRsW, 8>(p, b, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave, r16, g4);
+    else shared_up_tile<kF32, kRsW, 16>(p, b, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave, r16, g4);
+    return;
+  }
+  const int tile = 2 * (b - n_sh) + (wave >> 2);
+  const bool active = tile < p.T * p.E;
+  const int t = active ? tile / p.E : 0, e = active ? tile - t * p.E : 0;
+  float* segsum = reinterpret_cast<float*>(lds_up) + (wave >> 2) * kSegments;
+  gate_tile<1, 1, !kF32, kWBF16>(p.x, p.gate_w, p.T, p.H, p.E, p.score_func, p.scores, t, e, wave & 3, lane,
+                                 tid & 255, segsum, active);
+}
+
+// Shared down tile rb of k_route_sdown: output rows 16 rb .. 16 rb + 15 of
+// the shared expert, K (its intermediate) split over the block's waves in
+// 128-wide blocks (wave w: blocks w, w + kRsW, ...), bf16 MFMAs on the rows
+// of w2 and the hs planes read straight from global memory (B column c:
+// plane c & 1 of token t0 + c / 2, eight tokens per pass).  Wave sums added
+// in order, then hi + lo, rounded to x's dtype into shared_x.
 template <bool kF32>
-__global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_route_shared(
+__device__ __forceinline__ void shared_down_tile(const DecodeArgs& p, int rb, float (*red)[64][4], int lane,
+                                                 int wave) {
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int T = p.T, Is = p.Is, H = p.H;
+  const int row0 = rb * 16;
+  const uint32_t row = static_cast<uint32_t>(row0 + r16);
+  const int nkb = (Is + 127) / 128;
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  for (int t0 = 0; t0 < T; t0 += 8) {
+    const int t = min(t0 + (r16 >> 1), T - 1);   // columns past the last token repeat it (not used)
+    const uint16_t* hrow = ((r16 & 1) ? p.hs_lo : p.hs_hi) + static_cast<int64_t>(t) * Is;
+    f32x4 acc[4] = {z, z, z, z};
+    for (int kb = wave; kb < nkb; kb += 2 * kRsW) {
+      // two K blocks in flight, loads without conditions (past the end: the last block again)
+      RawBF16 w[2], h[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int kc = min(min(kb + j * kRsW, nkb - 1) * 128 + g4 * 32, Is - 32);
+        load_raw_nc(w[j], p.ws2, row, Is, kc);
+        load_raw_nc(h[j], hrow, 0, 0, kc);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int kbj = kb + j * kRsW;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const bool ok = kbj < nkb && kbj * 128 + g4 * 32 + 8 * jj < Is;
+          acc[jj] = mfma16(a_operand(w[j], jj), ok ? as_bf16x8(h[j].v[jj]) : bf16x8{}, acc[jj]);
+        }
+      }
+    }
+    *reinterpret_cast<f32x4*>(&red[wave][lane][0]) = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+    __syncthreads();
+    if (wave == 0) {
+      f32x4 a = z;
+      for (int w = 0; w < kRsW; ++w) a += *reinterpret_cast<const f32x4*>(&red[w][lane][0]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[q] += lane_xor1(a[q]);
+      const int tok = t0 + (r16 >> 1);
+      if ((r16 & 1) == 0 && tok < T) {
+        const int64_t o = static_cast<int64_t>(tok) * H + row0 + 4 * g4;
+        if constexpr (kF32) {
+          *reinterpret_cast<f32x4*>(static_cast<float*>(p.shared_x) + o) = a;
+        } else {
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.shared_x) + o) =
+              uint2{f32_to_bf16_bits(a[0]) | (uint32_t(f32_to_bf16_bits(a[1])) << 16),
+                    f32_to_bf16_bits(a[2]) | (uint32_t(f32_to_bf16_bits(a[3])) << 16)};
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Block 0: top-k of every token and the slot map of the routed kernels
+// (block_route); blocks 1 .. H/16: shared down tiles.  The routing block's
+// dependent loads and wave reductions overlap the shared expert's stream.
+template <bool kF32>
+__global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_route_sdown(
     DecodeArgs p) {
   extern __shared__ __align__(16) uint16_t lds_up[];
   if (blockIdx.x == 0) {
     block_route(*reinterpret_cast<BlockRoute*>(lds_up), p.scores, p.bias, p.T, p.E, p.k, p.route_scale,
                 p.table, true, p.route, reinterpret_cast<uint64_t*>(lds_up + kRsTabOffset / 2),
-                static_cast<int>((kRsRedBytes - kRsTabOffset) / 8));
+                static_cast<int>((route_lds_bytes(p.E) - kRsTabOffset) / 8));
     return;
   }
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // At one or two tokens the routing block ends the kernel: its score loads
-  // wait for whatever the tile block beside it on the same CU requested
-  // first.  The tile blocks wait ~0.5 us (19 x 64 clocks) before their first
-  // loads, so the routing block's go out ahead of them.
-  if (p.T <= 2) __builtin_amdgcn_s_sleep(19);
-  const int r16 = lane & 15, g4 = lane >> 4;
-  const int xs = p.H + 8;
-  uint16_t* xh = lds_up;
-  uint16_t* xl = lds_up + p.T * xs;
-  u32x4 xv[kUpXRegChunks][2];
-  const bool xreg = load_x<kF32, kRsW * 64>(p, xh, xl, xs, tid, xv);
-  if (p.T <= 8)
-    shared_up_tile<kF32, kRsW, 8>(p, static_cast<int>(blockIdx.x) - 1, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave,
-                                  r16, g4);
-  else
-    shared_up_tile<kF32, kRsW, 16>(p, static_cast<int>(blockIdx.x) - 1, xh, xl, xs, xreg, xv, lds_up, tid, lane,
-                                   wave, r16, g4);
+  // The routing block's loads (scores, bias, pointer table) are the kernel's
+  // critical path: behind the tiles' weight stream their latency grows
+  // several-fold, so the tiles hold their first loads back until those have
+  // had time to return.
+  if (p.T <= 2) __builtin_amdgcn_s_sleep(kRsTileDelay);
+  shared_down_tile<kF32>(p, static_cast<int>(blockIdx.x) - 1, reinterpret_cast<float (*)[64][4]>(lds_up), lane,
+                         wave);
 }
 
 // Routed gate/up of the decode pipeline.  Each block takes kUpItems row
@@ -1129,69 +1226,50 @@ __global__ __launch_bounds__(kStW * 64) void k_down_decode_staged(DecodeArgs p) 
 constexpr int kMxSlots = 8;   // routed experts per round of k_down_mx (all of them at one token)
 
 // Wave-private LDS of k_down_mx, after the wave partial sums: the round's h
-// planes of the wave's two K blocks [kMxSlots][3T][256 B] (B-operand order),
-// their E8M0 windows [kMxSlots][3T][8 B] (rounded up to 256 B) and the hs
-// hi / lo planes of the wave's K range [2T][256] bf16.
+// planes of the wave's two K blocks [kMxSlots][3T][256 B] (B-operand order)
+// and their E8M0 windows [kMxSlots][3T][8 B] (rounded up to 256 B).
+constexpr int kMxDnRedBytes = kStW * 64 * 4 * 4;   // wave partial sums
 constexpr int mx_dn_h_bytes(int T) { return kMxSlots * 3 * T * 256; }
 constexpr int mx_dn_s_bytes(int T) { return (kMxSlots * 3 * T * 8 + 255) / 256 * 256; }
-constexpr int mx_dn_wave_bytes(int T) { return mx_dn_h_bytes(T) + mx_dn_s_bytes(T) + 2 * T * 512; }
+constexpr int mx_dn_wave_bytes(int T) { return mx_dn_h_bytes(T) + mx_dn_s_bytes(T); }
 static_assert((kMxSlots * 3) % 4 == 0, "h DMA instructions cover whole (slot, column) pairs");
 
 // Down + combine of the decode pipeline for FP4 experts and T (one or two)
 // tokens on scaled FP4 x FP8 MFMAs.  Block = 16 output rows, kStW waves;
 // wave w owns the K blocks [kStKB*w, kStKB*w + kStKB) of every active
-// expert's w2 rows and of the shared w2 rows.  Everything of a round of
-// kMxSlots experts is in flight at once: first the wave's slices of the FP8 h
-// planes k_up_mx wrote (B column 3t + p: plane p of token t; zero planes for a
-// token not routed to the slot), of their E8M0 windows and of the hs planes,
-// 16 contiguous bytes per lane, then the shared w2 rows and every expert's w2
-// codes and scale windows.  The slices go to wave-private LDS as they land
-// (each store waits for its own load), and each expert is computed as its
-// weights land, one v_mfma_scale_f32_16x16x128_f8f6f4 per K block with the B
-// operand read back from LDS.  Slots past the active count re-read slot 0
-// and are computed with zero codes (straight-line code, so that every wait is
-// for the loads it needs only).  Shared: bf16 MFMAs on the hs hi / lo columns
-// (2t + plane).  Four routed accumulator chains added in order, the waves in
-// order, then a token's plane columns ((p0 + p1) + p2; hi + lo) and the final
-// add and cast.
+// expert's w2 rows.  Everything of a round of kMxSlots experts is in flight
+// at once: first the wave's slices of the FP8 h planes k_up_mx wrote (B
+// column 3t + p: plane p of token t; zero planes for a token not routed to
+// the slot) and of their E8M0 windows, 16 contiguous bytes per lane, then
+// every expert's w2 codes and scale windows.  The slices go to wave-private
+// LDS as they land (each store waits for its own load), and each expert is
+// computed as its weights land, one v_mfma_scale_f32_16x16x128_f8f6f4 per K
+// block with the B operand read back from LDS.  Slots past the active count
+// re-read slot 0 and are computed with zero codes (straight-line code, so
+// that every wait is for the loads it needs only).  Four accumulator chains
+// added in order, the waves in order, then a token's plane columns
+// ((p0 + p1) + p2) and the final add of the precomputed shared output and
+// cast.
 template <int T>
 __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
   extern __shared__ __align__(16) uint8_t lds_mx[];
   constexpr int C = 3 * T;
-  float (*red)[kStW][64][4] = reinterpret_cast<float (*)[kStW][64][4]>(lds_mx);
+  float (*red)[64][4] = reinterpret_cast<float (*)[64][4]>(lds_mx);
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
   const int row0 = blockIdx.x * 16;
   const uint32_t row = static_cast<uint32_t>(row0 + r16);
   const int U = p.active[0];
-  const int I = p.I, Is = p.Is;
+  const int I = p.I;
   const int kb0 = wave * kStKB;
-  uint8_t* hl = lds_mx + kStRedBytes + wave * mx_dn_wave_bytes(T);   // [kMxSlots][C][256]
-  uint8_t* sl = hl + mx_dn_h_bytes(T);                                // [kMxSlots][C][8]
-  uint16_t* hsl = reinterpret_cast<uint16_t*>(sl + mx_dn_s_bytes(T));  // [2T][256]
-  // B columns of this lane (past the last one, repeats of it; their results are not used)
-  const int bc = min(r16, C - 1), sc = min(r16, 2 * T - 1);
-  // 1. the wave's hs slice (column 2t + plane, 256 values from K = 128 kb0, clamped
-  // into the row) and the shared w2 rows; without a shared expert both read the
-  // start of the h planes and are not computed
-  const bool sh = Is > 0;
-  const uint16_t* dummy = reinterpret_cast<const uint16_t*>(p.hq);
-  u32x4 hsv[T];
-#pragma unroll
-  for (int q = 0; q < T; ++q) {
-    const int col = 2 * q + (lane >> 5);
-    const uint16_t* src = ((col & 1) ? p.hs_lo : p.hs_hi) + (col >> 1) * Is + min(kb0 * 128 + (lane & 31) * 8, Is - 8);
-    hsv[q] = ldg16(sh ? src : dummy);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  RawBF16 rs[kStKB];
-#pragma unroll
-  for (int j = 0; j < kStKB; ++j)
-    load_raw_nc(rs[j], sh ? p.ws2 : dummy, sh ? row : 0u, sh ? Is : 0, sh ? min((kb0 + j) * 128 + g4 * 32, Is - 32) : 0);
+  uint8_t* hl = lds_mx + kMxDnRedBytes + wave * mx_dn_wave_bytes(T);   // [kMxSlots][C][256]
+  uint8_t* sl = hl + mx_dn_h_bytes(T);                                  // [kMxSlots][C][8]
+  // B column of this lane (past the last one, repeats of it; their results are not used)
+  const int bc = min(r16, C - 1);
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-  f32x4 acc[4] = {z, z, z, z}, accs[4] = {z, z, z, z};
-  auto round = [&](int u0, auto first) {
-    // 2. the round's h planes and E8M0 windows (slots past U re-read slot 0):
+  f32x4 acc[4] = {z, z, z, z};
+  for (int u0 = 0; u0 < U; u0 += kMxSlots) {
+    // 1. the round's h planes and E8M0 windows (slots past U re-read slot 0):
     // lane l takes 16 bytes of (slot, column) pair 4q + l / 16, 4 bytes of pair 32q + l / 2
     constexpr int NH = kMxSlots * C / 4, NS = mx_dn_s_bytes(T) / 256;
     u32x4 hv[NH];
@@ -1209,7 +1287,7 @@ __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
       sv[q] = ldg<uint32_t>(p.hqs + static_cast<uint32_t>(su * C + c) * static_cast<uint32_t>(I / 32) + kb0 * 4 + 4 * (lane & 1));
     }
     __builtin_amdgcn_sched_barrier(0);
-    // 3. every expert's w2 codes and scale windows
+    // 2. every expert's w2 codes and scale windows
     u32x4 wc[kMxSlots][kStKB];
     u32x2 ws[kMxSlots];
 #pragma unroll
@@ -1222,28 +1300,12 @@ __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
       ws[i] = ldg<u32x2>(S + row * static_cast<uint32_t>(I / 32) + kb0 * 4);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // 4. the slices into the wave's LDS (in the lane order they were loaded)
-    if constexpr (decltype(first)::value) {
-#pragma unroll
-      for (int q = 0; q < T; ++q) *reinterpret_cast<u32x4*>(hsl + q * 512 + lane * 8) = hsv[q];
-    }
+    // 3. the slices into the wave's LDS (in the lane order they were loaded)
 #pragma unroll
     for (int q = 0; q < NH; ++q) *reinterpret_cast<u32x4*>(hl + q * 1024 + lane * 16) = hv[q];
 #pragma unroll
     for (int q = 0; q < NS; ++q) *reinterpret_cast<uint32_t*>(sl + q * 256 + lane * 4) = sv[q];
-    // 5. the shared product (first round), then the experts in slot order as they land
-    if constexpr (decltype(first)::value) {
-#pragma unroll
-      for (int j = 0; j < kStKB; ++j) {
-        // K blocks past the shared intermediate (and all of them without one) add zero
-        const bool ok = (kb0 + j) * 128 < Is;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const u32x4 b = *reinterpret_cast<const u32x4*>(hsl + sc * 256 + j * 128 + g4 * 32 + 8 * jj);
-          accs[jj] = mfma16(a_operand(rs[j], jj), ok ? as_bf16x8(b) : bf16x8{}, accs[jj]);
-        }
-      }
-    }
+    // 4. the experts in slot order as they land
 #pragma unroll
     for (int i = 0; i < kMxSlots; ++i) {
       const bool live = u0 + i < U;
@@ -1258,27 +1320,19 @@ __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
         acc[(2 * i + j) & 3] = mx_mfma(codes, wsb, lo, hi, hs, acc[(2 * i + j) & 3]);
       }
     }
-  };
-  round(0, std::true_type{});
-  for (int u0 = kMxSlots; u0 < U; u0 += kMxSlots) round(u0, std::false_type{});
-  *reinterpret_cast<f32x4*>(&red[0][wave][lane][0]) = ((acc[0] + acc[1]) + acc[2]) + acc[3];
-  *reinterpret_cast<f32x4*>(&red[1][wave][lane][0]) = ((accs[0] + accs[1]) + accs[2]) + accs[3];
+  }
+  *reinterpret_cast<f32x4*>(&red[wave][lane][0]) = ((acc[0] + acc[1]) + acc[2]) + acc[3];
   __syncthreads();
   if (wave == 0) {
-    f32x4 a = z, shv = z;
-    for (int w = 0; w < kStW; ++w) {
-      a += *reinterpret_cast<const f32x4*>(&red[0][w][lane][0]);
-      shv += *reinterpret_cast<const f32x4*>(&red[1][w][lane][0]);
-    }
-    // token t = r16 of this lane group: routed columns 3t .. 3t + 2, shared 2t, 2t + 1
+    f32x4 a = z;
+    for (int w = 0; w < kStW; ++w) a += *reinterpret_cast<const f32x4*>(&red[w][lane][0]);
+    // token t = r16 of this lane group: columns 3t .. 3t + 2
     const int t = min(r16, T - 1), gb = lane & 48;
-    f32x4 ra, rsh;
+    f32x4 ra;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < 4; ++q)
       ra[q] = (__shfl(a[q], gb + 3 * t, 64) + __shfl(a[q], gb + 3 * t + 1, 64)) + __shfl(a[q], gb + 3 * t + 2, 64);
-      rsh[q] = __shfl(shv[q], gb + 2 * t, 64) + __shfl(shv[q], gb + 2 * t + 1, 64);
-    }
-    if (r16 < T) down_epilogue(p, ra, rsh, row0, r16, g4);
+    if (r16 < T) down_epilogue(p, ra, z, row0, r16, g4);
   }
 }
 
@@ -1606,6 +1660,8 @@ DecodeArgs decode_args(const dsk_moe_desc& d, const Workspace& L, const ExpertsA
   p.scores = a.scores; p.bias = a.bias; p.table = a.table;
   p.E = d.n_experts; p.route_scale = d.route_scale;
   p.route = a.route;
+  p.gate_w = a.gate_w; p.score_func = d.score_func;
+  p.shared_x = a.ws + L.shared_x;
   return p;
 }
 
@@ -1631,14 +1687,32 @@ size_t rs_lds_bytes(const DecodeArgs& p) {
 
 }  // namespace
 
-hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
-                               hipStream_t s, int repeat) {
+hipError_t launch_gate_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
+                              int repeat) {
   const DecodeArgs p = decode_args(d, L, a);
-  const unsigned blocks = static_cast<unsigned>(1 + p.Is / (p.T <= 8 ? 8 : 16));
+  const int gate_blocks = (p.T * p.E + 1) / 2;
+  const unsigned blocks = static_cast<unsigned>(shared_up_tiles(p.T, p.Is) + gate_blocks);
   const size_t lds = rs_lds_bytes(p);
+  const bool wb = d.gate_dtype == DSK_DTYPE_BF16;
   for (int r = 0; r < repeat; ++r) {
-    if (p.x_f32) launch_kernel(k_route_shared<true>, blocks, kRsW * 64, lds, s, p);
-    else launch_kernel(k_route_shared<false>, blocks, kRsW * 64, lds, s, p);
+    if (p.x_f32 && wb) launch_kernel(k_gate_shared<true, true>, blocks, kRsW * 64, lds, s, p);
+    else if (p.x_f32) launch_kernel(k_gate_shared<true, false>, blocks, kRsW * 64, lds, s, p);
+    else if (wb) launch_kernel(k_gate_shared<false, true>, blocks, kRsW * 64, lds, s, p);
+    else launch_kernel(k_gate_shared<false, false>, blocks, kRsW * 64, lds, s, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_route_sdown(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
+                              int repeat) {
+  const DecodeArgs p = decode_args(d, L, a);
+  const unsigned blocks = static_cast<unsigned>(1 + (p.Is > 0 ? p.H / 16 : 0));
+  for (int r = 0; r < repeat; ++r) {
+    const size_t lds = route_lds_bytes(p.E) <= kMaxLds ? route_lds_bytes(p.E) : kRsRedBytes;
+    if (p.x_f32) launch_kernel(k_route_sdown<true>, blocks, kRsW * 64, lds, s, p);
+    else launch_kernel(k_route_sdown<false>, blocks, kRsW * 64, lds, s, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1702,8 +1776,10 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
     return launch_combine(d, L, a, s, repeat);
   }
   if (mx) {
+    // the shared expert's down ran beside the routing (no shared intermediate here)
+    if (d.inter_shared != 0) return hipErrorInvalidValue;
     for (int r = 0; r < repeat; ++r) {
-      const size_t lds = kStRedBytes + kStW * mx_dn_wave_bytes(d.tokens);
+      const size_t lds = kMxDnRedBytes + kStW * mx_dn_wave_bytes(d.tokens);
       if (d.tokens == 1) launch_kernel(k_down_mx<1>, static_cast<unsigned>(d.hidden / 16), kStW * 64, lds, s, p);
       else launch_kernel(k_down_mx<2>, static_cast<unsigned>(d.hidden / 16), kStW * 64, lds, s, p);
       if ((e = hipGetLastError()) != hipSuccess) return e;

@@ -133,6 +133,7 @@ struct Workspace {
                             // and their E8M0 bytes [T*k][3T][I/32] (mx_decode only)
   size_t y;                 // routed outputs          [T*k][H] f32
   size_t ys;                // shared output           [T][H]   f32
+  size_t shared_x;          // decode pipeline: shared output [T][H] (x dtype)
   size_t pf_tiles;          // prefill GEMM tile list  [2 + 2 * prefill_max_tiles]
   size_t total;
 };
@@ -180,15 +181,14 @@ inline bool decode_pipeline(const dsk_moe_desc& d) {
 // down kernels run the routed products as scaled FP4 x FP8 MFMAs, with the
 // activations split into FP8 planes (two for x, three for h) on the B side.
 // The down kernel's eight waves take two K blocks each of an intermediate of
-// kMxInter (and of a shared intermediate up to that size).
+// kMxInter (the shared expert runs in the decode pipeline's first two kernels).
 constexpr int kMxMaxTokens = 2;
 constexpr int kMxInter = 2048;
 inline bool mx_decode(const dsk_moe_desc& d) {
   // gate/up LDS: 21.5 KB of partial sums and exchange tiles, 2.07 T H bytes of activation planes
   const size_t up_lds = 32768 + static_cast<size_t>(d.tokens) * d.hidden * 3;
   return d.quant == DSK_QUANT_FP4 && d.x_dtype == DSK_DTYPE_BF16 && d.tokens <= kMxMaxTokens &&
-         decode_pipeline(d) && d.hidden % 128 == 0 && d.inter == kMxInter &&
-         d.inter_shared <= kMxInter && d.inter_shared % 128 == 0 && up_lds <= kMaxLds;
+         decode_pipeline(d) && d.hidden % 128 == 0 && d.inter == kMxInter && up_lds <= kMaxLds;
 }
 
 // ---------------------------------------------------------------- launchers
@@ -228,6 +228,7 @@ struct ExpertsArgs {
   const SlotDesc* desc; const int32_t* xrow; const float* wrow;
   const void* ws1; const void* ws3; const void* ws2;
   const void* shared_out;    // precomputed shared output [T][H] in x dtype (or null)
+  const void* gate_w;        // decode pipeline: gate weights [E][H] (gate dtype)
   const void* x;
   const float* weights;      // [T*k] by flat position
   const int32_t* counts; const int32_t* offsets; const int32_t* perm;
@@ -300,14 +301,16 @@ hipError_t launch_combine(const dsk_moe_desc& d, const Workspace& L, const Exper
                           int repeat);
 
 // Decode pipeline (decode_pipeline(d)), four kernels:
-//   launch_gate_scores    gate scores (a.scores);
-//   launch_route_shared   top-k and slot map (a.route) in one block beside the shared
-//                         expert's gate/up (hs);
-//   launch_experts_decode the routed gate/up, then the routed and shared down and the
-//                         combine in one kernel (stages as for launch_experts).
-hipError_t launch_gate_scores(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
-hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
-                               hipStream_t s, int repeat);
+//   launch_gate_shared    gate scores (a.scores) beside the shared expert's gate/up (hs);
+//   launch_route_sdown    top-k and slot map (a.route) in one block beside the shared
+//                         expert's down, written to the workspace's shared_x (x dtype);
+//   launch_experts_decode the routed gate/up, then the routed down and the combine in
+//                         one kernel (stages as for launch_experts), called with no
+//                         shared intermediate and shared_x as the precomputed output.
+hipError_t launch_gate_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
+                              int repeat);
+hipError_t launch_route_sdown(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
+                              int repeat);
 hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L,
                                  const ExpertsArgs& a, hipStream_t s, int repeat);
 
