@@ -1246,8 +1246,11 @@ static_assert((kMxSlots * 3) % 4 == 0, "h DMA instructions cover whole (slot, co
 // computed as its weights land, one v_mfma_scale_f32_16x16x128_f8f6f4 per K
 // block with the B operand read back from LDS.  Slots past the active count
 // re-read slot 0 and are computed with zero codes (straight-line code, so
-// that every wait is for the loads it needs only).  Four accumulator chains
-// added in order, the waves in order, then a token's plane columns
+// that every wait is for the loads it needs only).  One accumulator chain
+// per K block of the wave, each over the slots in order -- a token's sum does
+// not depend on the other token's experts (a slot the token is not routed to
+// adds exact zeros), so two tokens give the rows of two single-token calls --
+// the chains added in order, the waves in order, then a token's plane columns
 // ((p0 + p1) + p2) and the final add of the precomputed shared output and
 // cast.
 template <int T>
@@ -1267,7 +1270,7 @@ __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
   // B column of this lane (past the last one, repeats of it; their results are not used)
   const int bc = min(r16, C - 1);
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-  f32x4 acc[4] = {z, z, z, z};
+  f32x4 acc[kStKB] = {z, z};
   for (int u0 = 0; u0 < U; u0 += kMxSlots) {
     // 1. the round's h planes and E8M0 windows (slots past U re-read slot 0):
     // lane l takes 16 bytes of (slot, column) pair 4q + l / 16, 4 bytes of pair 32q + l / 2
@@ -1317,11 +1320,12 @@ __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
         const uint32_t hs = sl[(i * C + bc) * 8 + 4 * j + g4];
         const uint32_t wsb = ((j == 0 ? ws[i].x : ws[i].y) >> (8 * g4)) & 0xffu;
         const u32x4 codes = live ? wc[i][j] : u32x4{0u, 0u, 0u, 0u};
-        acc[(2 * i + j) & 3] = mx_mfma(codes, wsb, lo, hi, hs, acc[(2 * i + j) & 3]);
+        acc[j] = mx_mfma(codes, wsb, lo, hi, hs, acc[j]);
       }
     }
   }
-  *reinterpret_cast<f32x4*>(&red[wave][lane][0]) = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+  static_assert(kStKB == 2, "two K-block chains");
+  *reinterpret_cast<f32x4*>(&red[wave][lane][0]) = acc[0] + acc[1];
   __syncthreads();
   if (wave == 0) {
     f32x4 a = z;

@@ -13,7 +13,8 @@ slot has both tokens) and to different ones (slots with one token carry zero
 planes for the other), few experts (every slot shared), and activations
 spanning 2^-12 .. 2^12 inside each 32-value group (the small values lose their
 low bits relative to the group's largest, which bounds their share of the dot
-product).
+product).  At full size, two tokens give bit for bit the rows of two one-token
+calls.
 """
 
 from __future__ import annotations
@@ -121,3 +122,25 @@ def test_mx_decode_wide_range_activations():
     mag = torch.exp2(torch.randint(-12, 13, (2, 512), generator=g, device=DEV).float())
     x = (torch.randn((2, 512), generator=g, device=DEV) * mag).to(torch.bfloat16)
     _check(layer, x, L.LayerSpec(H=512, E=32, k=4, I=2048, I_shared=2048))
+
+
+def test_mx_decode_two_tokens_equal_two_single_calls():
+    """Full size (hidden 4096, 256 experts, top-8): a two-token call gives each
+    token's row bit for bit as a one-token call does (a token's sums run over
+    its own experts in ascending id, whatever the other token routes to; the
+    slots past the first eight run in a second round)."""
+    print("mx decode full size: B=2 rows == two B=1 calls", flush=True)
+    layer = gsynth.make_layer(hidden=4096, n_experts=256, top_k=8, inter=2048, inter_shared=2048,
+                              seed=760, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(761)
+    for rep in range(3):
+        x = torch.randn((2, 4096), generator=g, device=DEV).to(torch.bfloat16)
+        idx = torch.empty((2, 8), dtype=torch.int32, device=DEV)
+        both = layer(x, idx=idx).clone()
+        one0 = layer(x[0:1].contiguous()).clone()
+        one1 = layer(x[1:2].contiguous()).clone()
+        union = torch.unique(idx).numel()
+        print(f"rep {rep}: union {union}", flush=True)
+        assert union > 8
+        assert torch.equal(both[0:1].view(torch.int16), one0.view(torch.int16))
+        assert torch.equal(both[1:2].view(torch.int16), one1.view(torch.int16))
