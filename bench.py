@@ -118,15 +118,29 @@ def expert_bytes(quant: str = "fp4") -> int:
     return 2 * role_bytes(I, H, quant) + role_bytes(H, I, quant)
 
 
+def mx_decode(t: int, quant: str) -> bool:
+    """FP4 experts and one or two bf16 tokens at the full shape run the MX decode kernels."""
+    return quant == "fp4" and t <= 2
+
+
 def stage_bytes(u: int, t: int, quant: str) -> dict:
-    """Algorithmic HBM bytes of each decode-pipeline stage for u active experts, t tokens:
-    gate (fp32 gate + shared w1/w3 + x + scores + h_s planes), route (shared w2 + scores +
-    h_s planes + shared output), gate/up (routed w1/w3 + x + h planes), down (routed w2 +
-    h planes + shared output + out)."""
-    return {"gate": E * H * 4 + 2 * IS * H * 2 + t * H * 2 + t * E * 4 + t * IS * 4,
-            "route": H * IS * 2 + t * E * 4 + t * IS * 4 + t * H * 2,
-            "gate_up": u * 2 * role_bytes(I, H, quant) + t * H * 2 + t * K_TOP * I * 4,
-            "down": u * role_bytes(H, I, quant) + t * K_TOP * I * 4 + 2 * t * H * 2,
+    """Algorithmic HBM bytes of each decode-pipeline stage for u active experts, t tokens.
+    MX kernels: gate (fp32 gate + shared w1/w3 + x + scores + h_s planes), route (shared
+    w2 + scores + h_s planes + shared output), gate/up (routed w1/w3 + x + h planes), down
+    (routed w2 + h planes + shared output + out).  Otherwise: gate (fp32 gate + x +
+    scores), route (shared w1/w3 + scores + h_s planes), gate/up (as above), down (routed
+    w2 + shared w2 + h / h_s planes + out)."""
+    up = u * 2 * role_bytes(I, H, quant) + t * H * 2 + t * K_TOP * I * 4
+    if mx_decode(t, quant):
+        return {"gate": E * H * 4 + 2 * IS * H * 2 + t * H * 2 + t * E * 4 + t * IS * 4,
+                "route": H * IS * 2 + t * E * 4 + t * IS * 4 + t * H * 2,
+                "gate_up": up,
+                "down": u * role_bytes(H, I, quant) + t * K_TOP * I * 4 + 2 * t * H * 2,
+                "combine": 0}
+    return {"gate": E * H * 4 + t * H * 2 + t * E * 4,
+            "route": 2 * IS * H * 2 + t * E * 4 + t * IS * 4,
+            "gate_up": up,
+            "down": u * role_bytes(H, I, quant) + H * IS * 2 + t * K_TOP * I * 4 + t * IS * 4 + t * H * 2,
             "combine": 0}
 
 
@@ -540,7 +554,7 @@ def main() -> int:
         rs = summ["routed_stage"]
         routed_us = float(np.mean(r["stage_us"][:, 2] + r["stage_us"][:, 3]))
         achieved = rs["bytes_mean"] / (routed_us * 1e-6)
-        mx = args.quant == "fp4" and T <= 2
+        mx = mx_decode(T, args.quant)
         up_k = "k_up_q3" if (args.quant == "q3" and T <= 8) else ("k_up_mx" if mx else "k_up_stream")
         dn_k = ("k_down_q3" if args.quant == "q3" and T <= 4 else "k_down_mx" if mx else
                 "k_down_decode_staged" if T <= 2 else "k_down_grouped + k_combine")
@@ -548,7 +562,8 @@ def main() -> int:
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
                     "traffic": measured_traffic([up_k, dn_k], workload),
                     "kernel": f"routed-expert stage: {up_k} (routed w1/w3, SwiGLU x route weight) + "
-                              f"{dn_k} (routed w2, add of the shared output)",
+                              f"{dn_k} " + ("(routed w2, add of the shared output)" if mx else
+                                             "(routed and shared w2, combine)"),
                     "bytes_per_launch": rs["bytes_mean"],
                     "bytes_note": "routed-expert bytes only (U experts x 3 roles); the kernels also "
                                   "move activations (stages[*].bytes_mean)",

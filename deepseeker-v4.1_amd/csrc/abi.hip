@@ -83,7 +83,7 @@ Workspace workspace_layout(const dsk_moe_desc& d) {
   L.hqs = take(mx ? N * 3 * T * (I / 32) : 0);
   L.y = take(N * H * 4);
   L.ys = take(T * H * 4);
-  L.shared_x = take(decode_pipeline(d) && Is > 0 ? T * H * (d.x_dtype == DSK_DTYPE_F32 ? 4 : 2) : 0);
+  L.shared_x = take(mx && Is > 0 ? T * H * 2 : 0);
   L.pf_tiles = take(prefill_gemm(d) ? (2 + 2 * static_cast<size_t>(prefill_max_tiles(d))) * 4 : 0);
   L.total = o;
   return L;
@@ -291,7 +291,7 @@ int dsk::forward_layer(const dsk_moe_desc* d, const void* x, const void* gate_w,
   const bool decode = decode_pipeline(*d);
   StageTiming timing(ev);
   stage_open(kStageGate);
-  if (decode) {
+  if (decode && mx_decode(*d)) {
     // gate scores beside the shared expert's gate/up; the top-k and the slot map beside
     // the shared expert's down; then the routed experts, which add the shared output
     rc = hip_check(launch_gate_shared(*d, L, a, s, repeat), "gate / shared gate-up launch");
@@ -307,6 +307,14 @@ int dsk::forward_layer(const dsk_moe_desc* d, const void* x, const void* gate_w,
       ar.shared_out = ws + L.shared_x;
     }
     rc = hip_check(launch_experts_decode(dr, L, ar, s, repeat), "decode experts launch");
+  } else if (decode) {
+    // gate scores; then the top-k and the slot map beside the shared expert's gate/up
+    for (int r = 0; r < repeat && !rc; ++r) rc = hip_check(launch_gate_scores(*d, ra, s), "gate launch");
+    if (rc) return rc;
+    stage_open(kStageRoute);
+    rc = hip_check(launch_route_shared(*d, L, a, s, repeat), "route / shared gate-up launch");
+    if (rc) return rc;
+    rc = hip_check(launch_experts_decode(*d, L, a, s, repeat), "decode experts launch");
   } else {
     // gate (the fused router of a few tokens also selects and dispatches), then top-k + dispatch
     for (int r = 0; r < repeat && !rc; ++r)

@@ -51,6 +51,7 @@ struct DecodeArgs {
   const void* gate_w; int score_func;
   // shared output of k_route_sdown [T][H] (x dtype)
   void* shared_x;
+  int route_lds;                       // LDS bytes of the routing kernels' launch
   const void* x; int x_f32;
   const uint16_t* ws1; const uint16_t* ws3;   // shared w1, w3 [Is][H] bf16
   uint16_t* hs_hi; uint16_t* hs_lo;    // [T][Is]
@@ -296,12 +297,6 @@ constexpr int kRsW = 8;
 constexpr size_t kRsRedBytes = kRsW * 2 * 64 * 4 * 4;
 constexpr size_t kRsTabOffset = (sizeof(BlockRoute) + 15) / 16 * 16;
 static_assert(kRsTabOffset < kRsRedBytes, "routing block state must fit the route/shared LDS");
-// k_route_sdown: the routing state and the whole expert pointer table (read
-// once with the scores, so the slot descriptors need no dependent load).
-__host__ __device__ inline size_t route_lds_bytes(int E) {
-  const size_t need = kRsTabOffset + static_cast<size_t>(E) * sizeof(dsk_expert_ptrs);
-  return need > kRsRedBytes ? need : kRsRedBytes;
-}
 constexpr int kRsTileDelay = 60;   // x 64 clocks (~1.6 us)
 
 __host__ __device__ inline int shared_up_tiles(int T, int Is) { return Is / (T <= 8 ? 8 : 16); }
@@ -406,7 +401,7 @@ __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
   if (blockIdx.x == 0) {
     block_route(*reinterpret_cast<BlockRoute*>(lds_up), p.scores, p.bias, p.T, p.E, p.k, p.route_scale,
                 p.table, true, p.route, reinterpret_cast<uint64_t*>(lds_up + kRsTabOffset / 2),
-                static_cast<int>((route_lds_bytes(p.E) - kRsTabOffset) / 8));
+                static_cast<int>((p.route_lds - static_cast<int>(kRsTabOffset)) / 8));
     return;
   }
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -417,6 +412,37 @@ __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
   if (p.T <= 2) __builtin_amdgcn_s_sleep(kRsTileDelay);
   shared_down_tile<kF32>(p, static_cast<int>(blockIdx.x) - 1, reinterpret_cast<float (*)[64][4]>(lds_up), lane,
                          wave);
+}
+
+// Outside the MX kernels the decode pipeline keeps the shared expert's gate/up
+// beside the routing and its down in the routed down kernels (the gate kernel
+// alone before): block 0 runs the top-k and slot map, blocks 1 ..
+// shared_up_tiles the shared gate/up tiles -> hs.
+template <bool kF32>
+__global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_route_shared(
+    DecodeArgs p) {
+  extern __shared__ __align__(16) uint16_t lds_up[];
+  if (blockIdx.x == 0) {
+    block_route(*reinterpret_cast<BlockRoute*>(lds_up), p.scores, p.bias, p.T, p.E, p.k, p.route_scale,
+                p.table, true, p.route, reinterpret_cast<uint64_t*>(lds_up + kRsTabOffset / 2),
+                static_cast<int>((p.route_lds - static_cast<int>(kRsTabOffset)) / 8));
+    return;
+  }
+  const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // At one or two tokens the routing block ends the kernel: its score loads
+  // wait for whatever the tile block beside it on the same CU requested
+  // first.  The tile blocks wait ~0.5 us (19 x 64 clocks) before their first
+  // loads, so the routing block's go out ahead of them.
+  if (p.T <= 2) __builtin_amdgcn_s_sleep(19);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int xs = p.H + 8;
+  uint16_t* xh = lds_up;
+  uint16_t* xl = lds_up + p.T * xs;
+  u32x4 xv[kUpXRegChunks][2];
+  const bool xreg = load_x<kF32, kRsW * 64>(p, xh, xl, xs, tid, xv);
+  const int rt = static_cast<int>(blockIdx.x) - 1;
+  if (p.T <= 8) shared_up_tile<kF32, kRsW, 8>(p, rt, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave, r16, g4);
+  else shared_up_tile<kF32, kRsW, 16>(p, rt, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave, r16, g4);
 }
 
 // Routed gate/up of the decode pipeline.  Each block takes kUpItems row
@@ -1711,12 +1737,33 @@ hipError_t launch_gate_shared(const dsk_moe_desc& d, const Workspace& L, const E
 
 hipError_t launch_route_sdown(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
                               int repeat) {
-  const DecodeArgs p = decode_args(d, L, a);
+  DecodeArgs p = decode_args(d, L, a);
   const unsigned blocks = static_cast<unsigned>(1 + (p.Is > 0 ? p.H / 16 : 0));
+  // the pointer table does not fit beside the routing state (it is read per slot from
+  // global memory; an LDS copy of all of it, prefetched with the scores, measured slower)
+  const size_t lds = kRsRedBytes;
+  p.route_lds = static_cast<int>(lds);
   for (int r = 0; r < repeat; ++r) {
-    const size_t lds = route_lds_bytes(p.E) <= kMaxLds ? route_lds_bytes(p.E) : kRsRedBytes;
     if (p.x_f32) launch_kernel(k_route_sdown<true>, blocks, kRsW * 64, lds, s, p);
     else launch_kernel(k_route_sdown<false>, blocks, kRsW * 64, lds, s, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
+                               int repeat) {
+  DecodeArgs p = decode_args(d, L, a);
+  const unsigned blocks = static_cast<unsigned>(1 + shared_up_tiles(p.T, p.Is));
+  // the pointer table goes to LDS only where the activation planes leave room: prefetching
+  // all of it beside the shared tiles' stream was slower (q3 B=1 route stage 10.2 -> 11.1 us)
+  // than the slot map's dependent table loads
+  const size_t lds = rs_lds_bytes(p);
+  p.route_lds = static_cast<int>(lds);
+  for (int r = 0; r < repeat; ++r) {
+    if (p.x_f32) launch_kernel(k_route_shared<true>, blocks, kRsW * 64, lds, s, p);
+    else launch_kernel(k_route_shared<false>, blocks, kRsW * 64, lds, s, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -300,17 +300,25 @@ hipError_t launch_grouped_down(const dsk_moe_desc& d, const Workspace& L, const 
 hipError_t launch_combine(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
                           int repeat);
 
-// Decode pipeline (decode_pipeline(d)), four kernels:
+// Decode pipeline (decode_pipeline(d)), four kernels.  With the MX kernels
+// (mx_decode(d)):
 //   launch_gate_shared    gate scores (a.scores) beside the shared expert's gate/up (hs);
 //   launch_route_sdown    top-k and slot map (a.route) in one block beside the shared
 //                         expert's down, written to the workspace's shared_x (x dtype);
-//   launch_experts_decode the routed gate/up, then the routed down and the combine in
-//                         one kernel (stages as for launch_experts), called with no
-//                         shared intermediate and shared_x as the precomputed output.
+//   launch_experts_decode the routed gate/up and down, called with no shared
+//                         intermediate and shared_x as the precomputed shared output.
+// Otherwise:
+//   launch_gate_scores    gate scores (a.scores);
+//   launch_route_shared   top-k and slot map beside the shared expert's gate/up (hs);
+//   launch_experts_decode the routed gate/up, then the routed and shared down and the
+//                         combine in one kernel (stages as for launch_experts).
 hipError_t launch_gate_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
                               int repeat);
 hipError_t launch_route_sdown(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
                               int repeat);
+hipError_t launch_gate_scores(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
+hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
+                               int repeat);
 hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L,
                                  const ExpertsArgs& a, hipStream_t s, int repeat);
 

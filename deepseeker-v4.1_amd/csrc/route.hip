@@ -411,6 +411,11 @@ hipError_t launch_route_dispatch(const dsk_moe_desc& d, const RouteArgs& a, hipS
   return launch_dispatch(d, a.idx, a.weights, a.table, a.out, s);
 }
 
+hipError_t launch_gate_scores(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s) {
+  const GateArgs g = route_gate_args(d, a);
+  return d.tokens >= 16 ? launch_gate<4, 4, false>(d, g, s) : launch_gate<1, 1, false>(d, g, s);
+}
+
 size_t cap_union_lds(int T, int E, int k) {
   return static_cast<size_t>(T) * k * 4 + static_cast<size_t>(E) * 9;
 }
