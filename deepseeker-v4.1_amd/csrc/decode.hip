@@ -664,14 +664,27 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
   extern __shared__ __align__(16) uint16_t lds_up[];
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
-  const int groups = (p.up_tiles + kUpItems - 1) / kUpItems;
+  // the intermediate is kMxInter (the launcher's condition), so the block ->
+  // slot map needs no argument
+  constexpr int kTiles = kMxInter / 16;
+  constexpr int groups = (kTiles + kUpItems - 1) / kUpItems;
   const int rb = static_cast<int>(blockIdx.x);
   const int slot = rb / groups;
-  if (slot >= p.active[0]) return;
+  // the argument words the first loads address, read in one go
+  asm volatile("" ::"s"(p.active), "s"(p.desc), "s"(p.rowmap), "s"(p.wrow), "s"(p.x));
+  // the active count, the slot's weight pointers and (below) the dispatch row
+  // and x go out together: the descriptor array has an entry for every slot
+  // index (its pointers are used only for a live slot), so nothing waits for
+  // the count before the block's first weight batch
+  const int U = p.active[0];
+  const uint8_t* W1 = static_cast<const uint8_t*>(desc_ptr(p.desc, slot, 0));
+  const uint8_t* S1 = static_cast<const uint8_t*>(desc_ptr(p.desc, slot, 1));
+  const uint8_t* W3 = static_cast<const uint8_t*>(desc_ptr(p.desc, slot, 3));
+  const uint8_t* S3 = static_cast<const uint8_t*>(desc_ptr(p.desc, slot, 4));
   const int T = p.T, K = p.H;
   const int item = wave / kUpKS, ks = wave % kUpKS;
   const int rt = (rb % groups) * kUpItems + item;
-  const bool rok = rt < p.up_tiles;
+  const bool rok = rt < kTiles;
   char* base = reinterpret_cast<char*>(lds_up);
   float (*red)[kUpKS][2][64][4] = reinterpret_cast<float (*)[kUpKS][2][64][4]>(base);
   uint8_t* xch = reinterpret_cast<uint8_t*>(base + kMxUpXchOffset) + wave * 640;
@@ -691,15 +704,13 @@ __global__ __launch_bounds__(kUpW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
     const int c = min(tid + j * NT, xchunks - 1);   // no condition on the load (see load_raw_nc)
     xv[j] = ldg16(static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(c / cpr) * K + (c % cpr) * 8);
   }
+  // (the pointers are read before the count is tested)
+  asm volatile("" ::"s"(W1), "s"(S1), "s"(W3), "s"(S3));
+  if (slot >= U) return;
   // 2. the first weight batch
-  const SlotDesc* d = p.desc + slot;
   const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
   const int per = (nblk + kUpKS - 1) / kUpKS;
   const int k0 = min(ks * per, nblk), k1 = min(k0 + per, nblk);
-  const uint8_t* W1 = static_cast<const uint8_t*>(d->p[0]);
-  const uint8_t* S1 = static_cast<const uint8_t*>(d->p[1]);
-  const uint8_t* W3 = static_cast<const uint8_t*>(d->p[3]);
-  const uint8_t* S3 = static_cast<const uint8_t*>(d->p[4]);
   UpBatch<G> A, B;
   load_batch<G, true>(A, W1, S1, W3, S3, row, K, k0, k1, g4, rok);
   const bool tv = drow >= 0 && rok;
@@ -1267,11 +1278,13 @@ static_assert((kMxSlots * 3) % 4 == 0, "h DMA instructions cover whole (slot, co
 // at once: first the wave's slices of the FP8 h planes k_up_mx wrote (B
 // column 3t + p: plane p of token t; zero planes for a token not routed to
 // the slot) and of their E8M0 windows, 16 contiguous bytes per lane, then
-// every expert's w2 codes and scale windows.  The slices go to wave-private
-// LDS as they land (each store waits for its own load), and each expert is
-// computed as its weights land, one v_mfma_scale_f32_16x16x128_f8f6f4 per K
-// block with the B operand read back from LDS.  Slots past the active count
-// re-read slot 0 and are computed with zero codes (straight-line code, so
+// every expert's w2 codes and scale windows.  The h loads do not wait for
+// the active count (it arrives with the slots' descriptors), so they are
+// ahead of the weights of every block.  The slices go to wave-private LDS as
+// they land (each store waits for its own load), and each expert is computed
+// as its weights land, one v_mfma_scale_f32_16x16x128_f8f6f4 per K block with
+// the B operand read back from LDS.  Slots past the active count re-read slot
+// 0's weights and are computed with a zero B operand (straight-line code, so
 // that every wait is for the loads it needs only).  One accumulator chain
 // per K block of the wave, each over the slots in order -- a token's sum does
 // not depend on the other token's experts (a slot the token is not routed to
@@ -1288,7 +1301,8 @@ __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
   const int r16 = lane & 15, g4 = lane >> 4;
   const int row0 = blockIdx.x * 16;
   const uint32_t row = static_cast<uint32_t>(row0 + r16);
-  const int U = p.active[0];
+  const int U = p.active[0];   // at least 1 (every token has top_k >= 1 experts)
+  const int ms = min(p.E, T * p.k);   // slots of the h planes the gate/up grid covers
   const int I = p.I;
   const int kb0 = wave * kStKB;
   uint8_t* hl = lds_mx + kMxDnRedBytes + wave * mx_dn_wave_bytes(T);   // [kMxSlots][C][256]
@@ -1297,8 +1311,32 @@ __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
   const int bc = min(r16, C - 1);
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
   f32x4 acc[kStKB] = {z, z};
-  for (int u0 = 0; u0 < U; u0 += kMxSlots) {
-    // 1. the round's h planes and E8M0 windows (slots past U re-read slot 0):
+  // the shared output of this lane's output elements (wave 0, token min(r16, T - 1))
+  // before anything else, so that the epilogue does not wait for it
+  uint2 shr = {0u, 0u};
+  if (wave == 0 && p.shared_out)
+    shr = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.shared_out) +
+                                          static_cast<int64_t>(min(r16, T - 1)) * p.H + row0 + 4 * g4);
+  const uint8_t* W0 = static_cast<const uint8_t*>(desc_ptr(p.desc, 0, 6));
+  const uint8_t* S0 = static_cast<const uint8_t*>(desc_ptr(p.desc, 0, 7));
+  int u0 = 0;
+  do {
+    // (the round's start as an opaque value: nothing of a round is computed
+    // ahead of the previous one)
+    asm volatile("" : "+s"(u0));
+    // the round's descriptors go out with the count (entries below E exist for
+    // every index; a slot past the count takes slot 0's pointers), the h planes
+    // with them (they do not wait for the count), and only the weights wait
+    const uint8_t* Wr[kMxSlots];
+    const uint8_t* Sr[kMxSlots];
+#pragma unroll
+    for (int i = 0; i < kMxSlots; ++i) {
+      const int ui = min(u0 + i, p.E - 1);
+      Wr[i] = static_cast<const uint8_t*>(desc_ptr(p.desc, ui, 6));
+      Sr[i] = static_cast<const uint8_t*>(desc_ptr(p.desc, ui, 7));
+    }
+    // 1. the round's h planes and E8M0 windows (slot indices past the gate/up
+    // grid re-read its last slot; a slot past the count is not used):
     // lane l takes 16 bytes of (slot, column) pair 4q + l / 16, 4 bytes of pair 32q + l / 2
     constexpr int NH = kMxSlots * C / 4, NS = mx_dn_s_bytes(T) / 256;
     u32x4 hv[NH];
@@ -1306,38 +1344,50 @@ __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
 #pragma unroll
     for (int q = 0; q < NH; ++q) {
       const int pair = 4 * q + (lane >> 4), i = pair / C, c = pair - i * C;
-      const int su = u0 + i < U ? u0 + i : 0;
+      const int su = min(u0 + i, ms - 1);
       hv[q] = ldg16(p.hq + static_cast<uint32_t>(su * C + c) * static_cast<uint32_t>(I) + kb0 * 128 + (lane & 15) * 16);
     }
 #pragma unroll
     for (int q = 0; q < NS; ++q) {
       const int pair = min(32 * q + (lane >> 1), kMxSlots * C - 1), i = pair / C, c = pair - i * C;
-      const int su = u0 + i < U ? u0 + i : 0;
+      const int su = min(u0 + i, ms - 1);
       sv[q] = ldg<uint32_t>(p.hqs + static_cast<uint32_t>(su * C + c) * static_cast<uint32_t>(I / 32) + kb0 * 4 + 4 * (lane & 1));
     }
     __builtin_amdgcn_sched_barrier(0);
+    // (the descriptors are all read before the first weight load)
+    asm volatile("" ::"s"(Wr[0]), "s"(Wr[1]), "s"(Wr[2]), "s"(Wr[3]), "s"(Wr[4]), "s"(Wr[5]), "s"(Wr[6]),
+                 "s"(Wr[7]), "s"(Sr[0]), "s"(Sr[1]), "s"(Sr[2]), "s"(Sr[3]), "s"(Sr[4]), "s"(Sr[5]), "s"(Sr[6]),
+                 "s"(Sr[7]));
+    static_assert(kMxSlots == 8, "one operand per slot above");
     // 2. every expert's w2 codes and scale windows
     u32x4 wc[kMxSlots][kStKB];
     u32x2 ws[kMxSlots];
 #pragma unroll
     for (int i = 0; i < kMxSlots; ++i) {
-      const int su = u0 + i < U ? u0 + i : 0;
-      const uint8_t* W = static_cast<const uint8_t*>(desc_ptr(p.desc, su, 6));
-      const uint8_t* S = static_cast<const uint8_t*>(desc_ptr(p.desc, su, 7));
+      const bool live = u0 + i < U;
+      const uint8_t* W = live ? Wr[i] : W0;
+      const uint8_t* S = live ? Sr[i] : S0;
 #pragma unroll
       for (int j = 0; j < kStKB; ++j) wc[i][j] = ldg16(W + row * static_cast<uint32_t>(I / 2) + (kb0 + j) * 64 + g4 * 16);
       ws[i] = ldg<u32x2>(S + row * static_cast<uint32_t>(I / 32) + kb0 * 4);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // 3. the slices into the wave's LDS (in the lane order they were loaded)
+    // 3. the slices into the wave's LDS (in the lane order they were loaded); a
+    // slot past the count gets zero planes with scale bytes 1.0 (what it read
+    // may be anything, its weights are slot 0's), so it adds exact zeros
 #pragma unroll
-    for (int q = 0; q < NH; ++q) *reinterpret_cast<u32x4*>(hl + q * 1024 + lane * 16) = hv[q];
+    for (int q = 0; q < NH; ++q) {
+      const bool live = u0 + (4 * q + (lane >> 4)) / C < U;
+      *reinterpret_cast<u32x4*>(hl + q * 1024 + lane * 16) = live ? hv[q] : u32x4{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
-    for (int q = 0; q < NS; ++q) *reinterpret_cast<uint32_t*>(sl + q * 256 + lane * 4) = sv[q];
+    for (int q = 0; q < NS; ++q) {
+      const bool live = u0 + min(32 * q + (lane >> 1), kMxSlots * C - 1) / C < U;
+      *reinterpret_cast<uint32_t*>(sl + q * 256 + lane * 4) = live ? sv[q] : 0x7f7f7f7fu;
+    }
     // 4. the experts in slot order as they land
 #pragma unroll
     for (int i = 0; i < kMxSlots; ++i) {
-      const bool live = u0 + i < U;
 #pragma unroll
       for (int j = 0; j < kStKB; ++j) {
         const uint8_t* src = hl + (i * C + bc) * 256 + j * 128 + g4 * 32;
@@ -1345,11 +1395,11 @@ __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
         const u32x4 hi = *reinterpret_cast<const u32x4*>(src + 16);
         const uint32_t hs = sl[(i * C + bc) * 8 + 4 * j + g4];
         const uint32_t wsb = ((j == 0 ? ws[i].x : ws[i].y) >> (8 * g4)) & 0xffu;
-        const u32x4 codes = live ? wc[i][j] : u32x4{0u, 0u, 0u, 0u};
-        acc[j] = mx_mfma(codes, wsb, lo, hi, hs, acc[j]);
+        acc[j] = mx_mfma(wc[i][j], wsb, lo, hi, hs, acc[j]);
       }
     }
-  }
+    u0 += kMxSlots;
+  } while (u0 < U);
   static_assert(kStKB == 2, "two K-block chains");
   *reinterpret_cast<f32x4*>(&red[wave][lane][0]) = acc[0] + acc[1];
   __syncthreads();
@@ -1362,7 +1412,15 @@ __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       ra[q] = (__shfl(a[q], gb + 3 * t, 64) + __shfl(a[q], gb + 3 * t + 1, 64)) + __shfl(a[q], gb + 3 * t + 2, 64);
-    if (r16 < T) down_epilogue(p, ra, z, row0, r16, g4);
+    if (r16 < T) {
+      // bf16 x: the shared output is already in x's dtype
+      if (p.shared_out)
+        ra += f32x4{__uint_as_float(shr.x << 16), __uint_as_float(shr.x & 0xffff0000u),
+                    __uint_as_float(shr.y << 16), __uint_as_float(shr.y & 0xffff0000u)};
+      uint16_t* ob = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(r16) * p.H + row0 + 4 * g4;
+      *reinterpret_cast<uint2*>(ob) = uint2{f32_to_bf16_bits(ra[0]) | (uint32_t(f32_to_bf16_bits(ra[1])) << 16),
+                                            f32_to_bf16_bits(ra[2]) | (uint32_t(f32_to_bf16_bits(ra[3])) << 16)};
+    }
   }
 }
 
