@@ -295,9 +295,9 @@ constexpr int kRsW = 8;
 // them) its wave partial sums [kRsW][2][64][4] f32, a shared down tile's
 // wave partial sums [kRsW][64][4] f32, or two gate tiles' segment sums.
 constexpr size_t kRsRedBytes = kRsW * 2 * 64 * 4 * 4;
-constexpr size_t kRsTabOffset = (sizeof(BlockRoute) + 15) / 16 * 16;
+constexpr size_t kRsTabOffset = (kBlockRouteLds + 15) / 16 * 16;
 static_assert(kRsTabOffset < kRsRedBytes, "routing block state must fit the route/shared LDS");
-constexpr int kRsTileDelay = 60;   // x 64 clocks (~1.6 us)
+constexpr int kRsTileDelay = 15;   // x 64 clocks (~0.4 us)
 
 __host__ __device__ inline int shared_up_tiles(int T, int Is) { return Is / (T <= 8 ? 8 : 16); }
 
@@ -399,8 +399,8 @@ __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
     DecodeArgs p) {
   extern __shared__ __align__(16) uint16_t lds_up[];
   if (blockIdx.x == 0) {
-    block_route(*reinterpret_cast<BlockRoute*>(lds_up), p.scores, p.bias, p.T, p.E, p.k, p.route_scale,
-                p.table, true, p.route, reinterpret_cast<uint64_t*>(lds_up + kRsTabOffset / 2),
+    block_route(lds_up, p.scores, p.bias, p.T, p.E, p.k, p.route_scale, p.table, p.route,
+                reinterpret_cast<uint64_t*>(lds_up + kRsTabOffset / 2),
                 static_cast<int>((p.route_lds - static_cast<int>(kRsTabOffset)) / 8));
     return;
   }
@@ -423,8 +423,8 @@ __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
     DecodeArgs p) {
   extern __shared__ __align__(16) uint16_t lds_up[];
   if (blockIdx.x == 0) {
-    block_route(*reinterpret_cast<BlockRoute*>(lds_up), p.scores, p.bias, p.T, p.E, p.k, p.route_scale,
-                p.table, true, p.route, reinterpret_cast<uint64_t*>(lds_up + kRsTabOffset / 2),
+    block_route(lds_up, p.scores, p.bias, p.T, p.E, p.k, p.route_scale, p.table, p.route,
+                reinterpret_cast<uint64_t*>(lds_up + kRsTabOffset / 2),
                 static_cast<int>((p.route_lds - static_cast<int>(kRsTabOffset)) / 8));
     return;
   }

@@ -136,8 +136,9 @@ int dsk_cap_union(int32_t tokens, int32_t n_experts, int32_t top_k, int32_t budg
  * replaces the per-expert loop, the shared add and the final cast of
  * moe_layer (src/deepseeker/mlx_forward.py:388-419) and the shared expert
  * (src/deepseeker/mlx_runner.py:765-783).
- * table: device array [E] of dsk_expert_ptrs (entries of experts that
- * receive no token are never read); ws1/ws3/ws2: shared expert bf16 weights
+ * table: device array [E] of dsk_expert_ptrs (all E entries readable; the
+ * weights of experts that receive no token are never read, so their pointers
+ * may be anything); ws1/ws3/ws2: shared expert bf16 weights
  * (used when inter_shared > 0); shared_out: an already computed shared
  * expert output [T,H] in x_dtype, added instead when inter_shared == 0
  * (NULL: no shared expert); out [T,H] in x_dtype. */
