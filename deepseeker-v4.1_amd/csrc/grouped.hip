@@ -28,6 +28,7 @@ constexpr int kDKS = 1;             // down: K ranges of a row tile
 constexpr int kDW = kDI * kDKS;     // waves of a down block
 constexpr int kGNC = 8;             // dispatch rows (B columns) of a column tile
 constexpr int kStageQ = 2;          // 16-byte activation chunks per thread per staging pass
+constexpr int kDnRingFP4 = 4;       // down: FP4 weight batches in flight per wave
 
 static_assert(kGW == kDW, "both kernels use the same block size");
 
@@ -55,6 +56,9 @@ struct GroupedArgs {
 // temporaries), two for FP4 (20 bytes).
 template <typename Raw>
 constexpr int batch_blocks() { return std::is_same_v<Raw, RawFP4> ? 2 : 1; }
+// Weight batches in flight per wave in the down kernel.
+template <typename Raw>
+constexpr int down_ring() { return std::is_same_v<Raw, RawFP4> ? kDnRingFP4 : 2; }
 
 // Rows [c0, c0 + cols) of the slot's activations (row r comes from source row
 // src(r) of `base`, row stride `ld` elements, K elements) into LDS rows of
@@ -141,11 +145,22 @@ __device__ __forceinline__ void up_block(const GroupedArgs& p, LoadW load_w, WPt
         mma_block2(r1[i], r3[i], brow, kc, tv && kb + i < k1, ag, au);
       }
     };
-    for (int kb = k0; kb < k1; kb += 2 * G) {
-      mm(a1, a3, wa1, wa3, kb);
-      if (kb + 2 * G < k1) ld(a1, a3, wa1, wa3, kb + 2 * G);
-      if (kb + G < k1) mm(b1, b3, wb1, wb3, kb + G);
-      if (kb + 3 * G < k1) ld(b1, b3, wb1, wb3, kb + 3 * G);
+    // batches a, b alternate; pairs whose reloads both lie in the range run
+    // without conditions (exact waits, see down_block), the last pair reloads
+    // only what remains
+    const int nb = (k1 - k0 + G - 1) / G;
+    int j0 = 0;
+    for (; j0 + 4 <= nb; j0 += 2) {
+      mm(a1, a3, wa1, wa3, k0 + j0 * G);
+      ld(a1, a3, wa1, wa3, k0 + (j0 + 2) * G);
+      mm(b1, b3, wb1, wb3, k0 + (j0 + 1) * G);
+      ld(b1, b3, wb1, wb3, k0 + (j0 + 3) * G);
+    }
+    for (; j0 < nb; j0 += 2) {
+      mm(a1, a3, wa1, wa3, k0 + j0 * G);
+      if (j0 + 2 < nb) ld(a1, a3, wa1, wa3, k0 + (j0 + 2) * G);
+      if (j0 + 1 < nb) mm(b1, b3, wb1, wb3, k0 + (j0 + 1) * G);
+      if (j0 + 3 < nb) ld(b1, b3, wb1, wb3, k0 + (j0 + 3) * G);
     }
     if constexpr (kGKS > 1) {
       __syncthreads();   // every wave is done with the x tile
@@ -364,12 +379,13 @@ __device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, W
   uint16_t* thi = lds;                      // [kGNC][K + 8] hi plane
   uint16_t* tlo = lds + kGNC * hs;          // [kGNC][K + 8] lo plane
   float (*red)[kDKS][64][4] = reinterpret_cast<float (*)[kDKS][64][4]>(lds);   // over the h tile
+  constexpr int NB = down_ring<Raw>();
   for (int c0 = 0; c0 < n; c0 += kGNC) {
     const int cols = min(kGNC, n - c0);
-    Raw a[G], b[G];
+    Raw a[NB][G];
     // FP4: the scales of a batch's 2 blocks (all lane groups) as one 8-byte
     // window instead of one byte per lane and block; the byte is picked at use
-    u32x2 wa{}, wb{};
+    u32x2 wa[NB] = {};
     // no condition on the loads (see load_raw_nc): blocks past the range
     // re-read its last block (not computed)
     auto ld = [&](Raw (&r)[G], u32x2& w, int kb) {
@@ -383,8 +399,8 @@ __device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, W
         for (int i = 0; i < G; ++i) load_w(r[i], row, min(kb + i, k1 - 1) * 128 + g4 * 32);
       }
     };
-    ld(a, wa, k0);
-    ld(b, wb, k0 + G);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) ld(a[i], wa[i], k0 + i * G);
     stage_rows(thi, src_hi, K, K, cols, [&](int r) { return base + c0 + r; });
     stage_rows(tlo, src_lo, K, K, cols, [&](int r) { return base + c0 + r; });
     __syncthreads();
@@ -402,11 +418,28 @@ __device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, W
         mma_block(r[i], bl, kc, ok, acc);
       }
     };
-    for (int kb = k0; kb < k1; kb += 2 * G) {
-      mm(a, wa, kb);
-      if (kb + 2 * G < k1) ld(a, wa, kb + 2 * G);
-      if (kb + G < k1) mm(b, wb, kb + G);
-      if (kb + 3 * G < k1) ld(b, wb, kb + 3 * G);
+    // NB batches in a ring: each is multiplied, then reloaded NB batches ahead.
+    // Groups whose reloads all lie in the range run without conditions (a load
+    // under a condition makes the next use of an older batch wait for every
+    // load, as at a branch merge the wait counter cannot tell which were
+    // issued); the last groups reload only what remains.
+    const int nb = (k1 - k0 + G - 1) / G;
+    int j0 = 0;
+    for (; j0 + 2 * NB <= nb; j0 += NB) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        mm(a[i], wa[i], k0 + (j0 + i) * G);
+        ld(a[i], wa[i], k0 + (j0 + i + NB) * G);
+      }
+    }
+    for (; j0 < nb; j0 += NB) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        if (j0 + i < nb) {
+          mm(a[i], wa[i], k0 + (j0 + i) * G);
+          if (j0 + i + NB < nb) ld(a[i], wa[i], k0 + (j0 + i + NB) * G);
+        }
+      }
     }
     if constexpr (kDKS > 1) {
       __syncthreads();   // every wave is done with the h tile
