@@ -538,8 +538,9 @@ def main() -> int:
     prefill = T >= PREFILL_MIN_TOKENS
     workload = (f"full-size {args.quant.upper()} MoE layer {'prefill' if prefill else 'decode'}, B={T}"
                 + (f", Zipf({args.zipf}) gate bias" if args.zipf else ""))
-    timing = (f"kernel begin/end timestamps (HIP events carried by the launches), median over "
-              f"{args.timed_steps} steps of the same cold-weight rotation")
+    timing = (f"kernel begin/end timestamps (HIP events carried by the launches), "
+              f"{'median' if T >= PREFILL_MIN_TOKENS else 'mean'} over {args.timed_steps} steps of the "
+              f"same cold-weight rotation")
     if prefill:
         summ = prefill_summary(r, T, args.steps)
         up_us = summ["stages"]["gate_up"]["us"]["median"]
