@@ -13,6 +13,7 @@ namespace dsk {
 namespace {
 
 constexpr int kNormThreads = 256;
+// rows up to 4096 / 8192 wide are held in registers (4 / 8 chunks per thread)
 
 template <bool kBF16>
 __device__ __forceinline__ f32x4 ld4(const void* p, int64_t i) {
@@ -46,8 +47,11 @@ __device__ __forceinline__ float round_to(float v) {
 // Row r: h = x[r] (+ res[r]); h_out[r] = h (if given; may be x itself);
 // y[r] = rmsnorm(h) (if given).  H % 4 == 0; thread t handles the 4-element
 // chunks t, t + 256, ... in both passes, so an in-place h_out is re-read by
-// the thread that wrote it.
-template <bool kBF16>
+// the thread that wrote it.  With NC > 0 (rows up to NC * 1024 wide) the row
+// stays in registers: one round of loads instead of one per chunk (the loop
+// form's loads cannot pass the store to h_out, which may be x); chunks past
+// the row re-read the last one and add exact zeros to the (non-negative) sum.
+template <bool kBF16, bool kRes, bool kGamma, int NC>
 __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(const void* x, const void* res,
                                                           const float* __restrict__ gamma, int H, float eps,
                                                           void* h_out, void* __restrict__ y) {
@@ -56,6 +60,52 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(const void* x, const v
   const int64_t base = static_cast<int64_t>(blockIdx.x) * H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nch = H / 4;
+  if constexpr (NC > 0) {
+    // the row in registers: every load (x, residual, gamma) issued before the
+    // first use, then the same sums in the same order as the loop form below
+    f32x4 h[NC], r[NC], g[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = min(tid + i * kNormThreads, nch - 1);   // no condition on the loads
+      h[i] = ld4<kBF16>(x, base + 4 * c);
+      if constexpr (kRes) r[i] = ld4<kBF16>(res, base + 4 * c);
+      if constexpr (kGamma) g[i] = *reinterpret_cast<const f32x4*>(gamma + 4 * c);
+      else g[i] = f32x4{1.f, 1.f, 1.f, 1.f};
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = tid + i * kNormThreads;
+      const bool v = c < nch;
+      if constexpr (kRes) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) h[i][q] = round_to<kBF16>(h[i][q] + r[i][q]);
+        if (h_out && v) st4<kBF16>(h_out, base + 4 * c, h[i]);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ss = ss + (v ? h[i][q] * h[i][q] : 0.0f);
+    }
+    if (!y) return;
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) ss = ss + __shfl_xor(ss, s, 64);
+    if (lane == 0) wsum[wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kNormThreads / 64; ++w) tot = tot + wsum[w];
+    const float rstd = 1.0f / sqrtf(tot / static_cast<float>(H) + eps);
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = tid + i * kNormThreads;
+      if (c < nch) {
+        f32x4 o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = (h[i][q] * rstd) * g[i][q];
+        st4<kBF16>(y, base + 4 * c, o);
+      }
+    }
+    return;
+  } else {
   float ss = 0.0f;
   for (int c = tid; c < nch; c += kNormThreads) {
     f32x4 h = ld4<kBF16>(x, base + 4 * c);
@@ -95,6 +145,26 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(const void* x, const v
     for (int q = 0; q < 4; ++q) o[q] = (h[q] * rstd) * g[q];
     st4<kBF16>(y, base + 4 * c, o);
   }
+  }
+}
+
+template <bool kBF16, int NC>
+void launch_rmsnorm_nc(const void* x, const void* res, const float* gamma, int64_t rows, int H, float eps,
+                       void* h_out, void* y, hipStream_t s) {
+  const unsigned b = static_cast<unsigned>(rows);
+  if (res && gamma) launch_kernel(k_rmsnorm<kBF16, true, true, NC>, b, kNormThreads, 0, s, x, res, gamma, H, eps, h_out, y);
+  else if (res) launch_kernel(k_rmsnorm<kBF16, true, false, NC>, b, kNormThreads, 0, s, x, res, gamma, H, eps, h_out, y);
+  else if (gamma) launch_kernel(k_rmsnorm<kBF16, false, true, NC>, b, kNormThreads, 0, s, x, res, gamma, H, eps, h_out, y);
+  else launch_kernel(k_rmsnorm<kBF16, false, false, NC>, b, kNormThreads, 0, s, x, res, gamma, H, eps, h_out, y);
+}
+
+template <bool kBF16>
+void launch_rmsnorm_t(const void* x, const void* res, const float* gamma, int64_t rows, int H, float eps,
+                      void* h_out, void* y, hipStream_t s) {
+  const int nch = H / 4;
+  if (nch <= 4 * kNormThreads) launch_rmsnorm_nc<kBF16, 4>(x, res, gamma, rows, H, eps, h_out, y, s);
+  else if (nch <= 8 * kNormThreads) launch_rmsnorm_nc<kBF16, 8>(x, res, gamma, rows, H, eps, h_out, y, s);
+  else launch_rmsnorm_nc<kBF16, 0>(x, res, gamma, rows, H, eps, h_out, y, s);
 }
 
 }  // namespace
@@ -102,10 +172,8 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm(const void* x, const v
 hipError_t launch_rmsnorm(const void* x, const void* res, const float* gamma, int64_t rows, int H, float eps,
                           int dtype, void* h_out, void* y, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  if (dtype == DSK_DTYPE_BF16)
-    launch_kernel(k_rmsnorm<true>, static_cast<unsigned>(rows), kNormThreads, 0, s, x, res, gamma, H, eps, h_out, y);
-  else
-    launch_kernel(k_rmsnorm<false>, static_cast<unsigned>(rows), kNormThreads, 0, s, x, res, gamma, H, eps, h_out, y);
+  if (dtype == DSK_DTYPE_BF16) launch_rmsnorm_t<true>(x, res, gamma, rows, H, eps, h_out, y, s);
+  else launch_rmsnorm_t<false>(x, res, gamma, rows, H, eps, h_out, y, s);
   return hipGetLastError();
 }
 
