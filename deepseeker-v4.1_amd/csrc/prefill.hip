@@ -251,7 +251,231 @@ __device__ __forceinline__ void pf_gemm(LoadA load_a, const uint16_t* const (&br
   else pf_loop<false, P, Regs>(load_a, brow, nst, n_ct, lds, acc);
 }
 
-constexpr size_t kPfLdsBytes = 2 * static_cast<size_t>(Bf16Tile::kBytes + kPfBBytes);
+// ---------------------------------------------------------------------------
+// FP4 kernels' loop: the stage tiles go from global memory straight into LDS
+// (global_load_lds_dwordx4: lane i of a wave writes the 16 bytes it loaded at
+// the instruction's LDS base + 16 i), so no registers hold a stage between
+// its load and its store and no wave waits for a load before it can store.
+// Any 16-byte chunk can be sent to any LDS position: the gather of token rows
+// stays per lane, and 128-byte tile rows (64 bf16) are swizzled, chunk c of
+// row r at position c ^ ((r >> 1) & 7), so the fragment reads (lanes on 16
+// consecutive rows at one chunk) touch 16 distinct 16-byte bank groups with
+// no padding.  The wait for a stage and the barrier are one s_waitcnt vmcnt(N)
+// + s_barrier: the compiler's own barrier would wait for every load in flight.
+
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+// 2 bytes, written zero-extended to the lane's 4-byte LDS slot
+__device__ __forceinline__ void dma2(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)lds, 2, 0, 0);
+}
+
+// All but the newest N loads of this wave have landed (in LDS, for the DMA
+// loads), its LDS reads are complete, then the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
+
+// Stage chunk (row, chunk) loaded by lane i of load j of wave w, for 128-byte
+// rows spread over 4 loads per lane: LDS position p = (4 w + j) 64 + i.
+__device__ __forceinline__ int dma_row(int w, int j, int i) { return (4 * w + j) * 8 + (i >> 3); }
+__device__ __forceinline__ int dma_chunk(int w, int j, int i) { return swz(dma_row(w, j, i), i & 7); }
+
+// All but the newest n (0..7, wave-uniform) loads of this wave have landed.
+__device__ __forceinline__ void wait_barrier_n(int n) {
+  switch (n) {
+    case 0: wait_barrier<0>(); break;
+    case 1: wait_barrier<1>(); break;
+    case 2: wait_barrier<2>(); break;
+    case 3: wait_barrier<3>(); break;
+    case 4: wait_barrier<4>(); break;
+    case 5: wait_barrier<5>(); break;
+    case 6: wait_barrier<6>(); break;
+    default: wait_barrier<7>(); break;
+  }
+}
+
+// FP4 weights (K a multiple of 512).  Each load reads whole 64-byte pieces of
+// a row, so that a wave's load touches few cache lines: the codes of two
+// stages at once (64 bytes of a row), the E8M0 scales of eight stages at once
+// (16 bytes of a row).  The weights stream from beyond L2, so they are loaded
+// further ahead than the tokens: when stage st starts, the tokens of stage
+// st + 2, the codes of stages st + 4 and st + 5 (st even) and the scales of
+// stages st + 8 .. st + 15 (st a multiple of 8).  LDS: three token buffers
+// [256][128 B] (stage st in buffer st % 3), three code buffers [256][64 B]
+// (stage pair g in buffer g % 3; 16-byte chunk q of row r at position
+// q ^ ((r >> 2) & 3)), two scale buffers [256][16 B] (stages 8G..8G+7 in
+// buffer G & 1, loaded by waves 0-3).
+struct DmaFp4 {
+  static constexpr int kB = 0, kBBuf = 32768;
+  static constexpr int kC = 3 * kBBuf, kCBuf = 16384;
+  static constexpr int kS = kC + 3 * kCBuf, kSBuf = 4096;
+  static constexpr int kEnd = kS + 2 * kSBuf;
+  static constexpr bool kWaitNewest = true;   // the end of a stage waits for all but its own loads
+  const uint8_t* gc[2];   // this lane's code chunk of stage pair 0, loads j = 0, 1
+  const uint8_t* gs;      // its row's scales of stages 0..7 (waves 0-3)
+  const uint8_t* gb[4];   // token chunks of stage 0
+  // code load j of wave w, lane i: row and logical chunk (16 bytes of the row's 64)
+  __device__ __forceinline__ static int code_row(int w, int j, int i) { return ((2 * w + j) * 64 + i) >> 2; }
+  __device__ __forceinline__ static int code_chunk(int w, int j, int i) {
+    return (i & 3) ^ ((code_row(w, j, i) >> 2) & 3);
+  }
+  __device__ __forceinline__ void tokens(char* lds, int st, int wave) const {
+    char* b = lds + kB + (st % 3) * kBBuf;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(gb[j] + st * (kPfK * 2), b + (4 * wave + j) * 1024);
+  }
+  __device__ __forceinline__ void codes(char* lds, int g, int wave) const {
+    char* c = lds + kC + (g % 3) * kCBuf;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(gc[j] + g * kPfK, c + (2 * wave + j) * 1024);
+  }
+  __device__ __forceinline__ int scales(char* lds, int G, int wave) const {
+    if (wave >= 4) return 0;
+    dma16(gs + G * 16, lds + kS + (G & 1) * kSBuf + wave * 1024);
+    return 1;
+  }
+  // loads before stage 0; returns how many of them stage 0 need not wait for
+  __device__ __forceinline__ int prologue(char* lds, int nst, int wave) const {
+    scales(lds, 0, wave);
+    codes(lds, 0, wave);
+    if (nst > 2) codes(lds, 1, wave);
+    tokens(lds, 0, wave);
+    if (nst > 1) {
+      tokens(lds, 1, wave);
+      return 4;
+    }
+    return 0;
+  }
+  // loads issued when stage st starts; returns their count
+  __device__ __forceinline__ int issue_at(char* lds, int st, int nst, int wave) const {
+    int n = 0;
+    if (st + 2 < nst) {
+      tokens(lds, st + 2, wave);
+      n += 4;
+    }
+    if ((st & 1) == 0 && st + 4 < nst) {
+      codes(lds, (st + 4) >> 1, wave);
+      n += 2;
+    }
+    if ((st & 7) == 0 && st + 8 < nst) n += scales(lds, (st + 8) >> 3, wave);
+    return n;
+  }
+  __device__ __forceinline__ static const char* bbase(const char* lds, int st) { return lds + kB + (st % 3) * kBBuf; }
+  __device__ __forceinline__ static const char* abase(const char*, int) { return nullptr; }
+  struct Frag { u32x4 c[4]; float sc[4]; };
+  __device__ __forceinline__ static void frag_begin(Frag& f, const char* lds, int st, int wm, int lane) {
+    const int h = lane >> 5, l = lane & 31;
+    // rows 128 wm + 32 i + l share the chunk swizzle of l
+    const char* c = lds + kC + ((st >> 1) % 3) * kCBuf + (128 * wm + l) * 64 +
+                    ((((st & 1) * 2 + h) ^ ((l >> 2) & 3)) * 16);
+    const char* sp = lds + kS + ((st >> 3) & 1) * kSBuf + (128 * wm + l) * 16 + (st & 7) * 2 + h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f.c[i] = *reinterpret_cast<const u32x4*>(c + i * 32 * 64);
+      f.sc[i] = e8m0_to_f32(*reinterpret_cast<const uint8_t*>(sp + i * 32 * 16));
+    }
+  }
+  __device__ __forceinline__ static bf16x8 operand(const Frag& f, const char*, int i, int ks, int) {
+    const uint32_t w = ks == 0 ? f.c[i].x : (ks == 1 ? f.c[i].y : (ks == 2 ? f.c[i].z : f.c[i].w));
+    return fp4_word_to_bf16x8(w, f.sc[i]);
+  }
+};
+
+// bf16 weights (the shared expert): per stage, weights and tokens [256][128 B]
+// each, both swizzled; two buffers (three would not fit); the loads of stage
+// st + 1 are issued when stage st starts and waited for at its end.
+struct DmaBf16 {
+  static constexpr int kA = 0, kB = 32768, kBuf = kB + 32768;
+  static constexpr int kEnd = 2 * kBuf;
+  static constexpr bool kWaitNewest = false;
+  const uint8_t* ga[4];
+  const uint8_t* gb[4];
+  __device__ __forceinline__ void stage(char* lds, int st, int wave) const {
+    char* buf = lds + (st & 1) * kBuf;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dma16(ga[j] + st * (kPfK * 2), buf + kA + (4 * wave + j) * 1024);
+      dma16(gb[j] + st * (kPfK * 2), buf + kB + (4 * wave + j) * 1024);
+    }
+  }
+  __device__ __forceinline__ int prologue(char* lds, int, int wave) const {
+    stage(lds, 0, wave);
+    return 0;
+  }
+  __device__ __forceinline__ int issue_at(char* lds, int st, int nst, int wave) const {
+    if (st + 1 < nst) stage(lds, st + 1, wave);
+    return 0;
+  }
+  __device__ __forceinline__ static const char* bbase(const char* lds, int st) { return lds + (st & 1) * kBuf + kB; }
+  __device__ __forceinline__ static const char* abase(const char* lds, int st) { return lds + (st & 1) * kBuf + kA; }
+  struct Frag {};
+  __device__ __forceinline__ static void frag_begin(Frag&, const char*, int, int, int) {}
+  // arow: this lane's first weight row in the stage's tile; koff: its K step's chunk
+  __device__ __forceinline__ static bf16x8 operand(const Frag&, const char* arow, int i, int, int koff) {
+    return lds16(arow + i * 32 * 128 + koff);
+  }
+};
+
+// Main loop of one block tile with LDS DMA stages.  Per stage st: issue the
+// policy's loads; the previous stage's last K step's MFMAs; K steps 0-2;
+// operands of K step 3, kept; wait until stage st + 1 has landed, barrier.
+// Wave w multiplies weight rows 128 (w & 1) + [0, 128) by tokens
+// 64 (w >> 1) + [0, 64).
+template <bool kFull, class P>
+__device__ __forceinline__ void pf_loop_dma(const P& src, int nst, int n_ct, char* lds, f32x16 (&acc)[4][2]) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int wm = wave & 1, wn = wave >> 1, h = lane >> 5;
+  // rows 32 i + (lane & 31) of a 128-byte-row tile share the swizzle of lane & 31
+  int koff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) koff[ks] = swz(lane & 31, 4 * h + ks) * 16;
+  const int brow = (64 * wn + (lane & 31)) * 128;
+  const int arow = (128 * wm + (lane & 31)) * 128;
+  auto ops = [&](KOps& o, const typename P::Frag& fa, const char* B, const char* A, int ks) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) o.b[c] = lds16(B + brow + c * 32 * 128 + koff[ks]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o.a[i] = P::operand(fa, A + arow, i, ks, koff[ks]);
+  };
+  wait_barrier_n(src.prologue(lds, nst, wave));
+  KOps o, last;
+  for (int st = 0; st < nst; ++st) {
+    const int n = src.issue_at(lds, st, nst, wave);
+    typename P::Frag fa;
+    P::frag_begin(fa, lds, st, wm, lane);
+    const char* B = P::bbase(lds, st);
+    const char* A = P::abase(lds, st);
+    if (st > 0) pf_mma<kFull>(last, n_ct, acc);
+    ops(o, fa, B, A, 0);
+    pf_mma<kFull>(o, n_ct, acc);
+    ops(o, fa, B, A, 1);
+    pf_mma<kFull>(o, n_ct, acc);
+    ops(o, fa, B, A, 2);
+    pf_mma<kFull>(o, n_ct, acc);
+    ops(last, fa, B, A, 3);
+    if (P::kWaitNewest) wait_barrier_n(n);
+    else wait_barrier<0>();
+  }
+  pf_mma<kFull>(last, n_ct, acc);
+}
+
+template <class P>
+__device__ __forceinline__ void pf_gemm_dma(const P& src, int nst, int n_ct, char* lds, f32x16 (&acc)[4][2]) {
+  if (n_ct == 2) pf_loop_dma<true>(src, nst, n_ct, lds, acc);
+  else pf_loop_dma<false>(src, nst, n_ct, lds, acc);
+}
+
+static_assert(DmaBf16::kEnd <= DmaFp4::kEnd && 2 * (Bf16Tile::kBytes + kPfBBytes) <= DmaFp4::kEnd,
+              "every loop's stages fit the FP4 DMA loop's LDS");
+
+constexpr size_t kPfLdsBytes = DmaFp4::kEnd;
 static_assert(kPfLdsBytes <= kMaxLds, "LDS stage buffers do not fit");
 
 struct PfArgs {
@@ -311,35 +535,75 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_up(PfArgs p) {
   const int cnt = min(kPfToks, n_tok - first);
   const int t = threadIdx.x, lane = t & 63, wave = wave_id();
   const int wm = wave & 1, wn = wave >> 1;
-  const uint16_t* brow[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tn = min((t >> 3) + 64 * j, cnt - 1);
-    const int64_t xr = shared ? first + tn : p.xrow[tok_base + first + tn];
-    brow[j] = p.x + xr * p.H;
-  }
-  const int r = t >> 1, hf = t & 1;
-  const int role = (r >> 6) & 1;
-  const int64_t arow = rt * 128 + (r >> 7) * 64 + (r & 63);
   const int n_ct = max(0, min(2, (cnt - 64 * wn + 31) >> 5));
   const int K = p.H, nst = K / kPfK;
+  // local weight row r of the tile: w1 (r & 64 == 0) or w3 row rt*128 + (r >> 7)*64 + (r & 63)
+  auto role_of = [](int r) { return (r >> 6) & 1; };
+  auto arow_of = [&](int r) { return static_cast<int64_t>(rt * 128 + (r >> 7) * 64 + (r & 63)); };
+  auto xrow_of = [&](int r) {
+    const int tn = min(r, cnt - 1);
+    return static_cast<int64_t>(shared ? first + tn : p.xrow[tok_base + first + tn]);
+  };
   f32x16 acc[4][2];
   zero(acc);
-  if (shared) {
-    const uint16_t* W = role ? p.ws3 : p.ws1;
-    pf_gemm<Bf16Tile, StageBF16>([&](StageBF16& a, int st) { a.load(W, arow, K, st, hf); }, brow, nst, n_ct,
-                                 pf_lds, acc);
-  } else if constexpr (kQ3) {
-    const uint8_t* W = static_cast<const uint8_t*>(d->p[3 * role]);
-    const uint16_t* S = static_cast<const uint16_t*>(d->p[3 * role + 1]);
-    const uint16_t* B = static_cast<const uint16_t*>(d->p[3 * role + 2]);
-    pf_gemm<Bf16Tile, StageQ3>([&](StageQ3& a, int st) { a.load(W, S, B, arow, K, st, hf); }, brow, nst, n_ct,
-                               pf_lds, acc);
+  if constexpr (!kQ3) {
+    const uint8_t* gb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      gb[j] = reinterpret_cast<const uint8_t*>(p.x + xrow_of(dma_row(wave, j, lane)) * p.H) +
+              dma_chunk(wave, j, lane) * 16;
+    if (shared) {
+      DmaBf16 src;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = dma_row(wave, j, lane);
+        src.ga[j] = reinterpret_cast<const uint8_t*>((role_of(r) ? p.ws3 : p.ws1) + arow_of(r) * K) +
+                    dma_chunk(wave, j, lane) * 16;
+        src.gb[j] = gb[j];
+      }
+      pf_gemm_dma(src, nst, n_ct, pf_lds, acc);
+    } else if (K % 512 == 0) {
+      DmaFp4 src;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = DmaFp4::code_row(wave, j, lane);
+        src.gc[j] = static_cast<const uint8_t*>(d->p[3 * role_of(r)]) + arow_of(r) * (K / 2) +
+                    DmaFp4::code_chunk(wave, j, lane) * 16;
+      }
+      const int rs = (64 * wave + lane) & 255;
+      src.gs = static_cast<const uint8_t*>(d->p[3 * role_of(rs) + 1]) + arow_of(rs) * (K / 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) src.gb[j] = gb[j];
+      pf_gemm_dma(src, nst, n_ct, pf_lds, acc);
+    } else {
+      const uint16_t* brow[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) brow[j] = p.x + xrow_of((t >> 3) + 64 * j) * p.H;
+      const int r = t >> 1, hf = t & 1;
+      const uint8_t* W = static_cast<const uint8_t*>(d->p[3 * role_of(r)]);
+      const uint8_t* S = static_cast<const uint8_t*>(d->p[3 * role_of(r) + 1]);
+      const int64_t arow = arow_of(r);
+      pf_gemm<Fp4Tile, Fp4Tile::Regs>([&](Fp4Tile::Regs& a, int st) { a.load(W, S, arow, K, st, hf); }, brow,
+                                      nst, n_ct, pf_lds, acc);
+    }
   } else {
-    const uint8_t* W = static_cast<const uint8_t*>(d->p[3 * role]);
-    const uint8_t* S = static_cast<const uint8_t*>(d->p[3 * role + 1]);
-    pf_gemm<Fp4Tile, Fp4Tile::Regs>([&](Fp4Tile::Regs& a, int st) { a.load(W, S, arow, K, st, hf); }, brow,
-                                    nst, n_ct, pf_lds, acc);
+    const uint16_t* brow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) brow[j] = p.x + xrow_of((t >> 3) + 64 * j) * p.H;
+    const int r = t >> 1, hf = t & 1;
+    const int role = role_of(r);
+    const int64_t arow = arow_of(r);
+    if (shared) {
+      const uint16_t* W = role ? p.ws3 : p.ws1;
+      pf_gemm<Bf16Tile, StageBF16>([&](StageBF16& a, int st) { a.load(W, arow, K, st, hf); }, brow, nst, n_ct,
+                                   pf_lds, acc);
+    } else {
+      const uint8_t* W = static_cast<const uint8_t*>(d->p[3 * role]);
+      const uint16_t* S = static_cast<const uint16_t*>(d->p[3 * role + 1]);
+      const uint16_t* B = static_cast<const uint16_t*>(d->p[3 * role + 2]);
+      pf_gemm<Bf16Tile, StageQ3>([&](StageQ3& a, int st) { a.load(W, S, B, arow, K, st, hf); }, brow, nst, n_ct,
+                                 pf_lds, acc);
+    }
   }
   const int ld = shared ? p.Is : p.I;
   uint16_t* out = shared ? p.hs : p.h;
@@ -380,31 +644,63 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_down(PfArgs p) {
   const uint16_t* src = shared ? p.hs : p.h;
   const int t = threadIdx.x, lane = t & 63, wave = wave_id();
   const int wm = wave & 1, wn = wave >> 1;
-  const uint16_t* brow[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tn = min((t >> 3) + 64 * j, cnt - 1);
-    brow[j] = src + static_cast<int64_t>(tok_base + first + tn) * K;
-  }
-  const int hf = t & 1;
-  const int64_t arow = rt * 256 + (t >> 1);
+  auto hrow_of = [&](int r) { return static_cast<int64_t>(tok_base + first + min(r, cnt - 1)); };
   const int n_ct = max(0, min(2, (cnt - 64 * wn + 31) >> 5));
+  const int64_t row0 = static_cast<int64_t>(rt) * 256;   // first w2 row of the tile
   f32x16 acc[4][2];
   zero(acc);
-  if (shared) {
-    pf_gemm<Bf16Tile, StageBF16>([&](StageBF16& a, int st) { a.load(p.ws2, arow, K, st, hf); }, brow, nst, n_ct,
-                                 pf_lds, acc);
-  } else if constexpr (kQ3) {
-    const uint8_t* W = static_cast<const uint8_t*>(d->p[6]);
-    const uint16_t* S = static_cast<const uint16_t*>(d->p[7]);
-    const uint16_t* B = static_cast<const uint16_t*>(d->p[8]);
-    pf_gemm<Bf16Tile, StageQ3>([&](StageQ3& a, int st) { a.load(W, S, B, arow, K, st, hf); }, brow, nst, n_ct,
-                               pf_lds, acc);
+  if constexpr (!kQ3) {
+    const uint8_t* gb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      gb[j] = reinterpret_cast<const uint8_t*>(src + hrow_of(dma_row(wave, j, lane)) * K) +
+              dma_chunk(wave, j, lane) * 16;
+    if (shared) {
+      DmaBf16 s;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s.ga[j] = reinterpret_cast<const uint8_t*>(p.ws2 + (row0 + dma_row(wave, j, lane)) * K) +
+                  dma_chunk(wave, j, lane) * 16;
+        s.gb[j] = gb[j];
+      }
+      pf_gemm_dma(s, nst, n_ct, pf_lds, acc);
+    } else if (K % 512 == 0) {
+      DmaFp4 s;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        s.gc[j] = static_cast<const uint8_t*>(d->p[6]) + (row0 + DmaFp4::code_row(wave, j, lane)) * (K / 2) +
+                  DmaFp4::code_chunk(wave, j, lane) * 16;
+      s.gs = static_cast<const uint8_t*>(d->p[7]) + (row0 + ((64 * wave + lane) & 255)) * (K / 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s.gb[j] = gb[j];
+      pf_gemm_dma(s, nst, n_ct, pf_lds, acc);
+    } else {
+      const uint16_t* brow[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) brow[j] = src + hrow_of((t >> 3) + 64 * j) * K;
+      const uint8_t* W = static_cast<const uint8_t*>(d->p[6]);
+      const uint8_t* S = static_cast<const uint8_t*>(d->p[7]);
+      const int64_t arow = row0 + (t >> 1);
+      const int hf = t & 1;
+      pf_gemm<Fp4Tile, Fp4Tile::Regs>([&](Fp4Tile::Regs& a, int st) { a.load(W, S, arow, K, st, hf); }, brow,
+                                      nst, n_ct, pf_lds, acc);
+    }
   } else {
-    const uint8_t* W = static_cast<const uint8_t*>(d->p[6]);
-    const uint8_t* S = static_cast<const uint8_t*>(d->p[7]);
-    pf_gemm<Fp4Tile, Fp4Tile::Regs>([&](Fp4Tile::Regs& a, int st) { a.load(W, S, arow, K, st, hf); }, brow,
-                                    nst, n_ct, pf_lds, acc);
+    const uint16_t* brow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) brow[j] = src + hrow_of((t >> 3) + 64 * j) * K;
+    const int hf = t & 1;
+    const int64_t arow = row0 + (t >> 1);
+    if (shared) {
+      pf_gemm<Bf16Tile, StageBF16>([&](StageBF16& a, int st) { a.load(p.ws2, arow, K, st, hf); }, brow, nst,
+                                   n_ct, pf_lds, acc);
+    } else {
+      const uint8_t* W = static_cast<const uint8_t*>(d->p[6]);
+      const uint16_t* S = static_cast<const uint16_t*>(d->p[7]);
+      const uint16_t* B = static_cast<const uint16_t*>(d->p[8]);
+      pf_gemm<Bf16Tile, StageQ3>([&](StageQ3& a, int st) { a.load(W, S, B, arow, K, st, hf); }, brow, nst,
+                                 n_ct, pf_lds, acc);
+    }
   }
   float* out = shared ? p.ys : p.y;
 #pragma unroll

@@ -4,7 +4,9 @@ Routing indices bit-exact; outputs within the layer tolerance (cosine >= 0.99999
 and max|y - y_ref| / max|y_ref| <= 1e-2).  Cases cover ragged token tiles
 (expert row counts and T not multiples of 256), experts spanning several token
 tiles (Zipf-skewed gate bias), experts with a handful of rows, q3 experts, and
-the shared expert absent / precomputed.
+the shared expert absent / precomputed.  FP4 products whose K is a multiple of
+512 stage their tiles by LDS DMA, the others through registers: "fp4 k6 I256"
+(down K = 256) and "fp4 H768" (gate/up K = 768) take the second form.
 """
 
 from __future__ import annotations
@@ -41,6 +43,7 @@ def _check(spec, d, T, label, shared=True):
     ("fp4 mid ragged", L.LayerSpec(H=1024, E=64, k=8, I=512, I_shared=512), 300, None),
     ("fp4 mid zipf", L.LayerSpec(H=1024, E=64, k=8, I=512, I_shared=512), 1100, 1.1),
     ("fp4 k6 I256", L.LayerSpec(H=512, E=32, k=6, I=256, I_shared=384), 513, None),
+    ("fp4 H768", L.LayerSpec(H=768, E=16, k=4, I=512, I_shared=256), 300, 1.1),
     ("q3 mid zipf", L.LayerSpec(H=1024, E=64, k=8, I=512, I_shared=512, quant=L.QUANT_Q3), 700, 1.1),
 ])
 def test_prefill_layer(label, spec, T, zipf):
