@@ -282,6 +282,11 @@ __device__ __forceinline__ void wait_barrier() {
 
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
 
+// The DMA loads read 16-byte pieces at 16-byte steps from the given bases.
+__device__ __forceinline__ bool aligned16(const void* a, const void* b) {
+  return ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15u) == 0;
+}
+
 // Stage chunk (row, chunk) loaded by lane i of load j of wave w, for 128-byte
 // rows spread over 4 loads per lane: LDS position p = (4 w + j) 64 + i.
 __device__ __forceinline__ int dma_row(int w, int j, int i) { return (4 * w + j) * 8 + (i >> 3); }
@@ -562,7 +567,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_up(PfArgs p) {
         src.gb[j] = gb[j];
       }
       pf_gemm_dma(src, nst, n_ct, pf_lds, acc);
-    } else if (K % 512 == 0) {
+    } else if (K % 512 == 0 && aligned16(d->p[0], d->p[1]) && aligned16(d->p[3], d->p[4])) {
       DmaFp4 src;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -664,7 +669,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_down(PfArgs p) {
         s.gb[j] = gb[j];
       }
       pf_gemm_dma(s, nst, n_ct, pf_lds, acc);
-    } else if (K % 512 == 0) {
+    } else if (K % 512 == 0 && aligned16(d->p[6], d->p[7])) {
       DmaFp4 s;
 #pragma unroll
       for (int j = 0; j < 2; ++j)

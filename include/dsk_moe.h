@@ -72,7 +72,9 @@ typedef struct dsk_moe_desc {
 } dsk_moe_desc;
 
 /* Device pointers of one routed expert (an element of the device table
- * indexed by expert id).  b* are Q3 biases (NULL for FP4). */
+ * indexed by expert id).  b* are Q3 biases (NULL for FP4).  Code, scale and
+ * bias pointers 16-byte aligned (the kernels read them in 16-byte pieces; the
+ * prefill GEMM takes its register-staged loop for an FP4 expert that is not). */
 typedef struct dsk_expert_ptrs {
   const void* w1; const void* s1; const void* b1;
   const void* w3; const void* s3; const void* b3;
