@@ -85,6 +85,7 @@ Workspace workspace_layout(const dsk_moe_desc& d) {
   L.ys = take(T * H * 4);
   L.shared_x = take(mx && Is > 0 ? T * H * 2 : 0);
   L.pf_tiles = take(prefill_gemm(d) ? (2 + 2 * static_cast<size_t>(prefill_max_tiles(d))) * 4 : 0);
+  L.disp_hist = take(dispatch_hist_ints(static_cast<int>(N), static_cast<int>(E)) * 4);
   L.total = o;
   return L;
 }
@@ -194,6 +195,32 @@ int dsk_dispatch(const dsk_moe_desc* d, const int32_t* idx, int32_t* counts, int
                    "dsk_dispatch launch");
 }
 
+int dsk_dispatch_workspace_size(const dsk_moe_desc* d, size_t* bytes) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!bytes) return fail(DSK_EINVAL, "dsk_dispatch_workspace_size: bytes is NULL");
+  *bytes = dispatch_hist_ints(d->tokens * d->top_k, d->n_experts) * sizeof(int32_t);
+  return 0;
+}
+
+int dsk_dispatch_ws(const dsk_moe_desc* d, const int32_t* idx, int32_t* counts, int32_t* offsets,
+                    int32_t* perm, int32_t* rank, int32_t* active, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!idx || !counts || !offsets || !perm || !rank || !active)
+    return fail(DSK_EINVAL, "dsk_dispatch_ws: NULL pointer argument");
+  const size_t need = dispatch_hist_ints(d->tokens * d->top_k, d->n_experts) * sizeof(int32_t);
+  if (need > 0 && !workspace) return fail(DSK_EINVAL, "dsk_dispatch_ws: workspace is NULL");
+  if (workspace_bytes < need)
+    return fail(DSK_ESPACE, "dsk_dispatch_ws: workspace %zu bytes < required %zu", workspace_bytes, need);
+  if (need > 0 && !aligned(workspace, 256)) return fail(DSK_EALIGN, "dsk_dispatch_ws: workspace must be 256-byte aligned");
+  DispatchOut o{counts, offsets, perm, rank, active, nullptr, nullptr, nullptr,
+                need > 0 ? static_cast<int32_t*>(workspace) : nullptr};
+  return hip_check(launch_dispatch(*d, idx, nullptr, nullptr, o, static_cast<hipStream_t>(stream)),
+                   "dsk_dispatch_ws launch");
+}
+
 int dsk_experts(const dsk_moe_desc* d, const dsk_expert_ptrs* table, const void* ws1,
                 const void* ws3, const void* ws2, const void* shared_out, const void* x,
                 const float* weights,
@@ -277,7 +304,10 @@ int dsk::forward_layer(const dsk_moe_desc* d, const void* x, const void* gate_w,
   ra.out = DispatchOut{counts, offsets, perm, rank, active,
                        reinterpret_cast<SlotDesc*>(ws + L.desc),
                        reinterpret_cast<int32_t*>(ws + L.xrow),
-                       reinterpret_cast<float*>(ws + L.wrow)};
+                       reinterpret_cast<float*>(ws + L.wrow),
+                       dispatch_hist_ints(d->tokens * d->top_k, d->n_experts) > 0
+                           ? reinterpret_cast<int32_t*>(ws + L.disp_hist)
+                           : nullptr};
   ra.ctr = reinterpret_cast<unsigned int*>(ws + L.ctr);
   ra.rowmap = reinterpret_cast<int32_t*>(ws + L.rowmap);
   ExpertsArgs a{};

@@ -117,7 +117,16 @@ struct DispatchOut {
   SlotDesc* desc;            // [E] or null
   int32_t* xrow;             // [T*k] token of each dispatch row, or null
   float* wrow;               // [T*k] route weight of each dispatch row
+  int32_t* hist = nullptr;   // [blocks][E] per-block counts of the multi-block form, or null
 };
+
+// From this many (token, slot) positions, and with a histogram area, the
+// dispatch runs as three kernels over blocks of kDispBlockPositions.
+constexpr int kDispMultiMin = 8192;
+constexpr int kDispBlockPositions = 2048;
+inline size_t dispatch_hist_ints(int N, int E) {
+  return N >= kDispMultiMin ? static_cast<size_t>((N + kDispBlockPositions - 1) / kDispBlockPositions) * E : 0;
+}
 
 // ---------------------------------------------------------------- workspace
 // Regions of the caller-owned workspace used by dsk_moe_forward / dsk_experts.
@@ -125,6 +134,7 @@ struct Workspace {
   size_t scores, idx, wts, counts, offsets, perm, rank, active;  // routing
   size_t desc, xrow, wrow;  // dispatch descriptors
   size_t ctr;               // arrival counters of the fused router (zero between calls)
+  size_t disp_hist;         // per-block counts of the multi-block dispatch
   size_t rowmap;            // decode pipeline: [min(E,64)][T] token -> dispatch row
   size_t xb_hi, xb_lo;      // B-operand planes of x   [T][H]  (16-bit)
   size_t h_hi, h_lo;        // routed intermediate      [T*k][I] (16-bit)

@@ -58,6 +58,8 @@ SIGNATURES = {
     "dsk_workspace_size": (ctypes.c_int, [PDesc, ctypes.POINTER(_sz)]),
     "dsk_route": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "dsk_dispatch": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "dsk_dispatch_workspace_size": (ctypes.c_int, [PDesc, ctypes.POINTER(_sz)]),
+    "dsk_dispatch_ws": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "dsk_cap_union": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "dsk_experts": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _vp, _vp, _vp, _vp, _sz, _vp]),

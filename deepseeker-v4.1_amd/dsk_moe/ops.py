@@ -144,8 +144,10 @@ def cap_union(scores: torch.Tensor, idx: torch.Tensor, w: torch.Tensor, budget: 
               ptr(w), stream_of(dev))
 
 
-def dispatch(idx: torch.Tensor, n_experts: int) -> dict:
-    """counts, offsets, perm, rank, active of ``dsk_dispatch`` for idx [T,k] int32."""
+def dispatch(idx: torch.Tensor, n_experts: int, multi_block: bool = False) -> dict:
+    """counts, offsets, perm, rank, active of ``dsk_dispatch`` for idx [T,k] int32;
+    ``multi_block``: ``dsk_dispatch_ws`` (the forward call's own dispatch, several
+    workgroups from 8192 positions), same outputs."""
     dev = require_device(idx)
     if idx.dtype != torch.int32 or idx.dim() != 2:
         raise ValueError("idx must be a 2-D int32 tensor")
@@ -157,6 +159,14 @@ def dispatch(idx: torch.Tensor, n_experts: int) -> dict:
            "perm": torch.empty(n, dtype=torch.int32, device=dev),
            "rank": torch.empty(n, dtype=torch.int32, device=dev),
            "active": torch.empty(n_experts + 1, dtype=torch.int32, device=dev)}
+    if multi_block:
+        nb = ctypes.c_size_t()
+        _lib.call("dsk_dispatch_workspace_size", ctypes.byref(desc), ctypes.byref(nb))
+        ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=dev)
+        _lib.call("dsk_dispatch_ws", ctypes.byref(desc), ptr(idx), ptr(out["counts"]),
+                  ptr(out["offsets"]), ptr(out["perm"]), ptr(out["rank"]), ptr(out["active"]),
+                  ptr(ws), nb.value, stream_of(dev))
+        return out
     _lib.call("dsk_dispatch", ctypes.byref(desc), ptr(idx), ptr(out["counts"]),
               ptr(out["offsets"]), ptr(out["perm"]), ptr(out["rank"]), ptr(out["active"]),
               stream_of(dev))

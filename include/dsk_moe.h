@@ -117,6 +117,17 @@ int dsk_dispatch(const dsk_moe_desc* d, const int32_t* idx, int32_t* counts,
                  int32_t* offsets, int32_t* perm, int32_t* rank, int32_t* active,
                  void* stream);
 
+/* dsk_dispatch with the same outputs bit for bit, computed over several
+ * workgroups when T*k >= 8192 (per-workgroup counts in the caller's
+ * workspace, 256-byte aligned, of dsk_dispatch_workspace_size bytes; 0 bytes
+ * below 8192 positions, where it is dsk_dispatch).  No counterpart in the
+ * reference: the forward call's own dispatch, exposed so that callers with
+ * large batches and tests reach it. */
+int dsk_dispatch_workspace_size(const dsk_moe_desc* d, size_t* bytes);
+int dsk_dispatch_ws(const dsk_moe_desc* d, const int32_t* idx, int32_t* counts,
+                    int32_t* offsets, int32_t* perm, int32_t* rank, int32_t* active,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* Union cap of a lock-step batch: replaces cap_union
  * (src/deepseeker/mlx_forward.py:213-254), which moe_layer applies when
  * union_budget > 0 and the batch has more than one row (:294-305).  In place on

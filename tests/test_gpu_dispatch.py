@@ -1,5 +1,9 @@
 """GPU dispatch parity: counts, offsets, permutation, inverse and active list
-bit-identical to the oracle (stable counting sort by expert)."""
+bit-identical to the oracle (stable counting sort by expert), for the
+one-workgroup form (``dsk_dispatch``) and, from 8192 positions, the
+multi-workgroup form the forward call runs (``dsk_dispatch_ws``): position
+counts that are and are not multiples of a workgroup's 2048, a single expert
+taking every position, dropped entries and E up to 1024."""
 
 from __future__ import annotations
 
@@ -14,9 +18,9 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def check(idx: np.ndarray, n_experts: int):
-    print(f"dispatch shape={idx.shape} E={n_experts}", flush=True)
-    got = dsk_moe.dispatch(torch.from_numpy(idx.astype(np.int32)).to(DEV), n_experts)
+def check(idx: np.ndarray, n_experts: int, multi_block: bool = False):
+    print(f"dispatch shape={idx.shape} E={n_experts} multi_block={multi_block}", flush=True)
+    got = dsk_moe.dispatch(torch.from_numpy(idx.astype(np.int32)).to(DEV), n_experts, multi_block=multi_block)
     counts, offsets, perm, rank = D.dispatch(idx, n_experts)
     act = D.active_experts(counts)
     np.testing.assert_array_equal(got["counts"].cpu().numpy(), counts)
@@ -48,6 +52,25 @@ def test_dispatch_skewed_duplicates_and_drops():
     idx[idx >= 256] = -1                     # dropped slots
     idx[::17, 0] = -1
     check(idx, 256)
+
+
+@pytest.mark.parametrize("T,k,E", [(1024, 8, 256), (4096, 8, 256), (1100, 8, 256), (2049, 6, 384),
+                                   (1366, 6, 1024), (600, 16, 64), (64, 8, 256)])
+def test_dispatch_multi_block(T, k, E):
+    rng = np.random.default_rng(7 * T + E)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    check(idx, E, multi_block=True)
+
+
+def test_dispatch_multi_block_skewed_and_drops():
+    rng = np.random.default_rng(5)
+    idx = rng.zipf(1.2, size=(4096, 8)) - 1
+    idx[idx >= 256] = -1
+    idx[::13, 3] = -1
+    check(idx, 256, multi_block=True)
+    one = np.zeros((1500, 8), dtype=np.int64)      # every position on expert 0
+    one[::7, 1] = 255
+    check(one, 256, multi_block=True)
 
 
 def test_dispatch_real_trace_replay(golden):
