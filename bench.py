@@ -462,10 +462,12 @@ def read_rate(nbytes: int, steps: int) -> dict:
 
 
 def mfma_rate(n: int = 8192, steps: int = 20) -> dict:
-    """bf16 GEMM n x n x n through torch (hipBLASLt) with random N(0,1) operands and
-    with constant operands: the dense bf16 matrix rate this box sustains."""
+    """bf16 GEMM n x n x n through torch (hipBLASLt, A times B transposed: both
+    operands K-contiguous, as the weight rows and token rows of the prefill GEMM)
+    with random N(0,1) operands and with constant operands: the dense bf16 matrix
+    rate this box sustains."""
     dev = torch.device("cuda:0")
-    res = {"mode": "mfma", "gemm": f"bf16 {n}x{n}x{n}", "flop_per_call": 2 * n ** 3}
+    res = {"mode": "mfma", "gemm": f"bf16 {n}x{n}x{n}, A @ B^T", "flop_per_call": 2 * n ** 3}
     for kind in ("random", "constant"):
         if kind == "random":
             a = torch.randn((n, n), device=dev, dtype=torch.bfloat16)
@@ -473,12 +475,13 @@ def mfma_rate(n: int = 8192, steps: int = 20) -> dict:
         else:
             a = torch.full((n, n), 0.5, device=dev, dtype=torch.bfloat16)
             b = torch.full((n, n), 0.25, device=dev, dtype=torch.bfloat16)
+        c = torch.empty((n, n), device=dev, dtype=torch.bfloat16)
         for _ in range(3):
-            torch.matmul(a, b)
+            torch.matmul(a, b.t(), out=c)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(steps):
-            torch.matmul(a, b)
+            torch.matmul(a, b.t(), out=c)
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / steps
         res[f"TFLOPs_{kind}"] = round(2 * n ** 3 / dt / 1e12, 1)
