@@ -461,6 +461,26 @@ def read_rate(nbytes: int, steps: int) -> dict:
     return {"mode": "read", "bytes_read": nbytes, "ms": round(dt * 1e3, 4), "GBps": round(nbytes / dt / 1e9, 1)}
 
 
+def gemv_rate(rows: int = 65536, cols: int = 8192, steps: int = 20) -> dict:
+    """bf16 matrix-vector product through torch (rows x cols, 1 GiB): the rate at
+    which this box streams a weight matrix row by row into a GEMV."""
+    dev = torch.device("cuda:0")
+    w = torch.randn((rows, cols), device=dev, dtype=torch.bfloat16)
+    x = torch.randn((cols,), device=dev, dtype=torch.bfloat16)
+    y = torch.empty((rows,), device=dev, dtype=torch.bfloat16)
+    for _ in range(3):
+        torch.mv(w, x, out=y)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        torch.mv(w, x, out=y)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    nbytes = rows * cols * 2
+    del w
+    return {"mode": "gemv", "bytes_read": nbytes, "ms": round(dt * 1e3, 4), "GBps": round(nbytes / dt / 1e9, 1)}
+
+
 def mfma_rate(n: int = 8192, steps: int = 20) -> dict:
     """bf16 GEMM n x n x n through torch (hipBLASLt, A times B transposed: both
     operands K-contiguous, as the weight rows and token rows of the prefill GEMM)
@@ -589,7 +609,9 @@ def main() -> int:
     peaks = {"hbm_GBps_published": PEAK_HBM / 1e9, "bf16_TFLOPs_published": PEAK_BF16 / 1e12}
     cp = copy_rate(1 << 30, 20)
     rd = read_rate(1 << 31, 20)
-    peaks.update({"copy_GBps_measured": cp["GBps_read_plus_write"], "read_GBps_measured": rd["GBps"]})
+    gv = gemv_rate()
+    peaks.update({"copy_GBps_measured": cp["GBps_read_plus_write"], "read_GBps_measured": rd["GBps"],
+                  "gemv_read_GBps_measured": gv["GBps"]})
     mf = mfma_rate(8192, 10)
     peaks.update({"bf16_gemm_TFLOPs_measured_random": mf["TFLOPs_random"],
                   "bf16_gemm_TFLOPs_measured_constant": mf["TFLOPs_constant"]})
