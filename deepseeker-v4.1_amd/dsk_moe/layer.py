@@ -30,11 +30,16 @@ skips them) and each row keeps its weight sum; ``union_strict`` drops the
 one-expert rescue of rows that would lose everything; ``route_stats``
 (``{"coverage", "calls"}``) accumulates the retained weight share per row.
 
+``pinned_gather_fn(layer_id, x, idx, w)`` (``:313-321``), called after routing
+with host arrays in the trace hook's order, returns ``{expert: (rows,
+contrib)}``: each selected expert found there adds its weighted output rows
+``contrib`` at ``rows`` instead of being computed (``:388-393``); the other
+experts then run in float32 and the sum is cast once.
+
 Options of the reference that only concern SSD paging or MLX scheduling are
 accepted and have no effect on the result, which the reference documents as
 identical with or without them: ``pipeline``, ``async_submit_fn``,
-``async_finalize_fn`` (``:273-285``), ``pinned_gather_fn`` (``:313-321``) and
-``stack_gateup`` (``:140-156``).
+``async_finalize_fn`` (``:273-285``) and ``stack_gateup`` (``:140-156``).
 
 Extensions (keyword-only): ``score_func`` ("sqrtsoftplus", the reference's
 default, or "sigmoid"), ``route_scale`` (reference default 1.5), ``out``.
@@ -106,7 +111,7 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
               score_func: str = "sqrtsoftplus", route_scale: float = 1.5,
               out: torch.Tensor | None = None) -> torch.Tensor:
     """MoE layer forward on the GPU; returns ``[T, H]`` in x's dtype."""
-    del pipeline, async_submit_fn, async_finalize_fn, pinned_gather_fn, stack_gateup
+    del pipeline, async_submit_fn, async_finalize_fn, stack_gateup
     dev = require_device(x, gate_w, gate_b)
     if x.dim() != 2:
         raise ValueError(f"x must be [T, H], got {tuple(x.shape)}")
@@ -133,7 +138,7 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
             raise ValueError("out must match x in shape and dtype")
     stream = stream_of(dev)
     union = union_budget > 0 and t > 1
-    need_host = bank is None or trace_hook is not None or prefetch_fn is not None
+    need_host = bank is None or trace_hook is not None or prefetch_fn is not None or pinned_gather_fn is not None
     split = need_host or union      # route first, then dispatch + experts
 
     # Route (+ dispatch) first when the host must see the routing.
@@ -174,6 +179,10 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
             prefetch_fn(layer_id, uniq)
         if trace_hook is not None:
             trace_hook(layer_id, idx_h.flip(1).tolist(), w.cpu().flip(1).tolist())
+    pinned: dict = {}
+    if pinned_gather_fn is not None:
+        got = pinned_gather_fn(layer_id, x, idx_h.flip(1).numpy(), w.cpu().flip(1).numpy()) or {}
+        pinned = {int(ex): v for ex, v in got.items() if int(ex) in uniq}
 
     shared_out = None
     if shared_fn is not None and shared is None:
@@ -188,7 +197,9 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
     ws1 = shared.w1 if shared else None
     ws3 = shared.w3 if shared else None
     ws2 = shared.w2 if shared else None
-    if split:
+    if pinned:
+        _with_pinned(desc, x, idx, w, table, (ws1, ws3, ws2), shared_out, pinned, out, dev, keep)
+    elif split:
         from .ops import dispatch as _dispatch  # local: same device, same stream
         d = _dispatch(idx, e)
         _lib.call("dsk_experts", ctypes.byref(desc), ptr(table), ptr(ws1), ptr(ws3), ptr(ws2),
@@ -204,6 +215,56 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
         # Tensors referenced only through raw pointers must outlive the launches.
         torch.cuda.current_stream(dev).synchronize()
     return out
+
+
+def _with_pinned(desc, x, idx, w, table, shared_w, shared_out, pinned: dict, out, dev, keep: list) -> None:
+    """The layer with some selected experts supplied by a pinned-gather callback
+    (src/deepseeker/mlx_forward.py:313-321, 388-393): their ``(rows, contrib)``
+    (weighted output rows) are added instead of computing them.  The other
+    experts run in float32 (x is exact in float32), the contributions are added
+    per expert in ascending id, then the shared output rounded to x's dtype, and
+    the sum is cast once, as the reference's float32 scatter-add does."""
+    from .ops import dispatch as _dispatch
+    stream = stream_of(dev)
+    t, h = x.shape
+    e = desc.n_experts
+    idx_m = idx.clone()
+    for ex in pinned:
+        idx_m[idx_m == ex] = -1
+    # routed experts that are not pinned, float32 output
+    d32 = _lib.Desc.from_buffer_copy(desc)
+    d32.x_dtype = 1
+    d32.inter_shared = 0
+    x32 = x.to(torch.float32).contiguous()
+    acc = torch.empty((t, h), dtype=torch.float32, device=dev)
+    dd = _dispatch(idx_m, e)
+    ws = workspace(d32, dev)
+    _lib.call("dsk_experts", ctypes.byref(d32), ptr(table), None, None, None, None, ptr(x32), ptr(w),
+              ptr(dd["counts"]), ptr(dd["offsets"]), ptr(dd["perm"]), ptr(dd["rank"]), ptr(dd["active"]),
+              ptr(acc), ptr(ws), ws.numel(), stream)
+    keep += [dd, x32, idx_m]
+    for ex in sorted(pinned):
+        rows, contrib = pinned[ex]
+        rows = torch.as_tensor(rows, dtype=torch.int64).to(dev)
+        contrib = torch.as_tensor(contrib).to(device=dev, dtype=torch.float32)
+        if contrib.shape != (rows.numel(), h):
+            raise ValueError(f"pinned expert {ex}: contrib must be [len(rows), {h}]")
+        acc.index_add_(0, rows, contrib)
+    ws1, ws3, ws2 = shared_w
+    if ws1 is not None:
+        # the shared expert alone (no routed position), rounded to x's dtype
+        none = torch.full_like(idx, -1)
+        ds = _dispatch(none, e)
+        sh = torch.empty_like(x)
+        ws_s = workspace(desc, dev)
+        _lib.call("dsk_experts", ctypes.byref(desc), ptr(table), ptr(ws1), ptr(ws3), ptr(ws2), None, ptr(x),
+                  ptr(w), ptr(ds["counts"]), ptr(ds["offsets"]), ptr(ds["perm"]), ptr(ds["rank"]),
+                  ptr(ds["active"]), ptr(sh), ptr(ws_s), ws_s.numel(), stream)
+        keep += [ds, none]
+        acc += sh.to(torch.float32)
+    elif shared_out is not None:
+        acc += shared_out.to(torch.float32)
+    out.copy_(acc.to(x.dtype))
 
 
 def experts_forward(x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor, bank: ResidentBank,

@@ -101,13 +101,18 @@ def shared_forward(x32: torch.Tensor, ws1, ws3, ws2, limit: float) -> torch.Tens
 
 
 def moe_forward(x, gate_w, gate_b, bank: ExpertBank, shared, spec: LayerSpec,
-                routing: tuple | None = None) -> dict:
+                routing: tuple | None = None, pinned: dict | None = None) -> dict:
     """Whole layer.  ``x``: torch [T, H] bf16 or float32 (CPU); ``shared`` is
     ``(ws1, ws3, ws2)`` bf16 tensors or None.  Returns a dict with ``out``
     (x.dtype), ``y_ref`` (float32 before the final cast), ``idx``, ``w``,
     ``scores``, ``counts``, ``offsets``, ``perm``, ``rank``.
     ``routing``: the ``(idx, w, scores, logits)`` of ``router.route`` on these
     inputs when the caller already has it (it is not recomputed).
+    ``pinned``: ``{expert: (rows, contrib)}`` as a pinned-gather callback returns
+    it (src/deepseeker/mlx_forward.py:313-321): a selected expert found there
+    adds ``contrib`` [len(rows), H] (float32, already weighted) at ``rows`` in
+    its place in the ascending-expert sum instead of being computed
+    (:388-393); entries of experts that were not selected are ignored.
     """
     xt = x.detach().to("cpu")
     x32 = xt.to(torch.float32)
@@ -120,6 +125,11 @@ def moe_forward(x, gate_w, gate_b, bank: ExpertBank, shared, spec: LayerSpec,
     acc = torch.zeros((t, spec.H), dtype=torch.float32)
     wt = torch.from_numpy(w)
     for e in D.active_experts(counts):
+        if pinned is not None and int(e) in pinned:
+            prow, contrib = pinned[int(e)]
+            acc.index_add_(0, torch.as_tensor(np.asarray(prow), dtype=torch.int64),
+                           torch.as_tensor(contrib, dtype=torch.float32))
+            continue
         pos = perm[offsets[e]:offsets[e + 1]].astype(np.int64)
         rows = torch.from_numpy(pos // spec.k)
         cols = torch.from_numpy(pos % spec.k)

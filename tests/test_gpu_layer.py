@@ -248,3 +248,41 @@ def test_full_size_q3(T):
     np.testing.assert_array_equal(idx.cpu().numpy(), r["idx"])
     c, rel = assert_layer_close(out.float(), r["y_ref"])
     print(f"cos={c:.9f} rel={rel:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("T", [4, 40])
+def test_pinned_gather_contributions(cfg0, T):
+    """moe_layer(pinned_gather_fn=...): the callback's weighted rows replace the
+    selected experts it returns (reference mlx_forward.py:313-321, 388-393).
+    The callback here doubles the true contribution of every other selected
+    expert, so the output must follow the callback, not the bank."""
+    spec, _, _ = cfg0
+    print(f"layer pinned gather T={T}", flush=True)
+    d = synth.make_layer(spec, 7, T)
+    seen = {}
+
+    def pinned_fn(layer_id, x, idx_np, w_np):
+        seen["idx"] = np.array(idx_np)
+        sel = sorted({int(v) for v in np.asarray(idx_np).ravel() if v >= 0})[::2]
+        x32 = x.detach().cpu().float()
+        res = {}
+        for e in sel:
+            w1, w3, w2 = (torch.from_numpy(d["bank"].dequant(e, n)) for n in ("w1", "w3", "w2"))
+            rows, outs = [], []
+            for r in range(idx_np.shape[0]):
+                for c in range(idx_np.shape[1]):
+                    if int(idx_np[r, c]) == e:
+                        h = L.swiglu(x32[r:r + 1] @ w1.T, x32[r:r + 1] @ w3.T, spec.limit) * float(w_np[r, c])
+                        rows.append(r)
+                        outs.append(2.0 * (h @ w2.T)[0])
+            res[e] = (np.asarray(rows, dtype=np.int32), torch.stack(outs))
+        seen["res"] = res
+        return res
+
+    out = run_layer(d, spec, pinned_gather_fn=pinned_fn, layer_id=3)
+    plain = run_layer(d, spec)
+    r = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], d["shared"], spec, pinned=seen["res"])
+    # the callback sees the routing in the reference's order (the trace hook's)
+    np.testing.assert_array_equal(seen["idx"], np.flip(r["idx"], axis=1))
+    assert_layer_close(out.float(), r["y_ref"])
+    assert float((out.float() - plain.float()).abs().max()) > 1e-3

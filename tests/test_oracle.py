@@ -420,6 +420,40 @@ def test_layer_grouped_equals_per_token(tiny):
     np.testing.assert_allclose(routed.numpy(), acc.numpy(), rtol=1e-5, atol=1e-6)
 
 
+def _expert_contrib(spec, d, r, e):
+    """Rows routed to expert e and their weighted w2 outputs, one (token, slot) at a time."""
+    x32 = d["x"].float()
+    rows, outs = [], []
+    for t in range(x32.shape[0]):
+        js = [j for j in range(r["idx"].shape[1]) if int(r["idx"][t, j]) == e]
+        for j in js:
+            w1, w3, w2 = (torch.from_numpy(d["bank"].dequant(e, n)) for n in ("w1", "w3", "w2"))
+            h = L.swiglu(x32[t:t + 1] @ w1.T, x32[t:t + 1] @ w3.T, spec.limit) * float(r["w"][t, j])
+            rows.append(t)
+            outs.append((h @ w2.T)[0])
+    return np.asarray(rows, dtype=np.int32), torch.stack(outs)
+
+
+def test_layer_pinned_contributions(tiny):
+    # reference mlx_forward.py:313-321, 388-393: a pinned expert's rows and weighted
+    # outputs are added in its place instead of computing it
+    spec, d, r = tiny
+    sel = sorted({int(v) for v in r["idx"].ravel()})
+    e0, e1 = sel[0], sel[-1]
+    own = {e: _expert_contrib(spec, d, r, e) for e in (e0, e1)}
+    same = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], d["shared"], spec, pinned=own)
+    np.testing.assert_allclose(same["y_ref"].numpy(), r["y_ref"].numpy(), rtol=1e-5, atol=1e-6)
+    rows, contrib = own[e1]
+    zero = {e1: (rows, torch.zeros_like(contrib))}
+    dropped = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], d["shared"], spec, pinned=zero)
+    want = r["y_ref"].clone().index_add_(0, torch.from_numpy(rows.astype(np.int64)), -contrib)
+    np.testing.assert_allclose(dropped["y_ref"].numpy(), want.numpy(), rtol=1e-5, atol=1e-6)
+    unused = [e for e in range(spec.E) if e not in sel][0]
+    ignored = L.moe_forward(d["x"], d["gate_w"], d["gate_b"], d["bank"], d["shared"], spec,
+                            pinned={unused: (np.array([0], dtype=np.int32), torch.ones((1, spec.H)))})
+    np.testing.assert_array_equal(ignored["y_ref"].numpy(), r["y_ref"].numpy())
+
+
 def test_layer_shared_changes_output(tiny):
     # reference tests/test_mlx_forward.py:324-353
     spec, d, r = tiny
