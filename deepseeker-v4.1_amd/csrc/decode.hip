@@ -1627,12 +1627,15 @@ __global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
     const int nbs = Is / 128, per = (nbs + 3) / 4;
     const int k0 = min(s * per, nbs), k1 = min(k0 + per, nbs);
     RawBF16 rs[kDqSharedKB];
+    // the barrier first: issuing these loads before it held the barrier (and with
+    // it the routed waves' products) until the loads had gone out behind the
+    // routed ring's, while the shared products have time to spare
+    __syncthreads();
     if (k0 < k1) {
       // no condition on the loads (see load_raw_nc): past k1, the last block again (not computed)
 #pragma unroll
       for (int j = 0; j < kDqSharedKB; ++j) load_raw_nc(rs[j], p.ws2, row, Is, min(k0 + j, k1 - 1) * 128 + g4 * 32);
     }
-    __syncthreads();
     // A operand row 2t + plane
     const int ta = r16 >> 1;
     const uint16_t* sbase = ta < T ? ((r16 & 1) ? sh_l : sh_h) + ta * iss + 32 * g4 : zero;
