@@ -7,10 +7,11 @@
 // and the MFMA B operand (16 columns) is mostly empty.  A block takes one
 // slot (an active expert, or the shared expert as a pseudo-slot over all T
 // tokens) and a group of row tiles; it walks the slot's dispatch rows in
-// column tiles of kGNC.  For each column tile the waves issue their weight
-// loads first, the block gathers only that tile's activation rows into LDS
-// (x for gate/up, the h planes for down) while the weights are in flight,
-// and each wave then multiplies its K range; K ranges are added in a fixed
+// column tiles of kGNC.  For each column tile the block gathers only that
+// tile's activation rows into LDS (x for gate/up, the h planes for down), the
+// waves issue their first weight batches behind those loads (not in front of
+// them, where the LDS stores would wait for the weights too), and each wave
+// then multiplies its K range; K ranges are added in a fixed
 // order through LDS.  Gate/up writes h = SwiGLU(gate, up) * route weight by
 // dispatch row (hs by token for the shared expert); down writes one float32
 // output row per dispatch row (ys per token for the shared expert), which
@@ -126,10 +127,12 @@ __device__ __forceinline__ void up_block(const GroupedArgs& p, LoadW load_w, WPt
         }
       }
     };
-    ld(a1, a3, wa1, wa3, k0);
-    ld(b1, b3, wb1, wb3, k0 + G);
+    // the tile's activation rows first: their loads are then not queued behind the
+    // weights', so the LDS stores and the barrier do not wait for the weights
     if (shared) stage_rows(lds, p.x, K, K, cols, [&](int r) { return c0 + r; });
     else stage_rows(lds, p.x, K, K, cols, [&](int r) { return p.xrow[base + c0 + r]; });
+    ld(a1, a3, wa1, wa3, k0);
+    ld(b1, b3, wb1, wb3, k0 + G);
     __syncthreads();
     const bool tv = r16 < cols;
     const uint16_t* brow = lds + (tv ? r16 : 0) * xs;
@@ -399,10 +402,11 @@ __device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, W
         for (int i = 0; i < G; ++i) load_w(r[i], row, min(kb + i, k1 - 1) * 128 + g4 * 32);
       }
     };
-#pragma unroll
-    for (int i = 0; i < NB; ++i) ld(a[i], wa[i], k0 + i * G);
+    // the h rows first (see up_block)
     stage_rows(thi, src_hi, K, K, cols, [&](int r) { return base + c0 + r; });
     stage_rows(tlo, src_lo, K, K, cols, [&](int r) { return base + c0 + r; });
+#pragma unroll
+    for (int i = 0; i < NB; ++i) ld(a[i], wa[i], k0 + i * G);
     __syncthreads();
     const bool tv = r16 < cols;
     const uint16_t* bh = thi + (tv ? r16 : 0) * hs;
