@@ -28,7 +28,6 @@ constexpr int kDI = 8;              // down: row tiles of a block
 constexpr int kDKS = 1;             // down: K ranges of a row tile
 constexpr int kDW = kDI * kDKS;     // waves of a down block
 constexpr int kGNC = 8;             // dispatch rows (B columns) of a column tile
-constexpr int kStageQ = 2;          // 16-byte activation chunks per thread per staging pass
 constexpr int kDnRingFP4 = 4;       // down: FP4 weight batches in flight per wave
 
 static_assert(kGW == kDW, "both kernels use the same block size");
@@ -63,24 +62,33 @@ constexpr int down_ring() { return std::is_same_v<Raw, RawFP4> ? kDnRingFP4 : 2;
 
 // Rows [c0, c0 + cols) of the slot's activations (row r comes from source row
 // src(r) of `base`, row stride `ld` elements, K elements) into LDS rows of
-// stride K + 8, issued kStageQ chunks per thread at a time.
-template <typename Src>
-__device__ __forceinline__ void stage_rows(uint16_t* dst, const uint16_t* base, int ld, int K, int cols,
-                                           Src src) {
+// stride K + 8, Q chunks per thread in flight per pass.
+template <int Q, typename Src>
+__device__ __forceinline__ void stage_rows_q(uint16_t* dst, const uint16_t* base, int ld, int K, int cols,
+                                             Src src) {
   const int cpr = K / 8, chunks = cols * cpr, nt = blockDim.x;
-  for (int c = threadIdx.x; c < chunks; c += kStageQ * nt) {
-    u32x4 v[kStageQ];
+  for (int c = threadIdx.x; c < chunks; c += Q * nt) {
+    u32x4 v[Q];
 #pragma unroll
-    for (int q = 0; q < kStageQ; ++q) {
+    for (int q = 0; q < Q; ++q) {
       const int cc = min(c + q * nt, chunks - 1);   // no condition on the load (see load_raw_nc)
       v[q] = ldg16(base + static_cast<int64_t>(src(cc / cpr)) * ld + (cc % cpr) * 8);
     }
 #pragma unroll
-    for (int q = 0; q < kStageQ; ++q) {
+    for (int q = 0; q < Q; ++q) {
       const int cc = c + q * nt;
       if (cc < chunks) *reinterpret_cast<u32x4*>(dst + (cc / cpr) * (K + 8) + (cc % cpr) * 8) = v[q];
     }
   }
+}
+
+// Up to two chunks per thread: one pass of two; more: passes of four (a pass
+// is a round trip; four chunks where two would do cost their issue slots).
+template <typename Src>
+__device__ __forceinline__ void stage_rows(uint16_t* dst, const uint16_t* base, int ld, int K, int cols,
+                                           Src src) {
+  if (cols * (K / 8) <= 2 * static_cast<int>(blockDim.x)) stage_rows_q<2>(dst, base, ld, K, cols, src);
+  else stage_rows_q<4>(dst, base, ld, K, cols, src);
 }
 
 // Gate/up of one block: row tile rt (rows 16 rt ..) of w1 and w3 for the n
