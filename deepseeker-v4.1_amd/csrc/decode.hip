@@ -1425,37 +1425,45 @@ __global__ __launch_bounds__(kStW * 64) void k_down_mx(DecodeArgs p) {
 }
 
 // ---------------------------------------------------------------- q3 down, factored
-constexpr int kDqW = 8;             // waves: 0..3 routed, 4..7 shared
-constexpr int kDqRouted = 4;        // routed waves: one 512-code superblock of I each (I = 2048)
+constexpr int kDqRouted = 8;        // routed waves: half a 512-code superblock of I each (I = 2048)
+constexpr int kDqShared = 4;        // shared waves: a K quarter of Is each
+constexpr int kDqW = kDqRouted + kDqShared;   // waves: 0..7 routed, 8..11 shared
 constexpr int kDqMaxTokens = 4;     // A operand row 4t + 2h + plane
 constexpr int kDqRing = 8;          // routed experts in flight per wave
 constexpr int kDqSharedKB = 4;      // shared K blocks per shared wave (Is <= 2048)
 
-// One routed expert's w2 data of a routed wave: this lane's chunks of the
-// superblock's 4 blocks (3 x 16 bytes) and the (scale, bias) windows of its 8
-// groups (word j: groups 2j, 2j + 1 of block j).
+// One routed expert's w2 data of a routed wave: this lane's chunks of 2 blocks
+// (half hf of a superblock, whose lane slice holds 12 bytes per block: 24
+// bytes, as a 16-byte and an 8-byte load, both naturally aligned) and the
+// (scale, bias) windows of their 4 groups (word j: groups 2j, 2j + 1 of block j).
 struct DqSlot {
-  uint32_t c[4][3];
-  u32x4 s, b;
+  uint32_t c[2][3];
+  u32x2 s, b;
 };
 
 __device__ __forceinline__ void load_dq_slot(DqSlot& r, const DecodeArgs& p, int u, int U, uint32_t row,
-                                             int sbk, int g4) {
+                                             int sbk, int hf, int g4) {
   // no condition on the loads (see load_raw_nc): slots past U re-read slot 0
   // and are not computed; descriptors through the scalar cache (desc_ptr)
   const int su = u < U ? u : 0;
   const int I = p.I;
-  const auto c = gptr<u32x4>(static_cast<const uint8_t*>(desc_ptr(p.desc, su, 6)) +
-                             row * static_cast<uint32_t>(I / 8 * 3) + sbk * 192 + 48 * g4);
-#pragma unroll
-  for (int v = 0; v < 3; ++v) {
-    const u32x4 a = c[v];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) r.c[(4 * v + j) / 3][(4 * v + j) % 3] = a[j];
+  const uint8_t* cb = static_cast<const uint8_t*>(desc_ptr(p.desc, su, 6)) +
+                      row * static_cast<uint32_t>(I / 8 * 3) + sbk * 192 + 48 * g4 + 24 * hf;
+  uint32_t w[6];
+  if (hf == 0) {
+    const u32x4 a = *gptr<u32x4>(cb);
+    const u32x2 e = *gptr<u32x2>(cb + 16);
+    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3]; w[4] = e[0]; w[5] = e[1];
+  } else {
+    const u32x2 e = *gptr<u32x2>(cb);
+    const u32x4 a = *gptr<u32x4>(cb + 8);
+    w[0] = e[0]; w[1] = e[1]; w[2] = a[0]; w[3] = a[1]; w[4] = a[2]; w[5] = a[3];
   }
-  const uint32_t wo = (row * static_cast<uint32_t>(I / 64) + 8 * sbk) * 2;   // bytes
-  r.s = ldg16(static_cast<const uint8_t*>(desc_ptr(p.desc, su, 7)) + wo);
-  r.b = ldg16(static_cast<const uint8_t*>(desc_ptr(p.desc, su, 8)) + wo);
+#pragma unroll
+  for (int j = 0; j < 6; ++j) r.c[j / 3][j % 3] = w[j];
+  const uint32_t wo = (row * static_cast<uint32_t>(I / 64) + 8 * sbk + 4 * hf) * 2;   // bytes
+  r.s = ldg<u32x2>(static_cast<const uint8_t*>(desc_ptr(p.desc, su, 7)) + wo);
+  r.b = ldg<u32x2>(static_cast<const uint8_t*>(desc_ptr(p.desc, su, 8)) + wo);
 }
 
 // Final add and cast of one output element (token t, column n).
@@ -1479,9 +1487,11 @@ __device__ __forceinline__ void down_epilogue1(const DecodeArgs& p, float a, flo
 // the raw w2 codes the B operand (column = output row), and each group's
 // scale and bias are applied once per block: acc += s (D_hi + D_lo - 128 *
 // sum(h / m)) + b * sum(h).  Block = 16 output rows, kDqW waves: routed wave
-// w streams superblock w (4 K blocks, 48 contiguous bytes per lane) of every
-// active expert's w2 rows, kDqRing experts in flight; shared wave 4 + s takes
-// K quarter s of the shared expert's bf16 w2 rows.  Routed h rows are staged
+// w streams K blocks 2w, 2w + 1 (half w & 1 of superblock w >> 1, 24
+// contiguous bytes per lane) of every active expert's w2 rows, kDqRing experts
+// in flight (two routed waves per SIMD share the products that follow the
+// loads); shared wave kDqRouted + s takes K quarter s of the shared expert's
+// bf16 w2 rows.  Routed h rows are staged
 // in LDS with the 8q positions divided by 8 and their group sums, the shared
 // hs rows as they are.  A token's routed sum runs over its experts in slot
 // (ascending id) order, then the routed waves and the shared waves are each
@@ -1512,7 +1522,7 @@ __global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
   const int rm = p.rowmap[min(tid, U * T - 1)];
   {
     constexpr int NT = kDqW * 64;
-    constexpr int kStg = 6;                     // chunks per thread in flight (T = 1, k = 8: 4.5)
+    constexpr int kStg = 3;                     // chunks per thread in flight (T = 1, k = 8: 3)
     const int cpr = I / 8, hch = N * cpr, sch = T * (Is / 8);
     for (int c1 = 0; c1 < hch + sch; c1 += kStg * NT) {
       u32x4 lh[kStg], ll[kStg];
@@ -1574,12 +1584,12 @@ __global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
   if (tid < U * T) ldrow[tid] = rm;
   const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
   if (wave < kDqRouted) {
-    // 2. routed: superblock `wave` of every active expert's w2 rows
-    const int sbk = wave;
+    // 2. routed: K blocks 2 wave, 2 wave + 1 of every active expert's w2 rows
+    const int sbk = wave >> 1, hf = wave & 1;
     DqSlot ring[kDqRing];
 #pragma unroll
     for (int q = 0; q < kDqRing; ++q)
-      if (q < U) load_dq_slot(ring[q], p, q, U, row, sbk, g4);
+      if (q < U) load_dq_slot(ring[q], p, q, U, row, sbk, hf, g4);
     __syncthreads();
     // A operand row of this lane: token ta, group half ha, plane pa
     const int ta = r16 >> 2, ha = (r16 >> 1) & 1;
@@ -1591,10 +1601,10 @@ __global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
     auto mm = [&](const DqSlot& r, int u) {
       const int dra = arow ? ldrow[u * T + ta] : -1;
       const int dro = to < T ? ldrow[u * T + to] : -1;
-      const uint32_t sw[4] = {r.s.x, r.s.y, r.s.z, r.s.w}, bw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+      const uint32_t sw[2] = {r.s.x, r.s.y}, bw[2] = {r.b.x, r.b.y};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int kb = 4 * sbk + j;
+      for (int j = 0; j < 2; ++j) {
+        const int kb = 2 * wave + j;
         const uint16_t* ah = dra >= 0 ? aplane + dra * is + kb * 128 + 32 * g4 : zero;
         f32x4 d = z;
         d = mfma16(as_bf16x8(*reinterpret_cast<const u32x4*>(ah)), q3m_operand<0>(r.c[j], km), d);
@@ -1616,7 +1626,7 @@ __global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
         const int u = u0 + q;
         if (u < U) {
           mm(ring[q], u);
-          if (u + kDqRing < U) load_dq_slot(ring[q], p, u + kDqRing, U, row, sbk, g4);
+          if (u + kDqRing < U) load_dq_slot(ring[q], p, u + kDqRing, U, row, sbk, hf, g4);
         }
       }
     }
@@ -1658,10 +1668,9 @@ __global__ __launch_bounds__(kDqW * 64) void k_down_q3(DecodeArgs p) {
   if (wave == 0 && g4 < T) {
     float a = 0.0f, sh = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kDqRouted; ++w) {
-      a += red[0][w][g4][r16];
-      sh += red[1][w][g4][r16];
-    }
+    for (int w = 0; w < kDqRouted; ++w) a += red[0][w][g4][r16];
+#pragma unroll
+    for (int w = 0; w < kDqShared; ++w) sh += red[1][w][g4][r16];
     down_epilogue1(p, a, sh, row0 + r16, g4);
   }
 }
@@ -1900,7 +1909,7 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   }
   const int n_rows = d.tokens * d.top_k;
   const int max_u = d.n_experts < n_rows ? d.n_experts : n_rows;
-  if (q3 && d.tokens <= kDqMaxTokens && d.inter == kDqRouted * 512 && d.inter_shared <= 2048 &&
+  if (q3 && d.tokens <= kDqMaxTokens && d.inter == kDqRouted * 256 && d.inter_shared <= 2048 &&
       d.inter_shared % 128 == 0) {
     // factored q3 down: h planes, hs planes, group sums, partial sums, zeros, dispatch rows
     const size_t dq_lds = static_cast<size_t>(n_rows) * (d.inter + 8) * 4 +
