@@ -813,21 +813,24 @@ constexpr int kQ3fW = kQ3fItems * kQ3fKS;
 // Block = kQ3fItems row tiles x kQ3fKS K ranges (one wave each; at hidden
 // 4096 a wave's range is one 512-code superblock, so one batch per wave),
 // kTwo: two batches in flight where a range is longer (a separate variant,
-// so that the one-batch kernel keeps its registers); K ranges added in order.
-template <bool kWin, bool kF32, bool kTwo>
+// so that the one-batch kernel keeps its registers); kR = 2 (one batch per
+// range): each wave takes its K range of two row tiles, both batches issued
+// at once, so that every block of the launch is resident in one round; K
+// ranges added in order.
+template <bool kWin, bool kF32, bool kTwo, int kR = 1>
 __global__ __launch_bounds__(kQ3fW * 64) __attribute__((amdgpu_waves_per_eu(kF32 || !kWin || kTwo ? 3 : 4))) void k_up_q3(DecodeArgs p) {
+  static_assert(kR == 1 || (kR == 2 && !kTwo), "two row tiles per wave take one batch each");
   constexpr int G = kUpBatch;
   extern __shared__ __align__(16) uint16_t lds_up[];
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
-  const int groups = (p.up_tiles + kQ3fItems - 1) / kQ3fItems;
+  const int groups = (p.up_tiles + kQ3fItems * kR - 1) / (kQ3fItems * kR);
   const int rb = static_cast<int>(blockIdx.x);
   const int slot = rb / groups;
   if (slot >= p.active[0]) return;
   const int T = p.T, K = p.H;
   const int item = wave / kQ3fKS, ks = wave % kQ3fKS;
-  const int rt = (rb % groups) * kQ3fItems + item;
-  const bool rok = rt < p.up_tiles;
+  const int rt = ((rb % groups) * kQ3fItems + item) * kR;   // row tiles rt .. rt + kR - 1
   // this lane's A operand row: token ta, group half ha
   const int ta = r16 >> 1;
   const int drow_a = ta < T ? p.rowmap[slot * T + ta] : -1;
@@ -842,8 +845,8 @@ __global__ __launch_bounds__(kQ3fW * 64) __attribute__((amdgpu_waves_per_eu(kF32
   uint16_t* xl = lds_up + T * xs;
   float* xsum = reinterpret_cast<float*>(lds_up + (kF32 ? 2 : 1) * T * xs);   // [nblk][8][2][2]
   float (*red)[kQ3fKS][2][64][2] = reinterpret_cast<float (*)[kQ3fKS][2][64][2]>(xsum + nblk * kQ3fMaxTokens * 4);
-  const uint16_t* zero = reinterpret_cast<const uint16_t*>(red + kQ3fItems);   // 64 zero bytes
-  if (tid < 4) reinterpret_cast<u32x4*>(red + kQ3fItems)[tid] = u32x4{0u, 0u, 0u, 0u};
+  const uint16_t* zero = reinterpret_cast<const uint16_t*>(red + kQ3fItems * kR);   // 64 zero bytes
+  if (tid < 4) reinterpret_cast<u32x4*>(red + kQ3fItems * kR)[tid] = u32x4{0u, 0u, 0u, 0u};
   // activations: into registers when they fit (staged after the weight loads are issued)
   const bool xreg = xchunks <= NT;
   u32x4 xv0{}, xv1{};
@@ -873,7 +876,6 @@ __global__ __launch_bounds__(kQ3fW * 64) __attribute__((amdgpu_waves_per_eu(kF32
     }
   }
   const SlotDesc* d = p.desc + slot;
-  const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
   const int per = (nblk + kQ3fKS - 1) / kQ3fKS;
   const int k0 = min(ks * per, nblk), k1 = min(k0 + per, nblk);
   const uint8_t* W1 = static_cast<const uint8_t*>(d->p[0]);
@@ -884,10 +886,15 @@ __global__ __launch_bounds__(kQ3fW * 64) __attribute__((amdgpu_waves_per_eu(kF32
   // 0 (not stored), blocks past the wave's range re-read its last ones (not
   // computed: mm stops at k1); every wave has k1 > k0 here except the ones
   // past a short row, which clamp to the row's last block
-  const uint32_t rowc = rok ? row : 0u;
-  const uint32_t code_row = rowc * static_cast<uint32_t>(K / 8 * 3);
-  const uint32_t sb_row = rowc * static_cast<uint32_t>(K / 64) * 2;   // bytes
-  auto ld = [&](Q3Batch<G>& b, int kb0) {
+  uint32_t code_rows[kR], sb_rows[kR];
+#pragma unroll
+  for (int i = 0; i < kR; ++i) {
+    const uint32_t rowc = rt + i < p.up_tiles ? static_cast<uint32_t>((rt + i) * 16 + r16) : 0u;
+    code_rows[i] = rowc * static_cast<uint32_t>(K / 8 * 3);
+    sb_rows[i] = rowc * static_cast<uint32_t>(K / 64) * 2;   // bytes
+  }
+  auto ld = [&](Q3Batch<G>& b, int kb0, int ri) {
+    const uint32_t code_row = code_rows[ri], sb_row = sb_rows[ri];
     if constexpr (kWin) {
       // a batch is one 512-code superblock: this lane group's chunks of its
       // 4 blocks are 48 contiguous bytes (windowed: k1 - k0 is a multiple of 4, >= 4)
@@ -931,15 +938,18 @@ __global__ __launch_bounds__(kQ3fW * 64) __attribute__((amdgpu_waves_per_eu(kF32
   };
   // batch A streams while the activations are staged, then batch B
   Q3Batch<G> A, B;
-  ld(A, k0);
+  ld(A, k0, 0);
   if (xreg && tid < xchunks) stage_chunk_q3<kF32>(xh, xl, xsum, xs, cpr, tid, xv0, xv1);   // whole lane groups
-  if (kTwo) ld(B, k0 + G);
+  if (kTwo) ld(B, k0 + G, 0);
+  if (kR == 2) ld(B, k0, 1);
   const float wr0 = drow0 >= 0 ? p.wrow[drow0] : 0.0f;
   const float wr1 = drow1 >= 0 ? p.wrow[drow1] : 0.0f;
   __syncthreads();
-  float acc1[2] = {0.0f, 0.0f}, acc3[2] = {0.0f, 0.0f};
+  float acc1s[kR][2] = {}, acc3s[kR][2] = {};
   const Q3Masks km = q3_masks();
-  auto mm = [&](const Q3Batch<G>& b, int kb0) {
+  auto mm = [&](const Q3Batch<G>& b, int kb0, int ri) {
+    float (&acc1)[2] = acc1s[ri];
+    float (&acc3)[2] = acc3s[ri];
 #pragma unroll
     for (int i = 0; i < G; ++i) {
       const int kb = kb0 + i;
@@ -970,27 +980,35 @@ __global__ __launch_bounds__(kQ3fW * 64) __attribute__((amdgpu_waves_per_eu(kF32
   };
   if constexpr (kTwo) {
     for (int kb = k0; kb < k1; kb += 2 * G) {
-      mm(A, kb);
-      if (kb + 2 * G < k1) ld(A, kb + 2 * G);
-      if (kb + G < k1) mm(B, kb + G);
-      if (kb + 3 * G < k1) ld(B, kb + 3 * G);
+      mm(A, kb, 0);
+      if (kb + 2 * G < k1) ld(A, kb + 2 * G, 0);
+      if (kb + G < k1) mm(B, kb + G, 0);
+      if (kb + 3 * G < k1) ld(B, kb + 3 * G, 0);
     }
   } else {
-    mm(A, k0);   // the range is one batch
+    mm(A, k0, 0);   // the range is one batch
+    if constexpr (kR == 2) mm(B, k0, 1);
   }
   // K ranges added in order: ((r0 + r1) + r2) + ...
-  *reinterpret_cast<float2*>(&red[item][ks][0][lane][0]) = float2{acc1[0], acc1[1]};
-  *reinterpret_cast<float2*>(&red[item][ks][1][lane][0]) = float2{acc3[0], acc3[1]};
+#pragma unroll
+  for (int i = 0; i < kR; ++i) {
+    *reinterpret_cast<float2*>(&red[item * kR + i][ks][0][lane][0]) = float2{acc1s[i][0], acc1s[i][1]};
+    *reinterpret_cast<float2*>(&red[item * kR + i][ks][1][lane][0]) = float2{acc3s[i][0], acc3s[i][1]};
+  }
   __syncthreads();
-  if (ks == 0 && rok && (drow0 >= 0 || drow1 >= 0)) {
+#pragma unroll
+  for (int i = 0; i < kR; ++i) {
+  float (&acc1)[2] = acc1s[i];
+  float (&acc3)[2] = acc3s[i];
+  if (ks == 0 && rt + i < p.up_tiles && (drow0 >= 0 || drow1 >= 0)) {
 #pragma unroll
     for (int w = 1; w < kQ3fKS; ++w) {
-      const float2 g = *reinterpret_cast<const float2*>(&red[item][w][0][lane][0]);
-      const float2 u = *reinterpret_cast<const float2*>(&red[item][w][1][lane][0]);
+      const float2 g = *reinterpret_cast<const float2*>(&red[item * kR + i][w][0][lane][0]);
+      const float2 u = *reinterpret_cast<const float2*>(&red[item * kR + i][w][1][lane][0]);
       acc1[0] += g.x; acc1[1] += g.y;
       acc3[0] += u.x; acc3[1] += u.y;
     }
-    const int n = rt * 16 + r16;
+    const int n = (rt + i) * 16 + r16;
     if (drow0 >= 0) {
       uint16_t hh, hl;
       split_bf16(silu_clamped(acc1[0], acc3[0], p.limit) * wr0, hh, hl);
@@ -1003,6 +1021,7 @@ __global__ __launch_bounds__(kQ3fW * 64) __attribute__((amdgpu_waves_per_eu(kF32
       p.h_hi[static_cast<int64_t>(drow1) * p.I + n] = hh;
       p.h_lo[static_cast<int64_t>(drow1) * p.I + n] = hl;
     }
+  }
   }
 }
 
@@ -1773,7 +1792,7 @@ size_t up_lds_bytes(const DecodeArgs& p) {
 // sums [kQ3fItems][kQ3fKS][2][64][2] f32, 64 zero bytes.
 size_t up_q3_lds_bytes(const DecodeArgs& p) {
   return static_cast<size_t>(p.x_f32 ? 2 : 1) * p.T * (p.H + 8) * 2 +
-         static_cast<size_t>(p.H / 128) * kQ3fMaxTokens * 16 + kQ3fItems * kQ3fKS * 2 * 64 * 2 * 4 + 64;
+         static_cast<size_t>(p.H / 128) * kQ3fMaxTokens * 16 + kQ3fItems * 2 * kQ3fKS * 2 * 64 * 2 * 4 + 64;
 }
 
 size_t up_mx_lds_bytes(const DecodeArgs& p) {
@@ -1858,6 +1877,7 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   const bool q3fwin = d.hidden % (kQ3fKS * kUpBatch * 128) == 0;
   const bool q3f2 = (d.hidden / 128 + kQ3fKS - 1) / kQ3fKS > kUpBatch;   // a wave's range is two or more batches
   const unsigned q3f_blocks = static_cast<unsigned>(max_slots * ((p.up_tiles + kQ3fItems - 1) / kQ3fItems));
+  const unsigned q3f2_blocks = static_cast<unsigned>(max_slots * ((p.up_tiles + 2 * kQ3fItems - 1) / (2 * kQ3fItems)));
   if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   if (d.tokens >= kDecodeGroupedUpMin && grouped_path(d)) {
     e = launch_grouped_up_routed(d, L, a, a.route.desc, a.route.xrow, a.route.wrow, s, repeat);
@@ -1868,7 +1888,11 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
     const bool q3f = q3 && d.tokens <= kQ3fMaxTokens && q3f_lds <= kMaxLds;
     for (int r = 0; r < repeat; ++r) {
       if (q3f && !q3f2) {
-        if (q3fwin && !p.x_f32) launch_kernel(k_up_q3<true, false, false>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
+        // two row tiles per wave from 2 tokens (B=2: 38.9 -> 37.9 us; at one token, whose
+        // 8 slots fit the chip in about two rounds of one-tile blocks, 17.3 -> 18.2 us)
+        if (q3fwin && !p.x_f32 && d.tokens >= 2)
+          launch_kernel(k_up_q3<true, false, false, 2>, q3f2_blocks, kQ3fW * 64, q3f_lds, s, p);
+        else if (q3fwin && !p.x_f32) launch_kernel(k_up_q3<true, false, false>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
         else if (q3fwin) launch_kernel(k_up_q3<true, true, false>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
         else if (!p.x_f32) launch_kernel(k_up_q3<false, false, false>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
         else launch_kernel(k_up_q3<false, true, false>, q3f_blocks, kQ3fW * 64, q3f_lds, s, p);
