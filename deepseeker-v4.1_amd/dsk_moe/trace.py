@@ -20,7 +20,7 @@ therefore keeps:
   object whose ``kind`` is ``"engram"`` or ``"kv"``.
 
 The validity rules live in one table (``FIELDS``: per record kind, the fields
-with their presence and value rule) read by one checker (``check``); the
+with their presence and value rule) read by one validator (``check``); the
 file is handled by ``Trace`` (load / save / histogram / summary / per-layer
 token batches).  ``TraceSink`` turns the device routing of ``moe_layer``,
 ``MoELayer`` and ``MoEStack`` into routing records, and ``Trace.batches``

@@ -4,7 +4,7 @@ This package restates, on the CPU (numpy integer/byte work, torch fp32
 GEMMs), what the reference's MoE layer computes, so that the HIP library can
 be checked against it on identical inputs.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-import it, and only as the checker or as the timed CPU baseline.  The product
+import it, and only to compare against or as the timed CPU baseline.  The product
 path (``dsk_moe``) never imports it and never falls back to it.
 
 Modules and the reference code each one follows (paths relative to the

@@ -1,6 +1,6 @@
 """RMSNorm of a residual stream and the layer-stack composition, restated on the CPU.
 
-Test infrastructure only (the checker of the stack runner).
+Test infrastructure only (what the stack runner is compared against).
 
 Reference: ``rmsnorm`` (``src/deepseeker/mlx_forward.py:45-59``): for
 lower-precision inputs ``xf = f32(x)``, ``rstd = rsqrt(mean(xf * xf) + eps)``,

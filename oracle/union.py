@@ -1,7 +1,7 @@
 """The batch union cap of the reference (``cap_union``), restated on the CPU.
 
 Test infrastructure: only the tests, ``__graft_entry__.smoke`` and the
-benchmark's CPU baseline use this module, as the checker.
+benchmark's CPU baseline use this module, to compare against.
 
 Reference: ``src/deepseeker/mlx_forward.py:213-254`` (``cap_union``), called by
 ``moe_layer`` for lock-step batches of more than one row (``:294-305``) with

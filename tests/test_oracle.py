@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the checker.
+"""Pins the CPU oracle before the GPU results are compared against it.
 
 Each test names what it pins: the reference's own known-answer tests and
 seeded vectors (restated here, the reference cannot be imported), closed
