@@ -13,6 +13,15 @@
   multiple of 512: superblock tails and the non-factored q3 down).
 * Top-k 12 and 16 (the combine's rows past 8, and the decode pipeline's slot
   map with 16 selections per token).
+* The FP4 batch-sweep layer (hidden 4096, 256 experts, top-8, inter 2048) at
+  64 tokens, every row: the grouped path with ~160 experts, some of them over
+  several 8-row column tiles.
+* float32 activations at that shape (the reference's tests call the layer
+  with float32 x) at 1, 8 and 64 tokens: the general path's hi/lo bf16
+  operand split, routing bit-exact.
+* q3 experts through the prefill GEMM (from 128 tokens) at both full shapes:
+  hidden 4096 / inter 2048 at 256 tokens and the reference geometry at 160
+  tokens (routing of every row, output of every other row).
 
 Routing indices and weights bit-exact; outputs within the layer tolerance
 (cosine >= 0.99999 and max|y - y_ref| / max|y_ref| <= 1e-2).
@@ -115,3 +124,40 @@ def test_wide_topk(k, T):
     layer = gsynth.make_layer(hidden=1024, n_experts=64, top_k=k, inter=512, inter_shared=512,
                               seed=80 + k + T, device=DEV)
     check_layer(layer, _x(T, 1024, 800 + k + T), "fp4", f"top-{k} H1024 E64 I512")
+
+
+# ---------------------------------------------------------------- FP4 batch sweep layer, bf16 and float32 x
+@pytest.fixture(scope="module")
+def sweep_fp4():
+    layer = gsynth.make_layer(hidden=4096, n_experts=256, top_k=8, inter=2048, inter_shared=2048,
+                              quant="fp4", seed=11, device=DEV)
+    yield layer
+    del layer
+    torch.cuda.empty_cache()
+
+
+def test_fp4_batch64_all_rows(sweep_fp4):
+    check_layer(sweep_fp4, _x(64, 4096, 641), "fp4", "fp4 H4096 E256 k8 I2048 B=64")
+
+
+@pytest.mark.parametrize("T", [1, 8, 64])
+def test_fp32_activations_full_size(sweep_fp4, T):
+    """float32 x with values off the bf16 grid (the operand's hi/lo split matters)."""
+    g = torch.Generator(device=DEV).manual_seed(900 + T)
+    x = torch.randn((T, 4096), generator=g, device=DEV, dtype=torch.float32)
+    assert not torch.equal(x, x.to(torch.bfloat16).float())
+    check_layer(sweep_fp4, x, "fp4", "fp4 H4096 E256 k8 I2048 float32 x")
+
+
+# ---------------------------------------------------------------- q3 through the prefill GEMM at full shape
+@pytest.mark.parametrize("geometry,T", [("sweep", 256), ("reference", 160)])
+def test_q3_prefill_full_shape(geometry, T):
+    if geometry == "sweep":
+        kw = dict(hidden=4096, n_experts=256, top_k=8, inter=2048, inter_shared=2048)
+    else:
+        kw = dict(REF_GEOMETRY)
+    layer = gsynth.make_layer(**kw, quant="q3", seed=53, device=DEV)
+    H = kw["hidden"]
+    check_layer(layer, _x(T, H, 5300 + T), "q3", f"q3 prefill {geometry} H{H}", rows=list(range(0, T, 2)))
+    del layer
+    torch.cuda.empty_cache()

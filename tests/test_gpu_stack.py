@@ -4,11 +4,13 @@ RMSNorm rows bit-exact against the oracle's defined order.  Small mixed FP4 /
 q3 stacks are checked layer by layer on the device's own stream values
 (normalised rows bit-exact, routing bit-exact, layer outputs within the layer
 tolerance).  The full-size 40-layer stack (layers 0-19 FP4, 20-39 q3) is
-checked through properties: a 2-token verify step equals two 1-token steps
-bit for bit (at one and two tokens the same decode kernels run, and each adds
-a token's terms in an order that does not depend on the other token), and
-replays of the captured HIP graph equal the eager run, with eager work
-between replays.
+checked layer by layer against the oracle at one and two tokens (normalised
+rows and routing bit-exact, every layer's output within the layer tolerance,
+the final residual sum bit-exact) and through properties: a 2-token verify
+step equals two 1-token steps bit for bit (at one and two tokens the same
+decode kernels run, and each adds a token's terms in an order that does not
+depend on the other token), and replays of the captured HIP graph equal the
+eager run, with eager work between replays.
 """
 
 from __future__ import annotations
@@ -90,6 +92,36 @@ def stack40():
     yield MoEStack(layers, eps=1e-6)
     del layers
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_full_stack_layerwise(stack40, T):
+    """Every one of the 40 full-size layers against the oracle on the device's own stream values."""
+    from conftest import DeviceBankView
+    from test_gpu_fullshape import _spec
+    print(f"stack 40 layers layer by layer T={T}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(90 + T)
+    x = torch.randn((T, 4096), generator=g, device=DEV).to(torch.bfloat16)
+    rec = []
+    out = stack40(x, record=rec).cpu()
+    assert len(rec) == 40
+    for l, (h, y, idx, dl) in enumerate(rec):
+        layer = stack40.layers[l]
+        quant = "fp4" if l < 20 else "q3"
+        _, y_ref = S.rmsnorm(h.float().cpu().numpy(), 1e-6, dtype="bf16")
+        np.testing.assert_array_equal(y.float().cpu().numpy(), y_ref)
+        idx_h = idx.cpu().numpy()
+        shared = tuple(t.cpu() for t in (layer.shared.w1, layer.shared.w3, layer.shared.w2))
+        view = DeviceBankView(layer.bank).prefetch(idx_h.ravel())
+        try:
+            r = L.moe_forward(y.cpu(), layer.gate_w.cpu(), layer.gate_b.cpu(), view, shared, _spec(layer, quant))
+        finally:
+            view.close()
+        np.testing.assert_array_equal(idx_h, r["idx"])
+        c, rel = assert_layer_close(dl.float().cpu(), r["y_ref"])
+        print(f"layer {l} {quant}: cos={c:.9f} rel={rel:.2e}", flush=True)
+    h_last, d_last = rec[-1][0].float().cpu().numpy(), rec[-1][3].float().cpu().numpy()
+    np.testing.assert_array_equal(out.float().numpy(), S.round_to(h_last + d_last, "bf16"))
 
 
 def test_full_stack_verify_and_graph(stack40):
