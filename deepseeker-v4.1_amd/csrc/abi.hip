@@ -251,6 +251,31 @@ int dsk_experts(const dsk_moe_desc* d, const dsk_expert_ptrs* table, const void*
                    "dsk_experts launch");
 }
 
+int dsk_expert_rows(const dsk_moe_desc* d, const dsk_expert_ptrs* table, const void* x,
+                    const float* weights, const int32_t* counts, const int32_t* offsets,
+                    const int32_t* perm, const int32_t* rank, const int32_t* active, float* rows,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_expert_desc(d);
+  if (rc) return rc;
+  if (d->inter_shared != 0)
+    return fail(DSK_EINVAL, "dsk_expert_rows: inter_shared must be 0 (routed experts only), got %d",
+                d->inter_shared);
+  if (!table || !x || !weights || !counts || !offsets || !perm || !rank || !active || !rows || !workspace)
+    return fail(DSK_EINVAL, "dsk_expert_rows: NULL pointer argument");
+  if (!aligned(x, 16) || !aligned(rows, 16) || !aligned(workspace, 256))
+    return fail(DSK_EALIGN, "dsk_expert_rows: x/rows need 16-byte, workspace 256-byte alignment");
+  const Workspace L = workspace_layout(*d);
+  if (workspace_bytes < L.total)
+    return fail(DSK_ESPACE, "workspace %zu bytes < required %zu", workspace_bytes, L.total);
+  ExpertsArgs a{};
+  a.table = table; a.x = x; a.weights = weights;
+  a.counts = counts; a.offsets = offsets; a.perm = perm; a.rank = rank; a.active = active;
+  a.ws = static_cast<char*>(workspace);
+  a.rows_out = rows;
+  return hip_check(launch_experts(*d, L, a, static_cast<hipStream_t>(stream), 1),
+                   "dsk_expert_rows launch");
+}
+
 }  // extern "C"
 
 int dsk::check_forward(const dsk_moe_desc* d, const void* x, const void* gate_w,

@@ -245,6 +245,7 @@ struct ExpertsArgs {
   const int32_t* rank; const int32_t* active;
   void* out;
   char* ws;                  // workspace base
+  float* rows_out;           // dsk_expert_rows: the per-row outputs go here and nothing is combined
   const int32_t* rowmap;     // decode pipeline: [slot][T] dispatch row of token t, -1 if none
   // decode pipeline: gate scores and selection bias in, routing out
   float* scores; const float* bias;
@@ -280,10 +281,16 @@ hipError_t launch_rmsnorm(const void* x, const void* res, const float* gamma, in
 
 // Prefill GEMM path (prefill_gemm(d)): tile list, gate/up, down; the caller
 // runs the combine.  Opens the gate/up and down stages.
+// Where the expert kernels write their per-dispatch-row float32 outputs.
+inline float* rows_buffer(float* rows_out, char* ws, const Workspace& L) {
+  return rows_out ? rows_out : reinterpret_cast<float*>(ws + L.y);
+}
+
 struct PrefillArgs {
   const SlotDesc* desc; const int32_t* active; const int32_t* xrow; const float* wrow;
   const void* x; const void* ws1; const void* ws3; const void* ws2;
   char* ws;
+  float* rows_out;           // per-row outputs instead of the workspace's (or null)
 };
 hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, const PrefillArgs& a,
                                   hipStream_t s, int repeat);

@@ -567,13 +567,13 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
   const uint16_t* xb_hi = static_cast<const uint16_t*>(a.x);
   const uint16_t* xb_lo = nullptr;
   if (prefill_gemm(d)) {
-    PrefillArgs pa{desc, a.active, xrow, wrow, a.x, a.ws1, a.ws3, a.ws2, a.ws};
+    PrefillArgs pa{desc, a.active, xrow, wrow, a.x, a.ws1, a.ws3, a.ws2, a.ws, a.rows_out};
     if ((e = launch_experts_prefill(d, L, pa, s, repeat)) != hipSuccess) return e;
-    return launch_combine(d, L, a, s, repeat);
+    return a.rows_out ? hipSuccess : launch_combine(d, L, a, s, repeat);
   }
   if (grouped_path(d)) {
     if ((e = launch_experts_grouped(d, L, a, desc, xrow, wrow, s, repeat)) != hipSuccess) return e;
-    return launch_combine(d, L, a, s, repeat);
+    return a.rows_out ? hipSuccess : launch_combine(d, L, a, s, repeat);
   }
   if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   if (x_f32) {
@@ -611,7 +611,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
   dn.desc = desc; dn.active = a.active;
   dn.ws2 = static_cast<const uint16_t*>(a.ws2);
   dn.h_hi = u.h_hi; dn.h_lo = u.h_lo; dn.hs_hi = u.hs_hi; dn.hs_lo = u.hs_lo;
-  dn.y = reinterpret_cast<float*>(a.ws + L.y);
+  dn.y = rows_buffer(a.rows_out, a.ws, L);
   dn.ys = reinterpret_cast<float*>(a.ws + L.ys);
   dn.tiles = H / 16;
   dn.shared_blocks = Is > 0 ? H / 16 : 0;
@@ -620,7 +620,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
     e = nt == 1 ? launch_down<1>(dn, down_blocks, q3, s) : nt == 2 ? launch_down<2>(dn, down_blocks, q3, s) : launch_down<4>(dn, down_blocks, q3, s);
     if (e != hipSuccess) return e;
   }
-  return launch_combine(d, L, a, s, repeat);
+  return a.rows_out ? hipSuccess : launch_combine(d, L, a, s, repeat);
 }
 
 }  // namespace dsk

@@ -666,7 +666,7 @@ GroupedArgs grouped_args(const dsk_moe_desc& d, const Workspace& L, const Expert
   p.h_lo = reinterpret_cast<uint16_t*>(a.ws + L.h_lo);
   p.hs_hi = reinterpret_cast<uint16_t*>(a.ws + L.hs_hi);
   p.hs_lo = reinterpret_cast<uint16_t*>(a.ws + L.hs_lo);
-  p.y = reinterpret_cast<float*>(a.ws + L.y);
+  p.y = rows_buffer(a.rows_out, a.ws, L);
   p.ys = reinterpret_cast<float*>(a.ws + L.ys);
   p.q3f = up_q3f(d) ? 1 : 0;
   p.q3fd = down_q3f(d) ? 1 : 0;

@@ -791,7 +791,7 @@ hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, con
   p.ws2 = static_cast<const uint16_t*>(a.ws2);
   p.h = reinterpret_cast<uint16_t*>(a.ws + L.h_hi);
   p.hs = reinterpret_cast<uint16_t*>(a.ws + L.hs_hi);
-  p.y = reinterpret_cast<float*>(a.ws + L.y);
+  p.y = rows_buffer(a.rows_out, a.ws, L);
   p.ys = reinterpret_cast<float*>(a.ws + L.ys);
 
   if ((e = stage_open(kStageUp)) != hipSuccess) return e;

@@ -14,11 +14,12 @@ from ._lib import DskError, load as load_library
 from .bank import ResidentBank, SharedExpert
 from .checkpoint import Checkpoint, build_manifest, fp8_block_dequant
 from .layer import MoELayer, moe_layer
+from .pinned import expert_rows, gather_pinned_contributions
 from .stack import MoEStack, rmsnorm
 from .trace import Geometry, Trace, TraceSink
 from .ops import (align_block_size, dispatch, fp4_dequant, fp4_quantize, q3_dequant,
                   q3_quantize, q3_repack, route, workspace_size)
 
 __all__ = ["Checkpoint", "DskError", "MoELayer", "MoEStack", "ResidentBank", "SharedExpert", "TraceSink", "align_block_size",
-           "build_manifest", "dispatch", "fp4_dequant", "fp8_block_dequant", "fp4_quantize", "load_library", "moe_layer",
+           "build_manifest", "dispatch", "expert_rows", "gather_pinned_contributions", "fp4_dequant", "fp8_block_dequant", "fp4_quantize", "load_library", "moe_layer",
            "q3_dequant", "q3_quantize", "q3_repack", "rmsnorm", "route", "workspace_size", "Geometry", "Trace"]

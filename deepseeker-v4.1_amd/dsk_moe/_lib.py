@@ -63,6 +63,7 @@ SIGNATURES = {
     "dsk_cap_union": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "dsk_experts": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "dsk_expert_rows": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "dsk_moe_forward": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                        _vp, _vp, _vp, _sz, _vp]),
     "dsk_moe_forward_timed": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

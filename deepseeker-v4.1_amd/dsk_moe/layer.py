@@ -34,7 +34,11 @@ one-expert rescue of rows that would lose everything; ``route_stats``
 with host arrays in the trace hook's order, returns ``{expert: (rows,
 contrib)}``: each selected expert found there adds its weighted output rows
 ``contrib`` at ``rows`` instead of being computed (``:388-393``); the other
-experts then run in float32 and the sum is cast once.
+experts' weighted rows are computed with x in float32 (``dsk_expert_rows``),
+each row's contributions are added in ascending expert order, the pinned
+ones in their place, and the sum is cast once.  ``dsk_moe.pinned``'s
+``gather_pinned_contributions`` is a device version of the reference's
+callback body (``:159-210``).
 
 Options of the reference that only concern SSD paging or MLX scheduling are
 accepted and have no effect on the result, which the reference documents as
@@ -49,6 +53,7 @@ from __future__ import annotations
 
 import ctypes
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -60,7 +65,6 @@ from .ops import make_desc, ptr, require_device, stream_of, workspace, workspace
 def _coverage(w_before: torch.Tensor, idx_capped: torch.Tensor) -> float:
     """Share of the batch's gate weight the cap retained (before rescaling), summed as
     the reference does (numpy float32, its slot order: ascending key)."""
-    import numpy as np
     wb = w_before.cpu().numpy()[:, ::-1]
     kept = idx_capped.cpu().numpy()[:, ::-1] >= 0
     total = float(wb.sum())
@@ -198,7 +202,7 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
     ws3 = shared.w3 if shared else None
     ws2 = shared.w2 if shared else None
     if pinned:
-        _with_pinned(desc, x, idx, w, table, (ws1, ws3, ws2), shared_out, pinned, out, dev, keep)
+        _with_pinned(desc, x, idx, w, table, (ws1, ws3, ws2), shared_out, pinned, uniq, out, dev, keep)
     elif split:
         from .ops import dispatch as _dispatch  # local: same device, same stream
         d = _dispatch(idx, e)
@@ -217,39 +221,57 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor,
     return out
 
 
-def _with_pinned(desc, x, idx, w, table, shared_w, shared_out, pinned: dict, out, dev, keep: list) -> None:
+def _with_pinned(desc, x, idx, w, table, shared_w, shared_out, pinned: dict, uniq: list, out, dev,
+                 keep: list) -> None:
     """The layer with some selected experts supplied by a pinned-gather callback
-    (src/deepseeker/mlx_forward.py:313-321, 388-393): their ``(rows, contrib)``
-    (weighted output rows) are added instead of computing them.  The other
-    experts run in float32 (x is exact in float32), the contributions are added
-    per expert in ascending id, then the shared output rounded to x's dtype, and
-    the sum is cast once, as the reference's float32 scatter-add does."""
+    (src/deepseeker/mlx_forward.py:313-321, 388-393).  The other selected
+    experts' weighted rows come from ``dsk_expert_rows`` (x in float32); then,
+    as the reference's float32 scatter-add, every row's contributions are added
+    from zero expert by expert in ascending id -- an expert of the callback
+    adds its ``contrib`` rows at its ``rows`` in its place -- followed by the
+    shared output rounded to x's dtype, and the sum is cast once."""
     from .ops import dispatch as _dispatch
+    from .pinned import expert_rows
     stream = stream_of(dev)
     t, h = x.shape
     e = desc.n_experts
     idx_m = idx.clone()
     for ex in pinned:
         idx_m[idx_m == ex] = -1
-    # routed experts that are not pinned, float32 output
-    d32 = _lib.Desc.from_buffer_copy(desc)
-    d32.x_dtype = 1
-    d32.inter_shared = 0
-    x32 = x.to(torch.float32).contiguous()
-    acc = torch.empty((t, h), dtype=torch.float32, device=dev)
-    dd = _dispatch(idx_m, e)
-    ws = workspace(d32, dev)
-    _lib.call("dsk_experts", ctypes.byref(d32), ptr(table), None, None, None, None, ptr(x32), ptr(w),
-              ptr(dd["counts"]), ptr(dd["offsets"]), ptr(dd["perm"]), ptr(dd["rank"]), ptr(dd["active"]),
-              ptr(acc), ptr(ws), ws.numel(), stream)
-    keep += [dd, x32, idx_m]
+    quant = "fp4" if desc.quant == _lib.QUANT_FP4 else "q3"
+    computed, counts = expert_rows(x, idx_m, w, table, e, quant, desc.inter, limit=desc.limit)
+    idx_mh = idx_m.cpu().numpy()
+    # source rows: 0 = zeros, then the computed rows (dispatch order), then each pinned expert's rows
+    parts = [torch.zeros((1, h), dtype=torch.float32, device=dev), computed]
+    first = {}
+    base = 1 + computed.shape[0]
     for ex in sorted(pinned):
         rows, contrib = pinned[ex]
-        rows = torch.as_tensor(rows, dtype=torch.int64).to(dev)
+        rows = [int(r) for r in np.asarray(rows).ravel()]
         contrib = torch.as_tensor(contrib).to(device=dev, dtype=torch.float32)
-        if contrib.shape != (rows.numel(), h):
-            raise ValueError(f"pinned expert {ex}: contrib must be [len(rows), {h}]")
-        acc.index_add_(0, rows, contrib)
+        if contrib.shape != (len(rows), h) or any(not 0 <= r < t for r in rows):
+            raise ValueError(f"pinned expert {ex}: contrib must be [len(rows), {h}] with rows in [0, {t})")
+        parts.append(contrib)
+        first[ex] = (base, rows)
+        base += len(rows)
+    # per row, its sources in the order of the ascending-expert sum
+    order: list[list[int]] = [[] for _ in range(t)]
+    comp_row = 1
+    for ex in uniq:
+        if ex in first:
+            b, rows = first[ex]
+            for r, tok in enumerate(rows):
+                order[tok].append(b + r)
+        elif counts[ex]:
+            for tok in np.nonzero((idx_mh == ex).any(axis=1))[0]:
+                order[int(tok)].append(comp_row)
+                comp_row += 1
+    depth = max(1, max(len(o) for o in order))
+    src = torch.tensor([o + [0] * (depth - len(o)) for o in order], dtype=torch.int64).to(dev)
+    rows_all = torch.cat(parts)
+    acc = torch.zeros((t, h), dtype=torch.float32, device=dev)
+    for j in range(depth):
+        acc += rows_all.index_select(0, src[:, j])
     ws1, ws3, ws2 = shared_w
     if ws1 is not None:
         # the shared expert alone (no routed position), rounded to x's dtype

@@ -162,6 +162,21 @@ int dsk_experts(const dsk_moe_desc* d, const dsk_expert_ptrs* table,
                 const int32_t* active, void* out, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* Weighted output rows of every routed (token, expert) pair, not combined:
+ * replaces gather_pinned_contributions (src/deepseeker/mlx_forward.py:159-210),
+ * the banked gate/up and w2 products of the runner's pinned experts
+ * (src/deepseeker/mlx_runner.py:949-960).  rows [n, H] float32 receives, for
+ * dispatch row r (pairs in dsk_dispatch's order: expert ascending, then flat
+ * position t*k + j ascending, i.e. expert, token, slot), the row
+ * w2 (silu(min(x w1, L)) * clip(x w3, -L, L) * weight) of that pair; n is the
+ * number of pairs with an index in [0, E) and the buffer must hold T*k rows.
+ * Routed experts only: d->inter_shared must be 0.  Arguments otherwise as for
+ * dsk_experts (float32 x runs the products on bf16 hi/lo operands). */
+int dsk_expert_rows(const dsk_moe_desc* d, const dsk_expert_ptrs* table, const void* x,
+                    const float* weights, const int32_t* counts, const int32_t* offsets,
+                    const int32_t* perm, const int32_t* rank, const int32_t* active, float* rows,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* Whole layer: replaces moe_layer (src/deepseeker/mlx_forward.py:257-419):
  * dsk_route, dsk_dispatch and dsk_experts on one stream.  Shared-expert
  * arguments as for dsk_experts.  idx / weights are optional outputs

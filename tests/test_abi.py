@@ -77,6 +77,14 @@ def test_null_and_alignment_errors_before_launch():
     assert rc == -1 and b"128" in lib.dsk_last_error()   # q3 needs K multiples of 128
     rc = lib.dsk_experts(ctypes.byref(_desc(quant="q3", hidden=1056)), *([ctypes.c_void_p(256)] * 14), 1 << 30, None)
     assert rc == -1                                   # hidden % 128
+    rows_args = [ctypes.c_void_p(256)] * 10
+    rc = lib.dsk_expert_rows(ctypes.byref(_desc()), *rows_args, 1 << 30, None)
+    assert rc == -1 and b"inter_shared" in lib.dsk_last_error()    # routed experts only
+    rc = lib.dsk_expert_rows(ctypes.byref(_desc(inter_shared=0)), *rows_args[:8], ctypes.c_void_p(264),
+                             ctypes.c_void_p(256), 1 << 30, None)
+    assert rc == -2                                   # rows not 16-byte aligned
+    rc = lib.dsk_expert_rows(ctypes.byref(_desc(inter_shared=0)), *rows_args, 64, None)
+    assert rc == -5                                   # workspace too small
 
 
 def test_route_constants_match_oracle():
