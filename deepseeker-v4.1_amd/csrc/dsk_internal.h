@@ -177,6 +177,13 @@ inline bool prefill_gemm(const dsk_moe_desc& d) {
          d.inter % 128 == 0 && d.inter_shared % 128 == 0;
 }
 int prefill_max_tiles(const dsk_moe_desc& d);
+// The prefill GEMM's routed rows for the combine are rounded to bf16 when the
+// experts are FP4 (relative 2^-9 per row, inside the layer tolerance); q3
+// layers, whose dequantised weights are already rounded to bf16, and rows
+// handed to the caller stay float32.  Its shared output is always bf16.
+inline bool prefill_rows_bf16(const dsk_moe_desc& d, const float* rows_out) {
+  return d.quant == DSK_QUANT_FP4 && rows_out == nullptr;
+}
 
 inline bool decode_pipeline(const dsk_moe_desc& d) {
   // the gate/up kernel stages the tokens' activations (bf16 hi, and lo for

@@ -429,8 +429,20 @@ enum SharedMode { kNoShared = 0, kSharedF32 = 1, kSharedExt = 2 };
 
 constexpr int kCombineMaxK = 16;     // top-k the combine handles (validated on the host)
 constexpr int kCombineBatch = 8;     // rows of a token whose loads are issued together
-template <bool XBF16>
-__global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, const float* __restrict__ ys,
+// Four consecutive values of row r of y (float32, or bf16 when YBF16).
+template <bool YBF16>
+__device__ __forceinline__ f32x4 load_row4(const void* y, int64_t r, int H, int f) {
+  if constexpr (YBF16) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(y) + r * H + f);
+    return f32x4{__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                 __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
+  } else {
+    return *reinterpret_cast<const f32x4*>(static_cast<const float*>(y) + r * H + f);
+  }
+}
+
+template <bool XBF16, bool YBF16>
+__global__ __launch_bounds__(256) void k_combine(const void* __restrict__ y, const float* __restrict__ ys,
                                                  const void* __restrict__ shared_ext,
                                                  const int32_t* __restrict__ rank, int H, int k,
                                                  int shared_mode, void* __restrict__ out) {
@@ -459,12 +471,12 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, co
   }
   f32x4 v[kCombineBatch];
 #pragma unroll
-  for (int q = 0; q < kCombineBatch; ++q) v[q] = *reinterpret_cast<const f32x4*>(y + static_cast<int64_t>(rows[q]) * H + f);
+  for (int q = 0; q < kCombineBatch; ++q) v[q] = load_row4<YBF16>(y, rows[q], H, f);
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int q = 0; q < kCombineBatch; ++q)
     if (q < n) acc += v[q];
-  for (int i = kCombineBatch; i < n; ++i) acc += *reinterpret_cast<const f32x4*>(y + static_cast<int64_t>(rows[i]) * H + f);
+  for (int i = kCombineBatch; i < n; ++i) acc += load_row4<YBF16>(y, rows[i], H, f);
   const int64_t o = static_cast<int64_t>(t) * H + f;
   if (shared_mode == kSharedF32) {
     f32x4 s = *reinterpret_cast<const f32x4*>(ys + o);
@@ -528,17 +540,26 @@ hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t s) {
 hipError_t launch_combine(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,
                           int repeat) {
   const int T = d.tokens, H = d.hidden, Is = d.inter_shared, k = d.top_k;
-  const float* y = reinterpret_cast<const float*>(a.ws + L.y);
+  const void* y = a.ws + L.y;
   const float* ys = reinterpret_cast<const float*>(a.ws + L.ys);
   dim3 cg(static_cast<unsigned>(T), static_cast<unsigned>((H + 1023) / 1024));
-  const int mode = Is > 0 ? kSharedF32 : (a.shared_out ? kSharedExt : kNoShared);
+  int mode = Is > 0 ? kSharedF32 : (a.shared_out ? kSharedExt : kNoShared);
+  const void* shared_ext = a.shared_out;
+  const bool pf = prefill_gemm(d);
+  if (pf && Is > 0) {            // the prefill GEMM wrote the shared output already rounded to bf16
+    mode = kSharedExt;
+    shared_ext = ys;
+  }
+  const bool ybf = pf && prefill_rows_bf16(d, nullptr);
   hipError_t e = stage_open(kStageCombine);
   if (e != hipSuccess) return e;
   for (int r = 0; r < repeat; ++r) {
     if (d.x_dtype == DSK_DTYPE_F32)
-      launch_kernel(k_combine<false>, cg, 256, 0, s, y, ys, a.shared_out, a.rank, H, k, mode, a.out);
+      launch_kernel(k_combine<false, false>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
+    else if (ybf)
+      launch_kernel(k_combine<true, true>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
     else
-      launch_kernel(k_combine<true>, cg, 256, 0, s, y, ys, a.shared_out, a.rank, H, k, mode, a.out);
+      launch_kernel(k_combine<true, false>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return e;

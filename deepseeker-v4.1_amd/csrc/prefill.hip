@@ -493,7 +493,9 @@ struct PfArgs {
   const uint16_t* x;                        // [T][H] bf16
   const uint16_t* ws1; const uint16_t* ws3; const uint16_t* ws2;
   uint16_t* h; uint16_t* hs;                // [T*k][I], [T][Is] bf16
-  float* y; float* ys;                      // [T*k][H], [T][H] float32
+  float* y;                                 // [T*k][H] float32 (or bf16 when y_bf16)
+  uint16_t* ys;                             // [T][H] the shared output, rounded to bf16
+  int y_bf16;                               // routed rows rounded to bf16 (FP4 layer, combined here)
   int row_tiles;                            // weight-row tiles per token tile
 };
 
@@ -707,19 +709,31 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_down(PfArgs p) {
                                  n_ct, pf_lds, acc);
     }
   }
-  float* out = shared ? p.ys : p.y;
+  // The shared output is rounded to bf16 here (the combine adds it rounded to
+  // x's dtype, bf16 on this path); routed rows stay float32 unless y_bf16.
+  const bool narrow = shared || p.y_bf16;
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const int n = 64 * wn + 32 * c + (lane & 31);
     if (n >= cnt) continue;
     const int64_t drow = tok_base + first + n;
+    const int64_t col0 = drow * p.H + rt * 256 + wm * 128 + 4 * (lane >> 5);
+    if (narrow) {
+      uint16_t* out = shared ? p.ys : reinterpret_cast<uint16_t*>(p.y);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float* dst = out + drow * p.H + rt * 256 + wm * 128 + 32 * i + 4 * (lane >> 5);
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<f32x4*>(dst + 8 * q) =
-            f32x4{acc[i][c][4 * q], acc[i][c][4 * q + 1], acc[i][c][4 * q + 2], acc[i][c][4 * q + 3]};
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<uint2*>(out + col0 + 32 * i + 8 * q) =
+              uint2{pack_bf16x2(acc[i][c][4 * q], acc[i][c][4 * q + 1]),
+                    pack_bf16x2(acc[i][c][4 * q + 2], acc[i][c][4 * q + 3])};
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<f32x4*>(p.y + col0 + 32 * i + 8 * q) =
+              f32x4{acc[i][c][4 * q], acc[i][c][4 * q + 1], acc[i][c][4 * q + 2], acc[i][c][4 * q + 3]};
     }
   }
 }
@@ -792,7 +806,8 @@ hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, con
   p.h = reinterpret_cast<uint16_t*>(a.ws + L.h_hi);
   p.hs = reinterpret_cast<uint16_t*>(a.ws + L.hs_hi);
   p.y = rows_buffer(a.rows_out, a.ws, L);
-  p.ys = reinterpret_cast<float*>(a.ws + L.ys);
+  p.ys = reinterpret_cast<uint16_t*>(a.ws + L.ys);
+  p.y_bf16 = prefill_rows_bf16(d, a.rows_out) ? 1 : 0;
 
   if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   p.row_tiles = (I > Is ? I : Is) / 128;
