@@ -1,8 +1,9 @@
 // Router math shared by the router kernels and the fused decode kernel:
 // score functions, gate logits of a tile, biased top-k, arrival counters.
 // Every function here evaluates floating point in one fixed order without
-// contraction (the pragma opens each body), because the expert indices must
-// be bit-identical to the CPU oracle.  The order is described in route.hip.
+// contraction (the pragma opens each body; the gate's fused multiply-adds are
+// explicit), because the expert indices must be bit-identical to the CPU
+// oracle.  The order is described in route.hip.
 #pragma once
 
 #include "dispatch_block.h"
@@ -136,8 +137,7 @@ __device__ __forceinline__ void gate_tile(const void* x, const void* gw, int T, 
         for (int i = 0; i < TW; ++i)
 #pragma unroll
           for (int j = 0; j < EW; ++j) {
-            const float prod = (ok ? xv[q][i][v] : 0.0f) * (ok ? wv[q][j][v] : 0.0f);
-            p[i][j] = p[i][j] + prod;
+            p[i][j] = __builtin_fmaf(ok ? xv[q][i][v] : 0.0f, ok ? wv[q][j][v] : 0.0f, p[i][j]);
           }
     }
   }

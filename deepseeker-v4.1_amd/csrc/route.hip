@@ -8,10 +8,11 @@
 // without contraction, and the pragma below makes that explicit):
 //   logit  H is cut into 256-element steps and the steps into 4 segments of
 //          ceil(steps/4); wave w of a block owns segment w.  Lane l keeps a
-//          float32 partial that adds, over the segment's steps m and then
-//          v = 0..3, the rounded product x[256m+4l+v] * W[e][256m+4l+v]; an XOR
-//          butterfly (s = 32..1: p[l] = p[l] + p[l^s]) gives the segment sum
-//          s_w, and z = ((s_0 + s_1) + s_2) + s_3.
+//          float32 partial that starts at +0 and takes, over the segment's
+//          steps m and then v = 0..3, p = fma(x[256m+4l+v], W[e][256m+4l+v], p)
+//          (one rounding per step); an XOR butterfly (s = 32..1:
+//          p[l] = p[l] + p[l^s]) gives the segment sum s_w, and
+//          z = ((s_0 + s_1) + s_2) + s_3.
 //   score  in double with this file's own exp (Cody-Waite ln2 split, degree-14
 //          Taylor in Horner form) and log1p (2*atanh(u/(2+u)), odd series),
 //          rounded once to float; sqrt-softplus takes the correctly rounded
@@ -102,8 +103,8 @@ __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ scores,
 // tile; wave w owns tokens 8 (w & 3) + [0, 8) and experts 8 (w >> 2) +
 // [0, 8), and lane l the partial l of each of its 64 (token, expert) pairs.
 // Each 256-element step m is staged through LDS (double-buffered: x [32][256],
-// W [16][256]) and every partial adds, for v = 0..3, the rounded product at
-// position 256m + 4l + v: the order of the definition above.  At the end of a
+// W [16][256]) and every partial takes, for v = 0..3, the fused multiply-add
+// at position 256m + 4l + v: the order of the definition above.  At the end of a
 // segment the 64 partials of each pair are combined by the same XOR tree,
 // computed as a reduce-scatter: at stride s a lane keeps the upper half of
 // its pairs if bit s of its lane id is set and adds the partner's (lane ^ s)
@@ -209,8 +210,7 @@ __global__ __launch_bounds__(kGwThreads, 1) void k_gate_wide(GateArgs g) {
       for (int v = 0; v < 4; ++v)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float prod = xv[i][v] * wv[v];
-          p[8 * i + j] = p[8 * i + j] + prod;
+          p[8 * i + j] = __builtin_fmaf(xv[i][v], wv[v], p[8 * i + j]);
         }
     }
     if (m + 1 < steps) store((m + 1) & 1);

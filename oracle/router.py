@@ -11,14 +11,15 @@ Routing indices must be bit-identical between this oracle and the GPU, so
 every floating-point step has one defined order that the HIP kernel mirrors:
 
 1. Gate logit ``z[t, e]``: H is cut into 256-element steps ``m`` (positions
-   >= H contribute +0) and the steps into 4 segments of ``S = ceil(steps/4)``
+   >= H contribute nothing) and the steps into 4 segments of ``S = ceil(steps/4)``
    consecutive steps (segment w holds steps [w*S, (w+1)*S)).  In each segment,
-   64 partial sums: partial ``l`` accumulates, for its steps ``m`` in order and
-   then ``v = 0..3``, the float32 product ``x[256*m + 4*l + v] * W[256*m + 4*l + v]``
-   (product rounded, then sum rounded; no fused multiply-add).  The 64
-   partials are combined by an XOR butterfly (for s = 32, 16, 8, 4, 2, 1:
-   ``p[l] = p[l] + p[l ^ s]``) into the segment sum ``s_w = p[0]``, and
-   ``z = ((s_0 + s_1) + s_2) + s_3``.
+   64 partial sums: partial ``l`` starts at +0 and takes, for its steps ``m`` in
+   order and then ``v = 0..3``, ``p = fma(x[256*m + 4*l + v], W[256*m + 4*l + v], p)``
+   (the IEEE fused multiply-add: one rounding).  The 64 partials are combined
+   by an XOR butterfly (for s = 32, 16, 8, 4, 2, 1: ``p[l] = p[l] + p[l ^ s]``)
+   into the segment sum ``s_w = p[0]``, and ``z = ((s_0 + s_1) + s_2) + s_3``.
+   The chains are evaluated by ``oracle/gate_fma.c`` (C ``fmaf``), built on
+   first use by ``oracle/build_c.py``.
 2. Scores are computed in float64 from ``z`` with this module's own ``exp``
    (Cody-Waite reduction by ln2 split in a 32-bit-exact high part and a low
    part, degree-14 Taylor polynomial in Horner form, ``ldexp``) and
@@ -32,7 +33,9 @@ every floating-point step has one defined order that the HIP kernel mirrors:
 4. ``w_j = (s_j / (((s_0 + s_1) + ...) + 1e-20)) * route_scale`` in float32,
    the sum taken in selection order.
 
-Parity: the closed forms are pinned in the tests by the reference's own
+Parity: the fused chain is pinned in the tests by an exact-rational scalar
+restatement (every fma rounded once from the exact value, ties to even) and by
+inputs where an unfused product would differ; the closed forms are pinned by the reference's own
 torch router recipe (``tests/test_mlx_numerics.py:69-89``), the invariants
 of ``tests/test_batch.py:321-337`` and ``tests/test_mlx_forward.py:161-177``,
 and by comparing ``exp``/``log1p``/``sqrt`` with ``math`` on many points.
@@ -41,8 +44,10 @@ and by comparing ``exp``/``log1p``/``sqrt`` with ``math`` on many points.
 from __future__ import annotations
 
 import concurrent.futures as cf
+import ctypes
 import math
 import os
+import threading
 from fractions import Fraction
 
 import numpy as np
@@ -122,53 +127,66 @@ def sqrt_round_f32(v: np.ndarray) -> np.ndarray:
 
 GATE_SEGMENTS = 4
 
+_LIB = None
+_LIB_LOCK = threading.Lock()
 
-def gate_logits(x: np.ndarray, gate_w: np.ndarray, chunk_elems: int = 1 << 19,
-                workers: int | None = None) -> np.ndarray:
-    """z = f32(x) @ f32(W).T in the fixed segment/lane order described in the module docstring.
+
+def _gate_lib() -> ctypes.CDLL:
+    """The oracle's C gate chains (``oracle/gate_fma.c``), built on first use."""
+    global _LIB
+    with _LIB_LOCK:
+        if _LIB is None:
+            from . import build_c
+            if not build_c.LIB.exists():
+                build_c.build()
+            lib = ctypes.CDLL(str(build_c.LIB))
+            fn = lib.dsk_oracle_gate_fma
+            fn.restype = None
+            fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                           ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32]
+            _LIB = lib
+    return _LIB
+
+
+def _by_step(a: np.ndarray, steps: int) -> np.ndarray:
+    """[N, H] float32 -> [N, steps, 4, 64]: element (m, v, l) is position 256 m + 4 l + v (zero past H)."""
+    n, h = a.shape
+    hp = steps * GATE_STEP
+    if hp != h:
+        a = np.pad(a, ((0, 0), (0, hp - h)))
+    return np.ascontiguousarray(a.reshape(n, steps, GATE_LANES, GATE_VEC).transpose(0, 1, 3, 2))
+
+
+def gate_logits(x: np.ndarray, gate_w: np.ndarray, workers: int | None = None,
+                force_libm: bool = False) -> np.ndarray:
+    """z = f32(x) @ f32(W).T in the fixed segment/lane order of the module docstring.
 
     x: [T, H] (any float dtype, converted exactly to float32), gate_w: [E, H].
     Token chunks are independent, so they are spread over ``workers`` threads
-    (numpy releases the GIL in its elementwise loops); the arithmetic of every
-    logit is the same whatever the chunking.
+    (the C chains run without the GIL); every logit's arithmetic is the same
+    whatever the chunking.  ``force_libm`` evaluates every fma through the C
+    library's ``fmaf`` instead of the CPU's FMA instruction (same results).
     """
     x = np.asarray(x, dtype=np.float32)
     w = np.asarray(gate_w, dtype=np.float32)
     t, h = x.shape
     e = w.shape[0]
     steps = -(-h // GATE_STEP)
-    hp = steps * GATE_STEP
-    if hp != h:
-        x = np.pad(x, ((0, 0), (0, hp - h)))
-        w = np.pad(w, ((0, 0), (0, hp - h)))
-    xr = x.reshape(t, steps, GATE_LANES, GATE_VEC)
-    wr = w.reshape(e, steps, GATE_LANES, GATE_VEC)
-    seg = -(-steps // GATE_SEGMENTS)
+    xt, wt = _by_step(x, steps), _by_step(w, steps)
     out = np.empty((t, e), dtype=np.float32)
-    tc = max(1, chunk_elems // max(1, e * GATE_LANES))
-    lanes = np.arange(GATE_LANES)
+    lib = _gate_lib()
+    n = max(1, min(t, workers or min(16, os.cpu_count() or 1)))
+    bounds = [(t * i) // n for i in range(n + 1)]
 
-    def chunk(t0: int) -> None:
-        xs = xr[t0:t0 + tc]
-        z = None
-        for sw in range(GATE_SEGMENTS):
-            p = np.zeros((xs.shape[0], e, GATE_LANES), dtype=np.float32)
-            for m in range(sw * seg, min((sw + 1) * seg, steps)):
-                for v in range(GATE_VEC):
-                    p = p + xs[:, None, m, :, v] * wr[None, :, m, :, v]
-            for s in (32, 16, 8, 4, 2, 1):
-                p = p + p[:, :, lanes ^ s]
-            z = p[:, :, 0] if z is None else (z + p[:, :, 0]).astype(np.float32)
-        out[t0:t0 + tc] = z
+    def chunk(i: int) -> None:
+        lib.dsk_oracle_gate_fma(xt.ctypes.data, wt.ctypes.data, e, steps, bounds[i], bounds[i + 1],
+                                out.ctypes.data, 1 if force_libm else 0)
 
-    starts = list(range(0, t, tc))
-    n = min(len(starts), workers or min(16, os.cpu_count() or 1))
-    if n <= 1:
-        for t0 in starts:
-            chunk(t0)
+    if n == 1:
+        chunk(0)
     else:
         with cf.ThreadPoolExecutor(max_workers=n) as ex:
-            list(ex.map(chunk, starts))
+            list(ex.map(chunk, range(n)))
     return out
 
 

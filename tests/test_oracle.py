@@ -221,8 +221,28 @@ def test_ln2_split_exact():
     assert abs(float(hi + Fraction(R.LN2_LO)) - math.log(2)) == 0.0
 
 
-def _gate_scalar(x, w):
-    # the fixed order, one scalar at a time (float32 ops through numpy scalars)
+def _round_f32(v):
+    """The float32 nearest to the rational v, ties to even (v finite, in range)."""
+    from fractions import Fraction
+    if v == 0:
+        return np.float32(0.0)
+    f = np.float32(float(v))
+    cands = [f, np.nextafter(f, np.float32(-np.inf)), np.nextafter(f, np.float32(np.inf))]
+    err = [abs(Fraction(float(c)) - v) for c in cands]
+    best = min(err)
+    ties = [c for c, e in zip(cands, err) if e == best]
+    return min(ties, key=lambda c: int(np.float32(c).view(np.uint32)) & 1)
+
+
+def _fma_exact(a, b, c):
+    """fma(a, b, c) in float32: the exact value a*b + c rounded once."""
+    from fractions import Fraction
+    return _round_f32(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+def _gate_scalar(x, w, fused=True):
+    # the fixed order, one scalar at a time: fused steps from exact rationals,
+    # the butterfly and segment sums as float32 adds of numpy scalars
     h = x.shape[0]
     steps = -(-h // 256)
     seg = -(-steps // 4)
@@ -233,8 +253,11 @@ def _gate_scalar(x, w):
             for v in range(4):
                 for lane in range(64):
                     c = 256 * m + 4 * lane + v
-                    prod = np.float32(x[c]) * np.float32(w[c]) if c < h else np.float32(0.0)
-                    p[lane] = np.float32(p[lane] + prod)
+                    if c < h:
+                        if fused:
+                            p[lane] = _fma_exact(x[c], w[c], p[lane])
+                        else:
+                            p[lane] = np.float32(p[lane] + np.float32(np.float32(x[c]) * np.float32(w[c])))
         for s in (32, 16, 8, 4, 2, 1):
             p = [np.float32(p[i] + p[i ^ s]) for i in range(64)]
         z = p[0] if z is None else np.float32(z + p[0])
@@ -250,6 +273,26 @@ def test_gate_logits_vectorised_equals_scalar_order():
         for t in range(2):
             for e in range(3):
                 assert z[t, e] == _gate_scalar(x[t], w[e])
+
+
+def test_gate_logits_fused_not_unfused():
+    """Lane 0 takes x0*w0 = -(1 + 2^-11) and then (1 + 2^-12)^2 = 1 + 2^-11 + 2^-24:
+    fused, the chain keeps 2^-24; with the product rounded first (1 + 2^-11) it is 0."""
+    x = np.zeros((1, 256), dtype=np.float32)
+    w = np.zeros((1, 256), dtype=np.float32)
+    x[0, 0], w[0, 0] = 1.0, -(1.0 + 2.0 ** -11)
+    x[0, 1] = w[0, 1] = 1.0 + 2.0 ** -12
+    assert R.gate_logits(x, w)[0, 0] == np.float32(2.0 ** -24)
+    assert _gate_scalar(x[0], w[0]) == np.float32(2.0 ** -24)
+    assert _gate_scalar(x[0], w[0], fused=False) == 0.0
+
+
+def test_gate_logits_instruction_and_libm_forms_agree():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((5, 1000)) * np.exp(rng.standard_normal((5, 1000)) * 4)).astype(np.float32)
+    w = rng.standard_normal((7, 1000)).astype(np.float32)
+    np.testing.assert_array_equal(R.gate_logits(x, w).view(np.uint32),
+                                  R.gate_logits(x, w, force_libm=True).view(np.uint32))
 
 
 def test_gate_logits_close_to_float64():
