@@ -110,7 +110,9 @@ __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ scores,
 // its pairs if bit s of its lane id is set and adds the partner's (lane ^ s)
 // copy of them, so after strides 32..1 lane l holds the segment sum of pair l
 // -- the sum lane 0 of the full butterfly holds, at a sixth of the additions
-// and exchanges.
+// and exchanges.  The kernel is held to 128 registers, so two blocks share a
+// CU (four waves per SIMD): a step's products of one block run while the
+// other waits at its barrier or for its LDS reads.
 constexpr int kGwThreads = 512;
 constexpr int kGwTok = 32, kGwExp = 16;
 constexpr int kGateWideMinTokens = 128;
@@ -146,7 +148,7 @@ __device__ __forceinline__ void xor_reduce_scatter(float* vals, int lane) {
 }
 
 template <bool kXBF16, bool kWBF16>
-__global__ __launch_bounds__(kGwThreads, 1) void k_gate_wide(GateArgs g) {
+__global__ __launch_bounds__(kGwThreads, 4) void k_gate_wide(GateArgs g) {
 #pragma clang fp contract(off)
   constexpr int kSx = kXBF16 ? 2 : 4, kSw = kWBF16 ? 2 : 4;
   constexpr int kXBytes = kGwTok * 256 * kSx, kWBytes = kGwExp * 256 * kSw;
@@ -162,7 +164,12 @@ __global__ __launch_bounds__(kGwThreads, 1) void k_gate_wide(GateArgs g) {
   const int H = g.H, steps = (H + 255) / 256, seg = (steps + kSegments - 1) / kSegments;
   // staging: thread chunk c = tid + 512 q of the x tile ([32][256] elements,
   // 16-byte chunks), the same for W; addresses recomputed per step
+  // The loads are issued without conditions (a load under a per-lane
+  // condition compiles to a branch whose merge waits for it): a chunk past H
+  // re-reads the row's last in-range chunk and is zeroed by a mask when it
+  // is stored.
   u32x4 xr[kXChunks], wr[kWChunks];
+  uint32_t xkeep[kXChunks], wkeep[kWChunks];
   auto load = [&](int m) {
 #pragma unroll
     for (int q = 0; q < kXChunks; ++q) {
@@ -170,7 +177,8 @@ __global__ __launch_bounds__(kGwThreads, 1) void k_gate_wide(GateArgs g) {
       const int c = tid + kGwThreads * q;
       const int col = 256 * m + (c % per_row) * (16 / kSx);
       const int64_t row = min(t0 + c / per_row, g.T - 1);
-      xr[q] = col < H ? ldg16(static_cast<const char*>(g.x) + (row * H + col) * kSx) : u32x4{0u, 0u, 0u, 0u};
+      xkeep[q] = col < H ? ~0u : 0u;
+      xr[q] = ldg16(static_cast<const char*>(g.x) + (row * H + min(col, H - 16 / kSx)) * kSx);
     }
 #pragma unroll
     for (int q = 0; q < kWChunks; ++q) {
@@ -178,16 +186,18 @@ __global__ __launch_bounds__(kGwThreads, 1) void k_gate_wide(GateArgs g) {
       const int c = tid + kGwThreads * q;
       const int col = 256 * m + (c % per_row) * (16 / kSw);
       const int64_t row = min(e0 + c / per_row, g.E - 1);
-      wr[q] = col < H ? ldg16(static_cast<const char*>(g.gw) + (row * H + col) * kSw) : u32x4{0u, 0u, 0u, 0u};
+      wkeep[q] = col < H ? ~0u : 0u;
+      wr[q] = ldg16(static_cast<const char*>(g.gw) + (row * H + min(col, H - 16 / kSw)) * kSw);
     }
   };
   auto store = [&](int buf) {
     char* b = gw_lds + buf * kBuf;
 #pragma unroll
-    for (int q = 0; q < kXChunks; ++q) *reinterpret_cast<u32x4*>(b + 16 * (tid + kGwThreads * q)) = xr[q];
+    for (int q = 0; q < kXChunks; ++q)
+      *reinterpret_cast<u32x4*>(b + 16 * (tid + kGwThreads * q)) = xr[q] & xkeep[q];
 #pragma unroll
     for (int q = 0; q < kWChunks; ++q)
-      *reinterpret_cast<u32x4*>(b + kXBytes + 16 * (tid + kGwThreads * q)) = wr[q];
+      *reinterpret_cast<u32x4*>(b + kXBytes + 16 * (tid + kGwThreads * q)) = wr[q] & wkeep[q];
   };
   float p[64];
   float z = 0.0f;
@@ -198,7 +208,10 @@ __global__ __launch_bounds__(kGwThreads, 1) void k_gate_wide(GateArgs g) {
   __syncthreads();
   int done_segments = 0;
   for (int m = 0; m < steps; ++m) {
-    if (m + 1 < steps) load(m + 1);
+    // step m + 1 (the last step reloads itself: the loop body stays one
+    // block, so the loads, the products and the stores keep their order)
+    load(min(m + 1, steps - 1));
+    asm volatile("" ::: "memory");   // the loads go out before this step's LDS reads
     const char* b = gw_lds + (m & 1) * kBuf;
     f32x4 xv[8];
 #pragma unroll
@@ -213,7 +226,15 @@ __global__ __launch_bounds__(kGwThreads, 1) void k_gate_wide(GateArgs g) {
           p[8 * i + j] = __builtin_fmaf(xv[i][v], wv[v], p[8 * i + j]);
         }
     }
-    if (m + 1 < steps) store((m + 1) & 1);
+    // the staged chunks are stored after the products, so their loads have
+    // the whole step to arrive (the compiler would otherwise place the
+    // stores, and the wait for the loads, above the products: the empty asm
+    // statements take every partial, and the stores cannot pass the memory
+    // clobber); after the last step they go to the buffer nobody reads any more
+#pragma unroll
+    for (int i = 0; i < 64; ++i) asm volatile("" : "+v"(p[i]));
+    asm volatile("" ::: "memory");
+    store((m + 1) & 1);
     if (m + 1 == steps || (m + 1) % seg == 0) {
       xor_reduce_scatter<64, 32>(p, lane);
       z = done_segments == 0 ? p[0] : z + p[0];

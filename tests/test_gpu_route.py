@@ -88,11 +88,14 @@ def test_route_zipf_bias_skew():
 
 
 @pytest.mark.parametrize("T,H,E,k,score_func", [(128, 4096, 256, 8, "sigmoid"), (300, 1056, 100, 5, "sqrtsoftplus"),
-                                                (130, 64, 24, 3, "sigmoid"), (257, 2048, 384, 6, "sqrtsoftplus")])
+                                                (130, 64, 24, 3, "sigmoid"), (257, 2048, 384, 6, "sqrtsoftplus"),
+                                                (129, 256, 40, 4, "sigmoid"), (200, 512, 64, 6, "sigmoid")])
 @pytest.mark.parametrize("xdt,gdt", [("bf16", "f32"), ("f32", "f32"), ("bf16", "bf16"), ("f32", "bf16")])
 def test_route_wide_gate_bit_exact(T, H, E, k, score_func, xdt, gdt):
     """Batches of >= 128 tokens take the wide gate kernel (32x16 tiles staged through
-    LDS, segment sums by reduce-scatter); H = 64 and 1056 leave segments empty."""
+    LDS, segment sums by reduce-scatter); H = 64 and 1056 leave segments empty and
+    stage through registers, the multiples of 256 by LDS DMA (H = 256 and 512: one
+    and two steps, shorter than the DMA pipeline)."""
     g = torch.Generator().manual_seed(T + H + E)
     x = torch.randn((T, H), generator=g)
     x = x.to(torch.bfloat16) if xdt == "bf16" else x
