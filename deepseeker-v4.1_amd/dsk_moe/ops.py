@@ -101,10 +101,17 @@ def workspace(desc: _lib.Desc, device: torch.device) -> torch.Tensor:
     stream = torch.cuda.current_stream(device)
     key = (device.type, device.index, stream.cuda_stream)
     ws = _WS_CACHE.get(key)
+    capturing = torch.cuda.is_current_stream_capturing()
     if ws is None or ws.numel() < need:
+        if capturing:
+            # its zero-fill would only be recorded into the graph, and eager calls
+            # that reuse the cached workspace would find its counters undefined
+            raise RuntimeError("dsk_moe: no workspace of this size exists for the capturing stream; "
+                               "run the call once eagerly on that stream first, or pass a workspace "
+                               "made with ops.new_workspace")
         ws = new_workspace(need, device)
         _WS_CACHE[key] = ws
-    if torch.cuda.is_current_stream_capturing():
+    if capturing:
         _WS_CAPTURED[ws.data_ptr()] = ws
     return ws
 

@@ -286,3 +286,31 @@ def test_pinned_gather_contributions(cfg0, T):
     np.testing.assert_array_equal(seen["idx"], np.flip(r["idx"], axis=1))
     assert_layer_close(out.float(), r["y_ref"])
     assert float((out.float() - plain.float()).abs().max()) > 1e-3
+
+
+def test_capture_without_warmup_is_refused():
+    """A workspace cannot be created while its stream is captured (its zero-fill
+    would only be recorded into the graph): the call raises before any launch,
+    and after an eager call on that stream the capture works."""
+    spec = synth.tiny_spec()
+    d = synth.make_layer(spec, 3, 2)
+    layer = dsk_moe.MoELayer(d["gate_w"].to(DEV), d["gate_b"].to(DEV), to_bank(d["bank"]),
+                             to_shared(d["shared"]), spec.k)
+    x = d["x"].to(DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with pytest.raises(RuntimeError, match="no workspace"):
+            with torch.cuda.graph(g, stream=side):
+                layer(x)
+        want = layer(x).clone()              # eager call: the stream's workspace now exists
+        side.synchronize()
+        g2 = torch.cuda.CUDAGraph()
+        out = torch.empty_like(x)
+        with torch.cuda.graph(g2, stream=side):
+            layer(x, out=out)
+    for _ in range(2):
+        g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
