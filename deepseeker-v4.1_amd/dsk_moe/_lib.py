@@ -1,17 +1,20 @@
 """ctypes binding of libdsk_moe.so (the C ABI declared in include/dsk_moe.h).
 
-The library is loaded from this package directory.  Loading never falls
-back to anything else: if the shared library is missing, or no HIP device is
-visible when a compute entry point is called, the call raises.
+The library is loaded from this package directory (``DSK_MOE_LIBRARY`` may
+name another build of it, e.g. the host-sanitizer build
+``libdsk_moe_san.so``).  Loading never falls back to anything else: if the
+shared library is missing, or no HIP device is visible when a compute entry
+point is called, the call raises.
 """
 
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libdsk_moe.so"
+LIB_PATH = Path(os.environ.get("DSK_MOE_LIBRARY") or Path(__file__).resolve().parent / "libdsk_moe.so")
 
 ABI_VERSION = 1
 
