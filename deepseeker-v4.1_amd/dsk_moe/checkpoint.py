@@ -203,13 +203,25 @@ class Checkpoint:
         return len(ids)
 
     # -------------------------------------------------------------- device objects
-    def expert_format(self, layer: int) -> str:
-        """``"fp4"`` or ``"q3"``: the routed-expert format of ``layer`` (expert 0's w1)."""
-        base = f"layers.{layer}.ffn.experts.0.w1"
+    def _format_of(self, layer: int, e: int) -> str:
+        base = f"layers.{layer}.ffn.experts.{e}.w1"
         w = self.entry(base + ".weight")
         if w["dtype"] == "U32_Q3_AFFINE" or (base + ".bias") in self.by_name:
             return "q3"
         return "fp4"
+
+    def expert_format(self, layer: int) -> str:
+        """``"fp4"`` or ``"q3"``: the routed-expert format of ``layer``.  Every expert
+        is checked: a resident bank (and the kernels reading it) hold one format
+        per layer, so a partly requantised layer is refused with its expert lists."""
+        fmts = [self._format_of(layer, e) for e in range(self.n_experts(layer))]
+        if len(set(fmts)) > 1:
+            q3 = [e for e, f in enumerate(fmts) if f == "q3"]
+            fp4 = [e for e, f in enumerate(fmts) if f == "fp4"]
+            raise ValueError(f"layer {layer}: mixed routed-expert formats (q3: experts {q3[:8]}"
+                             f"{'...' if len(q3) > 8 else ''}; FP4: experts {fp4[:8]}{'...' if len(fp4) > 8 else ''}); "
+                             f"a resident layer holds one format -- requantise all of its experts")
+        return fmts[0]
 
     def _load_q3_bank(self, layer: int, dev: torch.device, E: int) -> ResidentBank:
         roles = {}

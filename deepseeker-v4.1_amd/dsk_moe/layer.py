@@ -29,6 +29,10 @@ largest summed gate score are kept, dropped slots become -1 (the dispatch
 skips them) and each row keeps its weight sum; ``union_strict`` drops the
 one-expert rescue of rows that would lose everything; ``route_stats``
 (``{"coverage", "calls"}``) accumulates the retained weight share per row.
+The cap runs in one block that holds the batch's (token, slot) pairs:
+T * top_k * 4 + E * 9 bytes must fit 160 KB of LDS (at 256 experts and
+top-8, up to 5048 tokens); a larger batch raises ``DskError``
+(DSK_EUNSUPPORTED) before anything runs.
 
 ``pinned_gather_fn(layer_id, x, idx, w)`` (``:313-321``), called after routing
 with host arrays in the trace hook's order, returns ``{expert: (rows,

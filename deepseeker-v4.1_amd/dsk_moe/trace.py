@@ -326,3 +326,64 @@ class TraceSink:
                  seed: int | None = None) -> Trace:
         return Trace(geometry.header(repo_id=repo_id, revision=revision, source=source, seed=seed),
                      list(self.records))
+
+
+# ------------------------------------------------------------------ the reference's function names
+# Tooling written against the reference's module (``src/deepseeker/trace.py``)
+# calls these names; each is a thin call into the classes above and returns
+# what the reference's function of that name returns.
+
+def arch_config(manifest: dict) -> dict:
+    """``{n_layers, n_routed_experts, top_k}`` of a manifest's architecture block."""
+    g = Geometry.of_manifest(manifest)
+    return {"n_layers": g.n_layers, "n_routed_experts": g.n_routed_experts, "top_k": g.top_k}
+
+
+def make_header(repo_id: str, revision: str, source: str, cfg: dict, seed: int | None = None) -> dict:
+    """The header line for the geometry ``cfg`` (ValueError on a bad geometry)."""
+    g = Geometry(cfg.get("n_layers"), cfg.get("n_routed_experts"), cfg.get("top_k"))
+    return g.header(repo_id=repo_id, revision=revision, source=source, seed=seed)
+
+
+def validate_record(record: dict, header: dict) -> list[str]:
+    """The problems of one record against a header's geometry (empty: valid)."""
+    return check(record, Geometry.of_header(header))
+
+
+def write_trace(path, header: dict, records: list[dict]) -> int:
+    """Header and records as JSONL; returns the number of records."""
+    return Trace(header, list(records)).save(path)
+
+
+def read_trace(path) -> tuple[dict, list[dict]]:
+    """``(header, records)`` of a checked trace file (ValueError at the first broken line)."""
+    t = Trace.load(path)
+    return t.header, t.records
+
+
+def expert_records(records: list[dict]) -> list[dict]:
+    """Routing records only (subsystem events left out)."""
+    return [r for r in records if _is_routing(r)]
+
+
+def layer_histogram(records: list[dict], n_layers: int) -> dict[int, dict[int, int]]:
+    """Per layer, ``{expert: times selected}`` over the routing records."""
+    out: dict[int, dict[int, int]] = {layer: {} for layer in range(n_layers)}
+    for r in expert_records(records):
+        bucket = out[r["layer"]]
+        for e in r["experts"]:
+            bucket[e] = bucket.get(e, 0) + 1
+    return out
+
+
+def trace_stats(header: dict, records: list[dict]) -> dict:
+    """The reference's summary keys: ``records``, ``requests``,
+    ``unique_experts_per_layer`` ({layer: distinct experts}), ``mean_unique``
+    (their mean over the header's layers) and ``adjacent_same_set_ratio``."""
+    rows = expert_records(records)
+    s = Trace(header, rows).summary()
+    unique = {layer: int(n) for layer, n in enumerate(s["distinct_experts_per_layer"])}
+    n_layers = header["n_layers"]
+    return {"records": s["records"], "requests": s["requests"], "unique_experts_per_layer": unique,
+            "mean_unique": sum(unique.values()) / n_layers if n_layers else 0.0,
+            "adjacent_same_set_ratio": s["adjacent_same_set_ratio"]}

@@ -19,16 +19,17 @@ from oracle import formats as F
 from oracle import layer as L
 
 
-def make_checkpoint(root: Path, spec: L.LayerSpec, seed: int) -> dict:
+def make_checkpoint(root: Path, spec: L.LayerSpec, seed: int, fp4_experts: frozenset = frozenset()) -> dict:
     """``spec.quant`` "fp4": routed experts as I8 codes + F8_E8M0 scales; "q3": as the
     reference's q3 variant stores them, U32_Q3_AFFINE words [N, 3K/32] of row-major
-    3-byte packs + F16 scale / bias [N, K/64]."""
+    3-byte packs + F16 scale / bias [N, K/64].  ``fp4_experts``: experts kept in FP4
+    in a q3 layer (a partly requantised checkpoint)."""
     rng = np.random.default_rng(seed)
     H, E, I, Is = spec.H, spec.E, spec.I, spec.I_shared
     experts, dense = {}, {}
-    q3 = spec.quant == L.QUANT_Q3
     roles = {"w1": [], "w3": [], "w2": []}
     for e in range(E):
+        q3 = spec.quant == L.QUANT_Q3 and e not in fp4_experts
         for role, (n, k) in (("w1", (I, H)), ("w2", (H, I)), ("w3", (I, H))):
             w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
             base = f"layers.0.ffn.experts.{e}.{role}"
@@ -44,7 +45,8 @@ def make_checkpoint(root: Path, spec: L.LayerSpec, seed: int) -> dict:
                 experts[base + ".weight"] = ("I8", packed.shape, packed.tobytes())
                 experts[base + ".scale"] = ("F8_E8M0", scales.shape, scales.tobytes())
                 roles[role].append((packed, scales))
-    bank = L.ExpertBank(spec.quant, {r: tuple(np.stack(c) for c in zip(*parts)) for r, parts in roles.items()})
+    bank = None if fp4_experts else L.ExpertBank(
+        spec.quant, {r: tuple(np.stack(c) for c in zip(*parts)) for r, parts in roles.items()})
     shared = []
     for role, (n, k) in (("w1", (Is, H)), ("w2", (H, Is)), ("w3", (Is, H))):
         codes = rng.integers(0, 256, size=(n, k), dtype=np.uint8)

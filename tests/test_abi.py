@@ -118,3 +118,15 @@ def test_ops_reject_cpu_tensors():
     x = torch.zeros(2, 64, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="HIP device"):
         ops.route(x, torch.zeros(8, 64), torch.zeros(8), 2)
+
+
+def test_cap_union_size_limit_is_a_clean_rejection():
+    """The union cap keeps a batch's (token, slot) pairs and per-expert sums in one
+    block's LDS (T*top_k*4 + E*9 bytes of 160 KB): at 256 experts, top-8, up to
+    5048 tokens; beyond that DSK_EUNSUPPORTED before any launch."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    assert lib.dsk_cap_union(5049, 256, 8, 64, 0, p, p, p, None) == -3
+    assert b"beyond the one-block cap" in lib.dsk_last_error()
+    with pytest.raises(_lib.DskError, match="DSK_EUNSUPPORTED"):
+        _lib.call("dsk_cap_union", 8192, 256, 8, 64, 0, p, p, p, None)

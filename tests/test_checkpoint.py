@@ -124,3 +124,16 @@ def test_synthetic_checkpoint_bytes(tmp_path):
     packed, scales = d["bank"].roles["w2"]
     assert ck.read("layers.0.ffn.experts.2.w2.weight") == packed[2].tobytes()
     assert ck.read("layers.0.ffn.experts.2.w2.scale") == scales[2].tobytes()
+
+
+def test_mixed_format_layer_is_refused(tmp_path):
+    """A q3 layer with two experts left in FP4 (the reference's requantisation
+    script takes an expert subset): the format check names both lists."""
+    spec = L.LayerSpec(H=256, E=6, k=2, I=128, I_shared=128, quant=L.QUANT_Q3)
+    d = make_checkpoint(tmp_path, spec, 4, fp4_experts=frozenset({1, 4}))
+    ck = Checkpoint(tmp_path, d["manifest"])
+    with pytest.raises(ValueError, match=r"mixed routed-expert formats \(q3: experts \[0, 2, 3, 5\]; FP4: experts \[1, 4\]\)"):
+        ck.expert_format(0)
+    whole = tmp_path / "q3"
+    d = make_checkpoint(whole, spec, 4)
+    assert Checkpoint(whole, d["manifest"]).expert_format(0) == "q3"

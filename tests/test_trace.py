@@ -110,3 +110,30 @@ def test_reference_recorded_trace():
 def test_geometry_of_real_manifest():
     m = json.loads((GOLDEN / "manifest_layer0_subset.json").read_text())
     assert Geometry.of_manifest(m) == Geometry(40, 384, 6)
+
+
+def test_reference_function_names(tmp_path):
+    """The reference module's functions (src/deepseeker/trace.py:35-208) under
+    their names, with its return shapes: hand-computed on a small trace."""
+    from dsk_moe import trace as T
+    m = json.loads((GOLDEN / "manifest_layer0_subset.json").read_text())
+    assert T.arch_config(m) == {"n_layers": 40, "n_routed_experts": 384, "top_k": 6}
+    h = T.make_header("r", "v", "synthetic", {"n_layers": 2, "n_routed_experts": 16, "top_k": 2}, seed=3)
+    assert h["schema"] == "deepseeker.trace/v1" and h["seed"] == 3 and h["kind"] == "header"
+    with pytest.raises(ValueError):
+        T.make_header("r", "v", "s", {"n_layers": 0, "n_routed_experts": 16, "top_k": 2})
+    recs = [{"request_id": "a", "token_pos": p, "layer": 0, "experts": e}
+            for p, e in enumerate([[1, 2], [2, 1], [3, 4]])]
+    recs += [{"request_id": "b", "token_pos": 0, "layer": 1, "experts": [5, 6]},
+             {"kind": "event", "request_id": "b", "token_pos": 0, "layer": 1, "extra": {"kind": "kv"}}]
+    assert T.validate_record(recs[0], h) == []
+    assert T.validate_record({"request_id": "a", "token_pos": 0, "layer": 2, "experts": [1, 2]}, h)
+    path = tmp_path / "t.jsonl"
+    assert T.write_trace(path, h, recs) == 5
+    h2, back = T.read_trace(path)
+    assert h2 == h and back == recs
+    assert len(T.expert_records(back)) == 4
+    assert T.layer_histogram(back, 2) == {0: {1: 2, 2: 2, 3: 1, 4: 1}, 1: {5: 1, 6: 1}}
+    st = T.trace_stats(h, back)
+    assert st == {"records": 4, "requests": 2, "unique_experts_per_layer": {0: 4, 1: 2},
+                  "mean_unique": 3.0, "adjacent_same_set_ratio": 0.5}
