@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include "dsk_internal.h"
+#include "resnorm.h"
 
 namespace dsk {
 
@@ -301,11 +302,18 @@ int dsk::check_forward(const dsk_moe_desc* d, const void* x, const void* gate_w,
   return DSK_OK;
 }
 
+bool dsk::resnorm_fusable(const dsk_moe_desc& d) {
+  // the first kernel of the decode pipeline is k_gate_shared (MX) or the
+  // one-token-tile gate k_gate<1, 1>; both hold the rows in LDS
+  return decode_pipeline(d) && (mx_decode(d) || d.tokens < 16) && d.x_dtype == DSK_DTYPE_BF16 &&
+         d.hidden % 4 == 0 && d.hidden <= kResNormMaxHidden && d.tokens <= kResNormRows;
+}
+
 int dsk::forward_layer(const dsk_moe_desc* d, const void* x, const void* gate_w,
                        const float* gate_b, const dsk_expert_ptrs* table, const void* ws1,
                        const void* ws3, const void* ws2, const void* shared_out, void* out,
                        int32_t* idx, float* weights, void* workspace, size_t workspace_bytes,
-                       void* stream, void* const* events, int repeat) {
+                       void* stream, void* const* events, int repeat, const ResNorm* rn) {
   int rc = check_forward(d, x, gate_w, gate_b, table, ws1, ws3, ws2, shared_out, out, workspace, false, events,
                          repeat);
   if (rc) return rc;
@@ -346,6 +354,17 @@ int dsk::forward_layer(const dsk_moe_desc* d, const void* x, const void* gate_w,
   const bool decode = decode_pipeline(*d);
   StageTiming timing(ev);
   stage_open(kStageGate);
+  if (rn && !resnorm_fusable(*d)) {
+    // the residual update and RMSNorm as their own kernel, then the layer on its rows
+    for (int r = 0; r < repeat && !rc; ++r)
+      rc = hip_check(launch_rmsnorm(rn->h, rn->d, rn->gamma, d->tokens, d->hidden, rn->eps, d->x_dtype,
+                                    rn->h_out, rn->x_out, s),
+                     "residual rmsnorm launch");
+    if (rc) return rc;
+    rn = nullptr;
+  }
+  ra.rn = rn;
+  a.rn = rn;
   if (decode && mx_decode(*d)) {
     // gate scores beside the shared expert's gate/up; the top-k and the slot map beside
     // the shared expert's down; then the routed experts, which add the shared output
@@ -389,6 +408,46 @@ int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, co
                     float* weights, void* workspace, size_t workspace_bytes, void* stream) {
   return forward_layer(d, x, gate_w, gate_b, table, ws1, ws3, ws2, shared_out, out, idx, weights,
                        workspace, workspace_bytes, stream, nullptr, 1);
+}
+
+int dsk_moe_forward_residual(const dsk_moe_desc* d, const dsk_residual* r, const void* gate_w,
+                             const float* gate_b, const dsk_expert_ptrs* table, const void* ws1,
+                             const void* ws3, const void* ws2, void* out, int32_t* idx, float* weights,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  if (!d || !r) return fail(DSK_EINVAL, "dsk_moe_forward_residual: NULL desc or residual");
+  if (!r->h || !r->d || !r->h_out || !r->x_out)
+    return fail(DSK_EINVAL, "dsk_moe_forward_residual: h, d, h_out and x_out are required");
+  if (!(r->eps >= 0.0f)) return fail(DSK_EINVAL, "dsk_moe_forward_residual: eps must be >= 0");
+  if (!aligned(r->h, 16) || !aligned(r->d, 16) || !aligned(r->h_out, 16) || !aligned(r->x_out, 16) ||
+      (r->gamma && !aligned(r->gamma, 16)))
+    return fail(DSK_EALIGN, "dsk_moe_forward_residual: stream pointers must be 16-byte aligned");
+  int rc = check_forward(d, r->x_out, gate_w, gate_b, table, ws1, ws3, ws2, nullptr, out, workspace, false,
+                         nullptr, 1);
+  if (rc) return rc;
+  const size_t bytes = static_cast<size_t>(d->tokens) * d->hidden * (d->x_dtype == DSK_DTYPE_BF16 ? 2 : 4);
+  auto overlap = [bytes](const void* a, const void* b) {
+    const char* x = static_cast<const char*>(a);
+    const char* y = static_cast<const char*>(b);
+    return x < y + bytes && y < x + bytes;
+  };
+  if (overlap(r->x_out, r->h) || overlap(r->x_out, r->d) || overlap(r->x_out, r->h_out) ||
+      overlap(r->x_out, out) || overlap(r->h_out, r->d) ||
+      (r->h_out != r->h && overlap(r->h_out, r->h)))
+    return fail(DSK_EINVAL, "dsk_moe_forward_residual: x_out and h_out must not overlap the other buffers "
+                "(h_out may be h itself)");
+  ResNorm rn{static_cast<const uint16_t*>(r->h), static_cast<const uint16_t*>(r->d), r->gamma, r->eps,
+             static_cast<uint16_t*>(r->h_out), static_cast<uint16_t*>(r->x_out)};
+  if (r->h_out == r->h) {
+    // in place: every block of a fused first kernel reads h, so the update runs as its own kernel
+    rc = hip_check(launch_rmsnorm(r->h, r->d, r->gamma, d->tokens, d->hidden, r->eps, d->x_dtype, r->h_out,
+                                  r->x_out, static_cast<hipStream_t>(stream)),
+                   "residual rmsnorm launch");
+    if (rc) return rc;
+    return forward_layer(d, r->x_out, gate_w, gate_b, table, ws1, ws3, ws2, nullptr, out, idx, weights,
+                         workspace, workspace_bytes, stream, nullptr, 1);
+  }
+  return forward_layer(d, r->x_out, gate_w, gate_b, table, ws1, ws3, ws2, nullptr, out, idx, weights,
+                       workspace, workspace_bytes, stream, nullptr, 1, &rn);
 }
 
 int dsk_moe_forward_timed(const dsk_moe_desc* d, const void* x, const void* gate_w,

@@ -14,6 +14,7 @@
 // src/deepseeker/mlx_runner.py:765-783).
 #include "block_route.h"
 #include "mx.h"
+#include "resnorm.h"
 #include "tile.h"
 
 namespace dsk {
@@ -61,6 +62,7 @@ struct DecodeArgs {
   const void* shared_out;              // precomputed shared output [T][H] (x dtype) or null
   void* out;                           // [T][H] x dtype
   int up_tiles;                        // I / 16
+  ResNorm rn; int norm;                // norm: k_gate_shared computes x from the residual stream
 };
 
 // One x chunk (8 values at column `col` of token row t) into the LDS planes.
@@ -208,11 +210,14 @@ __device__ __forceinline__ void put_staged_x(const DecodeArgs& p, uint16_t* xh, 
 // K blocks are then all in flight in the registers of two, and twice the
 // tiles spread the shared stream over twice the CUs.  Called after the
 // block's x chunks have been loaded into registers; writes them to LDS once
-// its own weight loads are in flight.
-template <bool kF32, int NW, int ROWS>
+// its own weight loads are in flight.  kNorm: called after the loads of the
+// residual rows instead (resnorm_issue into rin), and normalises them
+// into the planes once its weight loads are in flight.
+template <bool kF32, int NW, int ROWS, bool kNorm = false>
 __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint16_t* xh, uint16_t* xl, int xs,
                                                bool xreg, const u32x4 (&xv)[kUpXRegChunks][2], uint16_t* lds,
-                                               int tid, int lane, int wave, int r16, int g4) {
+                                               int tid, int lane, int wave, int r16, int g4,
+                                               ResNormIn<NW * 64>* rin = nullptr, float* rn_wsum = nullptr) {
   const int T = p.T, K = p.H;
   const uint32_t row = static_cast<uint32_t>(rt * ROWS + (r16 & (ROWS - 1)));
   const int nblk = (K + 127) / 128;
@@ -232,8 +237,13 @@ __device__ __forceinline__ void shared_up_tile(const DecodeArgs& p, int rt, uint
   };
   ld(a1, a3, k0);
   ld(b1, b3, k0 + kStep);
-  if (xreg) put_staged_x<kF32, NW * 64>(p, xh, xl, xs, tid, xv);
-  __syncthreads();
+  if constexpr (kNorm) {
+    // the rows (their loads issued before these) normalised into the planes; ends on a barrier
+    resnorm_rows<NW * 64>(p.rn, T, K, xh, xs, rt == 0, rn_wsum, *rin);
+  } else {
+    if (xreg) put_staged_x<kF32, NW * 64>(p, xh, xl, xs, tid, xv);
+    __syncthreads();
+  }
   const uint16_t* bh = xh + (tv ? tok : 0) * xs;
   const uint16_t* bl = xl + (tv ? tok : 0) * xs;
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
@@ -298,16 +308,24 @@ constexpr size_t kRsRedBytes = kRsW * 2 * 64 * 4 * 4;
 constexpr size_t kRsTabOffset = (kBlockRouteLds + 15) / 16 * 16;
 static_assert(kRsTabOffset < kRsRedBytes, "routing block state must fit the route/shared LDS");
 constexpr int kRsTileDelay = 15;   // x 64 clocks (~0.4 us)
+// k_gate_shared's gate blocks: the normalised rows after the two tiles' segment sums
+constexpr size_t kGsNormOffset = 64;
 
 __host__ __device__ inline int shared_up_tiles(int T, int Is) { return Is / (T <= 8 ? 8 : 16); }
 
 // Blocks [0, shared_up_tiles): one shared gate/up tile each; the rest: two
 // gate tiles each (waves 0-3 and 4-7: one token x one expert of the score
 // grid, tile = token * E + expert, as the router's own gate kernel).
-template <bool kF32, bool kWBF16>
+// kNorm: with the residual stream given, every block normalises the rows
+// itself (into its activation planes, or after the gate tiles' segment sums)
+// while its first weights load, and block 0 also writes the new stream and
+// the rows for the later kernels (resnorm.h).
+template <bool kF32, bool kWBF16, bool kNorm = false>
 __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gate_shared(
     DecodeArgs p) {
+  static_assert(!(kNorm && kF32), "the residual stream is bf16");
   extern __shared__ __align__(16) uint16_t lds_up[];
+  __shared__ float rn_wsum[kResNormWsum];
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_sh = shared_up_tiles(p.T, p.Is);
   const int b = static_cast<int>(blockIdx.x);
@@ -317,6 +335,15 @@ __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
     uint16_t* xh = lds_up;
     uint16_t* xl = lds_up + p.T * xs;
     u32x4 xv[kUpXRegChunks][2];
+    if constexpr (kNorm) {
+      ResNormIn<kRsW * 64> in;
+      resnorm_issue<kRsW * 64>(p.rn, p.T, p.H, in);
+      asm volatile("" ::: "memory");   // the rows' loads first: waiting for them leaves the weights in flight
+      // T <= kResNormRows: 8-row tiles
+      shared_up_tile<kF32, kRsW, 8, true>(p, b, xh, xl, xs, false, xv, lds_up, tid, lane, wave, r16, g4, &in,
+                                          rn_wsum);
+      return;
+    }
     const bool xreg = load_x<kF32, kRsW * 64>(p, xh, xl, xs, tid, xv);
     if (p.T <= 8) shared_up_tile<kF32, kRsW, 8>(p, b, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave, r16, g4);
     else shared_up_tile<kF32, kRsW, 16>(p, b, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave, r16, g4);
@@ -326,8 +353,20 @@ __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
   const bool active = tile < p.T * p.E;
   const int t = active ? tile / p.E : 0, e = active ? tile - t * p.E : 0;
   float* segsum = reinterpret_cast<float*>(lds_up) + (wave >> 2) * kSegments;
-  gate_tile<1, 1, !kF32, kWBF16>(p.x, p.gate_w, p.T, p.H, p.E, p.score_func, p.scores, t, e, wave & 3, lane,
-                                 tid & 255, segsum, active);
+  if constexpr (kNorm) {
+    uint16_t* y = lds_up + kGsNormOffset / 2;
+    ResNormIn<kRsW * 64> in;
+    resnorm_issue<kRsW * 64>(p.rn, p.T, p.H, in);
+    asm volatile("" ::: "memory");
+    GateWFirst<1, 1, kWBF16> pre;
+    gate_w_issue<1, 1, kWBF16>(p.gate_w, p.H, p.E, e, wave & 3, lane, active, pre);
+    resnorm_rows<kRsW * 64>(p.rn, p.T, p.H, y, p.H, b == 0, rn_wsum, in);
+    gate_tile<1, 1, true, kWBF16, true>(y, p.gate_w, p.T, p.H, p.E, p.score_func, p.scores, t, e, wave & 3,
+                                        lane, tid & 255, segsum, active, &pre);
+  } else {
+    gate_tile<1, 1, !kF32, kWBF16>(p.x, p.gate_w, p.T, p.H, p.E, p.score_func, p.scores, t, e, wave & 3, lane,
+                                   tid & 255, segsum, active);
+  }
 }
 
 // Shared down tile rb of k_route_sdown: output rows 16 rb .. 16 rb + 15 of
@@ -1781,6 +1820,10 @@ DecodeArgs decode_args(const dsk_moe_desc& d, const Workspace& L, const ExpertsA
   p.route = a.route;
   p.gate_w = a.gate_w; p.score_func = d.score_func;
   p.shared_x = a.ws + L.shared_x;
+  if (a.rn) {
+    p.rn = *a.rn;
+    p.norm = 1;
+  }
   return p;
 }
 
@@ -1811,10 +1854,15 @@ hipError_t launch_gate_shared(const dsk_moe_desc& d, const Workspace& L, const E
   const DecodeArgs p = decode_args(d, L, a);
   const int gate_blocks = (p.T * p.E + 1) / 2;
   const unsigned blocks = static_cast<unsigned>(shared_up_tiles(p.T, p.Is) + gate_blocks);
-  const size_t lds = rs_lds_bytes(p);
+  size_t lds = rs_lds_bytes(p);
+  const size_t norm_lds = kGsNormOffset + static_cast<size_t>(p.T) * p.H * 2;
+  if (p.norm && norm_lds > lds) lds = norm_lds;
   const bool wb = d.gate_dtype == DSK_DTYPE_BF16;
+  if (p.norm && p.x_f32) return hipErrorInvalidValue;   // the residual stream is bf16 (resnorm_fusable)
   for (int r = 0; r < repeat; ++r) {
-    if (p.x_f32 && wb) launch_kernel(k_gate_shared<true, true>, blocks, kRsW * 64, lds, s, p);
+    if (p.norm && wb) launch_kernel(k_gate_shared<false, true, true>, blocks, kRsW * 64, lds, s, p);
+    else if (p.norm) launch_kernel(k_gate_shared<false, false, true>, blocks, kRsW * 64, lds, s, p);
+    else if (p.x_f32 && wb) launch_kernel(k_gate_shared<true, true>, blocks, kRsW * 64, lds, s, p);
     else if (p.x_f32) launch_kernel(k_gate_shared<true, false>, blocks, kRsW * 64, lds, s, p);
     else if (wb) launch_kernel(k_gate_shared<false, true>, blocks, kRsW * 64, lds, s, p);
     else launch_kernel(k_gate_shared<false, false>, blocks, kRsW * 64, lds, s, p);

@@ -69,12 +69,13 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-// float -> bf16 bits, round to nearest even (NaN stays NaN).
+// float -> bf16 bits, round to nearest even (NaN stays NaN, made quiet).
+// Both results are formed and one is selected: no branch per element.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t nan = (u >> 16) | 0x40u;
+  return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? nan : rne);
 }
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
@@ -216,8 +217,11 @@ hipError_t launch_route(const dsk_moe_desc& d, const void* x, const void* gate_w
 
 // Router + top-k + dispatch.  Small batches run as one kernel whose last
 // blocks do the top-k and the dispatch; larger ones as three kernels.
+struct ResNorm;   // resnorm.h: the stack's residual update + RMSNorm, fused into a layer's first kernel
+
 struct RouteArgs {
   const void* x; const void* gate_w; const float* gate_b;
+  const ResNorm* rn;        // non-null: the gate kernel computes x itself (resnorm.h)
   float* scores; int32_t* idx; float* weights;
   const dsk_expert_ptrs* table;
   DispatchOut out;
@@ -253,6 +257,7 @@ struct ExpertsArgs {
   void* out;
   char* ws;                  // workspace base
   float* rows_out;           // dsk_expert_rows: the per-row outputs go here and nothing is combined
+  const ResNorm* rn;         // non-null: the first kernel computes x itself (resnorm.h)
   const int32_t* rowmap;     // decode pipeline: [slot][T] dispatch row of token t, -1 if none
   // decode pipeline: gate scores and selection bias in, routing out
   float* scores; const float* bias;
@@ -282,7 +287,11 @@ int check_forward(const dsk_moe_desc* d, const void* x, const void* gate_w, cons
 int forward_layer(const dsk_moe_desc* d, const void* x, const void* gate_w, const float* gate_b,
                   const dsk_expert_ptrs* table, const void* ws1, const void* ws3, const void* ws2,
                   const void* shared_out, void* out, int32_t* idx, float* weights, void* workspace,
-                  size_t workspace_bytes, void* stream, void* const* events, int repeat);
+                  size_t workspace_bytes, void* stream, void* const* events, int repeat,
+                  const ResNorm* rn = nullptr);
+// The decode pipeline's first kernel takes the residual update and RMSNorm
+// itself (bf16 stream, one or two tokens, rows up to 4096 wide).
+bool resnorm_fusable(const dsk_moe_desc& d);
 hipError_t launch_rmsnorm(const void* x, const void* res, const float* gamma, int64_t rows, int H, float eps,
                           int dtype, void* h_out, void* y, hipStream_t s);
 

@@ -81,52 +81,103 @@ __device__ __forceinline__ float score_of(float z, int score_func) {
   return sqrt_round_f32(sp);
 }
 
+// Four gate operands as loaded (bf16 bits or float) and as floats.
+template <bool kBF16> struct GateRaw { using T = f32x4; };
+template <> struct GateRaw<true> { using T = uint2; };
+
 template <bool kBF16>
-__device__ __forceinline__ f32x4 load4(const void* base, int64_t elem) {
+__device__ __forceinline__ typename GateRaw<kBF16>::T load_raw4(const void* base, int64_t elem) {
+  if constexpr (kBF16) return *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + elem);
+  else return *reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + elem);
+}
+
+template <bool kBF16>
+__device__ __forceinline__ f32x4 raw4_f32(const typename GateRaw<kBF16>::T& raw) {
   if constexpr (kBF16) {
-    uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + elem);
     return f32x4{__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
                  __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
   } else {
-    return *reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + elem);
+    return raw;
   }
 }
 
+template <bool kBF16>
+__device__ __forceinline__ f32x4 load4(const void* base, int64_t elem) {
+  return raw4_f32<kBF16>(load_raw4<kBF16>(base, elem));
+}
+
+// Steps (of 256 elements) per load batch of a gate tile.
+template <int TW, int EW> constexpr int kGateBatch = TW * EW == 1 ? 4 : 2;
+
+// The first load batch of a gate tile's weights, issued by gate_w_issue
+// ahead of work that produces x (gate_tile then takes them from here).
+template <int TW, int EW, bool kWBF16>
+struct GateWFirst {
+  typename GateRaw<kWBF16>::T w[kGateBatch<TW, EW>][EW];
+};
+
+// Segment [m0, m1) of wave w in steps of 256 elements.
+__device__ __forceinline__ void gate_segment(int H, int wave, bool active, int& m0, int& m1) {
+  const int steps = (H + 255) / 256;
+  const int seg = (steps + kSegments - 1) / kSegments;
+  m0 = wave * seg;
+  m1 = active ? min(m0 + seg, steps) : m0;
+}
+
+// Element offset of lane's four values in step min(mb, m1 - 1) (clamped to
+// the row, so that every load is in bounds; steps past the segment are
+// zeroed before the product).
+__device__ __forceinline__ int gate_col(int mb, int m1, int lane, int H) {
+  return min(256 * max(min(mb, m1 - 1), 0) + 4 * lane, H - 4);
+}
+
+template <int TW, int EW, bool kWBF16>
+__device__ __forceinline__ void gate_w_issue(const void* gw, int H, int E, int e0, int wave, int lane,
+                                             bool active, GateWFirst<TW, EW, kWBF16>& f) {
+  int m0, m1;
+  gate_segment(H, wave, active, m0, m1);
+#pragma unroll
+  for (int q = 0; q < kGateBatch<TW, EW>; ++q) {
+    const int c = gate_col(m0 + q, m1, lane, H);
+#pragma unroll
+    for (int j = 0; j < EW; ++j) f.w[q][j] = load_raw4<kWBF16>(gw, static_cast<int64_t>(min(e0 + j, E - 1)) * H + c);
+  }
+}
 
 // Gate logits and scores of a TW-token x EW-expert tile by 4 waves (wave w
 // owns segment w of H; see the order above).  `gtid` is the thread index
 // within the 4-wave group; segsum is [4][TW*EW] floats of LDS.  Contains a
 // __syncthreads() (reached also when !active: then nothing is loaded or
 // written).
-template <int TW, int EW, bool kXBF16, bool kWBF16>
+template <int TW, int EW, bool kXBF16, bool kWBF16, bool kPre = false>
 __device__ __forceinline__ void gate_tile(const void* x, const void* gw, int T, int H, int E,
                                           int score_func, float* scores, int t0, int e0, int wave,
-                                          int lane, int gtid, float* segsum, bool active = true) {
+                                          int lane, int gtid, float* segsum, bool active = true,
+                                          const GateWFirst<TW, EW, kWBF16>* pre = nullptr) {
 #pragma clang fp contract(off)
   float p[TW][EW];
 #pragma unroll
   for (int i = 0; i < TW; ++i)
 #pragma unroll
     for (int j = 0; j < EW; ++j) p[i][j] = 0.0f;
-  const int steps = (H + 255) / 256;
-  const int seg = (steps + kSegments - 1) / kSegments;
-  const int m0 = wave * seg, m1 = active ? min(m0 + seg, steps) : m0;
+  int m0, m1;
+  gate_segment(H, wave, active, m0, m1);
   // The loads of kC steps are issued together and without conditions (a load
   // under a per-lane condition compiles to a branch whose merge waits for
   // it): out-of-range elements are read from an in-range place and zeroed
   // before the product, and steps past the segment add +0, which leaves a
   // partial that starts at +0 unchanged -- the sums are those of the plain
-  // loop, in the same order.
-  constexpr int kC = TW * EW == 1 ? 4 : 2;
-  for (int mb = m0; mb < m1; mb += kC) {
-    f32x4 xv[kC][TW], wv[kC][EW];
+  // loop, in the same order.  With kPre the first batch's weights were
+  // issued earlier (gate_w_issue, same places).
+  constexpr int kC = kGateBatch<TW, EW>;
+  // x loads and the products of the batch at step mb, weights given
+  auto batch = [&](int mb, const f32x4 (&wv)[kC][EW]) {
+    f32x4 xv[kC][TW];
 #pragma unroll
     for (int q = 0; q < kC; ++q) {
-      const int c = min(256 * min(mb + q, m1 - 1) + 4 * lane, H - 4);
+      const int c = gate_col(mb + q, m1, lane, H);
 #pragma unroll
       for (int i = 0; i < TW; ++i) xv[q][i] = load4<kXBF16>(x, static_cast<int64_t>(min(t0 + i, T - 1)) * H + c);
-#pragma unroll
-      for (int j = 0; j < EW; ++j) wv[q][j] = load4<kWBF16>(gw, static_cast<int64_t>(min(e0 + j, E - 1)) * H + c);
     }
 #pragma unroll
     for (int q = 0; q < kC; ++q) {
@@ -140,6 +191,28 @@ __device__ __forceinline__ void gate_tile(const void* x, const void* gw, int T, 
             p[i][j] = __builtin_fmaf(ok ? xv[q][i][v] : 0.0f, ok ? wv[q][j][v] : 0.0f, p[i][j]);
           }
     }
+  };
+  int mb = m0;
+  if constexpr (kPre) {
+    if (mb < m1) {
+      f32x4 wv[kC][EW];
+#pragma unroll
+      for (int q = 0; q < kC; ++q)
+#pragma unroll
+        for (int j = 0; j < EW; ++j) wv[q][j] = raw4_f32<kWBF16>(pre->w[q][j]);
+      batch(mb, wv);
+    }
+    mb += kC;
+  }
+  for (; mb < m1; mb += kC) {
+    f32x4 wv[kC][EW];
+#pragma unroll
+    for (int q = 0; q < kC; ++q) {
+      const int c = gate_col(mb + q, m1, lane, H);
+#pragma unroll
+      for (int j = 0; j < EW; ++j) wv[q][j] = load4<kWBF16>(gw, static_cast<int64_t>(min(e0 + j, E - 1)) * H + c);
+    }
+    batch(mb, wv);
   }
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1)

@@ -32,6 +32,7 @@
 
 #include "dispatch_block.h"
 #include "gate.h"
+#include "resnorm.h"
 #include "tile.h"
 
 #pragma clang fp contract(off)
@@ -47,10 +48,15 @@ struct GateArgs {
   const dsk_expert_ptrs* table;
   DispatchOut out;
   unsigned int* ctr;
+  ResNorm rn; int norm;     // norm: x is h + d normalised here (resnorm.h); block 0 writes it out
 };
 
+// Byte offset of the normalised rows in k_gate's LDS (after the segment sums and flags).
+constexpr size_t kGateNormOffset = 512;
+
 // Block = 4 waves (one segment each) x a TW-token x EW-expert tile.
-template <int TW, int EW, bool kXBF16, bool kWBF16, bool kFused>
+// kNorm: x is the residual stream's update normalised here (resnorm.h).
+template <int TW, int EW, bool kXBF16, bool kWBF16, bool kFused, bool kNorm = false>
 __global__ __launch_bounds__(256) void k_gate(GateArgs g) {
   extern __shared__ float smem[];
   float* segsum = smem;                       // [4][TW*EW]
@@ -60,8 +66,25 @@ __global__ __launch_bounds__(256) void k_gate(GateArgs g) {
   const int et = blockIdx.x % n_et, tt = blockIdx.x / n_et;
   const int t0 = tt * TW, e0 = et * EW;
   const int T = g.T, E = g.E;
-  gate_tile<TW, EW, kXBF16, kWBF16>(g.x, g.gw, T, g.H, E, g.score_func, g.scores, t0, e0, wave, lane,
-                                    threadIdx.x, segsum);
+  if constexpr (kNorm) {
+    // every block normalises the rows itself (LDS, row stride H) while its
+    // first gate weights load; block 0 also writes the new residual stream and
+    // the rows for the layer's later kernels
+    static_assert(!kFused && kXBF16, "the stream is bf16 and the scores go to the top-k kernel");
+    __shared__ float rn_wsum[kResNormWsum];
+    uint16_t* y = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(smem) + kGateNormOffset);
+    ResNormIn<256> in;
+    resnorm_issue<256>(g.rn, T, g.H, in);
+    asm volatile("" ::: "memory");   // the rows' loads first: waiting for them leaves the weights in flight
+    GateWFirst<TW, EW, kWBF16> pre;
+    gate_w_issue<TW, EW, kWBF16>(g.gw, g.H, E, e0, wave, lane, true, pre);
+    resnorm_rows<256>(g.rn, T, g.H, y, g.H, blockIdx.x == 0, rn_wsum, in);
+    gate_tile<TW, EW, kXBF16, kWBF16, true>(y, g.gw, T, g.H, E, g.score_func, g.scores, t0, e0, wave, lane,
+                                            threadIdx.x, segsum, true, &pre);
+  } else {
+    gate_tile<TW, EW, kXBF16, kWBF16>(g.x, g.gw, T, g.H, E, g.score_func, g.scores, t0, e0, wave, lane,
+                                      threadIdx.x, segsum);
+  }
   if constexpr (kFused) {
     const int n_tt = (T + TW - 1) / TW;
     __threadfence();
@@ -268,7 +291,21 @@ hipError_t launch_gate(const dsk_moe_desc& d, const GateArgs& g, hipStream_t s) 
   const unsigned blocks = static_cast<unsigned>(n_et * n_tt);
   size_t lds = (kSegments * TW * EW + 4) * sizeof(float);
   if (kFused) lds += static_cast<size_t>(4 * d.n_experts + d.n_experts + 32) * sizeof(int32_t);
+  static_assert(kFused || (kSegments * TW * EW + 4) * sizeof(float) <= kGateNormOffset,
+                "segment sums before the rows");
   const bool xb = d.x_dtype == DSK_DTYPE_BF16, wb = d.gate_dtype == DSK_DTYPE_BF16;
+  if (g.norm) {
+    // the residual form: one-token tiles of a bf16 stream only (resnorm_fusable)
+    if constexpr (TW == 1 && EW == 1 && !kFused) {
+      if (!xb) return hipErrorInvalidValue;
+      lds = kGateNormOffset + static_cast<size_t>(d.tokens) * d.hidden * 2;
+      if (wb) launch_kernel(k_gate<1, 1, true, true, false, true>, blocks, 256, lds, s, g);
+      else launch_kernel(k_gate<1, 1, true, false, false, true>, blocks, 256, lds, s, g);
+      return hipGetLastError();
+    } else {
+      return hipErrorInvalidValue;
+    }
+  }
   if (xb && wb) launch_kernel(k_gate<TW, EW, true, true, kFused>, blocks, 256, lds, s, g);
   else if (xb) launch_kernel(k_gate<TW, EW, true, false, kFused>, blocks, 256, lds, s, g);
   else if (wb) launch_kernel(k_gate<TW, EW, false, true, kFused>, blocks, 256, lds, s, g);
@@ -419,6 +456,10 @@ GateArgs route_gate_args(const dsk_moe_desc& d, const RouteArgs& a) {
   g.table = a.table;
   g.out = a.out;
   g.ctr = a.ctr;
+  if (a.rn) {
+    g.rn = *a.rn;
+    g.norm = 1;
+  }
   return g;
 }
 

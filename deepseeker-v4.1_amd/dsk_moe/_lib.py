@@ -53,6 +53,12 @@ class ExpertPtrs(ctypes.Structure):
     _fields_ = [(n, _vp) for n in ("w1", "s1", "b1", "w3", "s3", "b3", "w2", "s2", "b2")]
 
 
+class Residual(ctypes.Structure):
+    """Mirror of ``dsk_residual``."""
+
+    _fields_ = [("h", _vp), ("d", _vp), ("gamma", _vp), ("eps", ctypes.c_float), ("h_out", _vp), ("x_out", _vp)]
+
+
 PDesc = ctypes.POINTER(Desc)
 
 SIGNATURES = {
@@ -69,6 +75,8 @@ SIGNATURES = {
     "dsk_expert_rows": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "dsk_moe_forward": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                        _vp, _vp, _vp, _sz, _vp]),
+    "dsk_moe_forward_residual": (ctypes.c_int, [PDesc, ctypes.POINTER(Residual), _vp, _vp, _vp, _vp, _vp, _vp,
+                                                _vp, _vp, _vp, _vp, _sz, _vp]),
     "dsk_moe_forward_timed": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                              _vp, _vp, _vp, _sz, _vp, _vp, _i32]),
     "dsk_moe_forward_noalloc": (ctypes.c_int, [PDesc, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

@@ -366,6 +366,43 @@ class MoELayer:
             trace(layer_id, idx.flip(1).tolist(), w.flip(1).tolist())
         return out
 
+    def forward_residual(self, h: torch.Tensor, d: torch.Tensor, h_out: torch.Tensor, x_out: torch.Tensor,
+                         out: torch.Tensor, gamma: torch.Tensor | None = None, eps: float = 1e-6,
+                         idx: torch.Tensor | None = None, w: torch.Tensor | None = None,
+                         trace=None, layer_id: int = 0, ws: torch.Tensor | None = None) -> torch.Tensor:
+        """One step of a layer stack (``dsk_moe_forward_residual``): ``h_out = h + d``
+        (rounded to the stream's dtype), ``x_out = rmsnorm(h_out) * gamma``, then the
+        layer on ``x_out`` into ``out`` (which may be ``d``).  With ``h_out`` a buffer
+        of its own, at one or two bf16 tokens, the layer's first kernel computes the
+        update itself."""
+        dev = require_device(h, d, h_out, x_out, out, self.gate_w)
+        t, hd = h.shape
+        for name, v in (("d", d), ("h_out", h_out), ("x_out", x_out), ("out", out)):
+            if v.shape != h.shape or v.dtype != h.dtype:
+                raise ValueError(f"{name} must match h in shape and dtype")
+        if gamma is not None and (gamma.dtype != torch.float32 or gamma.shape != (hd,)):
+            raise ValueError("gamma must be float32 [hidden]")
+        if trace is not None:
+            idx = idx if idx is not None else torch.empty((t, self.top_k), dtype=torch.int32, device=dev)
+            w = w if w is not None else torch.empty((t, self.top_k), dtype=torch.float32, device=dev)
+        desc = make_desc(tokens=t, hidden=hd, n_experts=self.bank.n_experts, top_k=self.top_k,
+                         inter=self.bank.inter, inter_shared=self.shared.inter if self.shared else 0,
+                         score_func=self.score_func, quant=self.bank.quant, x_dtype=h.dtype,
+                         gate_dtype=self.gate_w.dtype, route_scale=self.route_scale, limit=self.limit)
+        if ws is None:
+            ws = workspace(desc, dev)
+        elif ws.numel() < workspace_size(desc) or ws.device != dev:
+            raise ValueError(f"workspace of {ws.numel()} bytes on {ws.device} is too small for this call")
+        r = _lib.Residual(h.data_ptr(), d.data_ptr(), gamma.data_ptr() if gamma is not None else None,
+                          float(eps), h_out.data_ptr(), x_out.data_ptr())
+        s = self.shared
+        _lib.call("dsk_moe_forward_residual", ctypes.byref(desc), ctypes.byref(r), ptr(self.gate_w),
+                  ptr(self.gate_b), ptr(self.bank.table), ptr(s.w1 if s else None), ptr(s.w3 if s else None),
+                  ptr(s.w2 if s else None), ptr(out), ptr(idx), ptr(w), ptr(ws), ws.numel(), stream_of(dev))
+        if trace is not None:
+            trace(layer_id, idx.flip(1).tolist(), w.flip(1).tolist())
+        return out
+
     def workspace_bytes(self, tokens: int, x_dtype: torch.dtype = torch.bfloat16) -> int:
         """Workspace bytes a call on ``tokens`` rows of ``x_dtype`` needs."""
         return workspace_size(make_desc(

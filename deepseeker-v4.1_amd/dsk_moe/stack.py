@@ -7,10 +7,14 @@ and adds its output back.  ``MoEStack`` is that loop over MoE layers only:
 
     h_0 = x;  h_{l+1} = h_l + layer_l(rmsnorm(h_l))   (rounded to x's dtype)
 
-with every step on the device: one ``dsk_rmsnorm`` per layer boundary (the
-residual add fused with the next normalisation) and one ``dsk_moe_forward``
-per layer.  ``capture(tokens)`` records the whole stack as one HIP graph
-(after an eager warm-up, so the workspace and buffers exist outside the
+with every step on the device: ``dsk_rmsnorm`` of x and ``dsk_moe_forward``
+for the first layer, then per layer boundary ``dsk_moe_forward_residual``,
+which adds the previous layer's output to the stream, normalises it and runs
+the layer -- in the decode pipeline at one or two tokens inside the layer's
+first kernel (the stream alternates between two buffers, since that kernel's
+blocks all read the stream before one of them writes the update) -- and a
+final residual add.  ``capture(tokens)`` records the whole stack as one HIP
+graph (after an eager warm-up, so the workspace and buffers exist outside the
 graph) and ``replay(x)`` runs it.
 """
 
@@ -58,7 +62,7 @@ class MoEStack:
         self._graph = None
 
     def _buffers(self, x: torch.Tensor):
-        return torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)   # h, y, d
+        return tuple(torch.empty_like(x) for _ in range(4))   # h (two, alternating), y, d
 
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None, bufs=None,
                 record: list | None = None, trace=None, ws: torch.Tensor | None = None) -> torch.Tensor:
@@ -66,20 +70,22 @@ class MoEStack:
         layer, copies of (h_l, rmsnorm(h_l), idx_l, layer output); ``trace``
         (optional, e.g. a ``TraceSink``) receives every layer's routing as
         ``trace(layer, idx, weights)`` on the host."""
-        h, y, d = bufs if bufs is not None else self._buffers(x)
+        h0, h1, y, d = bufs if bufs is not None else self._buffers(x)
         if out is None:
             out = torch.empty_like(x)
         idx = None
         prev = x
         for l, layer in enumerate(self.layers):
-            if l == 0:
-                rmsnorm(x, self.eps, self.gammas[0], out=y)
-            else:
-                rmsnorm(prev, self.eps, self.gammas[l], residual=d, h_out=h, out=y)
-                prev = h
             if record is not None:
                 idx = torch.empty((x.shape[0], layer.top_k), dtype=torch.int32, device=x.device)
-            layer(y, out=d, idx=idx, trace=trace, layer_id=l, ws=ws)
+            if l == 0:
+                rmsnorm(x, self.eps, self.gammas[0], out=y)
+                layer(y, out=d, idx=idx, trace=trace, layer_id=l, ws=ws)
+            else:
+                h = h0 if l % 2 else h1
+                layer.forward_residual(prev, d, h, y, d, gamma=self.gammas[l], eps=self.eps, idx=idx,
+                                       trace=trace, layer_id=l, ws=ws)
+                prev = h
             if record is not None:
                 record.append((prev.clone(), y.clone(), idx, d.clone()))
         rmsnorm(prev, self.eps, residual=d, h_out=out, out=False)

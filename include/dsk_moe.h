@@ -188,6 +188,33 @@ int dsk_moe_forward(const dsk_moe_desc* d, const void* x, const void* gate_w,
                     int32_t* idx, float* weights, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* The residual stream between two layers of a stack, for
+ * dsk_moe_forward_residual. */
+typedef struct dsk_residual {
+  const void* h;        /* [T,H] the stream before this layer, x_dtype */
+  const void* d;        /* [T,H] the previous layer's output, x_dtype */
+  const float* gamma;   /* [H] RMSNorm weight, or NULL (ones) */
+  float eps;
+  void* h_out;          /* [T,H] h + d rounded to x_dtype (may be h itself) */
+  void* x_out;          /* [T,H] rmsnorm(h + d) * gamma: the layer's input */
+} dsk_residual;
+
+/* One step of the runner's layer loop (src/deepseeker/mlx_runner.py:2138-2145):
+ * the residual add and rmsnorm (src/deepseeker/mlx_forward.py:45-59), then
+ * moe_layer on the normalised rows -- the same results as dsk_rmsnorm(h, d,
+ * gamma, ..., h_out, x_out) followed by dsk_moe_forward(x = x_out), bit for
+ * bit.  In the decode pipeline at one or two bf16 tokens (rows up to 4096
+ * wide) with h_out a buffer of its own, the layer's first kernel computes the
+ * update itself (each block normalises the rows it needs, one block writes
+ * h_out and x_out), which saves a launch per layer; otherwise the update runs
+ * as its own kernel first.  x_out and h_out must not overlap the other
+ * buffers.  Shared-expert arguments as for dsk_moe_forward (no precomputed
+ * shared output). */
+int dsk_moe_forward_residual(const dsk_moe_desc* d, const dsk_residual* r, const void* gate_w,
+                             const float* gate_b, const dsk_expert_ptrs* table, const void* ws1,
+                             const void* ws3, const void* ws2, void* out, int32_t* idx, float* weights,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* dsk_moe_forward that times its five stages with DSK_STAGE_EVENTS hipEvent_t
  * created by the caller: events[2i] and events[2i+1] receive the begin
  * timestamp of stage i's first kernel and the end timestamp of its last

@@ -130,3 +130,20 @@ def test_cap_union_size_limit_is_a_clean_rejection():
     assert b"beyond the one-block cap" in lib.dsk_last_error()
     with pytest.raises(_lib.DskError, match="DSK_EUNSUPPORTED"):
         _lib.call("dsk_cap_union", 8192, 256, 8, 64, 0, p, p, p, None)
+
+
+def test_forward_residual_validation():
+    """dsk_moe_forward_residual rejects a missing residual, misaligned stream
+    pointers and an x_out that overlaps the stream, before any launch."""
+    lib = _lib.load()
+    d = _desc(tokens=1)
+    ptrs = [ctypes.c_void_p(1 << 20)] * 10          # gate_w .. workspace, all aligned
+    call = lambda r: lib.dsk_moe_forward_residual(ctypes.byref(d), r, *ptrs, 1 << 30, None)
+    assert call(None) == -1
+    row = 1024 * 2                                    # one bf16 row of hidden 1024
+    good = dict(h=1 << 24, d=(1 << 24) + 4 * row, gamma=None, eps=1e-6, h_out=(1 << 24) + 8 * row,
+                x_out=(1 << 24) + 12 * row)
+    assert call(ctypes.byref(_lib.Residual(**{**good, "h": (1 << 24) + 8}))) == -2
+    assert call(ctypes.byref(_lib.Residual(**{**good, "x_out": good["h"]}))) == -1
+    assert b"overlap" in lib.dsk_last_error()
+    assert call(ctypes.byref(_lib.Residual(**{**good, "eps": -1.0}))) == -1

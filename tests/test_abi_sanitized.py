@@ -38,7 +38,8 @@ def test_abi_checks_under_host_sanitizers():
     sys.path.insert(0, str(PKG))
     import build as B
     lib = B.LIB_SAN
-    if not lib.exists():
+    sources = list(B.CSRC.glob("*")) + [ROOT / "include" / "dsk_moe.h"]
+    if not lib.exists() or lib.stat().st_mtime < max(f.stat().st_mtime for f in sources):
         B.build(sanitize=True)
     env = dict(os.environ, LD_PRELOAD=rt, DSK_MOE_LIBRARY=str(lib),
                ASAN_OPTIONS="detect_leaks=0:halt_on_error=1:abort_on_error=0",

@@ -169,3 +169,47 @@ def test_captured_stack_keeps_its_workspace():
         want = stack(x).clone()
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {rep}"
+
+
+@pytest.mark.parametrize("case", ["mx-T1", "mx-T2", "q3-T1", "fp4-small-T2", "inplace-T1", "unfused-T5"])
+def test_forward_residual_equals_rmsnorm_then_layer(case):
+    """dsk_moe_forward_residual against dsk_rmsnorm + dsk_moe_forward: h_out, x_out
+    and the layer output bit for bit.  The MX pipeline (FP4, inter 2048) and the
+    gate kernel of the other decode configurations take the update into their
+    first kernel; in place (h_out = h) and at five tokens it runs as its own kernel."""
+    print(f"forward_residual {case}", flush=True)
+    kind, T = case.rsplit("-T", 1)
+    T = int(T)
+    if kind in ("mx", "inplace"):
+        layer = gsynth.make_layer(hidden=4096, n_experts=256, top_k=8, inter=2048, inter_shared=2048,
+                                  seed=900 + T, device=DEV)
+    elif kind == "q3":
+        layer = gsynth.make_layer(hidden=4096, n_experts=256, top_k=8, inter=2048, inter_shared=2048,
+                                  quant="q3", seed=910, device=DEV)
+    else:
+        layer = gsynth.make_layer(hidden=1024, n_experts=64, top_k=6, inter=512, inter_shared=512,
+                                  seed=920 + T, device=DEV)
+    H = layer.gate_w.shape[1]
+    g = torch.Generator(device=DEV).manual_seed(930 + T)
+    h = (torch.randn((T, H), generator=g, device=DEV) * 3).to(torch.bfloat16)
+    d = torch.randn((T, H), generator=g, device=DEV).to(torch.bfloat16)
+    gamma = torch.rand((H,), generator=g, device=DEV) + 0.5
+    # reference: the two calls
+    h_ref, y_ref = torch.empty_like(h), torch.empty_like(h)
+    rmsnorm(h, 1e-6, gamma, residual=d, h_out=h_ref, out=y_ref)
+    out_ref = layer(y_ref).clone()
+    # fused
+    x_out, out = torch.empty_like(h), torch.empty_like(h)
+    h_in = h.clone()
+    h_out = h_in if kind == "inplace" else torch.empty_like(h)
+    layer.forward_residual(h_in, d, h_out, x_out, out, gamma=gamma, eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(h_out.view(torch.int16), h_ref.view(torch.int16))
+    assert torch.equal(x_out.view(torch.int16), y_ref.view(torch.int16))
+    assert torch.equal(out.view(torch.int16), out_ref.view(torch.int16))
+    # the layer's output may overwrite d (as the stack does)
+    d2 = d.clone()
+    h_out2 = torch.empty_like(h)
+    layer.forward_residual(h, d2, h_out2, x_out, d2, gamma=gamma, eps=1e-6)
+    assert torch.equal(d2.view(torch.int16), out_ref.view(torch.int16))
+    assert torch.equal(h_out2.view(torch.int16), h_ref.view(torch.int16))
