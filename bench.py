@@ -160,6 +160,10 @@ def up_flops(t: int) -> int:
 PREFILL_MIN_TOKENS = 128     # batches from this size run the expert products as MFMA GEMM tiles
 
 
+TRAFFIC_SOURCE = ("read from profiles/traffic.json, not measured by this run: rocprofv3 --pmc FETCH_SIZE "
+                  "and WRITE_SIZE passes of the same workload, scaled by what they read for a 256 MiB copy")
+
+
 def measured_traffic(kernels: list[str], workload: str):
     """HBM bytes per launch of `kernels` (summed) from the committed rocprofv3 --pmc
     measurement (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size), or None
@@ -175,6 +179,13 @@ def measured_traffic(kernels: list[str], workload: str):
             return None
         total += int(entry["bytes_per_launch"])
     return total
+
+
+def traffic_fields(kernels: list[str], workload: str) -> dict:
+    """roofline["traffic"] and where it comes from."""
+    t = measured_traffic(kernels, workload)
+    return {"traffic": t, "traffic_source": TRAFFIC_SOURCE if t is not None else
+            "no committed FETCH_SIZE / WRITE_SIZE measurement for this kernel and workload"}
 
 
 def pct(a: np.ndarray) -> dict | None:
@@ -570,7 +581,7 @@ def main() -> int:
         achieved = up_flops(T) / (up_us * 1e-6)
         roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 1), "peak": PEAK_BF16 / 1e12,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4),
-                    "traffic": measured_traffic(["k_pf_up"], workload),
+                    **traffic_fields(["k_pf_up"], workload),
                     "kernel": f"k_pf_up (routed {args.quant.upper()} + shared bf16 w1/w3 GEMM tiles, SwiGLU epilogue)",
                     "flops_per_launch": int(up_flops(T)), "avg_launch_us": up_us, "timing": timing}
     else:
@@ -584,7 +595,7 @@ def main() -> int:
                 "k_down_decode_staged" if T <= 2 else "k_down_grouped + k_combine")
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
-                    "traffic": measured_traffic([up_k, dn_k], workload),
+                    **traffic_fields([up_k, dn_k], workload),
                     "kernel": f"routed-expert stage: {up_k} (routed w1/w3, SwiGLU x route weight) + "
                               f"{dn_k} " + ("(routed w2, add of the shared output)" if mx else
                                              "(routed and shared w2, combine)"),
