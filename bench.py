@@ -536,8 +536,11 @@ def main() -> int:
     ap.add_argument("--quant", choices=("fp4", "q3"), default="fp4", help="routed expert format")
     ap.add_argument("--zipf", type=float, default=None,
                     help="gate bias = log Zipf(s) popularity (skewed routing, as in the prefill sweep)")
-    ap.add_argument("--mode", choices=("layer", "copy", "read", "mfma"), default="layer")
+    ap.add_argument("--mode", choices=("layer", "copy", "read", "mfma", "stack"), default="layer",
+                    help="layer: the headline line; copy / read / mfma: the box's peaks; stack: only the "
+                         "40-layer stack at 1 and 2 tokens (--steps replays each)")
     ap.add_argument("--bytes", type=int, default=1 << 30)
+    ap.add_argument("--stack-batch", type=int, default=0, help="--mode stack: this batch size only")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the MoE-layer path is built and timed on a single "
@@ -555,6 +558,10 @@ def main() -> int:
         return 0
     if args.mode == "mfma":
         print(json.dumps(mfma_rate()), flush=True)
+        return 0
+    if args.mode == "stack":
+        batches = (args.stack_batch,) if args.stack_batch else (1, 2)
+        print(json.dumps(run_stack(40, batches, steps=args.steps)), flush=True)
         return 0
 
     t_gen = time.perf_counter()
@@ -590,7 +597,8 @@ def main() -> int:
         routed_us = float(np.mean(r["stage_us"][:, 2] + r["stage_us"][:, 3]))
         achieved = rs["bytes_mean"] / (routed_us * 1e-6)
         mx = mx_decode(T, args.quant)
-        up_k = "k_up_q3" if (args.quant == "q3" and T <= 8) else ("k_up_mx" if mx else "k_up_stream")
+        up_k = ("k_up_grouped" if T >= 8 else "k_up_q3" if args.quant == "q3" else
+                "k_up_mx" if mx else "k_up_stream")
         dn_k = ("k_down_q3" if args.quant == "q3" and T <= 4 else "k_down_mx" if mx else
                 "k_down_decode_staged" if T <= 2 else "k_down_grouped + k_combine")
         roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
