@@ -145,6 +145,7 @@ struct Workspace {
   size_t y;                 // routed outputs          [T*k][H] f32
   size_t ys;                // shared output           [T][H]   f32
   size_t shared_x;          // decode pipeline: shared output [T][H] (x dtype)
+  size_t xp;                // grouped FP4 gate/up: x as FP8 planes [T][2][H] + E8M0 [T][2][H/32]
   size_t pf_tiles;          // prefill GEMM tile list  [2 + 2 * prefill_max_tiles]
   size_t total;
 };

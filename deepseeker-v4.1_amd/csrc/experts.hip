@@ -429,78 +429,116 @@ enum SharedMode { kNoShared = 0, kSharedF32 = 1, kSharedExt = 2 };
 
 constexpr int kCombineMaxK = 16;     // top-k the combine handles (validated on the host)
 constexpr int kCombineBatch = 8;     // rows of a token whose loads are issued together
-// Four consecutive values of row r of y (float32, or bf16 when YBF16).
-template <bool YBF16>
-__device__ __forceinline__ f32x4 load_row4(const void* y, int64_t r, int H, int f) {
-  if constexpr (YBF16) {
-    const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(y) + r * H + f);
-    return f32x4{__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
-                 __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
+
+// V consecutive values (V = 4 or 8) at element offset f of a row of y
+// (float32, or bf16 when YBF16) or of a bf16 / float32 row, as floats.
+template <bool BF16, int V>
+__device__ __forceinline__ void load_vals(const void* row, int f, float (&o)[V]) {
+  if constexpr (BF16) {
+    const uint16_t* p = static_cast<const uint16_t*>(row) + f;
+    uint32_t w[V / 2];
+    if constexpr (V == 8) {
+      const u32x4 r = *reinterpret_cast<const u32x4*>(p);
+      w[0] = r[0]; w[1] = r[1]; w[2] = r[2]; w[3] = r[3];
+    } else {
+      const uint2 r = *reinterpret_cast<const uint2*>(p);
+      w[0] = r.x; w[1] = r.y;
+    }
+#pragma unroll
+    for (int i = 0; i < V / 2; ++i) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
   } else {
-    return *reinterpret_cast<const f32x4*>(static_cast<const float*>(y) + r * H + f);
+    const float* p = static_cast<const float*>(row) + f;
+#pragma unroll
+    for (int i = 0; i < V / 4; ++i) {
+      const f32x4 r = *reinterpret_cast<const f32x4*>(p + 4 * i);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[4 * i + q] = r[q];
+    }
   }
 }
 
-template <bool XBF16, bool YBF16>
+// One block per (token, 256 V-value column group).  The token's ranks, their
+// ascending order and the row addresses are the same for every lane: they
+// are read into scalar registers and sorted by the scalar unit, so the
+// vector work per value is its loads, its adds in order and the rounding.
+template <bool XBF16, bool YBF16, int V>
 __global__ __launch_bounds__(256) void k_combine(const void* __restrict__ y, const float* __restrict__ ys,
                                                  const void* __restrict__ shared_ext,
                                                  const int32_t* __restrict__ rank, int H, int k,
                                                  int shared_mode, void* __restrict__ out) {
+#pragma clang fp contract(off)
   const int t = blockIdx.x;
-  const int f = (blockIdx.y * 256 + threadIdx.x) * 4;
+  const int f = (blockIdx.y * 256 + threadIdx.x) * V;
   if (f >= H) return;
-  // The token's k ranks, then its first kCombineBatch rows, are each loaded
-  // together (no chain of dependent loads): ranks past k re-read rank k - 1,
-  // rows past n read row 0 and are not added.  Rows are added in ascending
-  // dispatch-row order.
-  int rk[kCombineMaxK];
-#pragma unroll
-  for (int j = 0; j < kCombineMaxK; ++j) rk[j] = rank[static_cast<int64_t>(t) * k + min(j, k - 1)];
+  // The token's k ranks (all loaded together; ranks past k re-read rank
+  // k - 1), sorted ascending without the dropped ones (-1): rows[0 .. n).
   int rows[kCombineMaxK];
 #pragma unroll
-  for (int j = 0; j < kCombineMaxK; ++j) rows[j] = 0;
+  for (int j = 0; j < kCombineMaxK; ++j)
+    rows[j] = __builtin_amdgcn_readfirstlane(rank[static_cast<int64_t>(t) * k + min(j, k - 1)]);
   int n = 0;
 #pragma unroll
   for (int j = 0; j < kCombineMaxK; ++j) {
     if (j >= k) break;
-    const int r = rk[j];
+    const int r = rows[j];
     if (r < 0) continue;
+    // insertion into rows[0 .. n) (rows[j] itself is past n: j >= n)
     int i = n++;
     while (i > 0 && rows[i - 1] > r) { rows[i] = rows[i - 1]; --i; }
     rows[i] = r;
   }
-  f32x4 v[kCombineBatch];
+  const size_t ebytes = YBF16 ? 2 : 4;
+  const char* yb = static_cast<const char*>(y);
+  // the first kCombineBatch rows' loads together (rows past n read row 0, not added)
+  float v[kCombineBatch][V];
 #pragma unroll
-  for (int q = 0; q < kCombineBatch; ++q) v[q] = load_row4<YBF16>(y, rows[q], H, f);
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < kCombineBatch; ++q) {
+    const int r = q < n ? rows[q] : 0;
+    load_vals<YBF16, V>(yb + static_cast<size_t>(r) * H * ebytes, f, v[q]);
+  }
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
 #pragma unroll
   for (int q = 0; q < kCombineBatch; ++q)
-    if (q < n) acc += v[q];
-  for (int i = kCombineBatch; i < n; ++i) acc += load_row4<YBF16>(y, rows[i], H, f);
-  const int64_t o = static_cast<int64_t>(t) * H + f;
-  if (shared_mode == kSharedF32) {
-    f32x4 s = *reinterpret_cast<const f32x4*>(ys + o);
-    if constexpr (XBF16) {
+    if (q < n) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) s[q] = bf16_bits_to_f32(f32_to_bf16_bits(s[q]));
+      for (int i = 0; i < V; ++i) acc[i] = acc[i] + v[q][i];
     }
-    acc += s;
+  for (int q = kCombineBatch; q < n; ++q) {
+    float w[V];
+    load_vals<YBF16, V>(yb + static_cast<size_t>(rows[q]) * H * ebytes, f, w);
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = acc[i] + w[i];
+  }
+  const size_t o = static_cast<size_t>(t) * H;
+  if (shared_mode == kSharedF32) {
+    float sv[V];
+    load_vals<false, V>(ys + o, f, sv);
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = acc[i] + (XBF16 ? bf16_bits_to_f32(f32_to_bf16_bits(sv[i])) : sv[i]);
   } else if (shared_mode == kSharedExt) {
-    if constexpr (XBF16) {
-      const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(shared_ext) + o);
-      acc += f32x4{__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
-                   __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
-    } else {
-      acc += *reinterpret_cast<const f32x4*>(static_cast<const float*>(shared_ext) + o);
-    }
+    float sv[V];
+    if constexpr (XBF16) load_vals<true, V>(static_cast<const uint16_t*>(shared_ext) + o, f, sv);
+    else load_vals<false, V>(static_cast<const float*>(shared_ext) + o, f, sv);
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = acc[i] + sv[i];
   }
   if constexpr (XBF16) {
-    uint16_t* ob = static_cast<uint16_t*>(out);
-    *reinterpret_cast<uint2*>(ob + o) =
-        uint2{f32_to_bf16_bits(acc[0]) | (uint32_t(f32_to_bf16_bits(acc[1])) << 16),
-              f32_to_bf16_bits(acc[2]) | (uint32_t(f32_to_bf16_bits(acc[3])) << 16)};
+    uint32_t w[V / 2];
+#pragma unroll
+    for (int i = 0; i < V / 2; ++i)
+      w[i] = f32_to_bf16_bits(acc[2 * i]) | (uint32_t(f32_to_bf16_bits(acc[2 * i + 1])) << 16);
+    uint16_t* ob = static_cast<uint16_t*>(out) + o + f;
+    if constexpr (V == 8) *reinterpret_cast<u32x4*>(ob) = u32x4{w[0], w[1], w[2], w[3]};
+    else *reinterpret_cast<uint2*>(ob) = uint2{w[0], w[1]};
   } else {
-    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + o) = acc;
+    float* of = static_cast<float*>(out) + o + f;
+#pragma unroll
+    for (int i = 0; i < V / 4; ++i) *reinterpret_cast<f32x4*>(of + 4 * i) = f32x4{acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]};
   }
 }
 
@@ -542,7 +580,11 @@ hipError_t launch_combine(const dsk_moe_desc& d, const Workspace& L, const Exper
   const int T = d.tokens, H = d.hidden, Is = d.inter_shared, k = d.top_k;
   const void* y = a.ws + L.y;
   const float* ys = reinterpret_cast<const float*>(a.ws + L.ys);
-  dim3 cg(static_cast<unsigned>(T), static_cast<unsigned>((H + 1023) / 1024));
+  // 8 values per lane for large batches (at T=4096 66 -> 62 us: the rank
+  // bookkeeping per value halves and the kernel reaches the HBM rate); small
+  // ones keep 4 and twice the blocks (B=64: 6.4 us against 7.0)
+  const bool v8 = H % 8 == 0 && T >= 128;
+  dim3 cg(static_cast<unsigned>(T), static_cast<unsigned>((H + (v8 ? 2047 : 1023)) / (v8 ? 2048 : 1024)));
   int mode = Is > 0 ? kSharedF32 : (a.shared_out ? kSharedExt : kNoShared);
   const void* shared_ext = a.shared_out;
   const bool pf = prefill_gemm(d);
@@ -554,12 +596,18 @@ hipError_t launch_combine(const dsk_moe_desc& d, const Workspace& L, const Exper
   hipError_t e = stage_open(kStageCombine);
   if (e != hipSuccess) return e;
   for (int r = 0; r < repeat; ++r) {
-    if (d.x_dtype == DSK_DTYPE_F32)
-      launch_kernel(k_combine<false, false>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
+    if (d.x_dtype == DSK_DTYPE_F32 && v8)
+      launch_kernel(k_combine<false, false, 8>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
+    else if (d.x_dtype == DSK_DTYPE_F32)
+      launch_kernel(k_combine<false, false, 4>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
+    else if (ybf && v8)
+      launch_kernel(k_combine<true, true, 8>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
     else if (ybf)
-      launch_kernel(k_combine<true, true>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
+      launch_kernel(k_combine<true, true, 4>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
+    else if (v8)
+      launch_kernel(k_combine<true, false, 8>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
     else
-      launch_kernel(k_combine<true, false>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
+      launch_kernel(k_combine<true, false, 4>, cg, 256, 0, s, y, ys, shared_ext, a.rank, H, k, mode, a.out);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return e;

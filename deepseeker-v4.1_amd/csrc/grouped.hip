@@ -16,7 +16,7 @@
 // dispatch row (hs by token for the shared expert); down writes one float32
 // output row per dispatch row (ys per token for the shared expert), which
 // the combine kernel adds in ascending expert id.
-#include "tile.h"
+#include "mx.h"
 
 namespace dsk {
 namespace {
@@ -48,6 +48,8 @@ struct GroupedArgs {
   int dn_groups, dn_shared;                      // down: the same
   int q3f;                                       // q3 gate/up in the factored form (up_block_q3f)
   int q3fd;                                      // q3 down in the factored form (down_block_q3f)
+  int mx;                                        // FP4 gate/up on scaled MFMAs: blocks per wave, or 0
+  uint8_t* xp;                                   // mx: x as FP8 planes [T][2][H], then E8M0 [T][2][H/32]
 };
 
 // K blocks per weight batch, two batches in flight per wave, within the
@@ -340,6 +342,172 @@ __device__ __forceinline__ void up_block_q3f(const GroupedArgs& p, const void* c
   }
 }
 
+// ---------------------------------------------------------------- MX gate/up (FP4 slots)
+// The FP4 slots' gate/up on v_mfma_scale_f32_16x16x128_f8f6f4 (mx.h): the
+// codes and E8M0 bytes go into the product as loaded, so a wave holds its
+// whole K range of both roles in flight (kGxMaxBlocks 128-code blocks: 16
+// bytes of codes and a 4-byte scale word per block, role and lane) for each
+// column tile.  The activations are two FP8 planes per token,
+// written once per call by k_x_planes in the B-operand layout; a column tile
+// copies its rows' planes into LDS (column 2r + p: plane p of the tile's row
+// r).  K ranges are added in wave order, then a row's two plane columns; h
+// leaves as the bf16 hi / lo pair of the other gate/up paths.
+constexpr int kGxMaxBlocks = 8;     // K blocks per wave held (H <= kGKS * 8 * 128)
+
+// Token t's two FP8 planes of x (v ~ q0 2^e + q1 2^(e-4) per 32-value group,
+// e = ilogb(group max) - 7, mx.h) into xp: plane row (t, p) holds H bytes, each
+// 128-value block in the B-operand byte order (b_perm), then the E8M0 bytes
+// of every (t, p, group).  One thread per 8 values; a group's four chunks are
+// in consecutive lanes.
+__global__ __launch_bounds__(256) void k_x_planes(const uint16_t* __restrict__ x, int T, int H,
+                                                  uint8_t* __restrict__ xp) {
+  const int cpr = H / 8, n = T * cpr;
+  const int c0 = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  const int c = min(c0, n - 1);   // every lane takes part in the group exchange
+  const int t = c / cpr, k8 = (c % cpr) * 8;
+  const u32x4 v = ldg16(x + static_cast<int64_t>(t) * H + k8);
+  const float f0[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
+  const float f1[4] = {__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
+                       __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u)};
+  float m = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) m = fmaxf(m, fmaxf(fabsf(f0[q]), fabsf(f1[q])));
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  const int e = fp8_plane_exp(m);
+  uint32_t w0[2], w1[2];
+  fp8_planes4<2>(f0, e, w0);
+  fp8_planes4<2>(f1, e, w1);
+  if (c0 < n) {
+    const int kb = k8 >> 7, kk = k8 & 127;
+    uint8_t* scales = xp + static_cast<size_t>(T) * 2 * H;
+#pragma unroll
+    for (int pl = 0; pl < 2; ++pl) {
+      const size_t prow = static_cast<size_t>(2 * t + pl);
+      *reinterpret_cast<uint2*>(xp + prow * H + kb * 128 + b_perm(kk)) = uint2{w0[pl], w1[pl]};
+      if ((k8 & 31) == 0) scales[prow * (H / 32) + (k8 >> 5)] = static_cast<uint8_t>(e8m0_byte(e - 4 * pl));
+    }
+  }
+}
+
+// LDS of up_block_mx: the column tile's planes [H/128][16][128] bytes, then
+// their E8M0 words [H/128][16] (4 bytes: the block's four groups); the K-range
+// partial sums [kGI][kGKS][2][64][4] f32 reuse the planes after the products.
+__host__ __device__ inline size_t gx_lds_bytes(int H) { return static_cast<size_t>(H / 128) * 16 * (128 + 4); }
+
+// Gate/up of one FP4 slot block: row tile rt of w1 / w3 for the n dispatch
+// rows base .. base + n - 1.  Every wave's range is PER = H / 128 / kGKS
+// blocks (the launcher's condition), so the weight loads are uniform role
+// pointers + one 32-bit lane offset + an immediate per block.
+template <int PER>
+__device__ __forceinline__ void up_block_mx(const GroupedArgs& p, const void* const* wp, int rt, bool rok, int n,
+                                            int base, uint8_t* lds) {
+  static_assert(PER <= kGxMaxBlocks, "blocks held per wave");
+  const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int item = wave / kGKS, ks = wave % kGKS;
+  const int K = p.H, nblk = K / 128;
+  const int k0 = ks * PER;
+  uint8_t* xq = lds;
+  uint32_t* xe = reinterpret_cast<uint32_t*>(lds + static_cast<size_t>(nblk) * 16 * 128);
+  float (*red)[kGKS][2][64][4] = reinterpret_cast<float (*)[kGKS][2][64][4]>(lds);
+  // the wave's range within each role (uniform), this lane's row within it (32 bits: one role < 4 GB)
+  const uint8_t* W1 = static_cast<const uint8_t*>(wp[0]) + k0 * 64;
+  const uint8_t* S1 = static_cast<const uint8_t*>(wp[1]) + k0 * 4;
+  const uint8_t* W3 = static_cast<const uint8_t*>(wp[3]) + k0 * 64;
+  const uint8_t* S3 = static_cast<const uint8_t*>(wp[4]) + k0 * 4;
+  const uint32_t row = rok ? static_cast<uint32_t>(rt * 16 + r16) : 0u;
+  const uint32_t cb = row * static_cast<uint32_t>(K / 2) + static_cast<uint32_t>(g4 * 16);
+  const uint32_t sb = row * static_cast<uint32_t>(K / 32);
+  const uint8_t* xs = p.xp + static_cast<size_t>(p.T) * 2 * K;   // the planes' E8M0 bytes
+  for (int c0 = 0; c0 < n; c0 += kGNC) {
+    const int cols = min(kGNC, n - c0);
+    // the wave's whole K range of both roles first (every product waits for it
+    // anyway), then the tile's plane rows (16-byte chunks) and their exponents
+    u32x4 c1[PER], c3[PER];
+    uint32_t s1[PER], s3[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      c1[i] = ldg16(W1 + cb + i * 64);
+      c3[i] = ldg16(W3 + cb + i * 64);
+      s1[i] = ldg<uint32_t>(S1 + sb + i * 4);
+      s3[i] = ldg<uint32_t>(S3 + sb + i * 4);
+    }
+    asm volatile("" ::: "memory");
+    {
+      const int cpr = K / 16, chunks = 2 * cols * cpr;
+      for (int ch = tid; ch < chunks; ch += 4 * kGW * 64) {
+        u32x4 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int cc = min(ch + q * kGW * 64, chunks - 1);   // no condition on the load
+          const int col = cc / cpr, j = cc % cpr;
+          const int tok = p.xrow[base + c0 + (col >> 1)];
+          v[q] = ldg16(p.xp + static_cast<size_t>(2 * tok + (col & 1)) * K + 16 * j);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int cc = ch + q * kGW * 64;
+          if (cc < chunks) {
+            const int col = cc / cpr, j = cc % cpr;   // j: 16-byte chunk of the row, block j / 8
+            *reinterpret_cast<u32x4*>(xq + ((j >> 3) * 16 + col) * 128 + 16 * (j & 7)) = v[q];
+          }
+        }
+      }
+      const int words = 2 * cols * nblk;
+      for (int wi = tid; wi < words; wi += kGW * 64) {
+        const int col = wi / nblk, kb = wi % nblk;
+        const int tok = p.xrow[base + c0 + (col >> 1)];
+        xe[kb * 16 + col] = ldg<uint32_t>(xs + static_cast<size_t>(2 * tok + (col & 1)) * (K / 32) + 4 * kb);
+      }
+    }
+    __syncthreads();
+    // B column of this lane: plane r16 & 1 of tile row r16 >> 1 (columns past
+    // the tile's rows repeat its last one; their results are not stored)
+    const int bc = min(r16, 2 * cols - 1);
+    f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int col = (k0 + i) * 16 + bc;
+      const u32x4* src = reinterpret_cast<const u32x4*>(xq + col * 128 + g4 * 32);
+      const u32x4 blo = src[0], bhi = src[1];
+      const uint32_t bs = (xe[col] >> (8 * g4)) & 0xffu;
+      ag = mx_mfma(c1[i], (s1[i] >> (8 * g4)) & 0xffu, blo, bhi, bs, ag);
+      au = mx_mfma(c3[i], (s3[i] >> (8 * g4)) & 0xffu, blo, bhi, bs, au);
+    }
+    __syncthreads();   // every wave is done with the planes
+    *reinterpret_cast<f32x4*>(&red[item][ks][0][lane][0]) = ag;
+    *reinterpret_cast<f32x4*>(&red[item][ks][1][lane][0]) = au;
+    __syncthreads();
+    if (ks == 0) {
+#pragma unroll
+      for (int w = 1; w < kGKS; ++w) {
+        ag += *reinterpret_cast<const f32x4*>(&red[item][w][0][lane][0]);
+        au += *reinterpret_cast<const f32x4*>(&red[item][w][1][lane][0]);
+      }
+      float g[4], u[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {   // the row's two plane columns (lanes 2r, 2r + 1)
+        g[q] = ag[q] + lane_xor1(ag[q]);
+        u[q] = au[q] + lane_xor1(au[q]);
+      }
+      const int rr = r16 >> 1;
+      if (rok && (r16 & 1) == 0 && rr < cols) {
+        const int r = base + c0 + rr;   // dispatch row
+        const float wr = p.wrow[r];
+        uint16_t hh[4], hl[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) split_bf16(silu_clamped(g[q], u[q], p.limit) * wr, hh[q], hl[q]);
+        const int64_t off = static_cast<int64_t>(r) * p.I + rt * 16 + 4 * g4;
+        *reinterpret_cast<uint2*>(p.h_hi + off) = uint2{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16)};
+        *reinterpret_cast<uint2*>(p.h_lo + off) = uint2{hl[0] | (uint32_t(hl[1]) << 16), hl[2] | (uint32_t(hl[3]) << 16)};
+      }
+    }
+    __syncthreads();   // the next column tile reuses the LDS
+  }
+}
+
 // Blocks [0, up_shared): the shared expert (bf16 w1/w3, all T tokens); the
 // others: up_groups blocks per slot.
 template <typename Raw>
@@ -364,6 +532,19 @@ __global__ __launch_bounds__(kGW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
     if (p.q3f) {   // one row tile per block (up_groups = I / 16)
       const int rt1 = rb % p.up_groups;
       up_block_q3f(p, wp, rt1, rt1 < p.I / 16, d->n_tok, d->tok_base, lds_g);
+      return;
+    }
+  }
+  if constexpr (std::is_same_v<Raw, RawFP4>) {
+    if (p.mx) {
+      uint8_t* lds = reinterpret_cast<uint8_t*>(lds_g);
+      const bool rok = rt < p.I / 16;
+      switch (p.mx) {   // blocks per wave: H / 128 / kGKS
+        case 2: up_block_mx<2>(p, wp, rt, rok, d->n_tok, d->tok_base, lds); break;
+        case 4: up_block_mx<4>(p, wp, rt, rok, d->n_tok, d->tok_base, lds); break;
+        case 6: up_block_mx<6>(p, wp, rt, rok, d->n_tok, d->tok_base, lds); break;
+        default: up_block_mx<8>(p, wp, rt, rok, d->n_tok, d->tok_base, lds); break;
+      }
       return;
     }
   }
@@ -616,13 +797,28 @@ k_down_grouped(GroupedArgs p) {
 // The factored q3 gate/up: every wave's K range whole superblocks.
 bool up_q3f(const dsk_moe_desc& d) { return d.quant == DSK_QUANT_Q3 && d.hidden % (kQ3gKS * 512) == 0; }
 
+// The FP4 gate/up on scaled MFMAs: bf16 x (planes made from it), every wave's
+// K range 2, 4, 6 or 8 whole blocks (up_block_mx's instances).
+bool up_mx(const dsk_moe_desc& d) {
+  const int per = d.hidden / 128 / kGKS;
+  return d.quant == DSK_QUANT_FP4 && d.x_dtype == DSK_DTYPE_BF16 && d.hidden % (kGKS * 256) == 0 &&
+         per >= 2 && per <= kGxMaxBlocks;
+}
+
 size_t up_lds(const dsk_moe_desc& d) {
   const size_t x_tile = static_cast<size_t>(kGNC) * (d.hidden + 8) * 2;
   const size_t red = static_cast<size_t>(kGI) * kGKS * 2 * 64 * 4 * sizeof(float);
   // factored q3: the x tile, its group sums [H/128][8][2][2] f32, 64 zero bytes
   const size_t q3f = x_tile + static_cast<size_t>(d.hidden / 128) * kQ3fMaxTokens * 16 + 64;
-  const size_t base = x_tile > red ? x_tile : red;
+  size_t base = x_tile > red ? x_tile : red;
+  if (up_mx(d) && gx_lds_bytes(d.hidden) > base) base = gx_lds_bytes(d.hidden);
   return up_q3f(d) && q3f > base ? q3f : base;
+}
+
+hipError_t launch_x_planes(const dsk_moe_desc& d, const GroupedArgs& p, hipStream_t s) {
+  const int64_t n = static_cast<int64_t>(d.tokens) * (d.hidden / 8);
+  launch_kernel(k_x_planes, static_cast<unsigned>((n + 255) / 256), 256, 0, s, p.x, d.tokens, d.hidden, p.xp);
+  return hipGetLastError();
 }
 
 // The factored q3 down: K = I whole superblocks.
@@ -670,6 +866,8 @@ GroupedArgs grouped_args(const dsk_moe_desc& d, const Workspace& L, const Expert
   p.ys = reinterpret_cast<float*>(a.ws + L.ys);
   p.q3f = up_q3f(d) ? 1 : 0;
   p.q3fd = down_q3f(d) ? 1 : 0;
+  p.mx = up_mx(d) ? d.hidden / 128 / kGKS : 0;
+  p.xp = reinterpret_cast<uint8_t*>(a.ws + L.xp);
   p.up_groups = p.q3f ? d.inter / 16 : d.inter / 16 / kGI;   // factored q3: one row tile per block
   p.up_shared = d.inter_shared / 16 / kGI;
   p.dn_groups = d.hidden / 16 / kDI;
@@ -702,6 +900,7 @@ hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, con
   hipError_t e;
   if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   for (int r = 0; r < repeat; ++r) {
+    if (p.mx && (e = launch_x_planes(d, p, s)) != hipSuccess) return e;
     if (d.quant == DSK_QUANT_Q3) launch_kernel(k_up_grouped<RawQ3>, up_blocks, kGW * 64, ul, s, p);
     else launch_kernel(k_up_grouped<RawFP4>, up_blocks, kGW * 64, ul, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -718,6 +917,10 @@ hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, c
   const unsigned blocks = static_cast<unsigned>(max_slots(d) * p.up_groups);
   const size_t lds = up_lds(d);
   for (int r = 0; r < repeat; ++r) {
+    if (p.mx) {
+      const hipError_t e = launch_x_planes(d, p, s);
+      if (e != hipSuccess) return e;
+    }
     if (d.quant == DSK_QUANT_Q3) launch_kernel(k_up_grouped<RawQ3>, blocks, kGW * 64, lds, s, p);
     else launch_kernel(k_up_grouped<RawFP4>, blocks, kGW * 64, lds, s, p);
     const hipError_t e = hipGetLastError();
