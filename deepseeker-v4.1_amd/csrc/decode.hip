@@ -1965,7 +1965,9 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   if ((e = stage_open(kStageDown)) != hipSuccess) return e;
   if (d.tokens >= kDecodeGroupedDownMin && grouped_path(d)) {
     // routed and shared down per slot (one output row per dispatch row), then the combine
-    if ((e = launch_grouped_down(d, L, a, a.route.desc, s, repeat)) != hipSuccess) return e;
+    // h in FP8 planes where the grouped gate/up wrote it (from kDecodeGroupedUpMin tokens)
+    const bool hpl = d.tokens >= kDecodeGroupedUpMin && grouped_h_planes(d);
+    if ((e = launch_grouped_down(d, L, a, a.route.desc, s, repeat, hpl)) != hipSuccess) return e;
     return launch_combine(d, L, a, s, repeat);
   }
   if (mx) {

@@ -146,6 +146,7 @@ struct Workspace {
   size_t ys;                // shared output           [T][H]   f32
   size_t shared_x;          // decode pipeline: shared output [T][H] (x dtype)
   size_t xp;                // grouped FP4 gate/up: x as FP8 planes [T][2][H] + E8M0 [T][2][H/32]
+  size_t hp;                // grouped FP4: h as FP8 planes [T*k][3][I] + E8M0 [T*k][3][I/32]
   size_t pf_tiles;          // prefill GEMM tile list  [2 + 2 * prefill_max_tiles]
   size_t total;
 };
@@ -327,8 +328,11 @@ hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, con
 hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                     const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
                                     int repeat);
+// h_planes: the routed h is in FP8 planes (the grouped gate/up ran and grouped_h_planes).
 hipError_t launch_grouped_down(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
-                               const SlotDesc* desc, hipStream_t s, int repeat);
+                               const SlotDesc* desc, hipStream_t s, int repeat, bool h_planes);
+// The grouped FP4 gate/up writes h as FP8 planes and the down reads them on scaled MFMAs.
+bool grouped_h_planes(const dsk_moe_desc& d);
 // out[t] = cast(sum of the token's routed rows y in ascending expert id +
 // shared); the combine stage.
 hipError_t launch_combine(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a, hipStream_t s,

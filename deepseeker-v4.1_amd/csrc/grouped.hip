@@ -50,6 +50,8 @@ struct GroupedArgs {
   int q3fd;                                      // q3 down in the factored form (down_block_q3f)
   int mx;                                        // FP4 gate/up on scaled MFMAs: blocks per wave, or 0
   uint8_t* xp;                                   // mx: x as FP8 planes [T][2][H], then E8M0 [T][2][H/32]
+  int hplanes;                                   // FP4 slots' h as FP8 planes, the down on scaled MFMAs
+  uint8_t* hp;                                   // hplanes: [T*k][3][I], then E8M0 [T*k][3][I/32]
 };
 
 // K blocks per weight batch, two batches in flight per wave, within the
@@ -421,6 +423,8 @@ __device__ __forceinline__ void up_block_mx(const GroupedArgs& p, const void* co
   const uint32_t cb = row * static_cast<uint32_t>(K / 2) + static_cast<uint32_t>(g4 * 16);
   const uint32_t sb = row * static_cast<uint32_t>(K / 32);
   const uint8_t* xs = p.xp + static_cast<size_t>(p.T) * 2 * K;   // the planes' E8M0 bytes
+  // the h planes' 16-row maxima [kGI][16] f32, past the partial sums
+  float* gmx = reinterpret_cast<float*>(lds + static_cast<size_t>(kGI) * kGKS * 2 * 64 * 4 * sizeof(float));
   for (int c0 = 0; c0 < n; c0 += kGNC) {
     const int cols = min(kGNC, n - c0);
     // the wave's whole K range of both roles first (every product waits for it
@@ -480,6 +484,7 @@ __device__ __forceinline__ void up_block_mx(const GroupedArgs& p, const void* co
     *reinterpret_cast<f32x4*>(&red[item][ks][0][lane][0]) = ag;
     *reinterpret_cast<f32x4*>(&red[item][ks][1][lane][0]) = au;
     __syncthreads();
+    float hv[4] = {0.f, 0.f, 0.f, 0.f};   // h of this lane's column and rows (ks == 0 waves)
     if (ks == 0) {
 #pragma unroll
       for (int w = 1; w < kGKS; ++w) {
@@ -493,15 +498,53 @@ __device__ __forceinline__ void up_block_mx(const GroupedArgs& p, const void* co
         u[q] = au[q] + lane_xor1(au[q]);
       }
       const int rr = r16 >> 1;
-      if (rok && (r16 & 1) == 0 && rr < cols) {
-        const int r = base + c0 + rr;   // dispatch row
-        const float wr = p.wrow[r];
+      const int r = base + c0 + min(rr, cols - 1);   // dispatch row (columns past the tile: its last)
+      const float wr = p.wrow[r];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) hv[q] = silu_clamped(g[q], u[q], p.limit) * wr;
+      if (!p.hplanes && rok && (r16 & 1) == 0 && rr < cols) {
         uint16_t hh[4], hl[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) split_bf16(silu_clamped(g[q], u[q], p.limit) * wr, hh[q], hl[q]);
+        for (int q = 0; q < 4; ++q) split_bf16(hv[q], hh[q], hl[q]);
         const int64_t off = static_cast<int64_t>(r) * p.I + rt * 16 + 4 * g4;
         *reinterpret_cast<uint2*>(p.h_hi + off) = uint2{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16)};
         *reinterpret_cast<uint2*>(p.h_lo + off) = uint2{hl[0] | (uint32_t(hl[1]) << 16), hl[2] | (uint32_t(hl[3]) << 16)};
+      }
+      if (p.hplanes) {
+        // one exponent per (row, 32-row group): the largest |h| of this tile's 16 rows
+        float m = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) m = fmaxf(m, fabsf(hv[q]));
+        m = max_over_rows(m);
+        // (addresses from a copy of the lane id made here: forms hoisted out of the
+        // column loop stayed live across the weight stream and spilled)
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        if (ln < 16) gmx[item * 16 + ln] = m;
+      }
+    }
+    if (p.hplanes) {
+      // h as three FP8 planes per dispatch row (the MX down's B operand): the
+      // block's two row tiles are one 32-row exponent group
+      __syncthreads();
+      int ln = lane;   // (as above)
+      asm volatile("" : "+v"(ln));
+      const int c16 = ln & 15, q4 = ln >> 4, rr = c16 >> 1;
+      if (ks == 0 && rok && (c16 & 1) == 0 && rr < cols) {
+        const int r = base + c0 + rr;
+        const int e = fp8_plane_exp(fmaxf(gmx[c16], gmx[16 + c16]));
+        uint32_t w[3];
+        fp8_planes4<3>(hv, e, w);
+        const int I = p.I, i0 = rt * 16 + 4 * q4;
+        uint8_t* dst = p.hp + static_cast<size_t>(3 * r) * I + (i0 >> 7) * 128 + b_perm(i0 & 127);
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) *reinterpret_cast<uint32_t*>(dst + static_cast<size_t>(pl) * I) = w[pl];
+        if (item == 0 && q4 == 0) {
+          uint8_t* sc = p.hp + static_cast<size_t>(p.T) * p.k * 3 * I;
+#pragma unroll
+          for (int pl = 0; pl < 3; ++pl)
+            sc[static_cast<size_t>(3 * r + pl) * (I / 32) + (i0 >> 5)] = static_cast<uint8_t>(e8m0_byte(e - 4 * pl));
+        }
       }
     }
     __syncthreads();   // the next column tile reuses the LDS
@@ -649,6 +692,91 @@ __device__ __forceinline__ void down_block(const GroupedArgs& p, LoadW load_w, W
   }
 }
 
+// Down of one FP4 slot block on scaled MFMAs: row tile rt (output rows
+// 16 rt ..) of w2 over K = I = 128 NKB, for the n dispatch rows base ..
+// base + n - 1, h as the gate/up's three FP8 planes per row (B column 3r + p:
+// five rows per column tile).  The wave's whole range of w2 codes and E8M0
+// words is issued first, then the tile's plane rows are copied into LDS;
+// one MFMA per block, a row's three plane columns added in order.  Writes
+// one float32 output row per dispatch row, as down_block.
+constexpr int kGdRows = 5;   // dispatch rows of an MX down column tile (15 B columns)
+
+__host__ __device__ inline size_t gd_lds_bytes(int I) { return static_cast<size_t>(I / 128) * 16 * (128 + 4); }
+
+template <int NKB>
+__device__ __forceinline__ void down_block_mx(const GroupedArgs& p, int slot, int rt, int n, int base,
+                                              uint8_t* lds) {
+  const int tid = threadIdx.x, lane = __lane_id();
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int I = p.I;
+  uint8_t* hq = lds;
+  uint32_t* he = reinterpret_cast<uint32_t*>(lds + static_cast<size_t>(NKB) * 16 * 128);
+  const uint8_t* W = static_cast<const uint8_t*>(desc_ptr(p.desc, slot, 6));
+  const uint8_t* S = static_cast<const uint8_t*>(desc_ptr(p.desc, slot, 7));
+  const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
+  const uint32_t cb = row * static_cast<uint32_t>(I / 2) + static_cast<uint32_t>(g4 * 16);
+  const uint32_t sb = row * static_cast<uint32_t>(I / 32);
+  const uint8_t* hs = p.hp + static_cast<size_t>(p.T) * p.k * 3 * I;   // the planes' E8M0 bytes
+  for (int c0 = 0; c0 < n; c0 += kGdRows) {
+    const int cols = min(kGdRows, n - c0);
+    u32x4 c[NKB];
+    uint32_t sc[NKB];
+#pragma unroll
+    for (int i = 0; i < NKB; ++i) {
+      c[i] = ldg16(W + cb + i * 64);
+      sc[i] = ldg<uint32_t>(S + sb + i * 4);
+    }
+    asm volatile("" ::: "memory");
+    {
+      const int cpr = I / 16, chunks = 3 * cols * cpr;
+      for (int ch = tid; ch < chunks; ch += 4 * kDW * 64) {
+        u32x4 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int cc = min(ch + q * kDW * 64, chunks - 1);   // no condition on the load
+          const int col = cc / cpr, j = cc % cpr;
+          v[q] = ldg16(p.hp + static_cast<size_t>(3 * (base + c0) + col) * I + 16 * j);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int cc = ch + q * kDW * 64;
+          if (cc < chunks) {
+            const int col = cc / cpr, j = cc % cpr;
+            *reinterpret_cast<u32x4*>(hq + ((j >> 3) * 16 + col) * 128 + 16 * (j & 7)) = v[q];
+          }
+        }
+      }
+      const int words = 3 * cols * NKB;
+      for (int wi = tid; wi < words; wi += kDW * 64) {
+        const int col = wi / NKB, kb = wi % NKB;
+        he[kb * 16 + col] = ldg<uint32_t>(hs + static_cast<size_t>(3 * (base + c0) + col) * (I / 32) + 4 * kb);
+      }
+    }
+    __syncthreads();
+    // B column of this lane: plane r16 % 3 of tile row r16 / 3 (columns past
+    // the tile's rows repeat its last one; their results are not stored)
+    const int bc = min(r16, 3 * cols - 1);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NKB; ++i) {
+      const int col = i * 16 + bc;
+      const u32x4* src = reinterpret_cast<const u32x4*>(hq + col * 128 + g4 * 32);
+      const u32x4 blo = src[0], bhi = src[1];
+      const uint32_t bs = (he[col] >> (8 * g4)) & 0xffu;
+      acc = mx_mfma(c[i], (sc[i] >> (8 * g4)) & 0xffu, blo, bhi, bs, acc);
+    }
+    // row t = r16 of this lane group: columns 3t .. 3t + 2, added in order
+    const int t = min(r16, cols - 1), gb = lane & 48;
+    f32x4 ra;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      ra[q] = (__shfl(acc[q], gb + 3 * t, 64) + __shfl(acc[q], gb + 3 * t + 1, 64)) + __shfl(acc[q], gb + 3 * t + 2, 64);
+    if (r16 < cols)
+      *reinterpret_cast<f32x4*>(p.y + static_cast<int64_t>(base + c0 + r16) * p.H + rt * 16 + 4 * g4) = ra;
+    __syncthreads();   // the next column tile reuses the LDS
+  }
+}
+
 // Down of one q3 block in the factored form (as up_block_q3f): output row
 // tile rt (one wave) over all of K = I in 512-code superblocks (I % 512 ==
 // 0), two in flight; A operand row 2t + h on the hi plane and then the lo
@@ -789,6 +917,17 @@ k_down_grouped(GroupedArgs p) {
       return;
     }
   }
+  if constexpr (std::is_same_v<Raw, RawFP4>) {
+    if (p.hplanes) {
+      uint8_t* lds = reinterpret_cast<uint8_t*>(lds_g);
+      switch (p.I / 128) {   // blocks of K per wave (grouped_h_planes)
+        case 4: down_block_mx<4>(p, slot, rt, d->n_tok, d->tok_base, lds); break;
+        case 8: down_block_mx<8>(p, slot, rt, d->n_tok, d->tok_base, lds); break;
+        default: down_block_mx<16>(p, slot, rt, d->n_tok, d->tok_base, lds); break;
+      }
+      return;
+    }
+  }
   auto load_w = [&](Raw& r, uint32_t row, int kc) { load_w2_nc(r, p.desc, slot, row, p.I, kc); };
   auto wptr = [&](int i) { return desc_ptr(p.desc, slot, 6 + i); };   // 0: w2 codes, 1: w2 scales
   down_block<Raw>(p, load_w, wptr, rt, d->n_tok, d->tok_base, false, lds_g);
@@ -804,6 +943,20 @@ bool up_mx(const dsk_moe_desc& d) {
   return d.quant == DSK_QUANT_FP4 && d.x_dtype == DSK_DTYPE_BF16 && d.hidden % (kGKS * 256) == 0 &&
          per >= 2 && per <= kGxMaxBlocks;
 }
+
+}  // namespace
+
+// h as FP8 planes and the FP4 down on scaled MFMAs: the gate/up on scaled MFMAs
+// (up_mx), I a whole 4, 8 or 16 blocks (down_block_mx's instances), and at most
+// 256 dispatch rows: at 8 and 20 tokens (top-8) the down went 57.9 -> 50.5 and
+// 102.8 -> 88.6 us, at 64 it stayed at 185 us while the planes epilogue added
+// 8.6 us to the gate/up.
+bool grouped_h_planes(const dsk_moe_desc& d) {
+  return up_mx(d) && (d.inter == 512 || d.inter == 1024 || d.inter == 2048) &&
+         static_cast<int64_t>(d.tokens) * d.top_k <= 256;
+}
+
+namespace {
 
 size_t up_lds(const dsk_moe_desc& d) {
   const size_t x_tile = static_cast<size_t>(kGNC) * (d.hidden + 8) * 2;
@@ -832,7 +985,9 @@ size_t down_lds(const dsk_moe_desc& d) {
   // factored q3: the h tile of I, its group sums [I/128][8][2][2] f32, 64 zero bytes
   const size_t q3f = 2 * static_cast<size_t>(kGNC) * (d.inter + 8) * 2 +
                      static_cast<size_t>(d.inter / 128) * kQ3fMaxTokens * 16 + 64;
-  return down_q3f(d) && q3f > base ? q3f : base;
+  const size_t mx = grouped_h_planes(d) ? gd_lds_bytes(d.inter) : 0;
+  const size_t b2 = mx > base ? mx : base;
+  return down_q3f(d) && q3f > b2 ? q3f : b2;
 }
 
 }  // namespace
@@ -868,6 +1023,8 @@ GroupedArgs grouped_args(const dsk_moe_desc& d, const Workspace& L, const Expert
   p.q3fd = down_q3f(d) ? 1 : 0;
   p.mx = up_mx(d) ? d.hidden / 128 / kGKS : 0;
   p.xp = reinterpret_cast<uint8_t*>(a.ws + L.xp);
+  p.hplanes = 0;   // set by the launchers where the grouped gate/up writes h
+  p.hp = reinterpret_cast<uint8_t*>(a.ws + L.hp);
   p.up_groups = p.q3f ? d.inter / 16 : d.inter / 16 / kGI;   // factored q3: one row tile per block
   p.up_shared = d.inter_shared / 16 / kGI;
   p.dn_groups = d.hidden / 16 / kDI;
@@ -894,7 +1051,8 @@ hipError_t grouped_down(const dsk_moe_desc& d, const GroupedArgs& p, hipStream_t
 hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                   const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
                                   int repeat) {
-  const GroupedArgs p = grouped_args(d, L, a, desc, xrow, wrow);
+  GroupedArgs p = grouped_args(d, L, a, desc, xrow, wrow);
+  p.hplanes = grouped_h_planes(d) ? 1 : 0;
   const unsigned up_blocks = static_cast<unsigned>(p.up_shared + max_slots(d) * p.up_groups);
   const size_t ul = up_lds(d);
   hipError_t e;
@@ -914,6 +1072,7 @@ hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, c
                                     int repeat) {
   GroupedArgs p = grouped_args(d, L, a, desc, xrow, wrow);
   p.up_shared = 0;
+  p.hplanes = grouped_h_planes(d) ? 1 : 0;
   const unsigned blocks = static_cast<unsigned>(max_slots(d) * p.up_groups);
   const size_t lds = up_lds(d);
   for (int r = 0; r < repeat; ++r) {
@@ -930,8 +1089,10 @@ hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, c
 }
 
 hipError_t launch_grouped_down(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
-                               const SlotDesc* desc, hipStream_t s, int repeat) {
-  return grouped_down(d, grouped_args(d, L, a, desc, nullptr, nullptr), s, repeat);
+                               const SlotDesc* desc, hipStream_t s, int repeat, bool h_planes) {
+  GroupedArgs p = grouped_args(d, L, a, desc, nullptr, nullptr);
+  p.hplanes = h_planes ? 1 : 0;
+  return grouped_down(d, p, s, repeat);
 }
 
 }  // namespace dsk
