@@ -425,33 +425,34 @@ __device__ __forceinline__ void up_block_mx(const GroupedArgs& p, const void* co
   const uint8_t* xs = p.xp + static_cast<size_t>(p.T) * 2 * K;   // the planes' E8M0 bytes
   // the h planes' 16-row maxima [kGI][16] f32, past the partial sums
   float* gmx = reinterpret_cast<float*>(lds + static_cast<size_t>(kGI) * kGKS * 2 * 64 * 4 * sizeof(float));
+  // the wave's whole K range of both roles first (every product waits for it
+  // anyway), held across the slot's column tiles; then per tile its plane rows
+  // (16-byte chunks) and their exponents
+  u32x4 c1[PER], c3[PER];
+  uint32_t s1[PER], s3[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    c1[i] = ldg16(W1 + cb + i * 64);
+    c3[i] = ldg16(W3 + cb + i * 64);
+    s1[i] = ldg<uint32_t>(S1 + sb + i * 4);
+    s3[i] = ldg<uint32_t>(S3 + sb + i * 4);
+  }
   for (int c0 = 0; c0 < n; c0 += kGNC) {
     const int cols = min(kGNC, n - c0);
-    // the wave's whole K range of both roles first (every product waits for it
-    // anyway), then the tile's plane rows (16-byte chunks) and their exponents
-    u32x4 c1[PER], c3[PER];
-    uint32_t s1[PER], s3[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      c1[i] = ldg16(W1 + cb + i * 64);
-      c3[i] = ldg16(W3 + cb + i * 64);
-      s1[i] = ldg<uint32_t>(S1 + sb + i * 4);
-      s3[i] = ldg<uint32_t>(S3 + sb + i * 4);
-    }
     asm volatile("" ::: "memory");
     {
       const int cpr = K / 16, chunks = 2 * cols * cpr;
-      for (int ch = tid; ch < chunks; ch += 4 * kGW * 64) {
-        u32x4 v[4];
+      for (int ch = tid; ch < chunks; ch += 2 * kGW * 64) {   // two chunks per thread in flight
+        u32x4 v[2];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < 2; ++q) {
           const int cc = min(ch + q * kGW * 64, chunks - 1);   // no condition on the load
           const int col = cc / cpr, j = cc % cpr;
           const int tok = p.xrow[base + c0 + (col >> 1)];
           v[q] = ldg16(p.xp + static_cast<size_t>(2 * tok + (col & 1)) * K + 16 * j);
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < 2; ++q) {
           const int cc = ch + q * kGW * 64;
           if (cc < chunks) {
             const int col = cc / cpr, j = cc % cpr;   // j: 16-byte chunk of the row, block j / 8
