@@ -63,6 +63,7 @@ struct DecodeArgs {
   void* out;                           // [T][H] x dtype
   int up_tiles;                        // I / 16
   ResNorm rn; int norm;                // norm: k_gate_shared computes x from the residual stream
+  uint8_t* xp;                         // k_route_shared: also write x's FP8 planes here (or null)
 };
 
 // One x chunk (8 values at column `col` of token row t) into the LDS planes.
@@ -482,6 +483,15 @@ __global__ __launch_bounds__(kRsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
   const int rt = static_cast<int>(blockIdx.x) - 1;
   if (p.T <= 8) shared_up_tile<kF32, kRsW, 8>(p, rt, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave, r16, g4);
   else shared_up_tile<kF32, kRsW, 16>(p, rt, xh, xl, xs, xreg, xv, lds_up, tid, lane, wave, r16, g4);
+  if constexpr (!kF32) {
+    if (p.xp && tid < 16) {
+      // x's FP8 planes for the grouped FP4 gate/up, 16 chunks per tile block (the
+      // 16 lanes iterate together: every group of four chunks is exchanged whole)
+      const int n = p.T * (p.H / 8), stride = (static_cast<int>(gridDim.x) - 1) * 16;
+      for (int c = rt * 16 + tid; c - tid < n; c += stride)
+        x_planes_chunk(static_cast<const uint16_t*>(p.x), p.T, p.H, min(c, n - 1), c < n, p.xp);
+    }
+  }
 }
 
 // Routed gate/up of the decode pipeline.  Each block takes kUpItems row
@@ -1797,6 +1807,15 @@ __global__ __launch_bounds__(kDownW * 64) void k_down_decode(DecodeArgs p) {
   }
 }
 
+// The routing kernel of the decode pipeline's non-MX form (k_route_shared) also
+// writes x's FP8 planes for the grouped FP4 gate/up that follows it (saves
+// that kernel's own launch): from kDecodeGroupedUpMin tokens, with shared tile
+// blocks to do it.
+bool route_writes_x_planes(const dsk_moe_desc& d) {
+  return d.tokens >= kDecodeGroupedUpMin && d.x_dtype == DSK_DTYPE_BF16 && d.inter_shared > 0 &&
+         grouped_path(d) && grouped_up_mx(d);
+}
+
 DecodeArgs decode_args(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a) {
   DecodeArgs p{};
   p.T = d.tokens; p.H = d.hidden; p.I = d.inter; p.Is = d.inter_shared; p.k = d.top_k;
@@ -1893,6 +1912,7 @@ hipError_t launch_route_shared(const dsk_moe_desc& d, const Workspace& L, const 
                                int repeat) {
   DecodeArgs p = decode_args(d, L, a);
   const unsigned blocks = static_cast<unsigned>(1 + shared_up_tiles(p.T, p.Is));
+  if (route_writes_x_planes(d)) p.xp = reinterpret_cast<uint8_t*>(a.ws + L.xp);
   // the pointer table goes to LDS only where the activation planes leave room: prefetching
   // all of it beside the shared tiles' stream was slower (q3 B=1 route stage 10.2 -> 11.1 us)
   // than the slot map's dependent table loads
@@ -1928,7 +1948,8 @@ hipError_t launch_experts_decode(const dsk_moe_desc& d, const Workspace& L, cons
   const unsigned q3f2_blocks = static_cast<unsigned>(max_slots * ((p.up_tiles + 2 * kQ3fItems - 1) / (2 * kQ3fItems)));
   if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   if (d.tokens >= kDecodeGroupedUpMin && grouped_path(d)) {
-    e = launch_grouped_up_routed(d, L, a, a.route.desc, a.route.xrow, a.route.wrow, s, repeat);
+    e = launch_grouped_up_routed(d, L, a, a.route.desc, a.route.xrow, a.route.wrow, s, repeat,
+                                 route_writes_x_planes(d));
     if (e != hipSuccess) return e;
   } else {
     // q3 up to 8 tokens: the factored kernel

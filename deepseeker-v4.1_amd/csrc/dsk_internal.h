@@ -325,9 +325,12 @@ hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, con
 // Its kernels one at a time, for the decode pipeline: the routed gate/up
 // alone (from kDecodeGroupedUpMin tokens) and the down (routed rows from h,
 // shared from hs; from kDecodeGroupedDownMin tokens).
+// x_planes_ready: the routing kernel already wrote x's FP8 planes (grouped_up_mx).
 hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                     const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
-                                    int repeat);
+                                    int repeat, bool x_planes_ready);
+// The grouped FP4 gate/up takes x as FP8 planes (Workspace::xp).
+bool grouped_up_mx(const dsk_moe_desc& d);
 // h_planes: the routed h is in FP8 planes (the grouped gate/up ran and grouped_h_planes).
 hipError_t launch_grouped_down(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                const SlotDesc* desc, hipStream_t s, int repeat, bool h_planes);

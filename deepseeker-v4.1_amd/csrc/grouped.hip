@@ -356,41 +356,14 @@ __device__ __forceinline__ void up_block_q3f(const GroupedArgs& p, const void* c
 // leaves as the bf16 hi / lo pair of the other gate/up paths.
 constexpr int kGxMaxBlocks = 8;     // K blocks per wave held (H <= kGKS * 8 * 128)
 
-// Token t's two FP8 planes of x (v ~ q0 2^e + q1 2^(e-4) per 32-value group,
-// e = ilogb(group max) - 7, mx.h) into xp: plane row (t, p) holds H bytes, each
-// 128-value block in the B-operand byte order (b_perm), then the E8M0 bytes
-// of every (t, p, group).  One thread per 8 values; a group's four chunks are
-// in consecutive lanes.
+// x's two FP8 planes (v ~ q0 2^e + q1 2^(e-4) per 32-value group, e =
+// ilogb(group max) - 7, mx.h) into xp (x_planes_chunk's layout), one thread
+// per 8 values.
 __global__ __launch_bounds__(256) void k_x_planes(const uint16_t* __restrict__ x, int T, int H,
                                                   uint8_t* __restrict__ xp) {
-  const int cpr = H / 8, n = T * cpr;
+  const int n = T * (H / 8);
   const int c0 = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
-  const int c = min(c0, n - 1);   // every lane takes part in the group exchange
-  const int t = c / cpr, k8 = (c % cpr) * 8;
-  const u32x4 v = ldg16(x + static_cast<int64_t>(t) * H + k8);
-  const float f0[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
-                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
-  const float f1[4] = {__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
-                       __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u)};
-  float m = 0.0f;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) m = fmaxf(m, fmaxf(fabsf(f0[q]), fabsf(f1[q])));
-  m = fmaxf(m, __shfl_xor(m, 1, 64));
-  m = fmaxf(m, __shfl_xor(m, 2, 64));
-  const int e = fp8_plane_exp(m);
-  uint32_t w0[2], w1[2];
-  fp8_planes4<2>(f0, e, w0);
-  fp8_planes4<2>(f1, e, w1);
-  if (c0 < n) {
-    const int kb = k8 >> 7, kk = k8 & 127;
-    uint8_t* scales = xp + static_cast<size_t>(T) * 2 * H;
-#pragma unroll
-    for (int pl = 0; pl < 2; ++pl) {
-      const size_t prow = static_cast<size_t>(2 * t + pl);
-      *reinterpret_cast<uint2*>(xp + prow * H + kb * 128 + b_perm(kk)) = uint2{w0[pl], w1[pl]};
-      if ((k8 & 31) == 0) scales[prow * (H / 32) + (k8 >> 5)] = static_cast<uint8_t>(e8m0_byte(e - 4 * pl));
-    }
-  }
+  x_planes_chunk(x, T, H, min(c0, n - 1), c0 < n, xp);   // every lane takes part in the group exchange
 }
 
 // LDS of up_block_mx: the column tile's planes [H/128][16][128] bytes, then
@@ -952,6 +925,8 @@ bool up_mx(const dsk_moe_desc& d) {
 // 256 dispatch rows: at 8 and 20 tokens (top-8) the down went 57.9 -> 50.5 and
 // 102.8 -> 88.6 us, at 64 it stayed at 185 us while the planes epilogue added
 // 8.6 us to the gate/up.
+bool grouped_up_mx(const dsk_moe_desc& d) { return up_mx(d); }
+
 bool grouped_h_planes(const dsk_moe_desc& d) {
   return up_mx(d) && (d.inter == 512 || d.inter == 1024 || d.inter == 2048) &&
          static_cast<int64_t>(d.tokens) * d.top_k <= 256;
@@ -1070,14 +1045,14 @@ hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, con
 
 hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                     const SlotDesc* desc, const int32_t* xrow, const float* wrow, hipStream_t s,
-                                    int repeat) {
+                                    int repeat, bool x_planes_ready) {
   GroupedArgs p = grouped_args(d, L, a, desc, xrow, wrow);
   p.up_shared = 0;
   p.hplanes = grouped_h_planes(d) ? 1 : 0;
   const unsigned blocks = static_cast<unsigned>(max_slots(d) * p.up_groups);
   const size_t lds = up_lds(d);
   for (int r = 0; r < repeat; ++r) {
-    if (p.mx) {
+    if (p.mx && !x_planes_ready) {
       const hipError_t e = launch_x_planes(d, p, s);
       if (e != hipSuccess) return e;
     }

@@ -113,4 +113,39 @@ __device__ __forceinline__ void fp8_planes4(const float (&v)[4], int e, uint32_t
   }
 }
 
+// Chunk c (8 values) of x [T][H] bf16 into the two-plane layout of the
+// grouped FP4 gate/up: plane row (t, p) holds H bytes, each 128-value block in
+// the B-operand byte order (b_perm), then the E8M0 bytes of every (t, p,
+// 32-group) after all plane rows.  The four chunks of a 32-group must be in
+// four consecutive lanes that all take part (the group maximum is exchanged);
+// `store` false: the lane takes part and writes nothing.
+__device__ __forceinline__ void x_planes_chunk(const uint16_t* x, int T, int H, int c, bool store, uint8_t* xp) {
+  const int cpr = H / 8;
+  const int t = c / cpr, k8 = (c % cpr) * 8;
+  const u32x4 v = *reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(t) * H + k8);
+  const float f0[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
+  const float f1[4] = {__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
+                       __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u)};
+  float m = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) m = fmaxf(m, fmaxf(fabsf(f0[q]), fabsf(f1[q])));
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  const int e = fp8_plane_exp(m);
+  uint32_t w0[2], w1[2];
+  fp8_planes4<2>(f0, e, w0);
+  fp8_planes4<2>(f1, e, w1);
+  if (store) {
+    const int kb = k8 >> 7, kk = k8 & 127;
+    uint8_t* scales = xp + static_cast<size_t>(T) * 2 * H;
+#pragma unroll
+    for (int pl = 0; pl < 2; ++pl) {
+      const size_t prow = static_cast<size_t>(2 * t + pl);
+      *reinterpret_cast<uint2*>(xp + prow * H + kb * 128 + b_perm(kk)) = uint2{w0[pl], w1[pl]};
+      if ((k8 & 31) == 0) scales[prow * (H / 32) + (k8 >> 5)] = static_cast<uint8_t>(e8m0_byte(e - 4 * pl));
+    }
+  }
+}
+
 }  // namespace dsk
