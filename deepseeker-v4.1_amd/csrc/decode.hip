@@ -27,7 +27,6 @@ constexpr int kUpXRegChunks = 1;       // x chunks per thread staged through reg
 constexpr int kUpBatch = 4;            // K blocks per weight batch (two batches in flight)
 constexpr int kDownW = 16;             // waves of a down block (split K = I and Is)
 constexpr int kDownGroup = 8;          // experts whose w2 blocks a wave holds at once
-constexpr int kDownHRegChunks = 2;     // h chunks per thread staged through registers
 // staged down kernel (all h rows in LDS)
 constexpr int kStW = 8;                // waves
 constexpr int kStKB = 2;               // K blocks of each expert per wave (I = kStW * kStKB * 128)

@@ -267,11 +267,6 @@ __device__ __forceinline__ void dma16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
                                    (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
-// 2 bytes, written zero-extended to the lane's 4-byte LDS slot
-__device__ __forceinline__ void dma2(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                   (__attribute__((address_space(3))) void*)lds, 2, 0, 0);
-}
 
 // All but the newest N loads of this wave have landed (in LDS, for the DMA
 // loads), its LDS reads are complete, then the workgroup barrier.
