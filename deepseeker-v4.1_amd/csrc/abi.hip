@@ -87,8 +87,13 @@ Workspace workspace_layout(const dsk_moe_desc& d) {
   L.shared_x = take(mx && Is > 0 ? T * H * 2 : 0);
   // the grouped FP4 gate/up's x planes: every batch the grouped path may take (below the
   // prefill GEMM), bf16 x
-  L.xp = take(d.quant == DSK_QUANT_FP4 && d.x_dtype == DSK_DTYPE_BF16 && !prefill_gemm(d) ? T * 2 * (H + H / 32) : 0);
-  L.hp = take(!prefill_gemm(d) && grouped_h_planes(d) ? N * 3 * (I + I / 32) : 0);
+  if (prefill_mx(d)) {
+    L.xp = take(T * (2 * H + H / 32));
+    L.hp = take(N * (2 * I + I / 32));
+  } else {
+    L.xp = take(d.quant == DSK_QUANT_FP4 && d.x_dtype == DSK_DTYPE_BF16 && !prefill_gemm(d) ? T * 2 * (H + H / 32) : 0);
+    L.hp = take(!prefill_gemm(d) && grouped_h_planes(d) ? N * 3 * (I + I / 32) : 0);
+  }
   L.pf_tiles = take(prefill_gemm(d) ? (2 + 2 * static_cast<size_t>(prefill_max_tiles(d))) * 4 : 0);
   L.disp_hist = take(dispatch_hist_ints(static_cast<int>(N), static_cast<int>(E)) * 4);
   L.total = o;

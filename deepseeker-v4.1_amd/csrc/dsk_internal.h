@@ -145,8 +145,10 @@ struct Workspace {
   size_t y;                 // routed outputs          [T*k][H] f32
   size_t ys;                // shared output           [T][H]   f32
   size_t shared_x;          // decode pipeline: shared output [T][H] (x dtype)
-  size_t xp;                // grouped FP4 gate/up: x as FP8 planes [T][2][H] + E8M0 [T][2][H/32]
-  size_t hp;                // grouped FP4: h as FP8 planes [T*k][3][I] + E8M0 [T*k][3][I/32]
+  size_t xp;                // grouped FP4 gate/up: x as FP8 planes [T][2][H] + E8M0 [T][2][H/32];
+                            // MX prefill: x as FP8 planes in stage rows [T][2H] + E8M0 [T][H/32]
+  size_t hp;                // grouped FP4: h as FP8 planes [T*k][3][I] + E8M0 [T*k][3][I/32];
+                            // MX prefill: h in stage rows [T*k][2I] + E8M0 [T*k][I/32]
   size_t pf_tiles;          // prefill GEMM tile list  [2 + 2 * prefill_max_tiles]
   size_t total;
 };
@@ -180,6 +182,11 @@ inline bool prefill_gemm(const dsk_moe_desc& d) {
          d.inter % 128 == 0 && d.inter_shared % 128 == 0;
 }
 int prefill_max_tiles(const dsk_moe_desc& d);
+// FP4 prefill GEMMs on the scaled FP4 x FP8 MFMAs (x and h as two FP8 planes;
+// K of both products a multiple of 512, the LDS DMA loop's).
+inline bool prefill_mx(const dsk_moe_desc& d) {
+  return prefill_gemm(d) && d.quant == DSK_QUANT_FP4 && d.hidden % 512 == 0 && d.inter % 512 == 0;
+}
 // The prefill GEMM's routed rows for the combine are rounded to bf16 when the
 // experts are FP4 (relative 2^-9 per row, inside the layer tolerance); q3
 // layers, whose dequantised weights are already rounded to bf16, and rows

@@ -30,12 +30,19 @@
 // x is bf16 (exact); h is rounded once to bf16 (relative 2^-9 per element),
 // where the decode and general kernels carry it as a bf16 hi/lo pair.
 //
+// FP4 experts with H and I multiples of 512 (and 16-byte aligned arrays) run
+// both products on the scaled FP4 x FP8 MFMA instead (the MX loop below):
+// x and h as two FP8 planes each, which hold their bf16 values exactly (see
+// the MX loop's note); on random data the part runs these at ~1.36x the
+// bf16 products' rate for the same work.  k_pf_planes writes x's planes
+// before the gate/up; the gate/up's epilogue writes h's.
+//
 // Tile list: one entry per 256 dispatch rows of every active expert, then the
 // shared expert's token tiles.  Workgroup b runs on XCD b mod 8; blocks are
 // mapped to (tile, weight-row tile) so that each XCD walks a contiguous range
 // with the row tiles of one token tile adjacent, which keeps that tile's
 // activations in the XCD's L2 while they are reused.
-#include "tile.h"
+#include "mx.h"
 
 namespace dsk {
 namespace {
@@ -311,15 +318,20 @@ __device__ __forceinline__ void wait_barrier_n(int n) {
 // [256][128 B] (stage st in buffer st % 3), three code buffers [256][64 B]
 // (stage pair g in buffer g % 3; 16-byte chunk q of row r at position
 // q ^ ((r >> 2) & 3)), two scale buffers [256][16 B] (stages 8G..8G+7 in
-// buffer G & 1, loaded by waves 0-3).
-struct DmaFp4 {
+// buffer G & 1, loaded by waves 0-3).  kMx: the token tile holds the
+// activations' two FP8 planes (same 128-byte rows) and two more buffers
+// [256][16 B] their E8M0 bytes of stages 8G..8G+7, loaded by waves 4-7.
+template <bool kMx>
+struct DmaFp4T {
   static constexpr int kB = 0, kBBuf = 32768;
   static constexpr int kC = 3 * kBBuf, kCBuf = 16384;
   static constexpr int kS = kC + 3 * kCBuf, kSBuf = 4096;
-  static constexpr int kEnd = kS + 2 * kSBuf;
+  static constexpr int kE = kS + 2 * kSBuf, kEBuf = 4096;
+  static constexpr int kEnd = kMx ? kE + 2 * kEBuf : kE;
   static constexpr bool kWaitNewest = true;   // the end of a stage waits for all but its own loads
   const uint8_t* gc[2];   // this lane's code chunk of stage pair 0, loads j = 0, 1
-  const uint8_t* gs;      // its row's scales of stages 0..7 (waves 0-3)
+  const uint8_t* gs;      // waves 0-3: its row's scales of stages 0..7; waves 4-7 (kMx): its
+                          // token row's E8M0 bytes of stages 0..7
   const uint8_t* gb[4];   // token chunks of stage 0
   // code load j of wave w, lane i: row and logical chunk (16 bytes of the row's 64)
   __device__ __forceinline__ static int code_row(int w, int j, int i) { return ((2 * w + j) * 64 + i) >> 2; }
@@ -337,9 +349,15 @@ struct DmaFp4 {
     for (int j = 0; j < 2; ++j) dma16(gc[j] + g * kPfK, c + (2 * wave + j) * 1024);
   }
   __device__ __forceinline__ int scales(char* lds, int G, int wave) const {
-    if (wave >= 4) return 0;
-    dma16(gs + G * 16, lds + kS + (G & 1) * kSBuf + wave * 1024);
-    return 1;
+    if (wave < 4) {
+      dma16(gs + G * 16, lds + kS + (G & 1) * kSBuf + wave * 1024);
+      return 1;
+    }
+    if constexpr (kMx) {
+      dma16(gs + G * 16, lds + kE + (G & 1) * kEBuf + (wave - 4) * 1024);
+      return 1;
+    }
+    return 0;
   }
   // loads before stage 0; returns how many of them stage 0 need not wait for
   __device__ __forceinline__ int prologue(char* lds, int nst, int wave) const {
@@ -387,6 +405,9 @@ struct DmaFp4 {
     return fp4_word_to_bf16x8(w, f.sc[i]);
   }
 };
+
+using DmaFp4 = DmaFp4T<false>;
+using DmaMx = DmaFp4T<true>;
 
 // bf16 weights (the shared expert): per stage, weights and tokens [256][128 B]
 // each, both swizzled; two buffers (three would not fit); the loads of stage
@@ -472,10 +493,120 @@ __device__ __forceinline__ void pf_gemm_dma(const P& src, int nst, int n_ct, cha
   else pf_loop_dma<false>(src, nst, n_ct, lds, acc);
 }
 
-static_assert(DmaBf16::kEnd <= DmaFp4::kEnd && 2 * (Bf16Tile::kBytes + kPfBBytes) <= DmaFp4::kEnd,
+// ---------------------------------------------------------------------------
+// MX loop: FP4 weights times activations held as two FP8 planes, on
+// v_mfma_scale_f32_32x32x64_f8f6f4 (one product per 64-code stage, weight row
+// tile and plane).  Operand layout (measured on the part): A lane l holds row
+// l & 31, codes [32g, 32g + 32) of the stage (g = l >> 5), low nibble first,
+// and the row's E8M0 byte of that 32-group; B lane l holds column l & 31 at
+// K [16g, 16g + 16) in bytes 0..15 and [32 + 16g, 32 + 16g + 16) in bytes
+// 16..31 and the column's E8M0 byte of 32-group g; C as the 32x32x16 bf16
+// product.  A stage's token tile row is 128 bytes: plane 0's 64 then plane
+// 1's, swizzled as the bf16 tiles.  Plane 1's scale is plane 0's / 16.
+//
+// Activation planes in global memory ("stage rows"): row r of K values takes
+// 2K bytes, 128 per 64-value stage (plane 0, then plane 1, plain K order),
+// and its E8M0 bytes [rows][K / 32] (plane 0's).  Two planes of a bf16 value
+// within 2^13 of its 32-group's largest magnitude are exact, so the products
+// are those of the bf16 operands; the part sums each stage's 64 products to
+// about 2^-14 of the sum of their magnitudes.
+
+__device__ __forceinline__ f32x16 mx32(const u32x4& a, uint32_t sa, const u32x4& blo, const u32x4& bhi,
+                                       uint32_t sb, const f32x16& c) {
+  const i32x8 av = {static_cast<int32_t>(a.x), static_cast<int32_t>(a.y), static_cast<int32_t>(a.z),
+                    static_cast<int32_t>(a.w), 0, 0, 0, 0};
+  const i32x8 bv = {static_cast<int32_t>(blo.x), static_cast<int32_t>(blo.y), static_cast<int32_t>(blo.z),
+                    static_cast<int32_t>(blo.w), static_cast<int32_t>(bhi.x), static_cast<int32_t>(bhi.y),
+                    static_cast<int32_t>(bhi.z), static_cast<int32_t>(bhi.w)};
+  // cbsz 4: A is FP4 (e2m1); blgp 0: B is FP8 (e4m3); scale bytes from bits 0..7
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 4, 0, 0, static_cast<int>(sa), 0,
+                                                         static_cast<int>(sb));
+}
+
+// One stage's operands of a wave: 4 weight fragments with their scale bytes,
+// 2 token fragments per plane with their scale bytes (plane 0's).
+struct MxOps {
+  u32x4 a[4];
+  uint32_t sa[4];
+  u32x4 b[2][2][2];   // [token fragment][plane][low / high 16 bytes]
+  uint32_t sb[2];
+};
+
+// 8 products of one plane: acc[i][c] += A(i) x B(c, plane); unless kFull,
+// token fragments c >= n_ct (wave-uniform) are skipped.
+template <bool kFull>
+__device__ __forceinline__ void mx_mma(const MxOps& o, int pl, int n_ct, f32x16 (&acc)[4][2]) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    if (kFull || c < n_ct) {
+      const uint32_t sb = o.sb[c] - 4u * static_cast<uint32_t>(pl);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i][c] = mx32(o.a[i], o.sa[i], o.b[c][pl][0], o.b[c][pl][1], sb, acc[i][c]);
+    }
+  }
+}
+
+// Main loop of one block tile on the MX products.  Per stage st: issue the
+// policy's loads; read the stage's operands (both planes); the previous
+// stage's plane-1 products (operands kept in registers); this stage's plane-0
+// products; wait until stage st + 1 has landed, barrier.  Wave w multiplies
+// weight rows 128 (w & 1) + [0, 128) by tokens 64 (w >> 1) + [0, 64).
+template <bool kFull>
+__device__ __forceinline__ void pf_loop_mx(const DmaMx& src, int nst, int n_ct, char* lds, f32x16 (&acc)[4][2]) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int wm = wave & 1, wn = wave >> 1, g = lane >> 5, l = lane & 31;
+  // token rows 64 wn + 32 c + l share the swizzle of l
+  int koff[2][2];
+#pragma unroll
+  for (int pl = 0; pl < 2; ++pl)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) koff[pl][hf] = swz(l, 4 * pl + 2 * hf + g) * 16;
+  const int brow = (64 * wn + l) * 128;
+  const int erow = (64 * wn + l) * 16 + g;
+  auto read = [&](MxOps& o, int st) {
+    const char* c = lds + DmaMx::kC + ((st >> 1) % 3) * DmaMx::kCBuf + (128 * wm + l) * 64 +
+                    ((((st & 1) * 2 + g) ^ ((l >> 2) & 3)) * 16);
+    const char* sp = lds + DmaMx::kS + ((st >> 3) & 1) * DmaMx::kSBuf + (128 * wm + l) * 16 + (st & 7) * 2 + g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o.a[i] = *reinterpret_cast<const u32x4*>(c + i * 32 * 64);
+      o.sa[i] = *reinterpret_cast<const uint8_t*>(sp + i * 32 * 16);
+    }
+    const char* B = lds + DmaMx::kB + (st % 3) * DmaMx::kBBuf + brow;
+    const char* E = lds + DmaMx::kE + ((st >> 3) & 1) * DmaMx::kEBuf + erow + (st & 7) * 2;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+#pragma unroll
+      for (int pl = 0; pl < 2; ++pl)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+          o.b[cc][pl][hf] = *reinterpret_cast<const u32x4*>(B + cc * 32 * 128 + koff[pl][hf]);
+      o.sb[cc] = *reinterpret_cast<const uint8_t*>(E + cc * 32 * 16);
+    }
+  };
+  wait_barrier_n(src.prologue(lds, nst, wave));
+  MxOps cur, prev;
+  for (int st = 0; st < nst; ++st) {
+    const int n = src.issue_at(lds, st, nst, wave);
+    read(cur, st);
+    if (st > 0) mx_mma<kFull>(prev, 1, n_ct, acc);
+    mx_mma<kFull>(cur, 0, n_ct, acc);
+    prev = cur;
+    wait_barrier_n(n);
+  }
+  mx_mma<kFull>(prev, 1, n_ct, acc);
+}
+
+__device__ __forceinline__ void pf_gemm_mx(const DmaMx& src, int nst, int n_ct, char* lds, f32x16 (&acc)[4][2]) {
+  if (n_ct == 2) pf_loop_mx<true>(src, nst, n_ct, lds, acc);
+  else pf_loop_mx<false>(src, nst, n_ct, lds, acc);
+}
+
+static_assert(DmaBf16::kEnd <= DmaMx::kEnd && DmaFp4::kEnd <= DmaMx::kEnd &&
+                  2 * (Bf16Tile::kBytes + kPfBBytes) <= DmaMx::kEnd,
               "every loop's stages fit the FP4 DMA loop's LDS");
 
-constexpr size_t kPfLdsBytes = DmaFp4::kEnd;
+constexpr size_t kPfLdsBytes = DmaMx::kEnd;
 static_assert(kPfLdsBytes <= kMaxLds, "LDS stage buffers do not fit");
 
 struct PfArgs {
@@ -492,7 +623,17 @@ struct PfArgs {
   uint16_t* ys;                             // [T][H] the shared output, rounded to bf16
   int y_bf16;                               // routed rows rounded to bf16 (FP4 layer, combined here)
   int row_tiles;                            // weight-row tiles per token tile
+  int mx;                                   // FP4 slots on the MX products (H, I multiples of 512)
+  const uint8_t* xq; const uint8_t* xe;     // x as FP8 planes in stage rows [T][2H], E8M0 [T][H/32]
+  uint8_t* hq; uint8_t* he;                 // h of the MX slots, the same form [T*k][2I], [T*k][I/32]
 };
+
+// A routed slot runs on the MX products when the layer allows it and its
+// six FP4 arrays are 16-byte aligned (the LDS DMA's pieces); the gate/up and
+// the down take the same decision, so h is in the form the down reads.
+__device__ __forceinline__ bool slot_mx(const PfArgs& p, const SlotDesc* d) {
+  return p.mx && aligned16(d->p[0], d->p[1]) && aligned16(d->p[3], d->p[4]) && aligned16(d->p[6], d->p[7]);
+}
 
 // Logical work unit of this block: contiguous per XCD (b mod 8), row tiles
 // of one token tile adjacent.
@@ -548,12 +689,15 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_up(PfArgs p) {
   };
   f32x16 acc[4][2];
   zero(acc);
+  bool mx = false;
   if constexpr (!kQ3) {
+    mx = !shared && slot_mx(p, d);
+    // x rows are 2H bytes in both forms (bf16, or the planes' stage rows)
+    const uint8_t* xbase = mx ? p.xq : reinterpret_cast<const uint8_t*>(p.x);
     const uint8_t* gb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      gb[j] = reinterpret_cast<const uint8_t*>(p.x + xrow_of(dma_row(wave, j, lane)) * p.H) +
-              dma_chunk(wave, j, lane) * 16;
+      gb[j] = xbase + xrow_of(dma_row(wave, j, lane)) * (2 * p.H) + dma_chunk(wave, j, lane) * 16;
     if (shared) {
       DmaBf16 src;
 #pragma unroll
@@ -564,6 +708,20 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_up(PfArgs p) {
         src.gb[j] = gb[j];
       }
       pf_gemm_dma(src, nst, n_ct, pf_lds, acc);
+    } else if (mx) {
+      DmaMx src;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = DmaMx::code_row(wave, j, lane);
+        src.gc[j] = static_cast<const uint8_t*>(d->p[3 * role_of(r)]) + arow_of(r) * (K / 2) +
+                    DmaMx::code_chunk(wave, j, lane) * 16;
+      }
+      const int rs = (64 * wave + lane) & 255;
+      src.gs = wave < 4 ? static_cast<const uint8_t*>(d->p[3 * role_of(rs) + 1]) + arow_of(rs) * (K / 32)
+                        : p.xe + xrow_of(rs) * (K / 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) src.gb[j] = gb[j];
+      pf_gemm_mx(src, nst, n_ct, pf_lds, acc);
     } else if (K % 512 == 0 && aligned16(d->p[0], d->p[1]) && aligned16(d->p[3], d->p[4])) {
       DmaFp4 src;
 #pragma unroll
@@ -606,6 +764,45 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_up(PfArgs p) {
       pf_gemm<Bf16Tile, StageQ3>([&](StageQ3& a, int st) { a.load(W, S, B, arow, K, st, hf); }, brow, nst, n_ct,
                                  pf_lds, acc);
     }
+  }
+  if (mx) {
+    // h rounded to bf16, then as two FP8 planes in stage rows: features
+    // f0 + [0, 32) of fragment i (f0 = rt 128 + wm 64 + 32 i) are one 32-group;
+    // this lane holds 16 of them, at 8 (r >> 2) + 4 g + (r & 3), lane l ^ 32
+    // (same token) the other 16.
+    const int g = lane >> 5;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int n = 64 * wn + 32 * c + (lane & 31);
+      if (n >= cnt) continue;
+      const int64_t drow = tok_base + first + n;
+      const float wr = p.wrow[drow];
+      uint8_t* hrow = p.hq + drow * (2 * p.I) + (2 * rt + wm) * 128;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        float hv[16];
+        float m = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float v = silu_clamped(acc[i][c][r], acc[i + 2][c][r], p.limit) * wr;
+          hv[r] = __uint_as_float(static_cast<uint32_t>(f32_to_bf16_bits(v)) << 16);
+          m = fmaxf(m, fabsf(hv[r]));
+        }
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        const int e = fp8_plane_exp(m);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float v4[4] = {hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]};
+          uint32_t w[2];
+          fp8_planes4<2>(v4, e, w);
+#pragma unroll
+          for (int pl = 0; pl < 2; ++pl)
+            *reinterpret_cast<uint32_t*>(hrow + 64 * pl + 32 * i + 8 * q + 4 * g) = w[pl];
+        }
+        if (g == 0) p.he[drow * (p.I / 32) + 4 * rt + 2 * wm + i] = static_cast<uint8_t>(e8m0_byte(e));
+      }
+    }
+    return;
   }
   const int ld = shared ? p.Is : p.I;
   uint16_t* out = shared ? p.hs : p.h;
@@ -652,11 +849,13 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_down(PfArgs p) {
   f32x16 acc[4][2];
   zero(acc);
   if constexpr (!kQ3) {
+    const bool mx = !shared && slot_mx(p, d);
+    // h rows are 2K bytes in both forms (bf16, or the planes' stage rows)
+    const uint8_t* hbase = mx ? p.hq : reinterpret_cast<const uint8_t*>(src);
     const uint8_t* gb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      gb[j] = reinterpret_cast<const uint8_t*>(src + hrow_of(dma_row(wave, j, lane)) * K) +
-              dma_chunk(wave, j, lane) * 16;
+      gb[j] = hbase + hrow_of(dma_row(wave, j, lane)) * (2 * K) + dma_chunk(wave, j, lane) * 16;
     if (shared) {
       DmaBf16 s;
 #pragma unroll
@@ -666,6 +865,17 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_down(PfArgs p) {
         s.gb[j] = gb[j];
       }
       pf_gemm_dma(s, nst, n_ct, pf_lds, acc);
+    } else if (mx) {
+      DmaMx s;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        s.gc[j] = static_cast<const uint8_t*>(d->p[6]) + (row0 + DmaMx::code_row(wave, j, lane)) * (K / 2) +
+                  DmaMx::code_chunk(wave, j, lane) * 16;
+      const int rs = (64 * wave + lane) & 255;
+      s.gs = wave < 4 ? static_cast<const uint8_t*>(d->p[7]) + (row0 + rs) * (K / 32) : p.he + hrow_of(rs) * (K / 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s.gb[j] = gb[j];
+      pf_gemm_mx(s, nst, n_ct, pf_lds, acc);
     } else if (K % 512 == 0 && aligned16(d->p[6], d->p[7])) {
       DmaFp4 s;
 #pragma unroll
@@ -731,6 +941,36 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_down(PfArgs p) {
               f32x4{acc[i][c][4 * q], acc[i][c][4 * q + 1], acc[i][c][4 * q + 2], acc[i][c][4 * q + 3]};
     }
   }
+}
+
+// x [T][H] bf16 as two FP8 planes in stage rows (the MX gate/up's B tiles):
+// thread c takes 8 values, the four threads of a 32-group are consecutive
+// lanes (H / 8 chunks per row, a multiple of 64, so whole waves leave).
+__global__ __launch_bounds__(256) void k_pf_planes(const uint16_t* __restrict__ x, int64_t chunks, int H,
+                                                  uint8_t* __restrict__ q, uint8_t* __restrict__ ex) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= chunks) return;
+  const int cpr = H / 8;
+  const int64_t t = c / cpr;
+  const int k8 = static_cast<int>(c - t * cpr) * 8;
+  const u32x4 v = ldg16(x + t * H + k8);
+  const float f0[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
+  const float f1[4] = {__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
+                       __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u)};
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(f0[i]), fabsf(f1[i])));
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  const int e = fp8_plane_exp(m);
+  uint32_t w0[2], w1[2];
+  fp8_planes4<2>(f0, e, w0);
+  fp8_planes4<2>(f1, e, w1);
+  uint8_t* row = q + t * (2 * H) + (k8 >> 6) * 128 + (k8 & 63);
+  *reinterpret_cast<uint2*>(row) = uint2{w0[0], w1[0]};
+  *reinterpret_cast<uint2*>(row + 64) = uint2{w0[1], w1[1]};
+  if ((k8 & 31) == 0) ex[t * (H / 32) + (k8 >> 5)] = static_cast<uint8_t>(e8m0_byte(e));
 }
 
 // Tile list from the dispatch descriptors (one block of 1024 threads; one
@@ -803,11 +1043,27 @@ hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, con
   p.y = rows_buffer(a.rows_out, a.ws, L);
   p.ys = reinterpret_cast<uint16_t*>(a.ws + L.ys);
   p.y_bf16 = prefill_rows_bf16(d, a.rows_out) ? 1 : 0;
+  p.mx = prefill_mx(d) ? 1 : 0;
+  if (p.mx) {
+    uint8_t* xp = reinterpret_cast<uint8_t*>(a.ws + L.xp);
+    p.xq = xp;
+    p.xe = xp + static_cast<size_t>(T) * 2 * H;
+    uint8_t* hp = reinterpret_cast<uint8_t*>(a.ws + L.hp);
+    p.hq = hp;
+    p.he = hp + static_cast<size_t>(T) * d.top_k * 2 * I;
+  }
 
   if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   p.row_tiles = (I > Is ? I : Is) / 128;
   const unsigned up_blocks = static_cast<unsigned>(max_tiles * p.row_tiles);
+  const int64_t x_chunks = static_cast<int64_t>(T) * (H / 8);
   for (int r = 0; r < repeat; ++r) {
+    if (p.mx) {
+      launch_kernel(k_pf_planes, static_cast<unsigned>((x_chunks + 255) / 256), 256, 0, s,
+                    static_cast<const uint16_t*>(a.x), x_chunks, H, const_cast<uint8_t*>(p.xq),
+                    const_cast<uint8_t*>(p.xe));
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     if (q3) launch_kernel(k_pf_up<true>, up_blocks, kPfThreads, kPfLdsBytes, s, p);
     else launch_kernel(k_pf_up<false>, up_blocks, kPfThreads, kPfLdsBytes, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
