@@ -94,7 +94,7 @@ Workspace workspace_layout(const dsk_moe_desc& d) {
     L.xp = take(d.quant == DSK_QUANT_FP4 && d.x_dtype == DSK_DTYPE_BF16 && !prefill_gemm(d) ? T * 2 * (H + H / 32) : 0);
     L.hp = take(!prefill_gemm(d) && grouped_h_planes(d) ? N * 3 * (I + I / 32) : 0);
   }
-  L.pf_tiles = take(prefill_gemm(d) ? (2 + 2 * static_cast<size_t>(prefill_max_tiles(d))) * 4 : 0);
+  L.pf_tiles = take(prefill_gemm(d) ? (3 + 2 * static_cast<size_t>(prefill_max_tiles(d))) * 4 : 0);
   L.disp_hist = take(dispatch_hist_ints(static_cast<int>(N), static_cast<int>(E)) * 4);
   L.total = o;
   return L;

@@ -149,7 +149,7 @@ struct Workspace {
                             // MX prefill: x as FP8 planes in stage rows [T][2H] + E8M0 [T][H/32]
   size_t hp;                // grouped FP4: h as FP8 planes [T*k][3][I] + E8M0 [T*k][3][I/32];
                             // MX prefill: h in stage rows [T*k][2I] + E8M0 [T*k][I/32]
-  size_t pf_tiles;          // prefill GEMM tile list  [2 + 2 * prefill_max_tiles]
+  size_t pf_tiles;          // prefill GEMM tile list  [2 + 2 * prefill_max_tiles] + the MX switch
   size_t total;
 };
 

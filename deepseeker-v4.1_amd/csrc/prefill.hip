@@ -318,20 +318,15 @@ __device__ __forceinline__ void wait_barrier_n(int n) {
 // [256][128 B] (stage st in buffer st % 3), three code buffers [256][64 B]
 // (stage pair g in buffer g % 3; 16-byte chunk q of row r at position
 // q ^ ((r >> 2) & 3)), two scale buffers [256][16 B] (stages 8G..8G+7 in
-// buffer G & 1, loaded by waves 0-3).  kMx: the token tile holds the
-// activations' two FP8 planes (same 128-byte rows) and two more buffers
-// [256][16 B] their E8M0 bytes of stages 8G..8G+7, loaded by waves 4-7.
-template <bool kMx>
-struct DmaFp4T {
+// buffer G & 1, loaded by waves 0-3).
+struct DmaFp4 {
   static constexpr int kB = 0, kBBuf = 32768;
   static constexpr int kC = 3 * kBBuf, kCBuf = 16384;
   static constexpr int kS = kC + 3 * kCBuf, kSBuf = 4096;
-  static constexpr int kE = kS + 2 * kSBuf, kEBuf = 4096;
-  static constexpr int kEnd = kMx ? kE + 2 * kEBuf : kE;
+  static constexpr int kEnd = kS + 2 * kSBuf;
   static constexpr bool kWaitNewest = true;   // the end of a stage waits for all but its own loads
   const uint8_t* gc[2];   // this lane's code chunk of stage pair 0, loads j = 0, 1
-  const uint8_t* gs;      // waves 0-3: its row's scales of stages 0..7; waves 4-7 (kMx): its
-                          // token row's E8M0 bytes of stages 0..7
+  const uint8_t* gs;      // its row's scales of stages 0..7 (waves 0-3)
   const uint8_t* gb[4];   // token chunks of stage 0
   // code load j of wave w, lane i: row and logical chunk (16 bytes of the row's 64)
   __device__ __forceinline__ static int code_row(int w, int j, int i) { return ((2 * w + j) * 64 + i) >> 2; }
@@ -349,15 +344,9 @@ struct DmaFp4T {
     for (int j = 0; j < 2; ++j) dma16(gc[j] + g * kPfK, c + (2 * wave + j) * 1024);
   }
   __device__ __forceinline__ int scales(char* lds, int G, int wave) const {
-    if (wave < 4) {
-      dma16(gs + G * 16, lds + kS + (G & 1) * kSBuf + wave * 1024);
-      return 1;
-    }
-    if constexpr (kMx) {
-      dma16(gs + G * 16, lds + kE + (G & 1) * kEBuf + (wave - 4) * 1024);
-      return 1;
-    }
-    return 0;
+    if (wave >= 4) return 0;
+    dma16(gs + G * 16, lds + kS + (G & 1) * kSBuf + wave * 1024);
+    return 1;
   }
   // loads before stage 0; returns how many of them stage 0 need not wait for
   __device__ __forceinline__ int prologue(char* lds, int nst, int wave) const {
@@ -405,9 +394,6 @@ struct DmaFp4T {
     return fp4_word_to_bf16x8(w, f.sc[i]);
   }
 };
-
-using DmaFp4 = DmaFp4T<false>;
-using DmaMx = DmaFp4T<true>;
 
 // bf16 weights (the shared expert): per stage, weights and tokens [256][128 B]
 // each, both swizzled; two buffers (three would not fit); the loads of stage
@@ -546,11 +532,81 @@ __device__ __forceinline__ void mx_mma(const MxOps& o, int pl, int n_ct, f32x16 
   }
 }
 
+// MX tiles run in workgroups of 4 waves (one per SIMD), two workgroups per
+// CU: a tile of 256 weight rows x 128 dispatch rows, K in stages of 64.
+// With one 8-wave workgroup per CU every stage's barrier held both waves of
+// a SIMD in the same phase (both loading, then both multiplying); two
+// independent workgroups drift apart, so one's products run while the
+// other waits.  LDS per workgroup (77 824 bytes): tokens 2 x [128][128 B]
+// (stage st in buffer st & 1, the plane rows' 128 bytes, chunk c of row r
+// at c ^ ((r >> 1) & 7)), codes 2 x [256][64 B] (stage pair g in buffer
+// g & 1, chunk q of row r at q ^ ((r >> 2) & 3)), weight scales 2 x
+// [256][16 B] and activation exponents 2 x [128][16 B] (stages 8G..8G+7 in
+// buffer G & 1).  Stage st + 1's tokens are loaded when stage st starts and
+// waited for at its end; code pair g + 1 when stage 2g starts (two stages
+// ahead); the scales of group G + 1 when stage 8G starts.
+constexpr int kMxThreads = 256;
+constexpr int kPfToksMx = 128;   // dispatch rows of an MX tile
+
+struct DmaMx {
+  static constexpr int kB = 0, kBBuf = 16384;
+  static constexpr int kC = 2 * kBBuf, kCBuf = 16384;
+  static constexpr int kS = kC + 2 * kCBuf, kSBuf = 4096;
+  static constexpr int kE = kS + 2 * kSBuf, kEBuf = 2048;
+  static constexpr int kEnd = kE + 2 * kEBuf;
+  const uint8_t* gb[4];   // this lane's token chunk of stage 0, loads j = 0..3
+  const uint8_t* gc[4];   // its code chunk of stage pair 0
+  const uint8_t* gs;      // the scales of weight row 64 w + lane, stages 0..7
+  const uint8_t* ge;      // waves 0, 1: the exponents of token row 64 w + lane, stages 0..7
+  // load j of wave w, lane i writes LDS position (4 w + j) 64 + i (16 bytes each)
+  __device__ __forceinline__ static int brow(int w, int j, int i) { return ((4 * w + j) * 64 + i) >> 3; }
+  __device__ __forceinline__ static int bchunk(int w, int j, int i) { return swz(brow(w, j, i), i & 7); }
+  __device__ __forceinline__ static int crow(int w, int j, int i) { return ((4 * w + j) * 64 + i) >> 2; }
+  __device__ __forceinline__ static int cchunk(int w, int j, int i) { return (i & 3) ^ ((crow(w, j, i) >> 2) & 3); }
+  __device__ __forceinline__ static int tbuf(int st) { return st & 1; }
+  __device__ __forceinline__ static int cbuf(int st) { return (st >> 1) & 1; }
+  __device__ __forceinline__ void tokens(char* lds, int st, int wave) const {
+    char* b = lds + kB + (st & 1) * kBBuf;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(gb[j] + st * (kPfK * 2), b + (4 * wave + j) * 1024);
+  }
+  __device__ __forceinline__ void codes(char* lds, int g, int wave) const {
+    char* c = lds + kC + (g & 1) * kCBuf;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(gc[j] + g * kPfK, c + (4 * wave + j) * 1024);
+  }
+  __device__ __forceinline__ int scales(char* lds, int G, int wave) const {
+    dma16(gs + G * 16, lds + kS + (G & 1) * kSBuf + wave * 1024);
+    if (wave >= 2) return 1;
+    dma16(ge + G * 16, lds + kE + (G & 1) * kEBuf + wave * 1024);
+    return 2;
+  }
+  // loads before stage 0 (all waited for)
+  __device__ __forceinline__ void prologue(char* lds, int nst, int wave) const {
+    scales(lds, 0, wave);
+    codes(lds, 0, wave);
+    tokens(lds, 0, wave);
+  }
+  // loads issued when stage st starts, stage st + 1's tokens first; returns
+  // how many were issued after them (the end of the stage need not wait)
+  __device__ __forceinline__ int issue_at(char* lds, int st, int nst, int wave) const {
+    if (st + 1 < nst) tokens(lds, st + 1, wave);
+    int n = 0;
+    if ((st & 1) == 0 && st + 2 < nst) {
+      codes(lds, (st >> 1) + 1, wave);
+      n += 4;
+    }
+    if ((st & 7) == 0 && st + 8 < nst) n += scales(lds, (st >> 3) + 1, wave);
+    return n;
+  }
+};
+
 // Main loop of one block tile on the MX products.  Per stage st: issue the
 // policy's loads; read the stage's operands (both planes); the previous
 // stage's plane-1 products (operands kept in registers); this stage's plane-0
-// products; wait until stage st + 1 has landed, barrier.  Wave w multiplies
-// weight rows 128 (w & 1) + [0, 128) by tokens 64 (w >> 1) + [0, 64).
+// products; wait until stage st + 1 has landed, barrier.  Wave w (0..3)
+// multiplies weight rows 128 (w & 1) + [0, 128) by tokens 64 (w >> 1) +
+// [0, 64).
 template <bool kFull>
 __device__ __forceinline__ void pf_loop_mx(const DmaMx& src, int nst, int n_ct, char* lds, f32x16 (&acc)[4][2]) {
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -564,7 +620,7 @@ __device__ __forceinline__ void pf_loop_mx(const DmaMx& src, int nst, int n_ct, 
   const int brow = (64 * wn + l) * 128;
   const int erow = (64 * wn + l) * 16 + g;
   auto read = [&](MxOps& o, int st) {
-    const char* c = lds + DmaMx::kC + ((st >> 1) % 3) * DmaMx::kCBuf + (128 * wm + l) * 64 +
+    const char* c = lds + DmaMx::kC + DmaMx::cbuf(st) * DmaMx::kCBuf + (128 * wm + l) * 64 +
                     ((((st & 1) * 2 + g) ^ ((l >> 2) & 3)) * 16);
     const char* sp = lds + DmaMx::kS + ((st >> 3) & 1) * DmaMx::kSBuf + (128 * wm + l) * 16 + (st & 7) * 2 + g;
 #pragma unroll
@@ -572,7 +628,7 @@ __device__ __forceinline__ void pf_loop_mx(const DmaMx& src, int nst, int n_ct, 
       o.a[i] = *reinterpret_cast<const u32x4*>(c + i * 32 * 64);
       o.sa[i] = *reinterpret_cast<const uint8_t*>(sp + i * 32 * 16);
     }
-    const char* B = lds + DmaMx::kB + (st % 3) * DmaMx::kBBuf + brow;
+    const char* B = lds + DmaMx::kB + DmaMx::tbuf(st) * DmaMx::kBBuf + brow;
     const char* E = lds + DmaMx::kE + ((st >> 3) & 1) * DmaMx::kEBuf + erow + (st & 7) * 2;
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
@@ -584,7 +640,8 @@ __device__ __forceinline__ void pf_loop_mx(const DmaMx& src, int nst, int n_ct, 
       o.sb[cc] = *reinterpret_cast<const uint8_t*>(E + cc * 32 * 16);
     }
   };
-  wait_barrier_n(src.prologue(lds, nst, wave));
+  src.prologue(lds, nst, wave);
+  wait_barrier<0>();
   MxOps cur, prev;
   for (int st = 0; st < nst; ++st) {
     const int n = src.issue_at(lds, st, nst, wave);
@@ -602,11 +659,12 @@ __device__ __forceinline__ void pf_gemm_mx(const DmaMx& src, int nst, int n_ct, 
   else pf_loop_mx<false>(src, nst, n_ct, lds, acc);
 }
 
-static_assert(DmaBf16::kEnd <= DmaMx::kEnd && DmaFp4::kEnd <= DmaMx::kEnd &&
-                  2 * (Bf16Tile::kBytes + kPfBBytes) <= DmaMx::kEnd,
+static_assert(DmaBf16::kEnd <= DmaFp4::kEnd && 2 * (Bf16Tile::kBytes + kPfBBytes) <= DmaFp4::kEnd,
               "every loop's stages fit the FP4 DMA loop's LDS");
 
-constexpr size_t kPfLdsBytes = DmaMx::kEnd;
+constexpr size_t kPfLdsBytes = DmaFp4::kEnd;
+constexpr size_t kMxLdsBytes = DmaMx::kEnd;
+static_assert(2 * kMxLdsBytes <= kMaxLds, "two MX workgroups share a CU's LDS");
 static_assert(kPfLdsBytes <= kMaxLds, "LDS stage buffers do not fit");
 
 struct PfArgs {
@@ -623,22 +681,15 @@ struct PfArgs {
   uint16_t* ys;                             // [T][H] the shared output, rounded to bf16
   int y_bf16;                               // routed rows rounded to bf16 (FP4 layer, combined here)
   int row_tiles;                            // weight-row tiles per token tile
-  int mx;                                   // FP4 slots on the MX products (H, I multiples of 512)
+  const int32_t* mx_on;                     // [0]: routed tiles on the MX kernels (k_pf_tiles)
   const uint8_t* xq; const uint8_t* xe;     // x as FP8 planes in stage rows [T][2H], E8M0 [T][H/32]
   uint8_t* hq; uint8_t* he;                 // h of the MX slots, the same form [T*k][2I], [T*k][I/32]
 };
 
-// A routed slot runs on the MX products when the layer allows it and its
-// six FP4 arrays are 16-byte aligned (the LDS DMA's pieces); the gate/up and
-// the down take the same decision, so h is in the form the down reads.
-__device__ __forceinline__ bool slot_mx(const PfArgs& p, const SlotDesc* d) {
-  return p.mx && aligned16(d->p[0], d->p[1]) && aligned16(d->p[3], d->p[4]) && aligned16(d->p[6], d->p[7]);
-}
-
-// Logical work unit of this block: contiguous per XCD (b mod 8), row tiles
-// of one token tile adjacent.
-__device__ __forceinline__ bool pf_unit(const PfArgs& p, int& tile, int& rt) {
-  const int R = p.tiles[0] * p.row_tiles;
+// Logical work unit of this block among tiles [t0, t0 + n): contiguous per
+// XCD (b mod 8), row tiles of one token tile adjacent.
+__device__ __forceinline__ bool pf_unit_in(const PfArgs& p, int t0, int n, int& tile, int& rt) {
+  const int R = n * p.row_tiles;
   const int b = blockIdx.x;
   if (b >= R) return false;
   const int xcd = b & 7;
@@ -647,7 +698,15 @@ __device__ __forceinline__ bool pf_unit(const PfArgs& p, int& tile, int& rt) {
   const int L = start + (b >> 3);
   tile = L / p.row_tiles;
   rt = L - tile * p.row_tiles;
+  tile += t0;
   return true;
+}
+
+// The 8-wave kernels' units: every tile, or only the shared expert's when
+// the routed tiles run on the MX kernels.
+__device__ __forceinline__ bool pf_unit(const PfArgs& p, int& tile, int& rt) {
+  return *p.mx_on ? pf_unit_in(p, p.tiles[1], p.tiles[0] - p.tiles[1], tile, rt)
+                  : pf_unit_in(p, 0, p.tiles[0], tile, rt);
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
@@ -689,15 +748,12 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_up(PfArgs p) {
   };
   f32x16 acc[4][2];
   zero(acc);
-  bool mx = false;
   if constexpr (!kQ3) {
-    mx = !shared && slot_mx(p, d);
-    // x rows are 2H bytes in both forms (bf16, or the planes' stage rows)
-    const uint8_t* xbase = mx ? p.xq : reinterpret_cast<const uint8_t*>(p.x);
     const uint8_t* gb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      gb[j] = xbase + xrow_of(dma_row(wave, j, lane)) * (2 * p.H) + dma_chunk(wave, j, lane) * 16;
+      gb[j] = reinterpret_cast<const uint8_t*>(p.x + xrow_of(dma_row(wave, j, lane)) * p.H) +
+              dma_chunk(wave, j, lane) * 16;
     if (shared) {
       DmaBf16 src;
 #pragma unroll
@@ -708,20 +764,6 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_up(PfArgs p) {
         src.gb[j] = gb[j];
       }
       pf_gemm_dma(src, nst, n_ct, pf_lds, acc);
-    } else if (mx) {
-      DmaMx src;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int r = DmaMx::code_row(wave, j, lane);
-        src.gc[j] = static_cast<const uint8_t*>(d->p[3 * role_of(r)]) + arow_of(r) * (K / 2) +
-                    DmaMx::code_chunk(wave, j, lane) * 16;
-      }
-      const int rs = (64 * wave + lane) & 255;
-      src.gs = wave < 4 ? static_cast<const uint8_t*>(d->p[3 * role_of(rs) + 1]) + arow_of(rs) * (K / 32)
-                        : p.xe + xrow_of(rs) * (K / 32);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) src.gb[j] = gb[j];
-      pf_gemm_mx(src, nst, n_ct, pf_lds, acc);
     } else if (K % 512 == 0 && aligned16(d->p[0], d->p[1]) && aligned16(d->p[3], d->p[4])) {
       DmaFp4 src;
 #pragma unroll
@@ -764,45 +806,6 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_up(PfArgs p) {
       pf_gemm<Bf16Tile, StageQ3>([&](StageQ3& a, int st) { a.load(W, S, B, arow, K, st, hf); }, brow, nst, n_ct,
                                  pf_lds, acc);
     }
-  }
-  if (mx) {
-    // h rounded to bf16, then as two FP8 planes in stage rows: features
-    // f0 + [0, 32) of fragment i (f0 = rt 128 + wm 64 + 32 i) are one 32-group;
-    // this lane holds 16 of them, at 8 (r >> 2) + 4 g + (r & 3), lane l ^ 32
-    // (same token) the other 16.
-    const int g = lane >> 5;
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int n = 64 * wn + 32 * c + (lane & 31);
-      if (n >= cnt) continue;
-      const int64_t drow = tok_base + first + n;
-      const float wr = p.wrow[drow];
-      uint8_t* hrow = p.hq + drow * (2 * p.I) + (2 * rt + wm) * 128;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        float hv[16];
-        float m = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float v = silu_clamped(acc[i][c][r], acc[i + 2][c][r], p.limit) * wr;
-          hv[r] = __uint_as_float(static_cast<uint32_t>(f32_to_bf16_bits(v)) << 16);
-          m = fmaxf(m, fabsf(hv[r]));
-        }
-        m = fmaxf(m, __shfl_xor(m, 32, 64));
-        const int e = fp8_plane_exp(m);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float v4[4] = {hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]};
-          uint32_t w[2];
-          fp8_planes4<2>(v4, e, w);
-#pragma unroll
-          for (int pl = 0; pl < 2; ++pl)
-            *reinterpret_cast<uint32_t*>(hrow + 64 * pl + 32 * i + 8 * q + 4 * g) = w[pl];
-        }
-        if (g == 0) p.he[drow * (p.I / 32) + 4 * rt + 2 * wm + i] = static_cast<uint8_t>(e8m0_byte(e));
-      }
-    }
-    return;
   }
   const int ld = shared ? p.Is : p.I;
   uint16_t* out = shared ? p.hs : p.h;
@@ -849,13 +852,11 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_down(PfArgs p) {
   f32x16 acc[4][2];
   zero(acc);
   if constexpr (!kQ3) {
-    const bool mx = !shared && slot_mx(p, d);
-    // h rows are 2K bytes in both forms (bf16, or the planes' stage rows)
-    const uint8_t* hbase = mx ? p.hq : reinterpret_cast<const uint8_t*>(src);
     const uint8_t* gb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      gb[j] = hbase + hrow_of(dma_row(wave, j, lane)) * (2 * K) + dma_chunk(wave, j, lane) * 16;
+      gb[j] = reinterpret_cast<const uint8_t*>(src + hrow_of(dma_row(wave, j, lane)) * K) +
+              dma_chunk(wave, j, lane) * 16;
     if (shared) {
       DmaBf16 s;
 #pragma unroll
@@ -865,17 +866,6 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_down(PfArgs p) {
         s.gb[j] = gb[j];
       }
       pf_gemm_dma(s, nst, n_ct, pf_lds, acc);
-    } else if (mx) {
-      DmaMx s;
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        s.gc[j] = static_cast<const uint8_t*>(d->p[6]) + (row0 + DmaMx::code_row(wave, j, lane)) * (K / 2) +
-                  DmaMx::code_chunk(wave, j, lane) * 16;
-      const int rs = (64 * wave + lane) & 255;
-      s.gs = wave < 4 ? static_cast<const uint8_t*>(d->p[7]) + (row0 + rs) * (K / 32) : p.he + hrow_of(rs) * (K / 32);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s.gb[j] = gb[j];
-      pf_gemm_mx(s, nst, n_ct, pf_lds, acc);
     } else if (K % 512 == 0 && aligned16(d->p[6], d->p[7])) {
       DmaFp4 s;
 #pragma unroll
@@ -943,6 +933,131 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_pf_down(PfArgs p) {
   }
 }
 
+// MX gate/up: a routed tile of 128 dispatch rows; local weight row r =
+// 0..255 of the unit is w1 (r & 64 == 0) or w3 row rt*128 + (r >> 7)*64 +
+// (r & 63), so wave rows 0..63 are gate rows and 64..127 the matching up
+// rows.  h is rounded to bf16, then written as two FP8 planes in stage rows:
+// features f0 + [0, 32) of fragment i (f0 = rt 128 + wm 64 + 32 i) are one
+// 32-group; this lane holds 16 of them, at 8 (r >> 2) + 4 g + (r & 3), lane
+// l ^ 32 (same token) the other 16.
+__global__ __launch_bounds__(kMxThreads, 2) void k_pf_mx_up(PfArgs p) {
+  extern __shared__ __align__(16) char mx_lds[];
+  int tile, rt;
+  if (!*p.mx_on || !pf_unit_in(p, 0, p.tiles[1], tile, rt)) return;
+  const int slot = p.tiles[2 + tile], first = p.tiles[2 + p.max_tiles + tile];
+  const SlotDesc* d = p.desc + slot;
+  const int tok_base = d->tok_base;
+  const int cnt = min(kPfToksMx, d->n_tok - first);
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int wm = wave & 1, wn = wave >> 1;
+  const int n_ct = max(0, min(2, (cnt - 64 * wn + 31) >> 5));
+  const int K = p.H;
+  auto role_of = [](int r) { return (r >> 6) & 1; };
+  auto arow_of = [&](int r) { return static_cast<int64_t>(rt * 128 + (r >> 7) * 64 + (r & 63)); };
+  auto xrow_of = [&](int r) { return static_cast<int64_t>(p.xrow[tok_base + first + min(r, cnt - 1)]); };
+  DmaMx src;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    src.gb[j] = p.xq + xrow_of(DmaMx::brow(wave, j, lane)) * (2 * K) + DmaMx::bchunk(wave, j, lane) * 16;
+    const int r = DmaMx::crow(wave, j, lane);
+    src.gc[j] = static_cast<const uint8_t*>(d->p[3 * role_of(r)]) + arow_of(r) * (K / 2) +
+                DmaMx::cchunk(wave, j, lane) * 16;
+  }
+  const int rs = 64 * wave + lane;
+  src.gs = static_cast<const uint8_t*>(d->p[3 * role_of(rs) + 1]) + arow_of(rs) * (K / 32);
+  src.ge = p.xe + xrow_of(rs & 127) * (K / 32);
+  f32x16 acc[4][2];
+  zero(acc);
+  pf_gemm_mx(src, K / kPfK, n_ct, mx_lds, acc);
+  const int g = lane >> 5;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int n = 64 * wn + 32 * c + (lane & 31);
+    if (n >= cnt) continue;
+    const int64_t drow = tok_base + first + n;
+    const float wr = p.wrow[drow];
+    uint8_t* hrow = p.hq + drow * (2 * p.I) + (2 * rt + wm) * 128;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float hv[16];
+      float m = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float v = silu_clamped(acc[i][c][r], acc[i + 2][c][r], p.limit) * wr;
+        hv[r] = __uint_as_float(static_cast<uint32_t>(f32_to_bf16_bits(v)) << 16);
+        m = fmaxf(m, fabsf(hv[r]));
+      }
+      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      const int e = fp8_plane_exp(m);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float v4[4] = {hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]};
+        uint32_t w[2];
+        fp8_planes4<2>(v4, e, w);
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl)
+          *reinterpret_cast<uint32_t*>(hrow + 64 * pl + 32 * i + 8 * q + 4 * g) = w[pl];
+      }
+      if (g == 0) p.he[drow * (p.I / 32) + 4 * rt + 2 * wm + i] = static_cast<uint8_t>(e8m0_byte(e));
+    }
+  }
+}
+
+// MX down: w2 rows rt*256 + [0, 256) by a routed tile of 128 dispatch rows,
+// from h's planes; routed rows in float32 or bf16 (y_bf16).
+__global__ __launch_bounds__(kMxThreads, 2) void k_pf_mx_down(PfArgs p) {
+  extern __shared__ __align__(16) char mx_lds[];
+  int tile, rt;
+  if (!*p.mx_on || !pf_unit_in(p, 0, p.tiles[1], tile, rt)) return;
+  const int slot = p.tiles[2 + tile], first = p.tiles[2 + p.max_tiles + tile];
+  const SlotDesc* d = p.desc + slot;
+  const int tok_base = d->tok_base;
+  const int cnt = min(kPfToksMx, d->n_tok - first);
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int wm = wave & 1, wn = wave >> 1;
+  const int n_ct = max(0, min(2, (cnt - 64 * wn + 31) >> 5));
+  const int K = p.I;
+  const int64_t row0 = static_cast<int64_t>(rt) * 256;
+  auto hrow_of = [&](int r) { return static_cast<int64_t>(tok_base + first + min(r, cnt - 1)); };
+  DmaMx src;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    src.gb[j] = p.hq + hrow_of(DmaMx::brow(wave, j, lane)) * (2 * K) + DmaMx::bchunk(wave, j, lane) * 16;
+    src.gc[j] = static_cast<const uint8_t*>(d->p[6]) + (row0 + DmaMx::crow(wave, j, lane)) * (K / 2) +
+                DmaMx::cchunk(wave, j, lane) * 16;
+  }
+  const int rs = 64 * wave + lane;
+  src.gs = static_cast<const uint8_t*>(d->p[7]) + (row0 + rs) * (K / 32);
+  src.ge = p.he + hrow_of(rs & 127) * (K / 32);
+  f32x16 acc[4][2];
+  zero(acc);
+  pf_gemm_mx(src, K / kPfK, n_ct, mx_lds, acc);
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int n = 64 * wn + 32 * c + (lane & 31);
+    if (n >= cnt) continue;
+    const int64_t drow = tok_base + first + n;
+    const int64_t col0 = drow * p.H + row0 + wm * 128 + 4 * (lane >> 5);
+    if (p.y_bf16) {
+      uint16_t* out = reinterpret_cast<uint16_t*>(p.y);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<uint2*>(out + col0 + 32 * i + 8 * q) =
+              uint2{pack_bf16x2(acc[i][c][4 * q], acc[i][c][4 * q + 1]),
+                    pack_bf16x2(acc[i][c][4 * q + 2], acc[i][c][4 * q + 3])};
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<f32x4*>(p.y + col0 + 32 * i + 8 * q) =
+              f32x4{acc[i][c][4 * q], acc[i][c][4 * q + 1], acc[i][c][4 * q + 2], acc[i][c][4 * q + 3]};
+    }
+  }
+}
+
 // x [T][H] bf16 as two FP8 planes in stage rows (the MX gate/up's B tiles):
 // thread c takes 8 values, the four threads of a 32-group are consecutive
 // lanes (H / 8 chunks per row, a multiple of 64, so whole waves leave).
@@ -974,14 +1089,26 @@ __global__ __launch_bounds__(256) void k_pf_planes(const uint16_t* __restrict__ 
 }
 
 // Tile list from the dispatch descriptors (one block of 1024 threads; one
-// thread per active expert slot, E <= 1024).
+// thread per active expert slot, E <= 1024): routed tiles, then the shared
+// expert's tiles of kPfToks tokens.  The routed tiles run on the MX kernels
+// (kPfToksMx rows each) when the layer allows it (mx) and every active
+// slot's six FP4 arrays are 16-byte aligned (the LDS DMA's pieces), else on
+// the 8-wave kernels (kPfToks rows each); tiles[2 + 2 max_tiles] says which.
 __global__ __launch_bounds__(1024) void k_pf_tiles(const SlotDesc* __restrict__ desc,
                                                    const int32_t* __restrict__ active, int E, int T,
-                                                   int with_shared, int max_tiles, int32_t* __restrict__ tiles) {
+                                                   int with_shared, int max_tiles, int mx,
+                                                   int32_t* __restrict__ tiles) {
   __shared__ int32_t wsum[16];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int n_act = min(active[0], E);
-  const int cnt = t < n_act ? (desc[t].n_tok + kPfToks - 1) / kPfToks : 0;
+  bool ok = true;
+  if (mx && t < n_act) {
+    const SlotDesc& d = desc[t];
+    ok = aligned16(d.p[0], d.p[1]) && aligned16(d.p[3], d.p[4]) && aligned16(d.p[6], d.p[7]);
+  }
+  const bool on = mx && __syncthreads_and(ok ? 1 : 0);
+  const int rtoks = on ? kPfToksMx : kPfToks;
+  const int cnt = t < n_act ? (desc[t].n_tok + rtoks - 1) / rtoks : 0;
   int incl = cnt;
 #pragma unroll
   for (int s = 1; s < 64; s <<= 1) {
@@ -998,7 +1125,7 @@ __global__ __launch_bounds__(1024) void k_pf_tiles(const SlotDesc* __restrict__ 
   const int off = base + incl - cnt;
   for (int j = 0; j < cnt; ++j) {
     tiles[2 + off + j] = t;
-    tiles[2 + max_tiles + off + j] = j * kPfToks;
+    tiles[2 + max_tiles + off + j] = j * rtoks;
   }
   const int sh = with_shared ? (T + kPfToks - 1) / kPfToks : 0;
   for (int j = t; j < sh; j += 1024) {
@@ -1008,6 +1135,7 @@ __global__ __launch_bounds__(1024) void k_pf_tiles(const SlotDesc* __restrict__ 
   if (t == 0) {
     tiles[0] = total + sh;
     tiles[1] = total;
+    tiles[2 + 2 * max_tiles] = on ? 1 : 0;
   }
 }
 
@@ -1017,7 +1145,8 @@ int prefill_max_tiles(const dsk_moe_desc& d) {
   const int n = d.tokens * d.top_k;
   const int slots = d.n_experts < n ? d.n_experts : n;
   const int shared = d.inter_shared > 0 ? (d.tokens + kPfToks - 1) / kPfToks : 0;
-  return (n + kPfToks - 1) / kPfToks + slots + shared;
+  const int rtoks = prefill_mx(d) ? kPfToksMx : kPfToks;   // the smaller tile when the layer may use it
+  return (n + rtoks - 1) / rtoks + slots + shared;
 }
 
 hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, const PrefillArgs& a,
@@ -1026,7 +1155,9 @@ hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, con
   const bool q3 = d.quant == DSK_QUANT_Q3;
   const int max_tiles = prefill_max_tiles(d);
   int32_t* tiles = reinterpret_cast<int32_t*>(a.ws + L.pf_tiles);
-  launch_kernel(k_pf_tiles, 1, 1024, 0, s, a.desc, a.active, d.n_experts, T, Is > 0 ? 1 : 0, max_tiles, tiles);
+  const bool mx = prefill_mx(d);
+  launch_kernel(k_pf_tiles, 1, 1024, 0, s, a.desc, a.active, d.n_experts, T, Is > 0 ? 1 : 0, max_tiles,
+                mx ? 1 : 0, tiles);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
 
@@ -1043,8 +1174,8 @@ hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, con
   p.y = rows_buffer(a.rows_out, a.ws, L);
   p.ys = reinterpret_cast<uint16_t*>(a.ws + L.ys);
   p.y_bf16 = prefill_rows_bf16(d, a.rows_out) ? 1 : 0;
-  p.mx = prefill_mx(d) ? 1 : 0;
-  if (p.mx) {
+  p.mx_on = tiles + 2 + 2 * max_tiles;
+  if (mx) {
     uint8_t* xp = reinterpret_cast<uint8_t*>(a.ws + L.xp);
     p.xq = xp;
     p.xe = xp + static_cast<size_t>(T) * 2 * H;
@@ -1053,17 +1184,24 @@ hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, con
     p.he = hp + static_cast<size_t>(T) * d.top_k * 2 * I;
   }
 
+  // MX layers: the routed tiles on the 4-wave MX kernels (two workgroups per
+  // CU), then the shared expert's on the 8-wave kernels; each kernel's grid
+  // covers its units for either tile size (k_pf_tiles decides on the device)
   if ((e = stage_open(kStageUp)) != hipSuccess) return e;
-  p.row_tiles = (I > Is ? I : Is) / 128;
-  const unsigned up_blocks = static_cast<unsigned>(max_tiles * p.row_tiles);
+  const int up_rows = (I > Is ? I : Is) / 128;
   const int64_t x_chunks = static_cast<int64_t>(T) * (H / 8);
   for (int r = 0; r < repeat; ++r) {
-    if (p.mx) {
+    if (mx) {
       launch_kernel(k_pf_planes, static_cast<unsigned>((x_chunks + 255) / 256), 256, 0, s,
                     static_cast<const uint16_t*>(a.x), x_chunks, H, const_cast<uint8_t*>(p.xq),
                     const_cast<uint8_t*>(p.xe));
       if ((e = hipGetLastError()) != hipSuccess) return e;
+      p.row_tiles = I / 128;
+      launch_kernel(k_pf_mx_up, static_cast<unsigned>(max_tiles * p.row_tiles), kMxThreads, kMxLdsBytes, s, p);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
     }
+    p.row_tiles = up_rows;
+    const unsigned up_blocks = static_cast<unsigned>(max_tiles * p.row_tiles);
     if (q3) launch_kernel(k_pf_up<true>, up_blocks, kPfThreads, kPfLdsBytes, s, p);
     else launch_kernel(k_pf_up<false>, up_blocks, kPfThreads, kPfLdsBytes, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -1072,6 +1210,10 @@ hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, con
   p.row_tiles = H / kPfRows;
   const unsigned down_blocks = static_cast<unsigned>(max_tiles * p.row_tiles);
   for (int r = 0; r < repeat; ++r) {
+    if (mx) {
+      launch_kernel(k_pf_mx_down, down_blocks, kMxThreads, kMxLdsBytes, s, p);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     if (q3) launch_kernel(k_pf_down<true>, down_blocks, kPfThreads, kPfLdsBytes, s, p);
     else launch_kernel(k_pf_down<false>, down_blocks, kPfThreads, kPfLdsBytes, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
