@@ -151,39 +151,65 @@ __device__ __forceinline__ f32x4 lds_f32x4(const char* row, int lane) {
   }
 }
 
+// Value of lane l ^ S (S = 8, 4, 2, 1): DPP within a row of 16 lanes (a
+// rotation by 8 is the XOR with 8 there), the LDS crossbar's swizzle for 4.
+template <int S>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int u = __float_as_int(v);
+  int r;
+  if constexpr (S == 8) r = __builtin_amdgcn_update_dpp(0, u, 0x128, 0xF, 0xF, false);        // row_ror:8
+  else if constexpr (S == 4) r = __builtin_amdgcn_ds_swizzle(u, 0x1F | (4 << 10));            // xor 4
+  else if constexpr (S == 2) r = __builtin_amdgcn_update_dpp(0, u, 0x4E, 0xF, 0xF, false);    // [2,3,0,1]
+  else r = __builtin_amdgcn_update_dpp(0, u, 0xB1, 0xF, 0xF, false);                          // [1,0,3,2]
+  return __int_as_float(r);
+}
+
 // Reduce-scatter of N values per lane across the 64 lanes at stride S (then
 // S/2 .. 1); on return lane l holds in vals[0 .. N/64) the tree sums of
-// values l*N/64 .. of the full XOR butterfly.
+// values l*N/64 .. of the full XOR butterfly.  At stride S a lane keeps the
+// upper half of its values if bit S of its id is set, else the lower half,
+// and adds the partner's (lane ^ S) copy of them.  Strides 32 and 16 are one
+// v_permlane32_swap / v_permlane16_swap per pair of values: the swap leaves
+// in each lane exactly the two addends of its kept value (vals[j] of lane l
+// and of lane l ^ S in the lower lanes, vals[j + N/2] of both in the upper
+// ones), and their sum is the same in either order.
 template <int N, int S>
 __device__ __forceinline__ void xor_reduce_scatter(float* vals, int lane) {
 #pragma clang fp contract(off)
-  if constexpr (S >= 1) {
+  if constexpr (S >= 16) {
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+      const uint32_t a = __float_as_uint(vals[j]), b = __float_as_uint(vals[j + N / 2]);
+      const auto sw = S == 32 ? __builtin_amdgcn_permlane32_swap(a, b, false, false)
+                              : __builtin_amdgcn_permlane16_swap(a, b, false, false);
+      vals[j] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    xor_reduce_scatter<N / 2, S / 2>(vals, lane);
+  } else if constexpr (S >= 1) {
     const bool upper = (lane & S) != 0;
 #pragma unroll
     for (int j = 0; j < N / 2; ++j) {
       const float send = upper ? vals[j] : vals[j + N / 2];
       const float mine = upper ? vals[j + N / 2] : vals[j];
-      const float recv = __shfl_xor(send, S, 64);
-      vals[j] = mine + recv;
+      vals[j] = mine + lane_xor<S>(send);
     }
     xor_reduce_scatter<N / 2, S / 2>(vals, lane);
   }
 }
 
-template <bool kXBF16, bool kWBF16>
-__global__ __launch_bounds__(kGwThreads, 4) void k_gate_wide(GateArgs g) {
+// kFull: the tile's 32 tokens and 16 experts all exist and H is a multiple
+// of 256, so the staging loads need no clamps and the stores no masks.
+template <bool kXBF16, bool kWBF16, bool kFull>
+__device__ __forceinline__ void gate_wide_tile(const GateArgs& g, char* gw_lds, int t0, int e0) {
 #pragma clang fp contract(off)
   constexpr int kSx = kXBF16 ? 2 : 4, kSw = kWBF16 ? 2 : 4;
   constexpr int kXBytes = kGwTok * 256 * kSx, kWBytes = kGwExp * 256 * kSw;
   constexpr int kBuf = kXBytes + kWBytes;
   constexpr int kXChunks = kXBytes / 16 / kGwThreads, kWChunks = kWBytes / 16 / kGwThreads;
   static_assert(kXChunks >= 1 && kWChunks >= 1, "staging chunks");
-  extern __shared__ __align__(16) char gw_lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wt = wave & 3, we = wave >> 2;
-  const int n_et = (g.E + kGwExp - 1) / kGwExp;
-  const int t0 = (blockIdx.x / n_et) * kGwTok, e0 = (blockIdx.x % n_et) * kGwExp;
   const int H = g.H, steps = (H + 255) / 256, seg = (steps + kSegments - 1) / kSegments;
   // staging: thread chunk c = tid + 512 q of the x tile ([32][256] elements,
   // 16-byte chunks), the same for W; addresses recomputed per step
@@ -193,34 +219,60 @@ __global__ __launch_bounds__(kGwThreads, 4) void k_gate_wide(GateArgs g) {
   // is stored.
   u32x4 xr[kXChunks], wr[kWChunks];
   uint32_t xkeep[kXChunks], wkeep[kWChunks];
-  auto load = [&](int m) {
+  // full tiles: each chunk's byte offset from the (uniform) array start,
+  // the step adds 256 elements (the arrays are below 2 GB: kFull's test)
+  uint32_t xo[kXChunks], wo[kWChunks];
+  if constexpr (kFull) {
 #pragma unroll
     for (int q = 0; q < kXChunks; ++q) {
       constexpr int per_row = 256 * kSx / 16;
       const int c = tid + kGwThreads * q;
-      const int col = 256 * m + (c % per_row) * (16 / kSx);
-      const int64_t row = min(t0 + c / per_row, g.T - 1);
-      xkeep[q] = col < H ? ~0u : 0u;
-      xr[q] = ldg16(static_cast<const char*>(g.x) + (row * H + min(col, H - 16 / kSx)) * kSx);
+      xo[q] = static_cast<uint32_t>(((t0 + c / per_row) * H + (c % per_row) * (16 / kSx)) * kSx);
     }
 #pragma unroll
     for (int q = 0; q < kWChunks; ++q) {
       constexpr int per_row = 256 * kSw / 16;
       const int c = tid + kGwThreads * q;
-      const int col = 256 * m + (c % per_row) * (16 / kSw);
-      const int64_t row = min(e0 + c / per_row, g.E - 1);
-      wkeep[q] = col < H ? ~0u : 0u;
-      wr[q] = ldg16(static_cast<const char*>(g.gw) + (row * H + min(col, H - 16 / kSw)) * kSw);
+      wo[q] = static_cast<uint32_t>(((e0 + c / per_row) * H + (c % per_row) * (16 / kSw)) * kSw);
+    }
+  }
+  auto load = [&](int m) {
+    if constexpr (kFull) {
+      const char* xbase = static_cast<const char*>(g.x) + static_cast<int64_t>(256 * kSx) * m;
+      const char* wbase = static_cast<const char*>(g.gw) + static_cast<int64_t>(256 * kSw) * m;
+#pragma unroll
+      for (int q = 0; q < kXChunks; ++q) xr[q] = ldg16(xbase + xo[q]);
+#pragma unroll
+      for (int q = 0; q < kWChunks; ++q) wr[q] = ldg16(wbase + wo[q]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < kXChunks; ++q) {
+        constexpr int per_row = 256 * kSx / 16;
+        const int c = tid + kGwThreads * q;
+        const int col = 256 * m + (c % per_row) * (16 / kSx);
+        const int64_t row = min(t0 + c / per_row, g.T - 1);
+        xkeep[q] = col < H ? ~0u : 0u;
+        xr[q] = ldg16(static_cast<const char*>(g.x) + (row * H + min(col, H - 16 / kSx)) * kSx);
+      }
+#pragma unroll
+      for (int q = 0; q < kWChunks; ++q) {
+        constexpr int per_row = 256 * kSw / 16;
+        const int c = tid + kGwThreads * q;
+        const int col = 256 * m + (c % per_row) * (16 / kSw);
+        const int64_t row = min(e0 + c / per_row, g.E - 1);
+        wkeep[q] = col < H ? ~0u : 0u;
+        wr[q] = ldg16(static_cast<const char*>(g.gw) + (row * H + min(col, H - 16 / kSw)) * kSw);
+      }
     }
   };
   auto store = [&](int buf) {
     char* b = gw_lds + buf * kBuf;
 #pragma unroll
     for (int q = 0; q < kXChunks; ++q)
-      *reinterpret_cast<u32x4*>(b + 16 * (tid + kGwThreads * q)) = xr[q] & xkeep[q];
+      *reinterpret_cast<u32x4*>(b + 16 * (tid + kGwThreads * q)) = kFull ? xr[q] : (xr[q] & xkeep[q]);
 #pragma unroll
     for (int q = 0; q < kWChunks; ++q)
-      *reinterpret_cast<u32x4*>(b + kXBytes + 16 * (tid + kGwThreads * q)) = wr[q] & wkeep[q];
+      *reinterpret_cast<u32x4*>(b + kXBytes + 16 * (tid + kGwThreads * q)) = kFull ? wr[q] : (wr[q] & wkeep[q]);
   };
   float p[64];
   float z = 0.0f;
@@ -270,6 +322,19 @@ __global__ __launch_bounds__(kGwThreads, 4) void k_gate_wide(GateArgs g) {
   for (int w = done_segments; w < kSegments; ++w) z = z + 0.0f;   // empty segments add +0
   const int t = t0 + 8 * wt + lane / 8, e = e0 + 8 * we + lane % 8;
   if (t < g.T && e < g.E) g.scores[static_cast<int64_t>(t) * g.E + e] = score_of(z, g.score_func);
+}
+
+template <bool kXBF16, bool kWBF16>
+__global__ __launch_bounds__(kGwThreads, 4) void k_gate_wide(GateArgs g) {
+  extern __shared__ __align__(16) char gw_lds[];
+  const int n_et = (g.E + kGwExp - 1) / kGwExp;
+  const int t0 = (blockIdx.x / n_et) * kGwTok, e0 = (blockIdx.x % n_et) * kGwExp;
+  const int64_t xbytes = static_cast<int64_t>(g.T) * g.H * (kXBF16 ? 2 : 4);
+  const int64_t wbytes = static_cast<int64_t>(g.E) * g.H * (kWBF16 ? 2 : 4);
+  if (t0 + kGwTok <= g.T && e0 + kGwExp <= g.E && g.H % 256 == 0 && xbytes < (1ll << 31) && wbytes < (1ll << 31))
+    gate_wide_tile<kXBF16, kWBF16, true>(g, gw_lds, t0, e0);
+  else
+    gate_wide_tile<kXBF16, kWBF16, false>(g, gw_lds, t0, e0);
 }
 
 hipError_t launch_gate_wide(const dsk_moe_desc& d, const GateArgs& g, hipStream_t s) {
