@@ -181,6 +181,12 @@ def measured_traffic(kernels: list[str], workload: str):
     return total
 
 
+def pf_up_kernels(quant: str) -> list[str]:
+    """The prefill gate/up stage's kernels: FP4 layers of the full shape run the
+    x planes, the routed MX tiles and the shared expert's bf16 tiles."""
+    return ["k_pf_planes", "k_pf_mx_up", "k_pf_up"] if quant == "fp4" else ["k_pf_up"]
+
+
 def traffic_fields(kernels: list[str], workload: str) -> dict:
     """roofline["traffic"] and where it comes from."""
     t = measured_traffic(kernels, workload)
@@ -289,7 +295,7 @@ def prefill_summary(r: dict, t: int, steps: int) -> dict:
     st = r["stage_us"]
     up = st[:, 2]
     return {"stages": {n: {"us": pct(st[:, j])} for j, n in enumerate(STAGES)},
-            "k_pf_up_mfma_frac": round(up_flops(t) / (float(np.median(up)) * 1e-6) / PEAK_BF16, 4),
+            "gate_up_mfma_frac": round(up_flops(t) / (float(np.median(up)) * 1e-6) / PEAK_BF16, 4),
             "layer": {"flops": layer_flops(t), "kernels_us": pct(r["layer_us"]),
                       "mfma_frac": round(layer_flops(t) / (float(np.median(r["layer_us"])) * 1e-6) / PEAK_BF16, 4),
                       "mfma_frac_wall": round(layer_flops(t) / (r["wall_s"] / steps) / PEAK_BF16, 4)},
@@ -588,8 +594,11 @@ def main() -> int:
         achieved = up_flops(T) / (up_us * 1e-6)
         roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 1), "peak": PEAK_BF16 / 1e12,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4),
-                    **traffic_fields(["k_pf_up"], workload),
-                    "kernel": f"k_pf_up (routed {args.quant.upper()} + shared bf16 w1/w3 GEMM tiles, SwiGLU epilogue)",
+                    **traffic_fields(pf_up_kernels(args.quant), workload),
+                    "kernel": ("gate/up stage: k_pf_planes (x as FP8 planes) + k_pf_mx_up (routed FP4 w1/w3 on "
+                               "scaled FP4 x FP8 MFMAs) + k_pf_up (shared bf16 w1/w3), SwiGLU epilogues"
+                               if args.quant == "fp4" else
+                               f"k_pf_up (routed {args.quant.upper()} + shared bf16 w1/w3 GEMM tiles, SwiGLU epilogue)"),
                     "flops_per_launch": int(up_flops(T)), "avg_launch_us": up_us, "timing": timing}
     else:
         summ = decode_summary(r, T, args.quant, args.steps)
