@@ -525,6 +525,198 @@ __device__ __forceinline__ void up_block_mx(const GroupedArgs& p, const void* co
   }
 }
 
+// The shared expert over more than kGNC tokens.  Its weights are 50 MB of
+// bf16 at hidden 4096 / inter 2048, which the column-tile walk above would
+// stream once per kGNC tokens (8x at 64 tokens).  Here a block's waves each
+// take one row tile (16 rows of one weight matrix) over the whole of K and
+// step through K together: at step s every wave multiplies K block s of its
+// rows against the same activation block (up to kGsCols tokens x 128 of K,
+// four 16-column MFMA tiles) staged in LDS.  The activations are
+// L2-resident and small next to the weights; they go through registers into
+// two LDS buffers, one barrier per step (gs_walk).  Weights stream once per
+// kGsCols tokens.
+constexpr int kGsCols = 64;              // tokens of a wide shared column group
+constexpr int kGsCT = kGsCols / 16;      // its 16-column MFMA tiles
+constexpr int kGsStride = 128 + 8;       // LDS row stride (elements) of a staged K block
+constexpr int kGsPlane = kGsCols * kGsStride;
+
+__host__ __device__ constexpr size_t gs_up_lds_bytes() { return 2 * size_t{kGsPlane} * 2; }
+__host__ __device__ constexpr size_t gs_down_lds_bytes() { return 2 * 2 * size_t{kGsPlane} * 2; }
+
+// K block kb of the group's rows g0 .. g0 + ncol - 1 of a [rows][ld] bf16
+// matrix: thread t's 16-byte chunks t and t + 512 (row c / 16, 8 elements
+// c % 16); rows past the group read its last row (never stored).
+__device__ __forceinline__ void gs_load(u32x4 (&v)[2], const uint16_t* m, int ld, int g0, int ncol, int kb) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int c = static_cast<int>(threadIdx.x) + q * kGW * 64;
+    const int r = min(c >> 4, ncol - 1);
+    v[q] = ldg16(m + static_cast<int64_t>(g0 + r) * ld + kb * 128 + (c & 15) * 8);
+  }
+}
+
+__device__ __forceinline__ void gs_store(const u32x4 (&v)[2], uint16_t* buf) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int c = static_cast<int>(threadIdx.x) + q * kGW * 64;
+    *reinterpret_cast<u32x4*>(buf + (c >> 4) * kGsStride + (c & 15) * 8) = v[q];
+  }
+}
+
+static_assert(kGW * 64 * 2 * 8 == kGsCols * 128, "two chunks per thread stage one K block of the group");
+
+// Steps 0 .. nb - 1 of a wide shared walk with rings of NB weight batches
+// and NB activation register slots, and two LDS buffers: mm(i, buf)
+// multiplies batch i against buffer buf, ldw(i, kb) reloads batch i with K
+// block kb, ldx(i, kb) loads K block kb's activations into slot i, stx(i,
+// buf) copies slot i into buffer buf.  Block t's activations are loaded NB
+// steps ahead, before the weights of block t, so copying them into LDS at
+// step t - 1 waits only for weights already used.  Loads past the end
+// re-read block nb - 1 (unused), so no load in the main loop sits under a
+// condition; the last steps load only what remains.
+template <int NB, typename MM, typename LW, typename LX, typename SX>
+__device__ __forceinline__ void gs_walk(int nb, MM mm, LW ldw, LX ldx, SX stx) {
+  constexpr int U = NB % 2 == 0 ? NB : 2 * NB;   // steps per pass: slots and buffers back in phase
+#pragma unroll
+  for (int i = 0; i < NB; ++i) ldx(i, min(i, nb - 1));
+#pragma unroll
+  for (int i = 0; i < NB; ++i) ldw(i, min(i, nb - 1));
+  stx(0, 0);
+  __syncthreads();
+  int s = 0;
+  for (; s + U <= nb; s += U) {
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      mm(i % NB, i & 1);
+      ldx(i % NB, min(s + i + NB, nb - 1));
+      ldw(i % NB, min(s + i + NB, nb - 1));
+      stx((i + 1) % NB, (i + 1) & 1);
+      __syncthreads();
+    }
+  }
+  // the last nb - s < U steps
+#pragma unroll
+  for (int i = 0; i < U - 1; ++i) {
+    if (s + i < nb) {
+      mm(i % NB, i & 1);
+      if (s + i + NB < nb) {
+        ldx(i % NB, s + i + NB);
+        ldw(i % NB, s + i + NB);
+      }
+      if (s + i + 1 < nb) stx((i + 1) % NB, (i + 1) & 1);
+      __syncthreads();
+    }
+  }
+}
+
+// Gate/up of the shared expert over more than kGNC tokens: waves 2i and
+// 2i + 1 take row tile 4b + i of w1 (gate) and of w3 (up), so that a wave
+// holds one role's accumulators and a ring of four weight batches; the up
+// wave hands its sums to the gate wave through LDS for SwiGLU.
+__device__ __forceinline__ void up_shared_wide(const GroupedArgs& p, int b, uint16_t* lds) {
+  constexpr int NB = 3;
+  const int lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int role = wave & 1, pair = wave >> 1;
+  const int rt = b * (kGW / 2) + pair;
+  const bool rok = rt < p.Is / 16;
+  const uint32_t row = rok ? static_cast<uint32_t>(rt * 16 + r16) : 0u;
+  const uint16_t* W = role ? p.ws3 : p.ws1;
+  const int K = p.H, nb = K / 128;
+  f32x4 (*xch)[kGsCT][64] = reinterpret_cast<f32x4 (*)[kGsCT][64]>(lds);   // [pair][tile][lane], after the walk
+  for (int g0 = 0; g0 < p.T; g0 += kGsCols) {
+    const int ncol = min(kGsCols, p.T - g0);
+    const int nct = (ncol + 15) / 16;
+    RawBF16 w[NB];
+    u32x4 xv[NB][2];
+    f32x4 acc[kGsCT];
+#pragma unroll
+    for (int c = 0; c < kGsCT; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto mm = [&](int i, int buf) {
+#pragma unroll
+      for (int c = 0; c < kGsCT; ++c)
+        if (c < nct) mma_block(w[i], lds + buf * kGsPlane + (c * 16 + r16) * kGsStride, g4 * 32, true, acc[c]);
+    };
+    auto ldw = [&](int i, int kb) { load_raw_nc(w[i], W, row, K, kb * 128 + g4 * 32); };
+    auto ldx = [&](int slot, int kb) { gs_load(xv[slot], p.x, K, g0, ncol, kb); };
+    auto stx = [&](int slot, int buf) { gs_store(xv[slot], lds + buf * kGsPlane); };
+    gs_walk<NB>(nb, mm, ldw, ldx, stx);   // ends with a barrier: the buffers are free
+    if (role) {
+#pragma unroll
+      for (int c = 0; c < kGsCT; ++c) xch[pair][c][lane] = acc[c];
+    }
+    __syncthreads();
+    if (!role && rok) {
+#pragma unroll
+      for (int c = 0; c < kGsCT; ++c) {
+        const int t = c * 16 + r16;
+        if (t < ncol) {
+          const f32x4 au = xch[pair][c][lane];
+          uint16_t hh[4], hl[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) split_bf16(silu_clamped(acc[c][q], au[q], p.limit), hh[q], hl[q]);
+          const int64_t off = static_cast<int64_t>(g0 + t) * p.Is + rt * 16 + 4 * g4;
+          *reinterpret_cast<uint2*>(p.hs_hi + off) =
+              uint2{hh[0] | (uint32_t(hh[1]) << 16), hh[2] | (uint32_t(hh[3]) << 16)};
+          *reinterpret_cast<uint2*>(p.hs_lo + off) =
+              uint2{hl[0] | (uint32_t(hl[1]) << 16), hl[2] | (uint32_t(hl[3]) << 16)};
+        }
+      }
+    }
+    __syncthreads();   // the exchange is read before the next group restages the buffers
+  }
+}
+
+static_assert(size_t{kGW / 2} * kGsCT * 64 * 16 <= gs_up_lds_bytes(), "the SwiGLU exchange fits the buffers");
+
+// Down of the shared expert over more than kGNC tokens, as up_shared_wide:
+// block b's eight waves each take one row tile of w2 (16 output rows) over
+// K = Is, the h planes (hi, lo) of up to kGsCols tokens staged per K block.
+__device__ __forceinline__ void down_shared_wide(const GroupedArgs& p, int b, uint16_t* lds) {
+  constexpr int NB = 2;
+  const int lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int rt = b * kDW + wave;
+  const uint32_t row = static_cast<uint32_t>(rt * 16 + r16);
+  const int K = p.Is, nb = K / 128;
+  for (int g0 = 0; g0 < p.T; g0 += kGsCols) {
+    const int ncol = min(kGsCols, p.T - g0);
+    const int nct = (ncol + 15) / 16;
+    RawBF16 w[NB];
+    u32x4 xh[NB][2], xl[NB][2];
+    f32x4 acc[kGsCT];
+#pragma unroll
+    for (int c = 0; c < kGsCT; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto mm = [&](int i, int buf) {
+      const uint16_t* hi = lds + buf * 2 * kGsPlane;
+#pragma unroll
+      for (int c = 0; c < kGsCT; ++c) {
+        if (c < nct) {
+          const int o = (c * 16 + r16) * kGsStride;
+          mma_block(w[i], hi + o, g4 * 32, true, acc[c]);
+          mma_block(w[i], hi + kGsPlane + o, g4 * 32, true, acc[c]);
+        }
+      }
+    };
+    auto ldw = [&](int i, int kb) { load_raw_nc(w[i], p.ws2, row, K, kb * 128 + g4 * 32); };
+    auto ldx = [&](int slot, int kb) {
+      gs_load(xh[slot], p.hs_hi, K, g0, ncol, kb);
+      gs_load(xl[slot], p.hs_lo, K, g0, ncol, kb);
+    };
+    auto stx = [&](int slot, int buf) {
+      gs_store(xh[slot], lds + buf * 2 * kGsPlane);
+      gs_store(xl[slot], lds + buf * 2 * kGsPlane + kGsPlane);
+    };
+    gs_walk<NB>(nb, mm, ldw, ldx, stx);
+#pragma unroll
+    for (int c = 0; c < kGsCT; ++c) {
+      const int t = c * 16 + r16;
+      if (t < ncol) *reinterpret_cast<f32x4*>(p.ys + static_cast<int64_t>(g0 + t) * p.H + rt * 16 + 4 * g4) = acc[c];
+    }
+    __syncthreads();   // the next group restages buffer 0
+  }
+}
+
 // Blocks [0, up_shared): the shared expert (bf16 w1/w3, all T tokens); the
 // others: up_groups blocks per slot.
 template <typename Raw>
@@ -533,6 +725,10 @@ __global__ __launch_bounds__(kGW * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   const int b = static_cast<int>(blockIdx.x);
   const int item = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / kGKS;
   if (b < p.up_shared) {
+    if (p.T > kGNC) {
+      up_shared_wide(p, b, lds_g);
+      return;
+    }
     const int rt = b * kGI + item;
     auto load_w = [&](RawBF16& r, int role, uint32_t row, int kc) { load_raw_nc(r, role ? p.ws3 : p.ws1, row, p.H, kc); };
     up_block<RawBF16>(p, load_w, [&](int) -> const void* { return p.ws1; }, rt, rt < p.Is / 16, p.T, 0, true, lds_g);
@@ -875,6 +1071,10 @@ k_down_grouped(GroupedArgs p) {
   const int b = static_cast<int>(blockIdx.x);
   const int item = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / kDKS;
   if (b < p.dn_shared) {
+    if (p.T > kGNC) {
+      down_shared_wide(p, b, lds_g);
+      return;
+    }
     const int rt = b * kDI + item;
     auto load_w = [&](RawBF16& r, uint32_t row, int kc) { load_raw_nc(r, p.ws2, row, p.Is, kc); };
     down_block<RawBF16>(p, load_w, [&](int) -> const void* { return p.ws2; }, rt, p.T, 0, true, lds_g);
@@ -941,6 +1141,7 @@ size_t up_lds(const dsk_moe_desc& d) {
   const size_t q3f = x_tile + static_cast<size_t>(d.hidden / 128) * kQ3fMaxTokens * 16 + 64;
   size_t base = x_tile > red ? x_tile : red;
   if (up_mx(d) && gx_lds_bytes(d.hidden) > base) base = gx_lds_bytes(d.hidden);
+  if (d.tokens > kGNC && d.inter_shared > 0 && gs_up_lds_bytes() > base) base = gs_up_lds_bytes();
   return up_q3f(d) && q3f > base ? q3f : base;
 }
 
@@ -962,7 +1163,8 @@ size_t down_lds(const dsk_moe_desc& d) {
   const size_t q3f = 2 * static_cast<size_t>(kGNC) * (d.inter + 8) * 2 +
                      static_cast<size_t>(d.inter / 128) * kQ3fMaxTokens * 16 + 64;
   const size_t mx = grouped_h_planes(d) ? gd_lds_bytes(d.inter) : 0;
-  const size_t b2 = mx > base ? mx : base;
+  size_t b2 = mx > base ? mx : base;
+  if (d.tokens > kGNC && d.inter_shared > 0 && gs_down_lds_bytes() > b2) b2 = gs_down_lds_bytes();
   return down_q3f(d) && q3f > b2 ? q3f : b2;
 }
 
@@ -1002,7 +1204,8 @@ GroupedArgs grouped_args(const dsk_moe_desc& d, const Workspace& L, const Expert
   p.hplanes = 0;   // set by the launchers where the grouped gate/up writes h
   p.hp = reinterpret_cast<uint8_t*>(a.ws + L.hp);
   p.up_groups = p.q3f ? d.inter / 16 : d.inter / 16 / kGI;   // factored q3: one row tile per block
-  p.up_shared = d.inter_shared / 16 / kGI;
+  // shared gate/up: past kGNC tokens, four row tiles per block (up_shared_wide)
+  p.up_shared = d.tokens > kGNC ? (d.inter_shared / 16 + kGW / 2 - 1) / (kGW / 2) : d.inter_shared / 16 / kGI;
   p.dn_groups = d.hidden / 16 / kDI;
   p.dn_shared = d.inter_shared > 0 ? p.dn_groups : 0;
   return p;

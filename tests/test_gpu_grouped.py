@@ -2,7 +2,9 @@
 and the prefill GEMM, bf16 activations) against the oracle.
 
 Routing indices bit-exact; outputs within the layer tolerance.  Cases: the
-full-size FP4 layer at T=20; mid-size layers with skewed routing (every
+full-size FP4 layer at T=20; mid-size layers up to 127 tokens (the shared
+expert's wide walk takes 64 tokens a pass: 100 and 127 take two, the second
+ragged); mid-size layers with skewed routing (every
 token to the same few experts, so each slot spans several column tiles of
 dispatch rows), q3 experts, no shared expert, a callable shared expert, the
 host-dispatch entry point (dsk_experts) reached through a callable
@@ -36,6 +38,7 @@ def _skewed(d, hot: int):
 
 @pytest.mark.parametrize("quant,T,hot", [
     ("fp4", 20, 0), ("fp4", 20, 8), ("fp4", 37, 8), ("q3", 24, 0), ("q3", 30, 8), ("fp4", 63, 0),
+    ("fp4", 100, 0), ("q3", 127, 0),
 ])
 def test_grouped_mid(quant, T, hot):
     print(f"grouped mid {quant} T={T} hot={hot}", flush=True)
