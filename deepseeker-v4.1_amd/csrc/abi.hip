@@ -91,7 +91,11 @@ Workspace workspace_layout(const dsk_moe_desc& d) {
     L.xp = take(T * (2 * H + H / 32));
     L.hp = take(N * (2 * I + I / 32));
   } else {
-    L.xp = take(d.quant == DSK_QUANT_FP4 && d.x_dtype == DSK_DTYPE_BF16 && !prefill_gemm(d) ? T * 2 * (H + H / 32) : 0);
+    // q3: x scaled for the factored gate/up [T][H] bf16, then its 64-group sums [T][H/64][2] f32
+    const bool bf16x = d.x_dtype == DSK_DTYPE_BF16 && !prefill_gemm(d);
+    L.xp = take(bf16x && d.quant == DSK_QUANT_FP4 ? T * 2 * (H + H / 32)
+                : bf16x && grouped_x_q3(d)     ? T * (2 * H + H / 8)
+                                               : 0);
     L.hp = take(!prefill_gemm(d) && grouped_h_planes(d) ? N * 3 * (I + I / 32) : 0);
   }
   L.pf_tiles = take(prefill_gemm(d) ? (3 + 2 * static_cast<size_t>(prefill_max_tiles(d))) * 4 : 0);

@@ -147,6 +147,8 @@ struct Workspace {
   size_t shared_x;          // decode pipeline: shared output [T][H] (x dtype)
   size_t xp;                // grouped FP4 gate/up: x as FP8 planes [T][2][H] + E8M0 [T][2][H/32];
                             // MX prefill: x as FP8 planes in stage rows [T][2H] + E8M0 [T][H/32]
+                            // grouped q3: x scaled for the factored gate/up [T][H] bf16 + 64-group
+                            // sums [T][H/64][2] f32
   size_t hp;                // grouped FP4: h as FP8 planes [T*k][3][I] + E8M0 [T*k][3][I/32];
                             // MX prefill: h in stage rows [T*k][2I] + E8M0 [T*k][I/32]
   size_t pf_tiles;          // prefill GEMM tile list  [2 + 2 * prefill_max_tiles] + the MX switch
@@ -338,6 +340,9 @@ hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, c
                                     int repeat, bool x_planes_ready);
 // The grouped FP4 gate/up takes x as FP8 planes (Workspace::xp).
 bool grouped_up_mx(const dsk_moe_desc& d);
+// The grouped q3 gate/up takes x scaled for the factored product, with its
+// 64-group sums (Workspace::xp).
+bool grouped_x_q3(const dsk_moe_desc& d);
 // h_planes: the routed h is in FP8 planes (the grouped gate/up ran and grouped_h_planes).
 hipError_t launch_grouped_down(const dsk_moe_desc& d, const Workspace& L, const ExpertsArgs& a,
                                const SlotDesc* desc, hipStream_t s, int repeat, bool h_planes);

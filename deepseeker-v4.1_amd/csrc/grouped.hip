@@ -212,18 +212,22 @@ __device__ __forceinline__ void up_block(const GroupedArgs& p, LoadW load_w, WPt
 // h-th 64-group), the B operand the raw codes.  Block = one row tile x kQ3gKS
 // K ranges (one wave each); every wave's range is whole 512-code superblocks
 // (hidden % (kQ3gKS * 512) == 0), one batch (superblock) in flight.  The
-// tile's x rows are staged first, divided by 8 at the 8q positions and with
-// their group sums; then the weights are issued.
+// tile's x rows (divided by 8 at the 8q positions, k_x_q3) and their group
+// sums are copied into LDS first; then the weights are issued.
 constexpr int kQ3gKS = kGW;
+constexpr int kQ3gMaxGroups = 128;   // 64-groups of a row: hidden up to 8192
 __device__ __forceinline__ void up_block_q3f(const GroupedArgs& p, const void* const* wp, int rt, bool rok, int n,
                                              int base, uint16_t* lds) {
   constexpr int G = 4;                       // K blocks per batch: one superblock
-  constexpr int kStg = 4;                    // x chunks per thread in flight while staging
   constexpr int NT = kGW * 64;
+  constexpr int kSumRegs = kQ3gMaxGroups * kGNC / NT;   // group sums per thread
+  static_assert(kSumRegs * NT == kQ3gMaxGroups * kGNC, "whole passes of group sums");
   const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
   const int ks = wave;
-  const int K = p.H, nblk = K / 128, cpr = K / 8;
+  const int K = p.H, nblk = K / 128, ng = K / 64;
+  const uint16_t* xq = reinterpret_cast<const uint16_t*>(p.xp);
+  const float* xg = reinterpret_cast<const float*>(p.xp + static_cast<size_t>(p.T) * K * 2);
   const int per = nblk / kQ3gKS;
   const int k0 = ks * per, k1 = k0 + per;
   const int xs = K + 8;
@@ -267,21 +271,26 @@ __device__ __forceinline__ void up_block_q3f(const GroupedArgs& p, const void* c
   const Q3Masks km = q3_masks();
   for (int c0 = 0; c0 < n; c0 += kGNC) {
     const int cols = min(kGNC, n - c0);
-    // the tile's x rows first (their registers are free again before the
-    // weights land), kStg chunks per thread in flight (cols * cpr is a
-    // multiple of 8: whole lane groups)
-    const int xch = cols * cpr;
-    for (int cb = 0; cb < xch; cb += kStg * NT) {
-      u32x4 v[kStg];
+    // the tile's x rows and group sums first (written once per call by
+    // k_x_q3; their registers are free again before the weights land): the
+    // sums' loads go out ahead of the rows', both stored once the rows land
+    {
+      const int nsum = cols * ng;
+      u32x2 sv[kSumRegs];   // {sum x, sum x / m} as loaded
 #pragma unroll
-      for (int j = 0; j < kStg; ++j) {
-        const int c = min(cb + j * NT + tid, xch - 1);
-        v[j] = ldg16(p.x + static_cast<int64_t>(p.xrow[base + c0 + c / cpr]) * K + (c % cpr) * 8);
+      for (int j = 0; j < kSumRegs; ++j) {
+        const int i = min(tid + j * NT, nsum - 1);
+        const int r = i / ng, gi = i - r * ng;
+        sv[j] = ldg<u32x2>(xg + (static_cast<int64_t>(p.xrow[base + c0 + r]) * ng + gi) * 2);
       }
+      stage_rows(xh, xq, K, K, cols, [&](int r) { return p.xrow[base + c0 + r]; });
 #pragma unroll
-      for (int j = 0; j < kStg; ++j) {
-        const int c = cb + j * NT + tid;
-        if (c < xch) stage_chunk_q3<false>(xh, nullptr, xsum, xs, cpr, c, v[j], u32x4{});
+      for (int j = 0; j < kSumRegs; ++j) {
+        const int i = tid + j * NT;
+        if (i < nsum) {
+          const int r = i / ng, gi = i - r * ng;
+          *reinterpret_cast<u32x2*>(xsum + (((gi >> 1) * kQ3fMaxTokens + r) * 2 + (gi & 1)) * 2) = sv[j];
+        }
       }
     }
     Q3Batch<G> A;
@@ -364,6 +373,26 @@ __global__ __launch_bounds__(256) void k_x_planes(const uint16_t* __restrict__ x
   const int n = T * (H / 8);
   const int c0 = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
   x_planes_chunk(x, T, H, min(c0, n - 1), c0 < n, xp);   // every lane takes part in the group exchange
+}
+
+// x for the factored q3 gate/up (up_block_q3f), once per call instead of once
+// per block: the values at 8q code positions divided by 8 as bf16 [T][H] (xq)
+// and every 64-group's {sum x, sum x / m} [T][H/64] (xg), as q3_chunk makes
+// them; the blocks copy the rows and sums of their column tile.
+__global__ __launch_bounds__(256) void k_x_q3(const uint16_t* __restrict__ x, int T, int H,
+                                              uint16_t* __restrict__ xq, float* __restrict__ xg) {
+  const int cpr = H / 8, n = T * cpr;
+  const int c = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  const int cl = min(c, n - 1);   // every lane takes part in the group's sums (past the end: not stored)
+  const int t = cl / cpr, cc = cl - t * cpr;
+  const int64_t o = static_cast<int64_t>(t) * H + cc * 8;
+  u32x4 hp, lp;
+  float sx, sxm;
+  q3_chunk<false>(cc, ldg16(x + o), u32x4{}, hp, lp, sx, sxm);
+  if (c < n) {
+    *reinterpret_cast<u32x4*>(xq + o) = hp;
+    if ((cc & 7) == 0) *reinterpret_cast<float2*>(xg + (static_cast<int64_t>(t) * (H / 64) + (cc >> 3)) * 2) = float2{sx, sxm};
+  }
 }
 
 // LDS of up_block_mx: the column tile's planes [H/128][16][128] bytes, then
@@ -1108,7 +1137,9 @@ k_down_grouped(GroupedArgs p) {
 }
 
 // The factored q3 gate/up: every wave's K range whole superblocks.
-bool up_q3f(const dsk_moe_desc& d) { return d.quant == DSK_QUANT_Q3 && d.hidden % (kQ3gKS * 512) == 0; }
+bool up_q3f(const dsk_moe_desc& d) {
+  return d.quant == DSK_QUANT_Q3 && d.hidden % (kQ3gKS * 512) == 0 && d.hidden <= kQ3gMaxGroups * 64;
+}
 
 // The FP4 gate/up on scaled MFMAs: bf16 x (planes made from it), every wave's
 // K range 2, 4, 6 or 8 whole blocks (up_block_mx's instances).
@@ -1127,6 +1158,8 @@ bool up_mx(const dsk_moe_desc& d) {
 // 8.6 us to the gate/up.
 bool grouped_up_mx(const dsk_moe_desc& d) { return up_mx(d); }
 
+bool grouped_x_q3(const dsk_moe_desc& d) { return up_q3f(d); }
+
 bool grouped_h_planes(const dsk_moe_desc& d) {
   return up_mx(d) && (d.inter == 512 || d.inter == 1024 || d.inter == 2048) &&
          static_cast<int64_t>(d.tokens) * d.top_k <= 256;
@@ -1143,6 +1176,14 @@ size_t up_lds(const dsk_moe_desc& d) {
   if (up_mx(d) && gx_lds_bytes(d.hidden) > base) base = gx_lds_bytes(d.hidden);
   if (d.tokens > kGNC && d.inter_shared > 0 && gs_up_lds_bytes() > base) base = gs_up_lds_bytes();
   return up_q3f(d) && q3f > base ? q3f : base;
+}
+
+hipError_t launch_x_q3(const dsk_moe_desc& d, const GroupedArgs& p, hipStream_t s) {
+  const int64_t n = static_cast<int64_t>(d.tokens) * (d.hidden / 8);
+  uint16_t* xq = reinterpret_cast<uint16_t*>(p.xp);
+  float* xg = reinterpret_cast<float*>(p.xp + static_cast<size_t>(d.tokens) * d.hidden * 2);
+  launch_kernel(k_x_q3, static_cast<unsigned>((n + 255) / 256), 256, 0, s, p.x, d.tokens, d.hidden, xq, xg);
+  return hipGetLastError();
 }
 
 hipError_t launch_x_planes(const dsk_moe_desc& d, const GroupedArgs& p, hipStream_t s) {
@@ -1238,6 +1279,7 @@ hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, con
   if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   for (int r = 0; r < repeat; ++r) {
     if (p.mx && (e = launch_x_planes(d, p, s)) != hipSuccess) return e;
+    if (p.q3f && (e = launch_x_q3(d, p, s)) != hipSuccess) return e;
     if (d.quant == DSK_QUANT_Q3) launch_kernel(k_up_grouped<RawQ3>, up_blocks, kGW * 64, ul, s, p);
     else launch_kernel(k_up_grouped<RawFP4>, up_blocks, kGW * 64, ul, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -1257,6 +1299,10 @@ hipError_t launch_grouped_up_routed(const dsk_moe_desc& d, const Workspace& L, c
   for (int r = 0; r < repeat; ++r) {
     if (p.mx && !x_planes_ready) {
       const hipError_t e = launch_x_planes(d, p, s);
+      if (e != hipSuccess) return e;
+    }
+    if (p.q3f) {
+      const hipError_t e = launch_x_q3(d, p, s);
       if (e != hipSuccess) return e;
     }
     if (d.quant == DSK_QUANT_Q3) launch_kernel(k_up_grouped<RawQ3>, blocks, kGW * 64, lds, s, p);

@@ -363,15 +363,14 @@ __device__ __forceinline__ u32x4 pack_bf16x8(const uint16_t* v) {
 // Tokens of the factored q3 gate/up (A operand row 2t + h for t < 8).
 constexpr int kQ3fMaxTokens = 8;
 
-// One activation chunk (8 values of token t, chunk cc of its row) for the
-// factored q3 product: the values at 8q code positions divided by 8 (exact),
-// as bf16 plane(s); the chunk's sum(x) and sum(x / m) are reduced over the 8
-// lanes of its 64-group (fixed order) and written to xsum[kb][t][h] =
-// {sum x, sum x / m}.  All lanes of an aligned 8-lane group call it together.
+// One activation chunk (8 values, chunk cc of its row) for the factored q3
+// product: the values at 8q code positions divided by 8 (exact), as bf16
+// plane(s) hp (and lp), and the chunk's sum(x) and sum(x / m) reduced over the
+// 8 lanes of its 64-group in a fixed order.  All lanes of an aligned 8-lane
+// group call it together.
 template <bool kF32>
-__device__ __forceinline__ void stage_chunk_q3(uint16_t* xh, uint16_t* xl, float* xsum, int xs, int cpr, int c,
-                                               const u32x4& v0, const u32x4& v1) {
-  const int t = c / cpr, cc = c % cpr;
+__device__ __forceinline__ void q3_chunk(int cc, const u32x4& v0, const u32x4& v1, u32x4& hp, u32x4& lp,
+                                         float& sx, float& sxm) {
   const uint32_t div8 = q3m_div8_pairs(cc & 3);
   float f[8];
   if constexpr (!kF32) {
@@ -387,7 +386,8 @@ __device__ __forceinline__ void stage_chunk_q3(uint16_t* xh, uint16_t* xl, float
     for (int i = 0; i < 8; ++i) f[i] = __uint_as_float(w[i]);
   }
   uint16_t h[8], l[8];
-  float sx = 0.0f, sxm = 0.0f;
+  sx = 0.0f;
+  sxm = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const bool d8 = (div8 >> (e >> 1)) & 1u;
@@ -403,14 +403,27 @@ __device__ __forceinline__ void stage_chunk_q3(uint16_t* xh, uint16_t* xl, float
       sxm += v;
     }
   }
-  const int off = t * xs + cc * 8;
-  *reinterpret_cast<u32x4*>(xh + off) = pack_bf16x8(h);
-  if constexpr (kF32) *reinterpret_cast<u32x4*>(xl + off) = pack_bf16x8(l);
+  hp = pack_bf16x8(h);
+  if constexpr (kF32) lp = pack_bf16x8(l);
 #pragma unroll
   for (int o = 1; o < 8; o <<= 1) {
     sx += __shfl_xor(sx, o, 8);
     sxm += __shfl_xor(sxm, o, 8);
   }
+}
+
+// q3_chunk of chunk cc of token t's row, staged: the plane(s) at row t of xh
+// (xl), stride xs, and the group sums at xsum[kb][t][h] = {sum x, sum x / m}.
+template <bool kF32>
+__device__ __forceinline__ void stage_chunk_q3(uint16_t* xh, uint16_t* xl, float* xsum, int xs, int cpr, int c,
+                                               const u32x4& v0, const u32x4& v1) {
+  const int t = c / cpr, cc = c % cpr;
+  u32x4 hp, lp;
+  float sx, sxm;
+  q3_chunk<kF32>(cc, v0, v1, hp, lp, sx, sxm);
+  const int off = t * xs + cc * 8;
+  *reinterpret_cast<u32x4*>(xh + off) = hp;
+  if constexpr (kF32) *reinterpret_cast<u32x4*>(xl + off) = lp;
   if ((cc & 7) == 0) {
     const int gi = cc >> 3;
     *reinterpret_cast<float2*>(xsum + (((gi >> 1) * kQ3fMaxTokens + t) * 2 + (gi & 1)) * 2) = float2{sx, sxm};
