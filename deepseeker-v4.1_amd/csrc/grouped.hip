@@ -1153,16 +1153,17 @@ bool up_mx(const dsk_moe_desc& d) {
 
 // h as FP8 planes and the FP4 down on scaled MFMAs: the gate/up on scaled MFMAs
 // (up_mx), I a whole 4, 8 or 16 blocks (down_block_mx's instances), and at most
-// 256 dispatch rows: at 8 and 20 tokens (top-8) the down went 57.9 -> 50.5 and
-// 102.8 -> 88.6 us, at 64 it stayed at 185 us while the planes epilogue added
-// 8.6 us to the gate/up.
+// 512 dispatch rows (measured up to there): at 8 and 20 tokens (top-8) the down
+// went 57.9 -> 50.5 and 102.8 -> 88.6 us; at 64 (once the shared expert's weights
+// streamed once per call) 173.3 -> 157.7 us while the planes epilogue added
+// 11.5 us to the gate/up.
 bool grouped_up_mx(const dsk_moe_desc& d) { return up_mx(d); }
 
 bool grouped_x_q3(const dsk_moe_desc& d) { return up_q3f(d); }
 
 bool grouped_h_planes(const dsk_moe_desc& d) {
   return up_mx(d) && (d.inter == 512 || d.inter == 1024 || d.inter == 2048) &&
-         static_cast<int64_t>(d.tokens) * d.top_k <= 256;
+         static_cast<int64_t>(d.tokens) * d.top_k <= 512;
 }
 
 namespace {
