@@ -704,9 +704,32 @@ __device__ __forceinline__ bool pf_unit_in(const PfArgs& p, int t0, int n, int& 
 
 // The 8-wave kernels' units: every tile, or only the shared expert's when
 // the routed tiles run on the MX kernels.
+// Units of tiles t0 .. t0 + n - 1 in 2-D blocks per XCD: XCD x takes a
+// quarter of the tiles (token tiles) times half the row tiles, so that its
+// workgroups, which run together, share each token tile's activations over
+// RT/2 row tiles and each row tile's weights over n/4 token tiles in its L2
+// (n % 4 == 0, RT % 2 == 0); the 1-D ranges of pf_unit_in share the weights
+// only over the XCD's n/8 token tiles.
+__device__ __forceinline__ bool pf_unit_2d(const PfArgs& p, int t0, int n, int& tile, int& rt) {
+  const int RT = p.row_tiles, R = n * RT;
+  const int b = blockIdx.x;
+  if (b >= R) return false;
+  const int xcd = b & 7, i = b >> 3;
+  const int tn = n >> 2, rn = RT >> 1;   // token tiles and row tiles of an XCD
+  tile = t0 + (xcd & 3) * tn + i / rn;
+  rt = (xcd >> 2) * rn + i % rn;
+  return true;
+}
+
+// The shared expert's units when the MX kernels take every routed tile
+// (2-D per XCD where the shapes allow), else every unit (1-D per XCD).
 __device__ __forceinline__ bool pf_unit(const PfArgs& p, int& tile, int& rt) {
-  return *p.mx_on ? pf_unit_in(p, p.tiles[1], p.tiles[0] - p.tiles[1], tile, rt)
-                  : pf_unit_in(p, 0, p.tiles[0], tile, rt);
+  if (*p.mx_on) {
+    const int n = p.tiles[0] - p.tiles[1];
+    return n % 4 == 0 && p.row_tiles % 2 == 0 ? pf_unit_2d(p, p.tiles[1], n, tile, rt)
+                                               : pf_unit_in(p, p.tiles[1], n, tile, rt);
+  }
+  return pf_unit_in(p, 0, p.tiles[0], tile, rt);
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
