@@ -541,6 +541,8 @@ hipError_t launch_route_dispatch(const dsk_moe_desc& d, const RouteArgs& a, hipS
   return launch_dispatch(d, a.idx, a.weights, a.table, a.out, s);
 }
 
+// Below 16 tokens one-token tiles stay the faster ones (8 tokens: 5.1 us against
+// 8.0-9.2 us for 2 x 4, 4 x 4 and 8 x 4 tiles).
 hipError_t launch_gate_scores(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s) {
   const GateArgs g = route_gate_args(d, a);
   return d.tokens >= 16 ? launch_gate<8, 4, false>(d, g, s) : launch_gate<1, 1, false>(d, g, s);
