@@ -1279,7 +1279,7 @@ hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, con
   hipError_t e;
   if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   for (int r = 0; r < repeat; ++r) {
-    if (p.mx && (e = launch_x_planes(d, p, s)) != hipSuccess) return e;
+    if (p.mx && !a.x_planes_ready && (e = launch_x_planes(d, p, s)) != hipSuccess) return e;
     if (p.q3f && (e = launch_x_q3(d, p, s)) != hipSuccess) return e;
     if (d.quant == DSK_QUANT_Q3) launch_kernel(k_up_grouped<RawQ3>, up_blocks, kGW * 64, ul, s, p);
     else launch_kernel(k_up_grouped<RawFP4>, up_blocks, kGW * 64, ul, s, p);
