@@ -365,10 +365,12 @@ int dsk::forward_layer(const dsk_moe_desc* d, const void* x, const void* gate_w,
   a.scores = scores; a.bias = gate_b;
   a.route = DecodeRoute{idx_buf, w_buf, ra.out.desc, active, ra.rowmap, ra.out.xrow, ra.out.wrow, rank};
   const bool decode = decode_pipeline(*d);
-  // the unfused top-k kernel writes x's FP8 planes for the grouped FP4 gate/up that follows
+  // the unfused top-k kernel writes x in the form the grouped gate/up that follows reads
+  // (FP8 planes for FP4 experts, the factored q3 form for q3 experts)
   if (!decode && d->tokens > kFusedMaxTokens && !rn && d->x_dtype == DSK_DTYPE_BF16 && !prefill_gemm(*d) &&
-      grouped_path(*d) && grouped_up_mx(*d)) {
+      grouped_path(*d) && (grouped_up_mx(*d) || grouped_x_q3(*d))) {
     ra.xp = reinterpret_cast<uint8_t*>(ws + L.xp);
+    ra.xq3 = d->quant == DSK_QUANT_Q3 ? 1 : 0;
     a.x_planes_ready = 1;
   }
   StageTiming timing(ev);

@@ -238,8 +238,9 @@ struct RouteArgs {
   DispatchOut out;
   unsigned int* ctr;        // [tokens + 1] arrival counters (fused path), zero between calls
   int32_t* rowmap;          // decode pipeline: [slot][tokens] token -> dispatch row map
-  uint8_t* xp;              // unfused top-k: also write x's FP8 planes here for the grouped
-                            // FP4 gate/up (Workspace::xp), or null
+  uint8_t* xp;              // unfused top-k: also write x here in the grouped gate/up's
+                            // form (Workspace::xp), or null:
+  int xq3;                  // the factored q3 form, else FP8 planes (FP4)
 };
 // Fused router + dispatch (general path).
 hipError_t launch_route_dispatch(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
@@ -275,7 +276,7 @@ struct ExpertsArgs {
   // decode pipeline: gate scores and selection bias in, routing out
   float* scores; const float* bias;
   DecodeRoute route;
-  int x_planes_ready;        // the routing kernels already wrote x's FP8 planes (RouteArgs::xp)
+  int x_planes_ready;        // the routing kernels already wrote x's FP8 planes / q3 form (RouteArgs::xp)
 };
 
 // Opens the gate/up, down and combine stages as it launches them.

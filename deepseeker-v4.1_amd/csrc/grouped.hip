@@ -376,23 +376,12 @@ __global__ __launch_bounds__(256) void k_x_planes(const uint16_t* __restrict__ x
 }
 
 // x for the factored q3 gate/up (up_block_q3f), once per call instead of once
-// per block: the values at 8q code positions divided by 8 as bf16 [T][H] (xq)
-// and every 64-group's {sum x, sum x / m} [T][H/64] (xg), as q3_chunk makes
-// them; the blocks copy the rows and sums of their column tile.
+// per block (x_q3_chunk); the blocks copy the rows and sums of their column tile.
 __global__ __launch_bounds__(256) void k_x_q3(const uint16_t* __restrict__ x, int T, int H,
                                               uint16_t* __restrict__ xq, float* __restrict__ xg) {
-  const int cpr = H / 8, n = T * cpr;
+  const int n = T * (H / 8);
   const int c = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
-  const int cl = min(c, n - 1);   // every lane takes part in the group's sums (past the end: not stored)
-  const int t = cl / cpr, cc = cl - t * cpr;
-  const int64_t o = static_cast<int64_t>(t) * H + cc * 8;
-  u32x4 hp, lp;
-  float sx, sxm;
-  q3_chunk<false>(cc, ldg16(x + o), u32x4{}, hp, lp, sx, sxm);
-  if (c < n) {
-    *reinterpret_cast<u32x4*>(xq + o) = hp;
-    if ((cc & 7) == 0) *reinterpret_cast<float2*>(xg + (static_cast<int64_t>(t) * (H / 64) + (cc >> 3)) * 2) = float2{sx, sxm};
-  }
+  x_q3_chunk(x, H, min(c, n - 1), c < n, xq, xg);   // every lane takes part in the group's sums
 }
 
 // LDS of up_block_mx: the column tile's planes [H/128][16][128] bytes, then
@@ -1280,7 +1269,7 @@ hipError_t launch_experts_grouped(const dsk_moe_desc& d, const Workspace& L, con
   if ((e = stage_open(kStageUp)) != hipSuccess) return e;
   for (int r = 0; r < repeat; ++r) {
     if (p.mx && !a.x_planes_ready && (e = launch_x_planes(d, p, s)) != hipSuccess) return e;
-    if (p.q3f && (e = launch_x_q3(d, p, s)) != hipSuccess) return e;
+    if (p.q3f && !a.x_planes_ready && (e = launch_x_q3(d, p, s)) != hipSuccess) return e;
     if (d.quant == DSK_QUANT_Q3) launch_kernel(k_up_grouped<RawQ3>, up_blocks, kGW * 64, ul, s, p);
     else launch_kernel(k_up_grouped<RawFP4>, up_blocks, kGW * 64, ul, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;

@@ -412,6 +412,24 @@ __device__ __forceinline__ void q3_chunk(int cc, const u32x4& v0, const u32x4& v
   }
 }
 
+// x for the factored q3 gate/up, chunk c of the T x H bf16 rows (every lane of
+// an aligned 8-lane group takes part; `store` false: the lane only adds to the
+// group's sums): the values at 8q code positions divided by 8 as bf16 [T][H]
+// (xq) and every 64-group's {sum x, sum x / m} [T][H/64] (xg), as q3_chunk
+// makes them.
+__device__ __forceinline__ void x_q3_chunk(const uint16_t* x, int H, int c, bool store, uint16_t* xq, float* xg) {
+  const int cpr = H / 8;
+  const int t = c / cpr, cc = c - t * cpr;
+  const int64_t o = static_cast<int64_t>(t) * H + cc * 8;
+  u32x4 hp, lp;
+  float sx, sxm;
+  q3_chunk<false>(cc, ldg16(x + o), u32x4{}, hp, lp, sx, sxm);
+  if (store) {
+    *reinterpret_cast<u32x4*>(xq + o) = hp;
+    if ((cc & 7) == 0) *reinterpret_cast<float2*>(xg + (static_cast<int64_t>(t) * (H / 64) + (cc >> 3)) * 2) = float2{sx, sxm};
+  }
+}
+
 // q3_chunk of chunk cc of token t's row, staged: the plane(s) at row t of xh
 // (xl), stride xs, and the group sums at xsum[kb][t][h] = {sum x, sum x / m}.
 template <bool kF32>
