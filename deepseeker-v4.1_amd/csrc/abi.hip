@@ -365,13 +365,15 @@ int dsk::forward_layer(const dsk_moe_desc* d, const void* x, const void* gate_w,
   a.scores = scores; a.bias = gate_b;
   a.route = DecodeRoute{idx_buf, w_buf, ra.out.desc, active, ra.rowmap, ra.out.xrow, ra.out.wrow, rank};
   const bool decode = decode_pipeline(*d);
-  // the unfused top-k kernel writes x in the form the grouped gate/up that follows reads
-  // (FP8 planes for FP4 experts, the factored q3 form for q3 experts)
-  if (!decode && d->tokens > kFusedMaxTokens && !rn && d->x_dtype == DSK_DTYPE_BF16 && !prefill_gemm(*d) &&
-      grouped_path(*d) && (grouped_up_mx(*d) || grouped_x_q3(*d))) {
-    ra.xp = reinterpret_cast<uint8_t*>(ws + L.xp);
-    ra.xq3 = d->quant == DSK_QUANT_Q3 ? 1 : 0;
-    a.x_planes_ready = 1;
+  // the unfused top-k kernel writes x in the form the gate/up that follows reads (FP8
+  // planes for FP4 experts, the factored q3 form for q3 experts; prefill: its MX planes)
+  if (!decode && d->tokens > kFusedMaxTokens && !rn && d->x_dtype == DSK_DTYPE_BF16) {
+    const bool pf = prefill_mx(*d);
+    if (pf || (!prefill_gemm(*d) && grouped_path(*d) && (grouped_up_mx(*d) || grouped_x_q3(*d)))) {
+      ra.xp = reinterpret_cast<uint8_t*>(ws + L.xp);
+      ra.xform = pf ? kXPrefillPlanes : d->quant == DSK_QUANT_Q3 ? kXGroupedQ3 : kXGroupedPlanes;
+      a.x_planes_ready = 1;
+    }
   }
   StageTiming timing(ev);
   stage_open(kStageGate);

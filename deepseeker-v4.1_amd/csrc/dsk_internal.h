@@ -230,6 +230,11 @@ hipError_t launch_route(const dsk_moe_desc& d, const void* x, const void* gate_w
 // blocks do the top-k and the dispatch; larger ones as three kernels.
 struct ResNorm;   // resnorm.h: the stack's residual update + RMSNorm, fused into a layer's first kernel
 
+// x as the gate/up after an unfused top-k reads it (written by the top-k's
+// trailing blocks): the grouped FP4 gate/up's FP8 planes, the grouped q3
+// gate/up's factored form, the prefill MX gate/up's FP8 planes.
+enum XForm : int { kXGroupedPlanes = 0, kXGroupedQ3 = 1, kXPrefillPlanes = 2 };
+
 struct RouteArgs {
   const void* x; const void* gate_w; const float* gate_b;
   const ResNorm* rn;        // non-null: the gate kernel computes x itself (resnorm.h)
@@ -238,9 +243,9 @@ struct RouteArgs {
   DispatchOut out;
   unsigned int* ctr;        // [tokens + 1] arrival counters (fused path), zero between calls
   int32_t* rowmap;          // decode pipeline: [slot][tokens] token -> dispatch row map
-  uint8_t* xp;              // unfused top-k: also write x here in the grouped gate/up's
-                            // form (Workspace::xp), or null:
-  int xq3;                  // the factored q3 form, else FP8 planes (FP4)
+  uint8_t* xp;              // unfused top-k: also write x here in the form of the gate/up
+                            // that follows (Workspace::xp), or null:
+  int xform;                // XForm
 };
 // Fused router + dispatch (general path).
 hipError_t launch_route_dispatch(const dsk_moe_desc& d, const RouteArgs& a, hipStream_t s);
@@ -322,6 +327,7 @@ struct PrefillArgs {
   const void* x; const void* ws1; const void* ws3; const void* ws2;
   char* ws;
   float* rows_out;           // per-row outputs instead of the workspace's (or null)
+  int x_planes_ready;        // the routing kernels already wrote x's FP8 planes
 };
 hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, const PrefillArgs& a,
                                   hipStream_t s, int repeat);

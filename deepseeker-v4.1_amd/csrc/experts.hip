@@ -636,7 +636,7 @@ hipError_t launch_experts(const dsk_moe_desc& d, const Workspace& L, const Exper
   const uint16_t* xb_hi = static_cast<const uint16_t*>(a.x);
   const uint16_t* xb_lo = nullptr;
   if (prefill_gemm(d)) {
-    PrefillArgs pa{desc, a.active, xrow, wrow, a.x, a.ws1, a.ws3, a.ws2, a.ws, a.rows_out};
+    PrefillArgs pa{desc, a.active, xrow, wrow, a.x, a.ws1, a.ws3, a.ws2, a.ws, a.rows_out, a.x_planes_ready};
     if ((e = launch_experts_prefill(d, L, pa, s, repeat)) != hipSuccess) return e;
     return a.rows_out ? hipSuccess : launch_combine(d, L, a, s, repeat);
   }

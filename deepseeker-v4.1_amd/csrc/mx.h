@@ -148,4 +148,36 @@ __device__ __forceinline__ void x_planes_chunk(const uint16_t* x, int T, int H, 
   }
 }
 
+// Chunk c (8 values) of x [T][H] bf16 into the prefill MX gate/up's two FP8
+// planes in stage rows: row t holds 2H bytes, each 64-value piece as its 64
+// plane-0 bytes then its 64 plane-1 bytes (q), and one E8M0 byte per (t,
+// 32-group) in ex.  The four chunks of a 32-group must be in four consecutive
+// lanes that all take part; `store` false: the lane takes part and writes
+// nothing.
+__device__ __forceinline__ void pf_planes_chunk(const uint16_t* x, int H, int64_t c, bool store, uint8_t* q,
+                                                uint8_t* ex) {
+  const int cpr = H / 8;
+  const int64_t t = c / cpr;
+  const int k8 = static_cast<int>(c - t * cpr) * 8;
+  const u32x4 v = *reinterpret_cast<const u32x4*>(x + t * H + k8);
+  const float f0[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
+  const float f1[4] = {__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
+                       __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u)};
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(f0[i]), fabsf(f1[i])));
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  const int e = fp8_plane_exp(m);
+  uint32_t w0[2], w1[2];
+  fp8_planes4<2>(f0, e, w0);
+  fp8_planes4<2>(f1, e, w1);
+  if (!store) return;
+  uint8_t* row = q + t * (2 * H) + (k8 >> 6) * 128 + (k8 & 63);
+  *reinterpret_cast<uint2*>(row) = uint2{w0[0], w1[0]};
+  *reinterpret_cast<uint2*>(row + 64) = uint2{w0[1], w1[1]};
+  if ((k8 & 31) == 0) ex[t * (H / 32) + (k8 >> 5)] = static_cast<uint8_t>(e8m0_byte(e));
+}
+
 }  // namespace dsk

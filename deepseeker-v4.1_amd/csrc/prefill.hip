@@ -1081,34 +1081,14 @@ __global__ __launch_bounds__(kMxThreads, 2) void k_pf_mx_down(PfArgs p) {
   }
 }
 
-// x [T][H] bf16 as two FP8 planes in stage rows (the MX gate/up's B tiles):
-// thread c takes 8 values, the four threads of a 32-group are consecutive
-// lanes (H / 8 chunks per row, a multiple of 64, so whole waves leave).
+// x [T][H] bf16 as two FP8 planes in stage rows (the MX gate/up's B tiles),
+// one chunk per thread (pf_planes_chunk; H / 8 chunks per row, a multiple of
+// 64, so whole waves leave).
 __global__ __launch_bounds__(256) void k_pf_planes(const uint16_t* __restrict__ x, int64_t chunks, int H,
                                                   uint8_t* __restrict__ q, uint8_t* __restrict__ ex) {
   const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (c >= chunks) return;
-  const int cpr = H / 8;
-  const int64_t t = c / cpr;
-  const int k8 = static_cast<int>(c - t * cpr) * 8;
-  const u32x4 v = ldg16(x + t * H + k8);
-  const float f0[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
-                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
-  const float f1[4] = {__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
-                       __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u)};
-  float m = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(f0[i]), fabsf(f1[i])));
-  m = fmaxf(m, __shfl_xor(m, 1, 64));
-  m = fmaxf(m, __shfl_xor(m, 2, 64));
-  const int e = fp8_plane_exp(m);
-  uint32_t w0[2], w1[2];
-  fp8_planes4<2>(f0, e, w0);
-  fp8_planes4<2>(f1, e, w1);
-  uint8_t* row = q + t * (2 * H) + (k8 >> 6) * 128 + (k8 & 63);
-  *reinterpret_cast<uint2*>(row) = uint2{w0[0], w1[0]};
-  *reinterpret_cast<uint2*>(row + 64) = uint2{w0[1], w1[1]};
-  if ((k8 & 31) == 0) ex[t * (H / 32) + (k8 >> 5)] = static_cast<uint8_t>(e8m0_byte(e));
+  pf_planes_chunk(x, H, c, true, q, ex);
 }
 
 // Tile list from the dispatch descriptors (one block of 1024 threads; one
@@ -1214,11 +1194,13 @@ hipError_t launch_experts_prefill(const dsk_moe_desc& d, const Workspace& L, con
   const int up_rows = (I > Is ? I : Is) / 128;
   const int64_t x_chunks = static_cast<int64_t>(T) * (H / 8);
   for (int r = 0; r < repeat; ++r) {
-    if (mx) {
+    if (mx && !a.x_planes_ready) {
       launch_kernel(k_pf_planes, static_cast<unsigned>((x_chunks + 255) / 256), 256, 0, s,
                     static_cast<const uint16_t*>(a.x), x_chunks, H, const_cast<uint8_t*>(p.xq),
                     const_cast<uint8_t*>(p.xe));
       if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    if (mx) {
       p.row_tiles = I / 128;
       launch_kernel(k_pf_mx_up, static_cast<unsigned>(max_tiles * p.row_tiles), kMxThreads, kMxLdsBytes, s, p);
       if ((e = hipGetLastError()) != hipSuccess) return e;

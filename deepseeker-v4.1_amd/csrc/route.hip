@@ -51,7 +51,7 @@ struct GateArgs {
   unsigned int* ctr;
   ResNorm rn; int norm;     // norm: x is h + d normalised here (resnorm.h); block 0 writes it out
   uint8_t* xp;              // k_topk: also write x for the grouped gate/up here, or null:
-  int xq3;                  // the factored q3 form (x_q3_chunk), else FP8 planes (x_planes_chunk)
+  int xform;                // XForm
 };
 
 // Byte offset of the normalised rows in k_gate's LDS (after the segment sums and flags).
@@ -114,24 +114,28 @@ __global__ __launch_bounds__(256) void k_gate(GateArgs g) {
 }
 
 // One wave per token: biased top-k + normalised weights (unfused path).
-// With xp, the blocks after the top-k's ((T + 3) / 4) write x in the grouped
-// gate/up's form, one 8-value chunk per thread: FP8 planes for FP4 experts
-// (k_x_planes' work), the factored q3 form with q3 (k_x_q3's), without a
-// launch of their own.
+// With xp, the blocks after the top-k's ((T + 3) / 4) write x in the form
+// of the gate/up that follows, one 8-value chunk per thread (XForm: the work
+// of k_x_planes, k_x_q3 or k_pf_planes, without a launch of its own).
 __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ scores,
                                               const float* __restrict__ bias, int T, int E,
                                               int k, float route_scale,
                                               int32_t* __restrict__ idx,
                                               float* __restrict__ weights, const uint16_t* __restrict__ x,
-                                              int H, uint8_t* __restrict__ xp, int q3) {
+                                              int H, uint8_t* __restrict__ xp, int form) {
   const int tb = (T + 3) / 4;
   if (static_cast<int>(blockIdx.x) >= tb) {
     const int n = T * (H / 8);
     const int c = (static_cast<int>(blockIdx.x) - tb) * 256 + static_cast<int>(threadIdx.x);
     // every lane takes part in the group exchange / sums
-    if (q3) x_q3_chunk(x, H, min(c, n - 1), c < n, reinterpret_cast<uint16_t*>(xp),
-                       reinterpret_cast<float*>(xp + static_cast<size_t>(T) * H * 2));
-    else x_planes_chunk(x, T, H, min(c, n - 1), c < n, xp);
+    const size_t plane_bytes = static_cast<size_t>(T) * H * 2;
+    if (form == kXGroupedQ3)
+      x_q3_chunk(x, H, min(c, n - 1), c < n, reinterpret_cast<uint16_t*>(xp),
+                 reinterpret_cast<float*>(xp + plane_bytes));
+    else if (form == kXPrefillPlanes)
+      pf_planes_chunk(x, H, min(c, n - 1), c < n, xp, xp + plane_bytes);
+    else
+      x_planes_chunk(x, T, H, min(c, n - 1), c < n, xp);
     return;
   }
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -419,7 +423,7 @@ hipError_t launch_route_unfused(const dsk_moe_desc& d, const GateArgs& g, hipStr
   const int64_t chunks = static_cast<int64_t>(d.tokens) * (d.hidden / 8);
   const unsigned blocks = static_cast<unsigned>((d.tokens + 3) / 4 + (g.xp ? (chunks + 255) / 256 : 0));
   launch_kernel(k_topk, blocks, 256, 0, s, g.scores, g.bias, d.tokens, d.n_experts, d.top_k, d.route_scale,
-                g.idx, g.weights, static_cast<const uint16_t*>(g.x), d.hidden, g.xp, g.xq3);
+                g.idx, g.weights, static_cast<const uint16_t*>(g.x), d.hidden, g.xp, g.xform);
   return hipGetLastError();
 }
 
@@ -544,7 +548,7 @@ GateArgs route_gate_args(const dsk_moe_desc& d, const RouteArgs& a) {
   g.out = a.out;
   g.ctr = a.ctr;
   g.xp = a.xp;
-  g.xq3 = a.xq3;
+  g.xform = a.xform;
   if (a.rn) {
     g.rn = *a.rn;
     g.norm = 1;
