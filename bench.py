@@ -183,8 +183,9 @@ def measured_traffic(kernels: list[str], workload: str):
 
 def pf_up_kernels(quant: str) -> list[str]:
     """The prefill gate/up stage's kernels: FP4 layers of the full shape run the
-    x planes, the routed MX tiles and the shared expert's bf16 tiles."""
-    return ["k_pf_planes", "k_pf_mx_up", "k_pf_up"] if quant == "fp4" else ["k_pf_up"]
+    routed MX tiles and the shared expert's bf16 tiles (x's FP8 planes are
+    written by the top-k kernel of the route stage)."""
+    return ["k_pf_mx_up", "k_pf_up"] if quant == "fp4" else ["k_pf_up"]
 
 
 def traffic_fields(kernels: list[str], workload: str) -> dict:
@@ -595,8 +596,8 @@ def main() -> int:
         roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 1), "peak": PEAK_BF16 / 1e12,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4),
                     **traffic_fields(pf_up_kernels(args.quant), workload),
-                    "kernel": ("gate/up stage: k_pf_planes (x as FP8 planes) + k_pf_mx_up (routed FP4 w1/w3 on "
-                               "scaled FP4 x FP8 MFMAs) + k_pf_up (shared bf16 w1/w3), SwiGLU epilogues"
+                    "kernel": ("gate/up stage: k_pf_mx_up (routed FP4 w1/w3 on scaled FP4 x FP8 MFMAs, x as "
+                               "FP8 planes from the top-k kernel) + k_pf_up (shared bf16 w1/w3), SwiGLU epilogues"
                                if args.quant == "fp4" else
                                f"k_pf_up (routed {args.quant.upper()} + shared bf16 w1/w3 GEMM tiles, SwiGLU epilogue)"),
                     "flops_per_launch": int(up_flops(T)), "avg_launch_us": up_us, "timing": timing}
