@@ -171,16 +171,19 @@ def test_captured_stack_keeps_its_workspace():
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {rep}"
 
 
-@pytest.mark.parametrize("case", ["mx-T1", "mx-T2", "q3-T1", "fp4-small-T2", "inplace-T1", "unfused-T5"])
+@pytest.mark.parametrize("case", ["mx-T1", "mx-T2", "q3-T1", "fp4-small-T2", "inplace-T1", "unfused-T5",
+                                  "fp4full-T64", "q3-T40", "unfused-T24"])
 def test_forward_residual_equals_rmsnorm_then_layer(case):
     """dsk_moe_forward_residual against dsk_rmsnorm + dsk_moe_forward: h_out, x_out
     and the layer output bit for bit.  The MX pipeline (FP4, inter 2048) and the
     gate kernel of the other decode configurations take the update into their
-    first kernel; in place (h_out = h) and at five tokens it runs as its own kernel."""
+    first kernel; in place (h_out = h) and from five tokens it runs as its own kernel.
+    From 9 tokens the reference call's top-k kernel also writes x's FP8 planes (or
+    the q3 form) for the grouped gate/up, the residual call a kernel of their own."""
     print(f"forward_residual {case}", flush=True)
     kind, T = case.rsplit("-T", 1)
     T = int(T)
-    if kind in ("mx", "inplace"):
+    if kind in ("mx", "inplace", "fp4full"):
         layer = gsynth.make_layer(hidden=4096, n_experts=256, top_k=8, inter=2048, inter_shared=2048,
                                   seed=900 + T, device=DEV)
     elif kind == "q3":
