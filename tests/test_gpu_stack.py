@@ -172,14 +172,15 @@ def test_captured_stack_keeps_its_workspace():
 
 
 @pytest.mark.parametrize("case", ["mx-T1", "mx-T2", "q3-T1", "fp4-small-T2", "inplace-T1", "unfused-T5",
-                                  "fp4full-T64", "q3-T40", "unfused-T24"])
+                                  "fp4full-T64", "q3-T40", "unfused-T24", "fp4full-T160"])
 def test_forward_residual_equals_rmsnorm_then_layer(case):
     """dsk_moe_forward_residual against dsk_rmsnorm + dsk_moe_forward: h_out, x_out
     and the layer output bit for bit.  The MX pipeline (FP4, inter 2048) and the
     gate kernel of the other decode configurations take the update into their
     first kernel; in place (h_out = h) and from five tokens it runs as its own kernel.
     From 9 tokens the reference call's top-k kernel also writes x's FP8 planes (or
-    the q3 form) for the grouped gate/up, the residual call a kernel of their own."""
+    the q3 form) for the grouped gate/up (from 128 tokens for the prefill GEMM), the
+    residual call a kernel of their own."""
     print(f"forward_residual {case}", flush=True)
     kind, T = case.rsplit("-T", 1)
     T = int(T)
